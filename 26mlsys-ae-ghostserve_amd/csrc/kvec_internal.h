@@ -36,6 +36,50 @@ __device__ __forceinline__ void st16(uint8_t* p, u32x4 v) {
     *reinterpret_cast<u32x4*>(p) = v;
 }
 
+// ------------------------------------------------------------- shard views
+// One shard buffer seen by a kernel.  Shards below 4 GiB use a buffer
+// resource: the row-plane offset rides in an SGPR (soffset), the lane offset
+// in one VGPR, and there is no 64-bit address arithmetic per access.  Larger
+// shards use 64-bit global addressing.  Loads are non-temporal (every byte is
+// read once per launch); stores carry sc0 sc1, which measured fastest for the
+// write streams of these kernels on MI355X.
+constexpr int kAuxLoadNT = 2;        // nt
+constexpr int kAuxStoreSC01 = 17;    // sc0 | sc1
+constexpr uint32_t kBufWord3 = 0x00020000;
+
+template <bool BUF>
+struct ShardView;
+
+template <>
+struct ShardView<true> {
+    __amdgpu_buffer_rsrc_t rs;
+    __device__ __forceinline__ ShardView(const uint8_t* p, uint64_t nbytes)
+        : rs(__builtin_amdgcn_make_buffer_rsrc((void*)p, (short)0, (int)(uint32_t)nbytes,
+                                               (int)kBufWord3)) {}
+    __device__ __forceinline__ u32x4 load(uint64_t row_off, uint32_t lane_off) const {
+        return __builtin_bit_cast(
+            u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, lane_off, (uint32_t)row_off, kAuxLoadNT));
+    }
+    __device__ __forceinline__ void store(uint64_t row_off, uint32_t lane_off, u32x4 v) const {
+        __builtin_amdgcn_raw_buffer_store_b128(v, rs, lane_off, (uint32_t)row_off, kAuxStoreSC01);
+    }
+};
+
+template <>
+struct ShardView<false> {
+    uint8_t* p;
+    __device__ __forceinline__ ShardView(const uint8_t* q, uint64_t) : p((uint8_t*)q) {}
+    __device__ __forceinline__ u32x4 load(uint64_t row_off, uint32_t lane_off) const {
+        return ld_stream(p + row_off, lane_off);
+    }
+    __device__ __forceinline__ void store(uint64_t row_off, uint32_t lane_off, u32x4 v) const {
+        st_stream(p + row_off, lane_off, v);
+    }
+};
+
+// A buffer resource addresses at most 2^32 - 1 bytes.
+inline bool fits_buffer(uint64_t nbytes) { return nbytes < (uint64_t(1) << 32); }
+
 // ------------------------------------------------------------- fast u32 div
 // Division of a 32-bit unsigned value by a run-time invariant divisor
 // (Granlund & Montgomery, "Division by invariant integers using

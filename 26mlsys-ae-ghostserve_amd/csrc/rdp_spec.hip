@@ -22,7 +22,6 @@ constexpr int kRdpMaxRows = kRdpMaxP - 1;
 constexpr int kRdpMaxShards = kRdpMaxP + 1;  // k+2 with k <= p-1
 constexpr int kRdpMaxOut = 2 * kRdpMaxRows;
 constexpr int kRdpNW = (kRdpMaxShards * kRdpMaxRows + 63) / 64;
-constexpr int kThreads = 256;
 
 typedef Ptrs<kRdpMaxShards> RdpPtrs;
 
@@ -129,75 +128,103 @@ constexpr RdpPlan make_rdp_plan(int P, int K, int e0, int e1) {
 }
 
 // ---------------------------------------------------------------- encode
-template <int P, int K>
-__global__ __launch_bounds__(kThreads) void rdp_encode_kernel(RdpPtrs d, uint8_t* __restrict__ Pp,
-                                                              uint8_t* __restrict__ Qp, uint64_t R,
-                                                              uint32_t nvec) {
-    constexpr int ROWS = P - 1;
-    const uint32_t u = blockIdx.x * kThreads + threadIdx.x;
-    if (u >= nvec) return;
-    const uint32_t off = u << 4;
-    u32x4 pr[ROWS], q[ROWS];
+// A block of kBS threads covers kBS*V consecutive 16-byte lane offsets of
+// every row plane (V = 2 for p <= 7, 1 above to bound register use); each
+// load instruction of a wave reads 1 KiB contiguous from one row plane.
+constexpr int kBS = 128;
+constexpr int rdp_vec(int P) { return P <= 7 ? 2 : 1; }
+
+template <int P, int K, bool BUF>
+__global__ __launch_bounds__(kBS) void rdp_encode_kernel(RdpPtrs d, uint8_t* __restrict__ Pp,
+                                                         uint8_t* __restrict__ Qp, uint64_t R,
+                                                         uint32_t nvec) {
+    constexpr int ROWS = P - 1, V = rdp_vec(P);
+    const uint64_t nb = ROWS * R;
+    const uint32_t u0 = blockIdx.x * (kBS * V) + threadIdx.x;
+    u32x4 pr[V][ROWS], q[V][ROWS];
 #pragma unroll
-    for (int r = 0; r < ROWS; ++r) {
-        pr[r] = u32x4{0, 0, 0, 0};
-        q[r] = u32x4{0, 0, 0, 0};
-    }
-#pragma unroll
-    for (int j = 0; j < K; ++j) {
+    for (int v = 0; v < V; ++v)
 #pragma unroll
         for (int r = 0; r < ROWS; ++r) {
-            const u32x4 x = ld_stream(d.p[j] + r * R, off);
-            pr[r] ^= x;
-            const int dg = (r + j) % P;
-            if (dg != P - 1) q[dg] ^= x;
+            pr[v][r] = u32x4{0, 0, 0, 0};
+            q[v][r] = u32x4{0, 0, 0, 0};
         }
+#pragma unroll
+    for (int j = 0; j < K; ++j) {
+        const ShardView<BUF> sv(d.p[j], nb);
+#pragma unroll
+        for (int r = 0; r < ROWS; ++r)
+#pragma unroll
+            for (int v = 0; v < V; ++v) {
+                const uint32_t u = u0 + v * kBS;
+                // lanes past the end read the plane start; their sums are dropped
+                const u32x4 x = sv.load(r * R, (u < nvec ? u : 0u) << 4);
+                pr[v][r] ^= x;
+                const int dg = (r + j) % P;
+                if (dg != P - 1) q[v][dg] ^= x;
+            }
     }
-    // P cell of row r lies on diagonal (r + p - 1) % p = r - 1.
+    const ShardView<BUF> sp(Pp, nb), sq(Qp, nb);
 #pragma unroll
-    for (int r = 1; r < ROWS; ++r) q[r - 1] ^= pr[r];
+    for (int v = 0; v < V; ++v) {
+        const uint32_t u = u0 + v * kBS;
+        if (u >= nvec) continue;
+        // P cell of row r lies on diagonal (r + p - 1) % p = r - 1.
 #pragma unroll
-    for (int r = 0; r < ROWS; ++r) {
-        st_stream(Pp + r * R, off, pr[r]);
-        st_stream(Qp + r * R, off, q[r]);
+        for (int r = 1; r < ROWS; ++r) q[v][r - 1] ^= pr[v][r];
+#pragma unroll
+        for (int r = 0; r < ROWS; ++r) {
+            sp.store(r * R, u << 4, pr[v][r]);
+            sq.store(r * R, u << 4, q[v][r]);
+        }
     }
 }
 
 // ---------------------------------------------------------------- decode
-template <int P, int K, int E0, int E1>
-__global__ __launch_bounds__(kThreads) void rdp_decode_kernel(RdpPtrs sh, uint64_t R,
-                                                              uint32_t nvec) {
-    constexpr int ROWS = P - 1;
+template <int P, int K, int E0, int E1, bool BUF>
+__global__ __launch_bounds__(kBS) void rdp_decode_kernel(RdpPtrs sh, uint64_t R, uint32_t nvec) {
+    constexpr int ROWS = P - 1, V = rdp_vec(P);
     constexpr int NC = (K + 2) * ROWS;
     constexpr RdpPlan plan = make_rdp_plan(P, K, E0, E1);
     static_assert(plan.ok, "RDP erasure pattern not decodable");
-    const uint32_t u = blockIdx.x * kThreads + threadIdx.x;
-    if (u >= nvec) return;
-    const uint32_t off = u << 4;
-    u32x4 acc[plan.nout];
+    const uint64_t nb = ROWS * R;
+    const uint32_t u0 = blockIdx.x * (kBS * V) + threadIdx.x;
+    u32x4 acc[V][plan.nout];
 #pragma unroll
-    for (int o = 0; o < plan.nout; ++o) acc[o] = u32x4{0, 0, 0, 0};
+    for (int v = 0; v < V; ++v)
+#pragma unroll
+        for (int o = 0; o < plan.nout; ++o) acc[v][o] = u32x4{0, 0, 0, 0};
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
         if (!((plan.need[c >> 6] >> (c & 63)) & 1)) continue;
-        const u32x4 x = ld_stream(sh.p[c / ROWS] + (c % ROWS) * R, off);
+        const ShardView<BUF> sv(sh.p[c / ROWS], nb);
 #pragma unroll
-        for (int o = 0; o < plan.nout; ++o)
-            if ((plan.mask[o][c >> 6] >> (c & 63)) & 1) acc[o] ^= x;
+        for (int v = 0; v < V; ++v) {
+            const uint32_t u = u0 + v * kBS;
+            const u32x4 x = sv.load((c % ROWS) * R, (u < nvec ? u : 0u) << 4);
+#pragma unroll
+            for (int o = 0; o < plan.nout; ++o)
+                if ((plan.mask[o][c >> 6] >> (c & 63)) & 1) acc[v][o] ^= x;
+        }
     }
 #pragma unroll
-    for (int o = 0; o < plan.nout; ++o) {
-        const int c = plan.out_cell[o];
-        st_stream(sh.p[c / ROWS] + (c % ROWS) * R, off, acc[o]);
+    for (int v = 0; v < V; ++v) {
+        const uint32_t u = u0 + v * kBS;
+        if (u >= nvec) continue;
+#pragma unroll
+        for (int o = 0; o < plan.nout; ++o) {
+            const int c = plan.out_cell[o];
+            const ShardView<BUF> sv(sh.p[c / ROWS], nb);
+            sv.store((c % ROWS) * R, u << 4, acc[v][o]);
+        }
     }
 }
 
 // Same map, read from the kernel argument: one output cell at a time, so the
 // accumulator stays a single register (re-read inputs hit L2).
-__global__ __launch_bounds__(kThreads) void rdp_decode_generic_kernel(RdpPtrs sh, RdpPlan plan,
-                                                                      int rows, uint64_t R,
-                                                                      uint32_t nvec) {
-    const uint32_t u = blockIdx.x * kThreads + threadIdx.x;
+__global__ __launch_bounds__(kBS) void rdp_decode_generic_kernel(RdpPtrs sh, RdpPlan plan, int rows,
+                                                                 uint64_t R, uint32_t nvec) {
+    const uint32_t u = blockIdx.x * kBS + threadIdx.x;
     if (u >= nvec) return;
     const uint32_t off = u << 4;
     for (int o = 0; o < plan.nout; ++o) {
@@ -219,56 +246,62 @@ __global__ __launch_bounds__(kThreads) void rdp_decode_generic_kernel(RdpPtrs sh
 typedef void (*EncFn)(RdpPtrs, uint8_t*, uint8_t*, uint64_t, uint32_t);
 typedef void (*DecFn)(RdpPtrs, uint64_t, uint32_t);
 
-template <int P, int K = 1>
+template <int P, bool BUF, int K = 1>
 EncFn pick_encode(int k) {
     if constexpr (K > P - 1) {
         return nullptr;
     } else {
-        if (k == K) return &rdp_encode_kernel<P, K>;
-        return pick_encode<P, K + 1>(k);
+        if (k == K) return &rdp_encode_kernel<P, K, BUF>;
+        return pick_encode<P, BUF, K + 1>(k);
     }
 }
 
+template <bool BUF>
 static EncFn encode_fn(int p, int k) {
     switch (p) {
-        case 3: return pick_encode<3>(k);
-        case 5: return pick_encode<5>(k);
-        case 7: return pick_encode<7>(k);
-        case 11: return pick_encode<11>(k);
-        case 13: return pick_encode<13>(k);
+        case 3: return pick_encode<3, BUF>(k);
+        case 5: return pick_encode<5, BUF>(k);
+        case 7: return pick_encode<7, BUF>(k);
+        case 11: return pick_encode<11, BUF>(k);
+        case 13: return pick_encode<13, BUF>(k);
         default: return nullptr;
     }
 }
 
-template <int P, int K, int E0, int E1>
+template <int P, int K, bool BUF, int E0, int E1>
 DecFn pick_decode_pair(int e1) {
     if constexpr (E1 > K + 1) {
         return nullptr;
     } else {
-        if (e1 == E1) return &rdp_decode_kernel<P, K, E0, E1>;
-        return pick_decode_pair<P, K, E0, E1 + 1>(e1);
+        if (e1 == E1) return &rdp_decode_kernel<P, K, E0, E1, BUF>;
+        return pick_decode_pair<P, K, BUF, E0, E1 + 1>(e1);
     }
 }
 
-template <int P, int K, int E0 = 0>
+template <int P, int K, bool BUF, int E0 = 0>
 DecFn pick_decode(int e0, int e1) {
     if constexpr (E0 > K + 1) {
         return nullptr;
     } else {
         if (e0 == E0) {
-            if (e1 < 0) return &rdp_decode_kernel<P, K, E0, -1>;
-            return pick_decode_pair<P, K, E0, E0 + 1>(e1);
+            if (e1 < 0) return &rdp_decode_kernel<P, K, E0, -1, BUF>;
+            return pick_decode_pair<P, K, BUF, E0, E0 + 1>(e1);
         }
-        return pick_decode<P, K, E0 + 1>(e0, e1);
+        return pick_decode<P, K, BUF, E0 + 1>(e0, e1);
     }
 }
 
-// Compile-time XOR networks are built for the full-width codes p = 3, 5, 7.
+// Compile-time XOR networks are built for the full-width codes p = 3, 5, 7
+// (shards below 4 GiB); everything else takes the generic kernel.
 static DecFn decode_fn(int p, int k, int e0, int e1) {
-    if (p == 7 && k == 6) return pick_decode<7, 6>(e0, e1);
-    if (p == 5 && k == 4) return pick_decode<5, 4>(e0, e1);
-    if (p == 3 && k == 2) return pick_decode<3, 2>(e0, e1);
+    if (p == 7 && k == 6) return pick_decode<7, 6, true>(e0, e1);
+    if (p == 5 && k == 4) return pick_decode<5, 4, true>(e0, e1);
+    if (p == 3 && k == 2) return pick_decode<3, 2, true>(e0, e1);
     return nullptr;
+}
+
+static unsigned rdp_grid(uint32_t nvec, int p) {
+    return blocks_for(nvec, kBS * rdp_vec(p));
 }
 
 static int check_geom(int k, int p, int64_t row_bytes, const char* fn) {
@@ -301,10 +334,11 @@ extern "C" int kvec_rdp_encode(const void* const* data, int k, void* P, void* Q,
     if (!aligned16(P) || !aligned16(Q))
         return set_error(KVEC_EINVAL, "kvec_rdp_encode: P/Q not 16-byte aligned");
     if (row_bytes == 0) return KVEC_OK;
-    EncFn fn = encode_fn(p, k);
+    const bool buf = fits_buffer(uint64_t(p - 1) * uint64_t(row_bytes));
+    EncFn fn = buf ? encode_fn<true>(p, k) : encode_fn<false>(p, k);
     if (!fn) return set_error(KVEC_EUNSUPPORTED, "kvec_rdp_encode: p=%d k=%d not built", p, k);
     const uint32_t nvec = uint32_t(row_bytes / 16);
-    hipLaunchKernelGGL(fn, dim3(blocks_for(nvec, kThreads)), dim3(kThreads), 0, as_stream(stream), d,
+    hipLaunchKernelGGL(fn, dim3(rdp_grid(nvec, p)), dim3(kBS), 0, as_stream(stream), d,
                        (uint8_t*)P, (uint8_t*)Q, uint64_t(row_bytes), nvec);
     return check_launch("kvec_rdp_encode");
 }
@@ -329,10 +363,13 @@ extern "C" int kvec_rdp_decode(void* const* shards, int k, int p, int64_t row_by
     if (b >= 0 && b < a) { int t = a; a = b; b = t; }
     if (a < 0 || row_bytes == 0) return KVEC_OK;
     const uint32_t nvec = uint32_t(row_bytes / 16);
-    const dim3 grid(blocks_for(nvec, kThreads)), block(kThreads);
-    if (DecFn fn = decode_fn(p, k, a, b)) {
-        hipLaunchKernelGGL(fn, grid, block, 0, as_stream(stream), s, uint64_t(row_bytes), nvec);
+    const bool buf = fits_buffer(uint64_t(p - 1) * uint64_t(row_bytes));
+    DecFn fn = buf ? decode_fn(p, k, a, b) : nullptr;
+    if (fn) {
+        hipLaunchKernelGGL(fn, dim3(rdp_grid(nvec, p)), dim3(kBS), 0, as_stream(stream), s,
+                           uint64_t(row_bytes), nvec);
     } else {
+        const dim3 grid(blocks_for(nvec, kBS)), block(kBS);
         RdpPlan plan = make_rdp_plan(p, k, a, b);
         if (!plan.ok)
             return set_error(KVEC_EDECODE, "kvec_rdp_decode: pattern (%d, %d) not decodable", a, b);

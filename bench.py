@@ -8,6 +8,9 @@ N(0,1) values from a seed.  One step = one encode of the whole chunk from its
 six data shard buffers (inputs resident in HBM) into the P and Q buffers.  Two
 buffer sets alternate so the 256 MB MALL cannot serve repeats.
 
+The 2-erasure decode of the same stripe set (all 28 shard pairs, each
+byte-compared against the originals at full size) is reported alongside.
+
 Algorithmic bytes per step = 536,870,912 read + 178,956,971 written
 = 715,827,883 B; `value` is that over the wall time of the timed steps, and
 `roofline.achieved` is that over the average kernel duration from HIP events
@@ -33,6 +36,21 @@ STREAM_BYTES = L * 2 * B * T * H * D * ES          # 536,870,912
 P_RDP, K_RDP = 7, 6
 PARITY_BYTES = -(-2 * STREAM_BYTES // K_RDP)        # 178,956,971 (2 of k=6 shards)
 ALG_BYTES = STREAM_BYTES + PARITY_BYTES             # 715,827,883
+
+
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "rdp_encode_p7k6_hbm_bytes.md")
+
+
+def measured_traffic():
+    """HBM bytes per encode launch from the committed rocprofv3 FETCH_SIZE /
+    WRITE_SIZE summary (calibrated against a copy of known size), or None."""
+    try:
+        for line in open(TRAFFIC_PROFILE):
+            if line.startswith("traffic_bytes_per_launch"):
+                return int(line.split("=")[1])
+    except OSError:
+        pass
+    return None
 
 
 def log(msg):
@@ -93,12 +111,44 @@ def time_kernel(torch, fn, sets, steps, warmup):
     return wall, kms
 
 
+def decode_all_pairs(pkg, torch, sets, R, seed):
+    """2-erasure decode of every shard pair, in a seeded order: zero the two
+    shards, decode, byte-compare against the originals at full size, then time
+    the decode on both buffer sets.  Returns per-pair kernel microseconds."""
+    import itertools
+    import random
+    pairs = list(itertools.combinations(range(K_RDP + 2), 2))
+    random.Random(seed).shuffle(pairs)
+    stream = torch.cuda.current_stream()
+    times = {}
+    for a, b in pairs:
+        for data, P, Q in sets:
+            shards = list(data) + [P, Q]
+            keep = [shards[a].clone(), shards[b].clone()]
+            shards[a].zero_()
+            shards[b].zero_()
+            pkg.spec.rdp_decode(shards, P_RDP, [a, b], R)
+            if not (torch.equal(shards[a], keep[0]) and torch.equal(shards[b], keep[1])):
+                raise RuntimeError(f"RDP decode of pair ({a}, {b}) is not byte-exact")
+            del keep
+        evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+               for _ in range(4)]
+        for i, (e0, e1) in enumerate(evs):
+            data, P, Q = sets[i % 2]
+            e0.record(stream)
+            pkg.spec.rdp_decode(list(data) + [P, Q], P_RDP, [a, b], R)
+            e1.record(stream)
+        torch.cuda.synchronize()
+        times[(a, b)] = sum(x.elapsed_time(y) for x, y in evs) * 1e3 / len(evs)
+    return times
+
+
 def cpu_baseline(oracle, torch, data, R, budget_s=10.0):
     import numpy as np
     host = [np.ascontiguousarray(d.cpu().numpy().reshape(P_RDP - 1, R)) for d in data]
     n, t = 0, 0.0
     t0 = time.perf_counter()
-    while t < budget_s and n < 200:
+    while t < budget_s:
         oracle.rdp_encode(host, P_RDP)
         n += 1
         t = time.perf_counter() - t0
@@ -120,6 +170,10 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-decode", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="also run three 256 MiB device copies (reference kernel of known "
+                         "size for HBM byte counters)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (the coding path runs on one GPU's "
@@ -154,6 +208,32 @@ def main():
     log(f"[bench] encode: wall {ms_step * 1e3:.1f} us/step, kernel {kavg * 1e3:.1f} us "
         f"(min {min(kms) * 1e3:.1f}) -> {achieved:.0f} GB/s")
 
+    dec_out = None
+    if not args.no_decode:
+        log("[bench] decode: all 28 erasure pairs, byte-exact round trip at full size")
+        dec = decode_all_pairs(pkg, torch, sets, R, args.seed)
+        dec_us = sum(dec.values()) / len(dec)
+        worst = max(dec, key=dec.get)
+        log(f"[bench] decode: mean {dec_us:.1f} us -> {ALG_BYTES / dec_us / 1e3:.0f} GB/s; "
+            f"slowest {worst} {dec[worst]:.1f} us")
+        dec_out = {
+            "pairs": len(dec),
+            "byte_exact": True,
+            "mean_us": round(dec_us, 2),
+            "gbs": round(ALG_BYTES / dec_us / 1e3, 2),
+            "frac_hbm_peak": round(ALG_BYTES / dec_us / 1e3 / HBM_PEAK_GBS, 4),
+            "slowest_pair": list(worst),
+            "slowest_us": round(dec[worst], 2),
+        }
+
+    if args.copy_calibration:
+        src = torch.empty(1 << 28, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
+
     cpu = None
     if not args.no_cpu_baseline:
         log("[bench] timing CPU oracle baseline")
@@ -186,9 +266,10 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": measured_traffic(),
         },
         "cpu_baseline": cpu,
+        "decode_2erasure": dec_out,
     }
     print(json.dumps(out), flush=True)
 
