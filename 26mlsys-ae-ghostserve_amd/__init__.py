@@ -4,11 +4,15 @@ Hand-written gfx950 HIP kernels behind the C ABI of ``libkvec.so``
 (include/kvec.h), with Python entry points that keep the reference's names and
 signatures:
 
+  xor         XOR single parity           (benchmark/xor/main.py)
+  rdp         star-diagonal P/Q "RDP"     (benchmark/rdp/main.py)
+  rs          Reed-Solomon over GF(2^16)  (benchmark/rs/main.py)
+  rdp_kv_ops  the serving plugin's inline extension (bench_ghostserve_rdp.py)
   spec        textbook RDP over a prime p, RS over GF(2^8) (stripe configs)
 
 Import the package with ``importlib.import_module("26mlsys-ae-ghostserve_amd")``
 (the directory name is not a Python identifier).
 """
-from . import _lib, spec  # noqa: F401
+from . import _lib, rdp, rdp_kv_ops, rs, spec, xor  # noqa: F401
 
-__all__ = ["spec"]
+__all__ = ["xor", "rdp", "rs", "rdp_kv_ops", "spec"]

@@ -31,6 +31,19 @@ SIGNATURES = {
     "kvec_rdp_encode": (_i, [_pp, _i, _vp, _vp, _i, _i64, _vp]),
     "kvec_rdp_decode": (_i, [_pp, _i, _i, _i64, _i, _i, _vp]),
     "kvec_rdp_row_bytes": (_i64, [_i64, _i, _i, _i64]),
+    "kvec_xor_encode": (_i, [_vp, _vp, _i, _i64, _vp]),
+    "kvec_xor_reconstruct": (_i, [_vp, _vp, _vp, _i64, _i, _vp, _i, _vp]),
+    "kvec_pack_kv": (_i, [_vp, _vp, _vp, _i, _i, _vp]),
+    "kvec_unpack_kv": (_i, [_vp, _vp, _i, _i, _vp]),
+    "kvec_gs_rdp_backup": (_i, [_vp, _vp, _vp, _i, _i, _i, _i, _i, _vp]),
+    "kvec_gs_rdp_recover": (_i, [_vp, _vp, _i, _i, _i, _i, _i, _i, _i, _vp]),
+    "kvec_gs_pack_row": (_i, [_vp, _vp, _vp, _i64, _i, _i64, _vp]),
+    "kvec_gs_rdp_parity": (_i, [_vp, _i, _i, _i, _vp]),
+    "kvec_rs16_pack": (_i, [_vp, _vp, _vp, _i64, _i64, _vp]),
+    "kvec_rs16_split": (_i, [_vp, _vp, _vp, _i64, _i64, _vp]),
+    "kvec_rs16_encode": (_i, [_vp, _vp, _i, _i, _i, _vp, _vp, _vp]),
+    "kvec_rs16_reconstruct": (_i, [_vp, _i, _i, _i, _vp, _i, _vp, _vp, _vp, _vp]),
+    "kvec_gf16_tables": (_i, [_vp, _vp]),
 }
 
 _lib = None

@@ -1,0 +1,316 @@
+// gs_xor_rdp.hip -- the reference's XOR and star-diagonal "RDP" codes,
+// bit-exact, on its packed [(rows), S] shard tensors.
+//
+//   XOR  benchmark/xor/kernel.cu:17-88 (+ pack/unpack :93-146 as copies)
+//   RDP  benchmark/rdp/kernel.cu:32-345 and bench_ghostserve_rdp.py:105-150
+//
+// The column work runs on the tile engine (tile_engine.h).  The diagonal
+// parity Q[d] = XOR_r D_r[(d - r) mod S] is formed without the per-row star
+// skip; a one-thread fix-up then XORs each row's star word back out of its
+// diagonal, which gives the reference's skip exactly (XOR is its own inverse)
+// without a per-word test in the streaming kernel.
+#include "tile_engine.h"
+
+namespace kvec {
+
+// ----------------------------------------------------------------- XOR rows
+// out[c] = XOR of in rows {lo..hi-1} \ {skip}, plus row `extra` when >= 0.
+struct RowSet {
+    int lo, hi, skip, extra;
+};
+
+__device__ __forceinline__ u32x4 xor_rows_window(const uint8_t* in, uint64_t Sb, RowSet rs,
+                                                 uint64_t c0) {
+    u32x4 acc = {0, 0, 0, 0};
+    for (int r = rs.lo; r < rs.hi; ++r)
+        if (r != rs.skip) acc ^= load_window16(in + uint64_t(r) * Sb + c0);
+    if (rs.extra >= 0) acc ^= load_window16(in + uint64_t(rs.extra) * Sb + c0);
+    return acc;
+}
+
+__device__ __forceinline__ u32x4 xor_rows_partial(const uint8_t* in, uint64_t Sb, RowSet rs,
+                                                  uint64_t c0, uint32_t n) {
+    u32x4 acc = {0, 0, 0, 0};
+    for (uint32_t i = 0; i < n; ++i) {
+        uint8_t b = 0;
+        for (int r = rs.lo; r < rs.hi; ++r)
+            if (r != rs.skip) b ^= in[uint64_t(r) * Sb + c0 + i];
+        if (rs.extra >= 0) b ^= in[uint64_t(rs.extra) * Sb + c0 + i];
+        acc = set_byte(acc, i, b);
+    }
+    return acc;
+}
+
+// One tile of XOR-of-rows, written to up to two outputs (row base addresses).
+__device__ __forceinline__ void xor_rows_tile(const uint8_t* in, uint64_t Sb, RowSet rs,
+                                              uint8_t* out0, uint8_t* out1, uint8_t* tile) {
+    const uint64_t t0 = uint64_t(blockIdx.x) * kTileBytes;
+    const uint32_t nbytes = uint32_t(Sb - t0 < uint64_t(kTileBytes) ? Sb - t0 : kTileBytes);
+    const uint64_t c0 = t0 + 16 * threadIdx.x;
+    u32x4 acc = {0, 0, 0, 0};
+    if (c0 + 16 <= Sb)
+        acc = xor_rows_window(in, Sb, rs, c0);
+    else if (c0 < Sb)
+        acc = xor_rows_partial(in, Sb, rs, c0, uint32_t(Sb - c0));
+    *reinterpret_cast<u32x4*>(tile + 16 * threadIdx.x) = acc;
+    __syncthreads();
+    if (out0) tile_store(out0 + t0, tile, nbytes);
+    if (out1) tile_store(out1 + t0, tile, nbytes);
+}
+
+__global__ __launch_bounds__(kTB) void xor_rows_kernel(const uint8_t* in, uint64_t Sb, RowSet rs,
+                                                       uint8_t* out0, uint8_t* out1) {
+    __shared__ __attribute__((aligned(16))) uint8_t tile[kTileBytes + 16];
+    xor_rows_tile(in, Sb, rs, out0, out1, tile);
+}
+
+// benchmark/xor/kernel.cu:47-88 with the missing index read on the device:
+// data row m < nd is P ^ the other data rows; m == nd recomputes P; anything
+// else leaves every buffer untouched.
+__global__ __launch_bounds__(kTB) void xor_reconstruct_kernel(const uint8_t* enc, uint8_t* rec,
+                                                              uint8_t* rec_missing, uint64_t Sb,
+                                                              int nd, const int32_t* missing_idx) {
+    __shared__ __attribute__((aligned(16))) uint8_t tile[kTileBytes + 16];
+    const int m = __builtin_amdgcn_readfirstlane(missing_idx[0]);
+    RowSet rs;
+    if (m >= 0 && m < nd)
+        rs = RowSet{0, nd, m, nd};
+    else if (m == nd)
+        rs = RowSet{0, nd, -1, -1};
+    else
+        return;
+    xor_rows_tile(enc, Sb, rs, rec + uint64_t(m) * Sb, rec_missing, tile);
+}
+
+// ----------------------------------------------------------------- gs RDP P/Q
+// Words (u16).  P[c] = XOR_r D_r[c]; Qfull[d] = XOR_r D_r[(d - r) mod S].
+__global__ __launch_bounds__(kTB) void gs_rdp_parity_kernel(uint16_t* sh, int nd, int64_t S) {
+    __shared__ __attribute__((aligned(16))) uint8_t tp[kTileBytes + 16];
+    __shared__ __attribute__((aligned(16))) uint8_t tq[kTileBytes + 16];
+    const uint8_t* base = reinterpret_cast<const uint8_t*>(sh);
+    const uint64_t Sb = uint64_t(S) * 2;
+    const int64_t w0 = int64_t(blockIdx.x) * (kTileBytes / 2) + 8 * threadIdx.x;
+    const uint64_t t0b = uint64_t(blockIdx.x) * kTileBytes;
+    const uint32_t nbytes = uint32_t(Sb - t0b < uint64_t(kTileBytes) ? Sb - t0b : kTileBytes);
+    u32x4 p = {0, 0, 0, 0}, q = {0, 0, 0, 0};
+    if (w0 + 8 <= S) {
+        for (int r = 0; r < nd; ++r) p ^= load_window16(base + (uint64_t(r) * S + w0) * 2);
+    } else if (w0 < S) {
+        for (int i = 0; i < int(S - w0); ++i) {
+            uint16_t a = 0;
+            for (int r = 0; r < nd; ++r) a ^= sh[uint64_t(r) * S + w0 + i];
+            p = set_byte(set_byte(p, 2 * i, uint8_t(a)), 2 * i + 1, uint8_t(a >> 8));
+        }
+    }
+    if (w0 + 8 <= S && w0 >= nd - 1) {
+        for (int r = 0; r < nd; ++r) q ^= load_window16(base + (uint64_t(r) * S + w0 - r) * 2);
+    } else if (w0 < S) {
+        const int n = int(S - w0 < 8 ? S - w0 : 8);
+        for (int i = 0; i < n; ++i) {
+            uint16_t a = 0;
+            for (int r = 0; r < nd; ++r) {
+                int64_t c = (w0 + i - r) % S;
+                if (c < 0) c += S;
+                a ^= sh[uint64_t(r) * S + c];
+            }
+            q = set_byte(set_byte(q, 2 * i, uint8_t(a)), 2 * i + 1, uint8_t(a >> 8));
+        }
+    }
+    *reinterpret_cast<u32x4*>(tp + 16 * threadIdx.x) = p;
+    *reinterpret_cast<u32x4*>(tq + 16 * threadIdx.x) = q;
+    __syncthreads();
+    uint8_t* out = reinterpret_cast<uint8_t*>(sh);
+    tile_store(out + uint64_t(nd) * Sb + t0b, tp, nbytes);
+    tile_store(out + uint64_t(nd + 1) * Sb + t0b, tq, nbytes);
+}
+
+// Remove each row's star word from its diagonal: the reference skips column
+// (star_base + r) % S of row r (C remainder: negative means no skip).  One
+// thread, rows in order, so coinciding diagonals compose exactly.
+__global__ void gs_rdp_star_fixup_kernel(uint16_t* sh, int nd, int64_t S, int star_base) {
+    if (threadIdx.x != 0 || blockIdx.x != 0) return;
+    uint16_t* Q = sh + uint64_t(nd + 1) * S;
+    for (int r = 0; r < nd; ++r) {
+        const int64_t star = (int64_t(star_base) + r) % S;
+        if (star < 0) continue;
+        const int64_t d = (star + r) % S;
+        Q[d] ^= sh[uint64_t(r) * S + star];
+    }
+}
+
+// ----------------------------------------------------------------- host side
+static int xor_rows(const uint8_t* in, uint64_t Sb, RowSet rs, uint8_t* out0, uint8_t* out1,
+                    hipStream_t st, const char* what) {
+    if (Sb == 0) return KVEC_OK;
+    hipLaunchKernelGGL(xor_rows_kernel, dim3(blocks_for(int64_t(Sb), kTileBytes)), dim3(kTB), 0, st,
+                       in, Sb, rs, out0, out1);
+    return check_launch(what);
+}
+
+static int copy_d2d(void* dst, const void* src, uint64_t n, hipStream_t st, const char* what) {
+    if (n == 0 || dst == src) return KVEC_OK;
+    hipError_t e = hipMemcpyAsync(dst, src, n, hipMemcpyDeviceToDevice, st);
+    if (e != hipSuccess) return set_error(KVEC_EHIP, "%s: %s", what, hipGetErrorString(e));
+    return KVEC_OK;
+}
+
+static int gs_rdp_parity(uint16_t* sh, int nd, int64_t S, int star_base, hipStream_t st,
+                         const char* what) {
+    if (nd <= 0 || S <= 0) return KVEC_OK;  // the reference kernel returns at once
+    hipLaunchKernelGGL(gs_rdp_parity_kernel, dim3(blocks_for(S * 2, kTileBytes)), dim3(kTB), 0, st, sh,
+                       nd, S);
+    int rc = check_launch(what);
+    if (rc) return rc;
+    hipLaunchKernelGGL(gs_rdp_star_fixup_kernel, dim3(1), dim3(64), 0, st, sh, nd, S, star_base);
+    return check_launch(what);
+}
+
+}  // namespace kvec
+
+using namespace kvec;
+
+// =========================== XOR (benchmark/xor/kernel.cu) ===================
+
+// encode_xor_launcher, benchmark/xor/kernel.cu:158-171
+extern "C" int kvec_xor_encode(const void* data_padded, void* shards, int data_shards,
+                               int64_t shard_size, void* stream) {
+    if (!data_padded || !shards) return set_error(KVEC_EINVAL, "kvec_xor_encode: null pointer");
+    if (data_shards < 1 || shard_size < 0)
+        return set_error(KVEC_EINVAL, "kvec_xor_encode: data_shards=%d shard_size=%lld", data_shards,
+                         (long long)shard_size);
+    hipStream_t st = as_stream(stream);
+    const uint64_t Sb = uint64_t(shard_size);
+    int rc = copy_d2d(shards, data_padded, Sb * data_shards, st, "kvec_xor_encode");
+    if (rc) return rc;
+    return xor_rows((const uint8_t*)data_padded, Sb, RowSet{0, data_shards, -1, -1},
+                    (uint8_t*)shards + Sb * data_shards, nullptr, st, "kvec_xor_encode");
+}
+
+// reconstruct_xor_launcher, benchmark/xor/kernel.cu:173-191
+extern "C" int kvec_xor_reconstruct(const void* encoded_data, void* recovered_data,
+                                    void* recovered_missing, int64_t shard_size, int data_shards,
+                                    const int32_t* missing_indices, int missing_count,
+                                    void* stream) {
+    if (missing_count != 1) return KVEC_OK;  // the reference kernel is a no-op
+    if (!encoded_data || !recovered_data || !recovered_missing || !missing_indices)
+        return set_error(KVEC_EINVAL, "kvec_xor_reconstruct: null pointer");
+    if (data_shards < 1 || shard_size < 0)
+        return set_error(KVEC_EINVAL, "kvec_xor_reconstruct: data_shards=%d shard_size=%lld",
+                         data_shards, (long long)shard_size);
+    if (shard_size == 0) return KVEC_OK;
+    const uint64_t Sb = uint64_t(shard_size);
+    hipLaunchKernelGGL(xor_reconstruct_kernel, dim3(blocks_for(int64_t(Sb), kTileBytes)), dim3(kTB), 0,
+                       as_stream(stream), (const uint8_t*)encoded_data, (uint8_t*)recovered_data,
+                       (uint8_t*)recovered_missing, Sb, data_shards, missing_indices);
+    return check_launch("kvec_xor_reconstruct");
+}
+
+// pack_kv_launcher, benchmark/xor/kernel.cu:193-207: K bytes then V bytes
+// (the little-endian byte split of a 16-bit word is the identity in memory).
+extern "C" int kvec_pack_kv(const void* key_input, const void* value_input, void* kv_bytes, int n,
+                            int seq_len, void* stream) {
+    if (n < 0 || seq_len < 0) return set_error(KVEC_EINVAL, "kvec_pack_kv: n=%d seq_len=%d", n, seq_len);
+    const uint64_t bytes = uint64_t(n) * uint64_t(seq_len) * 2;
+    if (bytes && (!key_input || !value_input || !kv_bytes))
+        return set_error(KVEC_EINVAL, "kvec_pack_kv: null pointer");
+    hipStream_t st = as_stream(stream);
+    int rc = copy_d2d(kv_bytes, key_input, bytes, st, "kvec_pack_kv");
+    if (rc) return rc;
+    return copy_d2d((uint8_t*)kv_bytes + bytes, value_input, bytes, st, "kvec_pack_kv");
+}
+
+// unpack_kv_launcher, benchmark/xor/kernel.cu:209-223 (stream-ordered; the
+// reference also blocks the host until the device is idle).
+extern "C" int kvec_unpack_kv(const void* kv_bytes, void* dequant_kv, int n, int seq_len,
+                              void* stream) {
+    if (n < 0 || seq_len < 0) return set_error(KVEC_EINVAL, "kvec_unpack_kv: n=%d seq_len=%d", n, seq_len);
+    const uint64_t bytes = uint64_t(n) * uint64_t(seq_len) * 4;
+    if (bytes && (!kv_bytes || !dequant_kv)) return set_error(KVEC_EINVAL, "kvec_unpack_kv: null pointer");
+    return copy_d2d(dequant_kv, kv_bytes, bytes, as_stream(stream), "kvec_unpack_kv");
+}
+
+// ====================== gs RDP (benchmark/rdp/kernel.cu) =====================
+
+// fused_backup_full_kv_launcher, benchmark/rdp/kernel.cu:366-395: pack the
+// token-major K|V words into the data rows (pack_scatter_kernel_full, :32-72,
+// drops words past row nd-1), then P and Q (compute_rdp_parity_kernel, :76-107).
+extern "C" int kvec_gs_rdp_backup(const void* K_TN, const void* V_TN, void* shards, int nd, int S,
+                                  int T, int n, int star_base, void* stream) {
+    if (!shards) return set_error(KVEC_EINVAL, "kvec_gs_rdp_backup: null shards");
+    hipStream_t st = as_stream(stream);
+    if (T > 0 && n > 0 && nd > 0 && S > 0) {
+        if (!K_TN || !V_TN) return set_error(KVEC_EINVAL, "kvec_gs_rdp_backup: null K/V");
+        const uint64_t tn = uint64_t(T) * uint64_t(n), cap = uint64_t(nd) * uint64_t(S);
+        const uint64_t nk = tn < cap ? tn : cap;
+        const uint64_t nv = 2 * tn < cap ? tn : (cap > tn ? cap - tn : 0);
+        int rc = copy_d2d(shards, K_TN, nk * 2, st, "kvec_gs_rdp_backup");
+        if (!rc) rc = copy_d2d((uint16_t*)shards + tn, V_TN, nv * 2, st, "kvec_gs_rdp_backup");
+        if (rc) return rc;
+    }
+    return gs_rdp_parity((uint16_t*)shards, nd, S, star_base, st, "kvec_gs_rdp_backup");
+}
+
+// fused_recovery_full_kv_launcher, benchmark/rdp/kernel.cu:397-521.  Indices
+// outside [0, nd) are dropped (:402-404).  Two distinct data rows a < b: the
+// launcher's last two kernels rebuild row a from P (:473-480), overwriting
+// every word the ring-walk kernels (:411-470) wrote, and then row b from P
+// (:482-490); that second rebuild returns row b's input bytes exactly
+// (P ^ a' ^ rest = b), so only row a is rewritten here.  One row: rebuilt
+// from P (:492-507).  Then the data rows are copied out (load_full_kernel,
+// :305-345), words past row nd-1 reading 0.
+extern "C" int kvec_gs_rdp_recover(void* shards, void* out_TN, int nd, int S, int T, int n,
+                                   int star_base, int missing_a, int missing_b, void* stream) {
+    (void)star_base;
+    if (!shards) return set_error(KVEC_EINVAL, "kvec_gs_rdp_recover: null shards");
+    hipStream_t st = as_stream(stream);
+    int a = (missing_a >= 0 && missing_a < nd) ? missing_a : -1;
+    int b = (missing_b >= 0 && missing_b < nd) ? missing_b : -1;
+    int t = -1;
+    if (a >= 0 && b >= 0 && a != b)
+        t = a < b ? a : b;
+    else if (a >= 0 && b < 0)
+        t = a;
+    else if (b >= 0 && a < 0)
+        t = b;
+    if (t >= 0 && S > 0) {
+        const uint64_t Sb = uint64_t(S) * 2;
+        uint8_t* base = (uint8_t*)shards;
+        int rc = xor_rows(base, Sb, RowSet{0, nd, t, nd}, base + uint64_t(t) * Sb, nullptr, st,
+                          "kvec_gs_rdp_recover");
+        if (rc) return rc;
+    }
+    if (T > 0 && n > 0 && nd > 0 && S > 0) {
+        if (!out_TN) return set_error(KVEC_EINVAL, "kvec_gs_rdp_recover: null output");
+        const uint64_t total = 2 * uint64_t(T) * uint64_t(n), cap = uint64_t(nd) * uint64_t(S);
+        const uint64_t nc = total < cap ? total : cap;
+        int rc = copy_d2d(out_TN, shards, nc * 2, st, "kvec_gs_rdp_recover");
+        if (rc) return rc;
+        if (total > nc) {
+            hipError_t e = hipMemsetAsync((uint16_t*)out_TN + nc, 0, (total - nc) * 2, st);
+            if (e != hipSuccess)
+                return set_error(KVEC_EHIP, "kvec_gs_rdp_recover: %s", hipGetErrorString(e));
+        }
+    }
+    return KVEC_OK;
+}
+
+// pack_row_from_block_launcher, bench_ghostserve_rdp.py:152-175:
+// rows[row] = K words then V words.
+extern "C" int kvec_gs_pack_row(const void* k_blk, const void* v_blk, void* rows, int64_t words,
+                                int row, int64_t S, void* stream) {
+    if (words < 0 || S < 2 * words || row < 0)
+        return set_error(KVEC_EINVAL, "kvec_gs_pack_row: need S >= 2*words (S=%lld, words=%lld)",
+                         (long long)S, (long long)words);
+    if (words && (!k_blk || !v_blk || !rows)) return set_error(KVEC_EINVAL, "kvec_gs_pack_row: null pointer");
+    hipStream_t st = as_stream(stream);
+    uint16_t* rp = (uint16_t*)rows + uint64_t(row) * uint64_t(S);
+    int rc = copy_d2d(rp, k_blk, uint64_t(words) * 2, st, "kvec_gs_pack_row");
+    if (rc) return rc;
+    return copy_d2d(rp + words, v_blk, uint64_t(words) * 2, st, "kvec_gs_pack_row");
+}
+
+// compute_rdp_parity_launcher, bench_ghostserve_rdp.py:177-199 (row stride S).
+extern "C" int kvec_gs_rdp_parity(void* rows, int nd, int S, int star_base, void* stream) {
+    if (!rows) return set_error(KVEC_EINVAL, "kvec_gs_rdp_parity: null rows");
+    return gs_rdp_parity((uint16_t*)rows, nd, S, star_base, as_stream(stream), "kvec_gs_rdp_parity");
+}

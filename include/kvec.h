@@ -62,6 +62,75 @@ int kvec_rdp_decode(void* const* shards, int k, int p, int64_t row_bytes, int e0
  * k*(p-1) row planes hold `stream_bytes` bytes.  Host-only arithmetic. */
 int64_t kvec_rdp_row_bytes(int64_t stream_bytes, int k, int p, int64_t granule);
 
+/* ============ gs family: XOR (benchmark/xor/kernel.cu, main.py) =========== */
+/* Byte shards, packed: shards = [(data_shards + 1), shard_size] bytes. */
+
+/* encode_xor_launcher, benchmark/xor/kernel.cu:158-171: copy the data rows of
+ * data_padded [data_shards*shard_size] into shards, then P = XOR of them. */
+int kvec_xor_encode(const void* data_padded, void* shards, int data_shards,
+                    int64_t shard_size, void* stream);
+/* reconstruct_xor_launcher, :173-191.  missing_indices: device int32 array of
+ * missing_count entries; only missing_count == 1 does anything: a data row
+ * m < data_shards is rebuilt from P, m == data_shards recomputes P.  The row is
+ * written to recovered_data (may alias encoded_data) and recovered_missing. */
+int kvec_xor_reconstruct(const void* encoded_data, void* recovered_data,
+                         void* recovered_missing, int64_t shard_size, int data_shards,
+                         const int32_t* missing_indices, int missing_count, void* stream);
+/* pack_kv_launcher / unpack_kv_launcher, :193-223: K bytes then V bytes of
+ * n*seq_len 16-bit words each (little-endian split == memory order). */
+int kvec_pack_kv(const void* key_input, const void* value_input, void* kv_bytes, int n,
+                 int seq_len, void* stream);
+int kvec_unpack_kv(const void* kv_bytes, void* dequant_kv, int n, int seq_len, void* stream);
+
+/* ====== gs family: star-diagonal RDP (benchmark/rdp/kernel.cu, main.py) ====== */
+/* u16 words, packed: shards = [(nd + 2), S]; P = row nd, Q = row nd+1.
+ * Q[d] = XOR_r D_r[(d - r) mod S], skipping column (star_base + r) % S of row r. */
+
+/* fused_backup_full_kv_launcher, benchmark/rdp/kernel.cu:366-395: K_TN, V_TN
+ * are [T, n] words; data rows get K_TN || V_TN (words past row nd-1 dropped),
+ * then P and Q.  The caller zero-initialises the padding words. */
+int kvec_gs_rdp_backup(const void* K_TN, const void* V_TN, void* shards, int nd, int S, int T,
+                       int n, int star_base, void* stream);
+/* fused_recovery_full_kv_launcher, :397-521: observable semantics of the
+ * reference (indices outside [0, nd) ignored; one data row is rebuilt from P;
+ * for two, the lower row is rebuilt from P and the other keeps its bytes),
+ * then out_TN [2*T*n] words = the data rows. */
+int kvec_gs_rdp_recover(void* shards, void* out_TN, int nd, int S, int T, int n, int star_base,
+                        int missing_a, int missing_b, void* stream);
+/* pack_row_from_block_launcher, bench_ghostserve_rdp.py:152-175:
+ * rows[row*S ..] = k_blk words then v_blk words (S >= 2*words). */
+int kvec_gs_pack_row(const void* k_blk, const void* v_blk, void* rows, int64_t words, int row,
+                     int64_t S, void* stream);
+/* compute_rdp_parity_launcher, bench_ghostserve_rdp.py:177-199: P, Q of the
+ * first nd rows of `rows` (row stride S words) into rows nd and nd+1. */
+int kvec_gs_rdp_parity(void* rows, int nd, int S, int star_base, void* stream);
+
+/* ======== gs family: RS over GF(2^16) (benchmark/rs/kernel.cu, main.py) ======= */
+/* u16 symbols, packed: shards = [(k + m), shard_size].  gf_exp / gf_log are
+ * the device tables of init_gf_tables() (poly 0x1100B). */
+
+/* pack_fp16_pair_to_u16, benchmark/rs/kernel.cu:225-243: out = K || V words. */
+int kvec_rs16_pack(const void* k, const void* v, void* out, int64_t N_k, int64_t N_v,
+                   void* stream);
+/* u16_to_fp16_split, :245-263: inverse of kvec_rs16_pack. */
+int kvec_rs16_split(const void* in, void* k_out, void* v_out, int64_t N_k, int64_t N_v,
+                    void* stream);
+/* encode_rs_u16, :265-285: copy data rows; Par_p = XOR_i D_i * alpha^((p+1) i).
+ * Limits: parity_shards <= 16, data_shards * parity_shards <= 48. */
+int kvec_rs16_encode(const void* data_padded, void* shards, int data_shards, int parity_shards,
+                     int shard_size, const uint16_t* gf_exp, const uint16_t* gf_log,
+                     void* stream);
+/* reconstruct_rs_u16_inplace, :287-312: rebuild the m data rows listed in the
+ * device int32 array missing_data from the parity rows in parity_used (device,
+ * m entries).  Parity rows are not rewritten.  Indices outside the tensor, or a
+ * repeated missing index, make the call write nothing. */
+int kvec_rs16_reconstruct(void* shards, int shard_size, int data_shards, int parity_shards,
+                          const int32_t* missing_data, int m, const int32_t* parity_used,
+                          const uint16_t* gf_exp, const uint16_t* gf_log, void* stream);
+/* init_gf_tables, benchmark/rs/main.py:39-54, into host arrays (exp: 131070
+ * entries, log: 65536). */
+int kvec_gf16_tables(uint16_t* gf_exp, uint16_t* gf_log);
+
 #ifdef __cplusplus
 }
 #endif

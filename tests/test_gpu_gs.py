@@ -1,0 +1,256 @@
+"""gs family (the reference's own codes) on the GPU, bit-exact against the
+oracle's restatement of benchmark/{xor,rdp,rs}/kernel.cu and
+bench_ghostserve_rdp.py, through the reference-compatible Python signatures."""
+import itertools
+
+import numpy as np
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+
+def dev(a, gpu):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(gpu)
+
+
+def host(t):
+    return t.cpu().numpy()
+
+
+# ------------------------------------------------------------------ XOR
+@pytest.mark.parametrize("nd,S", [(4, 262144), (8, 1000), (3, 17), (5, 1), (1, 33), (6, 4111),
+                                  (7, 16), (2, 4096 * 3 + 5)])
+def test_xor_encode_matches_oracle(pkg, ora, gpu, nd, S):
+    rng = np.random.default_rng(nd * 7 + S)
+    data = rng.integers(0, 256, nd * S, dtype=np.uint8)
+    want = ora.xor_encode(data, nd, S)
+    shards = torch.full((nd + 1, S), 0x5A, dtype=torch.uint8, device=gpu)
+    pkg.xor.xor_kernel.encode_xor(dev(data, gpu), shards, nd, S)
+    assert np.array_equal(host(shards), want)
+
+
+@pytest.mark.parametrize("nd,S", [(4, 262144), (8, 999), (3, 17), (5, 3)])
+def test_xor_reconstruct_matches_oracle(pkg, ora, gpu, nd, S):
+    rng = np.random.default_rng(S)
+    data = rng.integers(0, 256, nd * S, dtype=np.uint8)
+    ref = ora.xor_encode(data, nd, S)
+    for missing in [[m] for m in range(nd + 1)] + [[], [0, 1], [nd + 1], [-2]]:
+        sh = ref.copy()
+        if missing and 0 <= missing[0] <= nd:
+            sh[missing[0]] = rng.integers(0, 256, S, dtype=np.uint8)
+        want = sh.copy()
+        want_miss = np.full((1, S), 0xEE, np.uint8)
+        if len(missing) == 1 and 0 <= missing[0] <= nd:
+            want_miss = ora.xor_reconstruct(want, S, nd, missing)
+        else:
+            ora.xor_reconstruct(want, S, nd, missing)
+        d = dev(sh, gpu)
+        rec_miss = torch.full((1, S), 0xEE, dtype=torch.uint8, device=gpu)
+        mi = torch.tensor(missing, dtype=torch.int32, device=gpu)
+        pkg.xor.xor_kernel.reconstruct_xor(d, d, rec_miss, S, nd, mi)
+        assert np.array_equal(host(d), want), missing
+        assert np.array_equal(host(rec_miss), want_miss), missing
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float8_e4m3fn])
+@pytest.mark.parametrize("nd", [4, 8, 3])
+def test_xor_forward_backward_round_trip(pkg, ora, gpu, dtype, nd):
+    B, H, T, D = 1, 2, 37, 128
+    g = torch.Generator(device="cpu").manual_seed(nd)
+    k = torch.randn(B, H, T, D, generator=g).to(dtype)
+    v = torch.randn(B, H, T, D, generator=g).to(dtype)
+    pk = pkg.xor.forward_encode_kv(k.to(gpu), v.to(gpu), nd, 1)
+    es = k.element_size()
+    kb = k.contiguous().view(torch.uint8).numpy().reshape(-1)
+    vb = v.contiguous().view(torch.uint8).numpy().reshape(-1)
+    stream = np.concatenate([kb, vb])
+    S = pk["shard_size"]
+    assert pk["total_bytes"] == 2 * es * T * B * H * D
+    padded = np.zeros(nd * S, np.uint8)
+    padded[: stream.size] = stream
+    assert np.array_equal(host(pk["shards_KV"]), ora.xor_encode(padded, nd, S))
+    for miss in range(nd + 1):
+        pk2 = dict(pk)
+        pk2["shards_KV"] = pk["shards_KV"].clone()
+        kr, vr, st = pkg.xor.backwards_decode_kv(pk2, [miss])
+        assert kr.dtype == dtype and kr.shape == k.shape
+        assert torch.equal(kr.cpu().view(torch.uint8), k.view(torch.uint8))
+        assert torch.equal(vr.cpu().view(torch.uint8), v.view(torch.uint8))
+        assert set(st) == {"reconstruct_ms", "reconstruct_io", "unpack_io"}
+    with pytest.raises(ValueError):
+        pkg.xor.backwards_decode_kv(pk, [0, 1])
+    with pytest.raises(ValueError):
+        pkg.xor.forward_encode_kv(k.to(gpu), v.to(gpu), nd, 2)
+
+
+# ------------------------------------------------------------------ gs RDP
+@pytest.mark.parametrize("nd,S", [(8, 5000), (6, 101), (1, 9), (3, 2), (2, 1), (13, 4103),
+                                  (8, 2048), (8, 2049), (4, 16), (5, 24577), (8, 7)])
+@pytest.mark.parametrize("star_base", [0, 3, -1, -5, 10 ** 6])
+def test_gs_rdp_parity_matches_oracle(pkg, ora, gpu, nd, S, star_base):
+    rng = np.random.default_rng(nd * 1000 + S)
+    rows = np.zeros((nd + 2, S), np.uint16)
+    rows[:nd] = rng.integers(0, 65536, (nd, S), dtype=np.uint16)
+    rows[nd:] = 0xABCD
+    want = rows.copy()
+    ora.gs_parity(want, nd, S, star_base)
+    d = dev(rows, gpu)
+    pkg.rdp_kv_ops.compute_rdp_parity(d, nd, S, star_base)
+    assert np.array_equal(host(d), want)
+
+
+def test_gs_rdp_parity_row_stride_is_S(pkg, ora, gpu):
+    """compute_rdp_parity indexes with stride S even when rows is wider
+    (bench_ghostserve_rdp.py:185-198)."""
+    nd, S, W = 3, 40, 64
+    rng = np.random.default_rng(1)
+    rows = rng.integers(0, 65536, (nd + 3, W), dtype=np.uint16)
+    want = rows.reshape(-1)[: (nd + 2) * S].reshape(nd + 2, S).copy()
+    ora.gs_parity(want, nd, S, 1)
+    d = dev(rows, gpu)
+    pkg.rdp_kv_ops.compute_rdp_parity(d, nd, S, 1)
+    got = host(d).reshape(-1)
+    assert np.array_equal(got[: (nd + 2) * S], want.reshape(-1))
+    assert np.array_equal(got[(nd + 2) * S:], rows.reshape(-1)[(nd + 2) * S:])
+
+
+@pytest.mark.parametrize("B,H,T,D,nd", [(1, 8, 512, 128, 8), (2, 1, 33, 128, 6), (1, 2, 5, 64, 3),
+                                        (1, 1, 7, 3, 4)])
+def test_gs_backup_and_recovery(pkg, ora, gpu, B, H, T, D, nd):
+    g = torch.Generator(device="cpu").manual_seed(T)
+    K = torch.randn(B, H, T, D, generator=g).half()
+    V = torch.randn(B, H, T, D, generator=g).half()
+    n = B * H * D
+    pk = pkg.rdp.fused_backup_full_kv(K.to(gpu), V.to(gpu), nd, star_base=0)
+    K_TN = K.permute(2, 0, 1, 3).contiguous().view(T, n).view(torch.uint16).numpy()
+    V_TN = V.permute(2, 0, 1, 3).contiguous().view(T, n).view(torch.uint16).numpy()
+    want = ora.gs_backup(K_TN, V_TN, nd, 0)
+    assert set(pk) >= {"shards_KV", "shard_size", "seq_len", "n", "num_data_shards", "star_base",
+                       "shape_BHTD", "backup_ms", "pad_words"}
+    assert np.array_equal(host(pk["shards_KV"]), want)
+    S = pk["shard_size"]
+    for a, b in [(-1, -1), (0, 1), (nd - 1, 0), (2 % nd, -1), (-1, nd - 1), (nd, 1), (1, 1)]:
+        sh = want.copy()
+        # erase the named data rows, as a real loss would
+        for x in (a, b):
+            if 0 <= x < nd:
+                sh[x] = 0
+        exp = sh.copy()
+        ora.gs_recover(exp, nd, S, 0, a, b)
+        exp_out = ora.gs_load_full(exp, nd, S, T, n)
+        pk2 = dict(pk)
+        pk2["shards_KV"] = dev(sh, gpu)
+        kr, vr, st = pkg.rdp.fused_recovery_full_kv(pk2, a, b)
+        assert np.array_equal(host(pk2["shards_KV"]), exp), (a, b)
+        got = np.concatenate([kr.permute(2, 0, 1, 3).contiguous().cpu().view(torch.uint16).numpy().reshape(-1),
+                              vr.permute(2, 0, 1, 3).contiguous().cpu().view(torch.uint16).numpy().reshape(-1)])
+        assert np.array_equal(got, exp_out), (a, b)
+        assert "recover_ms" in st
+
+
+def test_gs_single_row_recovery_restores_kv(pkg, gpu):
+    B, H, T, D, nd = 1, 4, 64, 128, 8
+    K = torch.randn(B, H, T, D, device=gpu).half()
+    V = torch.randn(B, H, T, D, device=gpu).half()
+    pk = pkg.rdp.fused_backup_full_kv(K, V, nd)
+    pk["shards_KV"][5].view(torch.int16).zero_()
+    kr, vr, _ = pkg.rdp.fused_recovery_full_kv(pk, 5)
+    assert torch.equal(kr.view(torch.int16), K.view(torch.int16))
+    assert torch.equal(vr.view(torch.int16), V.view(torch.int16))
+
+
+def test_gs_pack_row(pkg, ora, gpu):
+    rng = np.random.default_rng(3)
+    world, w = 4, 1000
+    S = 2 * w + 1
+    rows = np.zeros((world + 2, S), np.uint16)
+    d = dev(rows, gpu)
+    for r in range(world):
+        k = rng.integers(0, 65536, w, dtype=np.uint16)
+        v = rng.integers(0, 65536, w, dtype=np.uint16)
+        ora.gs_pack_row(k, v, rows, r)
+        pkg.rdp_kv_ops.pack_row_from_block(dev(k, gpu).view(torch.float16).view(1, 1, w, 1),
+                                           dev(v, gpu).view(torch.float16).view(1, 1, w, 1), d, r)
+    assert np.array_equal(host(d), rows)
+    ora.gs_parity(rows, world, S, 2)
+    pkg.rdp_kv_ops.compute_rdp_parity(d, nd=world, S=S, star_base=2)
+    assert np.array_equal(host(d), rows)
+    with pytest.raises(RuntimeError):
+        pkg.rdp_kv_ops.pack_row_from_block(dev(np.zeros(S, np.uint16), gpu).view(torch.float16),
+                                           dev(np.zeros(S, np.uint16), gpu).view(torch.float16), d, 0)
+
+
+# ------------------------------------------------------------------ gs RS16
+@pytest.mark.parametrize("k,m,S", [(8, 2, 4096), (6, 2, 44741), (5, 3, 1000), (4, 1, 3),
+                                   (8, 0, 100), (10, 4, 2049), (1, 1, 77), (16, 3, 8)])
+def test_rs16_encode_matches_oracle(pkg, ora, gpu, k, m, S):
+    ex, lg = ora.gf16_tables()
+    rng = np.random.default_rng(k * 100 + m)
+    data = rng.integers(0, 65536, k * S, dtype=np.uint16)
+    data[rng.integers(0, k * S, k * S // 7)] = 0  # zeros take the reference's skip
+    want = ora.rs16_encode(data, k, m, S, ex, lg)
+    shards = torch.zeros((k + m, S), dtype=torch.uint16, device=gpu)
+    gex, glg = pkg.rs.device_gf_tables(gpu)
+    pkg.rs.rs_kernel.encode_rs_u16(dev(data, gpu), shards, k, m, S, gex, glg)
+    assert np.array_equal(host(shards), want)
+
+
+@pytest.mark.parametrize("k,m,S", [(8, 2, 4099), (6, 3, 1000), (5, 3, 9)])
+def test_rs16_reconstruct_matches_oracle(pkg, ora, gpu, k, m, S):
+    ex, lg = ora.gf16_tables()
+    rng = np.random.default_rng(S)
+    data = rng.integers(0, 65536, k * S, dtype=np.uint16)
+    ref = ora.rs16_encode(data, k, m, S, ex, lg)
+    gex, glg = pkg.rs.device_gf_tables(gpu)
+    for nm in range(1, m + 1):
+        for miss in list(itertools.combinations(range(k), nm))[:12]:
+            for pused in list(itertools.combinations(range(m), nm))[:3]:
+                sh = ref.copy()
+                sh[list(miss)] = rng.integers(0, 65536, (nm, S), dtype=np.uint16)
+                want = sh.copy()
+                ora.rs16_reconstruct(want, S, k, m, list(miss), list(pused), ex, lg)
+                assert np.array_equal(want, ref)
+                d = dev(sh, gpu)
+                pkg.rs.rs_kernel.reconstruct_rs_u16_inplace(
+                    d, S, k, m, torch.tensor(miss, dtype=torch.int32, device=gpu),
+                    torch.tensor(pused, dtype=torch.int32, device=gpu), gex, glg)
+                assert np.array_equal(host(d), want), (miss, pused)
+
+
+def test_rs16_bad_device_indices_write_nothing(pkg, gpu):
+    k, m, S = 6, 2, 100
+    d = torch.zeros((k + m, S), dtype=torch.uint16, device=gpu)
+    d.view(torch.int16).fill_(7)
+    gex, glg = pkg.rs.device_gf_tables(gpu)
+    pkg.rs.rs_kernel.reconstruct_rs_u16_inplace(
+        d, S, k, m, torch.tensor([0, 9], dtype=torch.int32, device=gpu),
+        torch.tensor([0, 1], dtype=torch.int32, device=gpu), gex, glg)
+    assert bool((d.view(torch.int16) == 7).all())
+
+
+@pytest.mark.parametrize("k,m", [(8, 2), (6, 2), (5, 3)])
+def test_rs16_forward_backward_round_trip(pkg, ora, gpu, k, m):
+    B, H, T, D = 1, 8, 63, 128
+    K = torch.randn(B, H, T, D, device=gpu).to(torch.bfloat16)
+    V = torch.randn(B, H, T, D, device=gpu).to(torch.bfloat16)
+    shards, meta = pkg.rs.forward_encode_kv(K, V, k, m)
+    assert set(meta) >= {"B", "H", "T", "D", "N_k", "N_v", "total", "pad", "shard_sz",
+                         "num_data", "num_parity"}
+    ex, lg = ora.gf16_tables()
+    S = meta["shard_sz"]
+    stream = np.zeros(k * S, np.uint16)
+    stream[: meta["total"]] = np.concatenate([K.cpu().view(torch.uint16).numpy().reshape(-1),
+                                              V.cpu().view(torch.uint16).numpy().reshape(-1)])
+    assert np.array_equal(host(shards), ora.rs16_encode(stream, k, m, S, ex, lg))
+    for missing in [[0, 1], [k - 1], [k, 2], [1, k + m - 1], [k, k + 1]][: m + 2]:
+        if len([x for x in missing if x < k]) > m - len([x for x in missing if x >= k]):
+            continue
+        er = shards.clone()
+        for x in missing:
+            er[x].view(torch.int16).zero_()
+        kr, vr = pkg.rs.backwards_decode_kv(er, meta, missing)
+        assert torch.equal(kr.view(torch.int16), K.view(torch.int16)), missing
+        assert torch.equal(vr.view(torch.int16), V.view(torch.int16)), missing
+    with pytest.raises(RuntimeError):
+        pkg.rs.backwards_decode_kv(shards.clone(), meta, list(range(m + 1)))
