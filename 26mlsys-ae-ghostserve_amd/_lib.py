@@ -31,6 +31,9 @@ SIGNATURES = {
     "kvec_rdp_encode": (_i, [_pp, _i, _vp, _vp, _i, _i64, _vp]),
     "kvec_rdp_decode": (_i, [_pp, _i, _i, _i64, _i, _i, _vp]),
     "kvec_rdp_row_bytes": (_i64, [_i64, _i, _i, _i64]),
+    "kvec_rs8_cauchy": (_i, [_i, _i, _vp]),
+    "kvec_rs8_encode": (_i, [_pp, _i, _pp, _i, _i64, _vp]),
+    "kvec_rs8_decode": (_i, [_pp, _i, _i, _i64, _vp, _i, _vp]),
     "kvec_xor_encode": (_i, [_vp, _vp, _i, _i64, _vp]),
     "kvec_xor_reconstruct": (_i, [_vp, _vp, _vp, _i64, _i, _vp, _i, _vp]),
     "kvec_pack_kv": (_i, [_vp, _vp, _vp, _i, _i, _vp]),

@@ -1,0 +1,321 @@
+// rs8_spec.hip -- systematic Reed-Solomon over GF(2^8) (poly 0x11D) with the
+// Cauchy parity block C[i][j] = 1 / ((k+i) ^ j), i < m, j < k.
+//
+// Encode and decode are the same operation: out_o = XOR_j M[o][j] * in_j over
+// separate shard buffers, with M = C for encode and, for decode, the rows of
+// the inverse of the surviving k x k block of [I; C] (and C times it for an
+// erased parity shard), computed on the host.
+//
+// Multiplication by a constant c is GF(2)-linear in x, so with x split into
+// bit fields x = f0 + f1*2^3 + f2*2^6 (3, 3 and 2 bits):
+//     x*c = T0[f0] ^ T1[f1] ^ T2[f2],   T0[v] = v*c, T1[v] = (v<<3)*c, T2[v] = (v<<6)*c.
+// Each table has at most 8 one-byte entries, i.e. two dwords, which is exactly
+// what one v_perm_b32 indexes: a byte-permute of the 8-byte table by the field
+// values of four data bytes at once.  Per 4 data bytes: 5 ops to extract the
+// fields (shared by all outputs) and 3 v_perm + 3 XOR per coefficient, with the
+// tables held in registers -- no LDS or memory lookups.
+#include "kvec_internal.h"
+
+namespace kvec {
+
+// ------------------------------------------------------------ GF(2^8) host side
+struct Gf8 {
+    uint8_t exp[512], log[256];
+    constexpr Gf8() : exp(), log() {
+        unsigned x = 1;
+        for (int i = 0; i < 255; ++i) {
+            exp[i] = uint8_t(x);
+            log[x] = uint8_t(i);
+            x <<= 1;
+            if (x & 0x100) x ^= 0x11D;
+        }
+        for (int i = 255; i < 512; ++i) exp[i] = exp[i - 255];
+    }
+    constexpr uint8_t mul(uint8_t a, uint8_t b) const {
+        return (a && b) ? exp[log[a] + log[b]] : 0;
+    }
+    constexpr uint8_t inv(uint8_t a) const { return a ? exp[255 - log[a]] : 0; }
+};
+static constexpr Gf8 kGf8{};
+
+constexpr int kRs8MaxK = 32;
+constexpr int kRs8MaxM = 8;
+constexpr int kRs8MaxCoef = 64;   // k * m (keeps the kernel arguments under 2 KiB)
+constexpr int kRs8BS = 128;
+
+// v_perm tables of one coefficient: {T0 lo, T0 hi, T1 lo, T1 hi, T2 lo, T2 hi}
+static void perm_tables(uint8_t c, uint32_t t[6]) {
+    for (int f = 0; f < 3; ++f) {
+        uint8_t e[8];
+        for (int v = 0; v < 8; ++v) e[v] = (f == 2 && v > 3) ? 0 : kGf8.mul(uint8_t(v << (3 * f)), c);
+        t[2 * f] = e[0] | (e[1] << 8) | (e[2] << 16) | (uint32_t(e[3]) << 24);
+        t[2 * f + 1] = e[4] | (e[5] << 8) | (e[6] << 16) | (uint32_t(e[7]) << 24);
+    }
+}
+
+// coefficient (o, j) of an nout x nin mix lives at t[o * nin + j]
+struct Gf8Mix {
+    uint32_t t[kRs8MaxCoef][6];
+};
+
+// ------------------------------------------------------------ device side
+__device__ __forceinline__ uint32_t gf8_mul4(uint32_t f0, uint32_t f1, uint32_t f2,
+                                             const uint32_t* t) {
+    // v_perm_b32 D, S0, S1, sel: selector bytes 0-3 pick S1 bytes, 4-7 S0 bytes
+    return __builtin_amdgcn_perm(t[1], t[0], f0) ^ __builtin_amdgcn_perm(t[3], t[2], f1) ^
+           __builtin_amdgcn_perm(t[5], t[4], f2);
+}
+
+template <int NIN, int NOUT, int V>
+__global__ __launch_bounds__(kRs8BS) void gf8_mix_kernel(Ptrs<kRs8MaxK> in, Ptrs<kRs8MaxM> out,
+                                                         Gf8Mix mix, uint32_t S, uint32_t nvec) {
+    const uint32_t u0 = blockIdx.x * (kRs8BS * V) + threadIdx.x;
+    u32x4 acc[V][NOUT];
+#pragma unroll
+    for (int v = 0; v < V; ++v)
+#pragma unroll
+        for (int o = 0; o < NOUT; ++o) acc[v][o] = u32x4{0, 0, 0, 0};
+#pragma unroll
+    for (int j = 0; j < NIN; ++j) {
+        const ShardView<true> sv(in.p[j], S);
+        u32x4 x[V];
+#pragma unroll
+        for (int v = 0; v < V; ++v) {
+            const uint32_t u = u0 + v * kRs8BS;
+            x[v] = sv.load(0, (u < nvec ? u : 0u) << 4);
+        }
+#pragma unroll
+        for (int v = 0; v < V; ++v) {
+            const uint32_t w[4] = {x[v].x, x[v].y, x[v].z, x[v].w};
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const uint32_t f0 = w[q] & 0x07070707u;
+                const uint32_t f1 = (w[q] >> 3) & 0x07070707u;
+                const uint32_t f2 = (w[q] >> 6) & 0x03030303u;
+#pragma unroll
+                for (int o = 0; o < NOUT; ++o) {
+                    const uint32_t pr = gf8_mul4(f0, f1, f2, mix.t[o * NIN + j]);
+                    if (q == 0) acc[v][o].x ^= pr;
+                    else if (q == 1) acc[v][o].y ^= pr;
+                    else if (q == 2) acc[v][o].z ^= pr;
+                    else acc[v][o].w ^= pr;
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int o = 0; o < NOUT; ++o) {
+        const ShardView<true> so(out.p[o], S);
+#pragma unroll
+        for (int v = 0; v < V; ++v) {
+            const uint32_t u = u0 + v * kRs8BS;
+            if (u < nvec) so.store(0, u << 4, acc[v][o]);
+        }
+    }
+}
+
+// Any shape: one output at a time, inputs re-read through L2.
+__global__ __launch_bounds__(kRs8BS) void gf8_mix_generic_kernel(Ptrs<kRs8MaxK> in,
+                                                                 Ptrs<kRs8MaxM> out, Gf8Mix mix,
+                                                                 int nin, int nout, uint64_t S,
+                                                                 uint64_t nvec) {
+    const uint64_t u = uint64_t(blockIdx.x) * kRs8BS + threadIdx.x;
+    if (u >= nvec) return;
+    for (int o = 0; o < nout; ++o) {
+        u32x4 acc = {0, 0, 0, 0};
+        for (int j = 0; j < nin; ++j) {
+            const u32x4 x = ld16(in.p[j] + (u << 4));
+            const uint32_t w[4] = {x.x, x.y, x.z, x.w};
+            uint32_t r[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+                r[q] = gf8_mul4(w[q] & 0x07070707u, (w[q] >> 3) & 0x07070707u,
+                                (w[q] >> 6) & 0x03030303u, mix.t[o * nin + j]);
+            acc ^= u32x4{r[0], r[1], r[2], r[3]};
+        }
+        st_stream(out.p[o], u << 4, acc);
+    }
+    (void)S;
+}
+
+typedef void (*MixFn)(Ptrs<kRs8MaxK>, Ptrs<kRs8MaxM>, Gf8Mix, uint32_t, uint32_t);
+
+template <int NIN, int NOUT>
+constexpr int mix_vec() {
+    return NIN * NOUT <= 12 ? 2 : 1;
+}
+
+#define KVEC_MIX(NIN, NOUT) \
+    if (nin == NIN && nout == NOUT) return &gf8_mix_kernel<NIN, NOUT, mix_vec<NIN, NOUT>()>;
+
+// Shapes of the stripe configurations (RS(6,2) encode and its 1/2-erasure
+// decodes, RS(5,3) and its decodes, RS(4,2), RS(8,2), RS(10,4)) are compiled
+// straight-line; other shapes run the generic kernel.
+static MixFn mix_fn(int nin, int nout, int* vec) {
+    auto pick = [&]() -> MixFn {
+        KVEC_MIX(6, 1) KVEC_MIX(6, 2)
+        KVEC_MIX(5, 1) KVEC_MIX(5, 2) KVEC_MIX(5, 3)
+        KVEC_MIX(4, 1) KVEC_MIX(4, 2)
+        KVEC_MIX(8, 1) KVEC_MIX(8, 2)
+        KVEC_MIX(10, 1) KVEC_MIX(10, 2) KVEC_MIX(10, 3) KVEC_MIX(10, 4)
+        return nullptr;
+    };
+    MixFn f = pick();
+    *vec = (nin * nout <= 12) ? 2 : 1;
+    return f;
+}
+#undef KVEC_MIX
+
+static int launch_mix(uint8_t* const* in, int nin, uint8_t* const* out, int nout,
+                      const uint8_t* M /* nout x nin */, int64_t S, hipStream_t st,
+                      const char* what) {
+    Ptrs<kRs8MaxK> pi{};
+    Ptrs<kRs8MaxM> po{};
+    Gf8Mix mix{};
+    for (int j = 0; j < nin; ++j) pi.p[j] = in[j];
+    for (int o = 0; o < nout; ++o) {
+        po.p[o] = out[o];
+        for (int j = 0; j < nin; ++j) perm_tables(M[o * nin + j], mix.t[o * nin + j]);
+    }
+    if (S == 0 || nout == 0) return KVEC_OK;
+    int vec = 1;
+    MixFn fn = fits_buffer(uint64_t(S)) ? mix_fn(nin, nout, &vec) : nullptr;
+    if (fn) {
+        const uint32_t nvec = uint32_t(S / 16);
+        hipLaunchKernelGGL(fn, dim3(blocks_for(nvec, kRs8BS * vec)), dim3(kRs8BS), 0, st, pi, po, mix,
+                           uint32_t(S), nvec);
+    } else {
+        const uint64_t nvec = uint64_t(S) / 16;
+        hipLaunchKernelGGL(gf8_mix_generic_kernel, dim3(unsigned((nvec + kRs8BS - 1) / kRs8BS)),
+                           dim3(kRs8BS), 0, st, pi, po, mix, nin, nout, uint64_t(S), nvec);
+    }
+    return check_launch(what);
+}
+
+static void cauchy(int k, int m, uint8_t* C) {
+    for (int i = 0; i < m; ++i)
+        for (int j = 0; j < k; ++j) C[i * k + j] = kGf8.inv(uint8_t((k + i) ^ j));
+}
+
+// Gauss-Jordan inverse of a k x k matrix over GF(2^8); false if singular.
+static bool gf8_invert(int k, const uint8_t* A, uint8_t* X) {
+    uint8_t M[kRs8MaxK][2 * kRs8MaxK];
+    for (int r = 0; r < k; ++r)
+        for (int c = 0; c < 2 * k; ++c) M[r][c] = c < k ? A[r * k + c] : uint8_t(c - k == r);
+    for (int c = 0; c < k; ++c) {
+        int piv = c;
+        while (piv < k && !M[piv][c]) ++piv;
+        if (piv == k) return false;
+        if (piv != c)
+            for (int x = 0; x < 2 * k; ++x) {
+                uint8_t t = M[c][x];
+                M[c][x] = M[piv][x];
+                M[piv][x] = t;
+            }
+        const uint8_t ip = kGf8.inv(M[c][c]);
+        for (int x = 0; x < 2 * k; ++x) M[c][x] = kGf8.mul(M[c][x], ip);
+        for (int r = 0; r < k; ++r) {
+            if (r == c || !M[r][c]) continue;
+            const uint8_t f = M[r][c];
+            for (int x = 0; x < 2 * k; ++x) M[r][x] ^= kGf8.mul(f, M[c][x]);
+        }
+    }
+    for (int r = 0; r < k; ++r)
+        for (int c = 0; c < k; ++c) X[r * k + c] = M[r][k + c];
+    return true;
+}
+
+static int check_rs8(int k, int m, int64_t S, const char* fn) {
+    if (k < 1 || m < 0 || k > kRs8MaxK || m > kRs8MaxM || k * m > kRs8MaxCoef)
+        return set_error(KVEC_EINVAL, "%s: k=%d m=%d (k <= %d, m <= %d, k*m <= %d)", fn, k, m, kRs8MaxK,
+                         kRs8MaxM, kRs8MaxCoef);
+    if (S < 0 || S % 16) return set_error(KVEC_EINVAL, "%s: shard_bytes=%lld must be a multiple of 16", fn,
+                                          (long long)S);
+    return KVEC_OK;
+}
+
+}  // namespace kvec
+
+using namespace kvec;
+
+extern "C" int kvec_rs8_cauchy(int k, int m, uint8_t* C) {
+    if (k < 1 || m < 0 || k + m > 256 || !C) return set_error(KVEC_EINVAL, "kvec_rs8_cauchy: k=%d m=%d", k, m);
+    cauchy(k, m, C);
+    return KVEC_OK;
+}
+
+extern "C" int kvec_rs8_encode(const void* const* data, int k, void* const* parity, int m,
+                               int64_t shard_bytes, void* stream) {
+    int rc = check_rs8(k, m, shard_bytes, "kvec_rs8_encode");
+    if (rc) return rc;
+    if (m == 0) return KVEC_OK;
+    if (!data || !parity) return set_error(KVEC_EINVAL, "kvec_rs8_encode: null pointer array");
+    uint8_t* in[kRs8MaxK];
+    uint8_t* out[kRs8MaxM];
+    for (int j = 0; j < k; ++j) {
+        if (!data[j] || !aligned16(data[j]))
+            return set_error(KVEC_EINVAL, "kvec_rs8_encode: data[%d] null or not 16-byte aligned", j);
+        in[j] = (uint8_t*)data[j];
+    }
+    for (int i = 0; i < m; ++i) {
+        if (!parity[i] || !aligned16(parity[i]))
+            return set_error(KVEC_EINVAL, "kvec_rs8_encode: parity[%d] null or not 16-byte aligned", i);
+        out[i] = (uint8_t*)parity[i];
+    }
+    uint8_t C[kRs8MaxM * kRs8MaxK];
+    cauchy(k, m, C);
+    return launch_mix(in, k, out, m, C, shard_bytes, as_stream(stream), "kvec_rs8_encode");
+}
+
+extern "C" int kvec_rs8_decode(void* const* shards, int k, int m, int64_t shard_bytes,
+                               const int32_t* erased, int n_erased, void* stream) {
+    int rc = check_rs8(k, m, shard_bytes, "kvec_rs8_decode");
+    if (rc) return rc;
+    if (!shards || (n_erased > 0 && !erased))
+        return set_error(KVEC_EINVAL, "kvec_rs8_decode: null pointer");
+    bool er[kRs8MaxK + kRs8MaxM] = {};
+    for (int q = 0; q < n_erased; ++q) {
+        if (erased[q] < 0 || erased[q] >= k + m)
+            return set_error(KVEC_EINVAL, "kvec_rs8_decode: erased index %d not in [0, %d)", erased[q], k + m);
+        er[erased[q]] = true;
+    }
+    int ne = 0;
+    for (int s = 0; s < k + m; ++s) {
+        if (!shards[s] || !aligned16(shards[s]))
+            return set_error(KVEC_EINVAL, "kvec_rs8_decode: shard %d null or not 16-byte aligned", s);
+        ne += er[s];
+    }
+    if (ne == 0) return KVEC_OK;
+    if (ne > m) return set_error(KVEC_EDECODE, "kvec_rs8_decode: %d erasures > m=%d", ne, m);
+    uint8_t C[kRs8MaxM * kRs8MaxK];
+    cauchy(k, m, C);
+    // the first k surviving shards, in index order
+    int surv[kRs8MaxK], ns = 0;
+    for (int s = 0; s < k + m && ns < k; ++s)
+        if (!er[s]) surv[ns++] = s;
+    uint8_t A[kRs8MaxK * kRs8MaxK], Ai[kRs8MaxK * kRs8MaxK];
+    for (int q = 0; q < k; ++q)
+        for (int j = 0; j < k; ++j)
+            A[q * k + j] = surv[q] < k ? uint8_t(surv[q] == j) : C[(surv[q] - k) * k + j];
+    if (!gf8_invert(k, A, Ai)) return set_error(KVEC_EDECODE, "kvec_rs8_decode: singular survivor block");
+    // rows of the decode matrix: data j -> Ai[j]; parity i -> C[i] * Ai
+    uint8_t M[kRs8MaxM * kRs8MaxK];
+    uint8_t* in[kRs8MaxK];
+    uint8_t* out[kRs8MaxM];
+    int no = 0;
+    for (int s = 0; s < k + m; ++s) {
+        if (!er[s]) continue;
+        for (int q = 0; q < k; ++q) {
+            uint8_t v = 0;
+            if (s < k) {
+                v = Ai[s * k + q];
+            } else {
+                for (int j = 0; j < k; ++j) v ^= kGf8.mul(C[(s - k) * k + j], Ai[j * k + q]);
+            }
+            M[no * k + q] = v;
+        }
+        out[no++] = (uint8_t*)shards[s];
+    }
+    for (int q = 0; q < k; ++q) in[q] = (uint8_t*)shards[surv[q]];
+    return launch_mix(in, k, out, no, M, shard_bytes, as_stream(stream), "kvec_rs8_decode");
+}

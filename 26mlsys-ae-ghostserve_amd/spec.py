@@ -12,8 +12,10 @@ into k consecutive shards of (p-1)*row_bytes bytes, zero-padded at the end.
 """
 from __future__ import annotations
 
+import ctypes
 from typing import Sequence
 
+import numpy as np
 import torch
 
 from . import _lib
@@ -90,3 +92,33 @@ def split_stream(stream: torch.Tensor, k: int, shard_bytes: int):
             t[: hi - lo].copy_(flat[lo:hi])
         out.append(t)
     return out
+
+
+# ------------------------------------------------------------------ RS GF(2^8)
+def rs8_cauchy(k: int, m: int) -> np.ndarray:
+    """The m x k Cauchy parity block C[i][j] = 1 / ((k+i) ^ j) over GF(2^8)/0x11D."""
+    C = np.zeros((m, k), np.uint8)
+    _lib.call("kvec_rs8_cauchy", int(k), int(m), C.ctypes.data)
+    return C
+
+
+def rs8_encode(data: Sequence[torch.Tensor], parity: Sequence[torch.Tensor]) -> None:
+    """parity[i] = XOR_j C[i][j] * data[j] (separate equally sized byte shards)."""
+    _lib.require_cuda(*data, *parity, what="RS shard")
+    nb = {_nbytes(t) for t in list(data) + list(parity)}
+    if len(nb) != 1:
+        raise ValueError("all shards must have the same size")
+    _lib.call("kvec_rs8_encode", _lib.ptr_array(data), len(data), _lib.ptr_array(parity),
+              len(parity), nb.pop(), _lib.stream_handle(data[0].device))
+
+
+def rs8_decode(shards: Sequence[torch.Tensor], k: int, erased: Sequence[int]) -> None:
+    """Rebuild the erased shards (data..., parity...) in place; at most m = len(shards)-k."""
+    _lib.require_cuda(*shards, what="RS shard")
+    nb = {_nbytes(t) for t in shards}
+    if len(nb) != 1:
+        raise ValueError("all shards must have the same size")
+    er = np.ascontiguousarray(sorted({int(e) for e in erased}), dtype=np.int32)
+    _lib.call("kvec_rs8_decode", _lib.ptr_array(shards), int(k), len(shards) - int(k), nb.pop(),
+              er.ctypes.data_as(ctypes.c_void_p) if er.size else None, int(er.size),
+              _lib.stream_handle(shards[0].device))

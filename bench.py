@@ -143,6 +143,85 @@ def decode_all_pairs(pkg, torch, sets, R, seed):
     return times
 
 
+def bench_rs8(pkg, torch, oracle, dev, seed, steps, warmup):
+    """RS(6,2) over GF(2^8)/0x11D (Cauchy) on a long-context stripe:
+    1 x 32,768 tokens x 32 layers x [2, 1, 128] bf16 = 512 MiB.  Encode is
+    sample-checked against the oracle; 2-erasure decodes (seeded patterns) are
+    byte-compared at full size.  Algorithmic bytes as for RDP: 715,827,883."""
+    import itertools
+    import random
+    import numpy as np
+    k, m = 6, 2
+    S = -(-STREAM_BYTES // (k * 16)) * 16
+    sets = []
+    for s in range(2):
+        g = torch.Generator(device=dev)
+        g.manual_seed(seed + 100 + s)
+        stream = torch.randn(STREAM_BYTES // ES, generator=g, device=dev,
+                             dtype=torch.float32).to(torch.bfloat16).view(torch.uint8)
+        data = pkg.spec.split_stream(stream, k, S)
+        del stream
+        par = [torch.empty(S, dtype=torch.uint8, device=dev) for _ in range(m)]
+        sets.append((data, par))
+    for data, par in sets:
+        pkg.spec.rs8_encode(data, par)
+    torch.cuda.synchronize()
+    rng = np.random.default_rng(seed + 7)
+    for si, (data, par) in enumerate(sets):
+        offs = np.sort(rng.choice(S // 16, 4096, replace=False)) * 16
+        idx = torch.from_numpy((offs[:, None] + np.arange(16)).reshape(-1)).to(dev)
+        sub = [np.ascontiguousarray(d[idx].cpu().numpy()) for d in data]
+        want = oracle.rs8_encode(sub, m)
+        for i in range(m):
+            if not np.array_equal(par[i][idx].cpu().numpy(), want[i]):
+                raise RuntimeError("RS8 encode mismatch vs oracle")
+
+    def enc(data, par):
+        pkg.spec.rs8_encode(data, par)
+
+    wall, kms = time_kernel(torch, enc, sets, steps, warmup)
+    enc_us = sum(kms) / len(kms) * 1e3
+    pats = list(itertools.combinations(range(k + m), 2))
+    random.Random(seed).shuffle(pats)
+    pats = pats[:6]
+    stream = torch.cuda.current_stream()
+    dec_us = []
+    for er in pats:
+        for data, par in sets:
+            sh = list(data) + list(par)
+            keep = [sh[e].clone() for e in er]
+            for e in er:
+                sh[e].zero_()
+            pkg.spec.rs8_decode(sh, k, er)
+            if not all(torch.equal(sh[e], kp) for e, kp in zip(er, keep)):
+                raise RuntimeError(f"RS8 decode of {er} is not byte-exact")
+            del keep
+        evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+               for _ in range(4)]
+        for i, (e0, e1) in enumerate(evs):
+            data, par = sets[i % 2]
+            e0.record(stream)
+            pkg.spec.rs8_decode(list(data) + list(par), k, er)
+            e1.record(stream)
+        torch.cuda.synchronize()
+        dec_us.append(sum(x.elapsed_time(y) for x, y in evs) * 1e3 / len(evs))
+    del sets
+    dmean = sum(dec_us) / len(dec_us)
+    return {
+        "workload": "rs8_cauchy_k6m2_1x32768tok_llama3.1-8b",
+        "shard_bytes": S,
+        "encode_us": round(enc_us, 2),
+        "encode_gbs": round(ALG_BYTES / enc_us / 1e3, 2),
+        "encode_frac_hbm_peak": round(ALG_BYTES / enc_us / 1e3 / HBM_PEAK_GBS, 4),
+        "encode_us_per_2048tok": round(enc_us / 16, 2),
+        "decode_patterns": [list(p) for p in pats],
+        "decode_byte_exact": True,
+        "decode_mean_us": round(dmean, 2),
+        "decode_gbs": round(ALG_BYTES / dmean / 1e3, 2),
+        "decode_frac_hbm_peak": round(ALG_BYTES / dmean / 1e3 / HBM_PEAK_GBS, 4),
+    }
+
+
 def cpu_baseline(oracle, torch, data, R, budget_s=10.0):
     import numpy as np
     host = [np.ascontiguousarray(d.cpu().numpy().reshape(P_RDP - 1, R)) for d in data]
@@ -171,6 +250,7 @@ def main():
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-decode", action="store_true")
+    ap.add_argument("--no-rs8", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run three 256 MiB device copies (reference kernel of known "
                          "size for HBM byte counters)")
@@ -226,6 +306,13 @@ def main():
             "slowest_us": round(dec[worst], 2),
         }
 
+    rs8 = None
+    if not args.no_rs8:
+        log("[bench] RS(6,2) GF(2^8) on the 1 x 32768-token stripe")
+        rs8 = bench_rs8(pkg, torch, oracle, dev, args.seed, args.steps, args.warmup)
+        log(f"[bench] rs8: encode {rs8['encode_us']:.1f} us ({rs8['encode_gbs']:.0f} GB/s), "
+            f"decode {rs8['decode_mean_us']:.1f} us ({rs8['decode_gbs']:.0f} GB/s)")
+
     if args.copy_calibration:
         src = torch.empty(1 << 28, dtype=torch.uint8, device=dev)
         dst = torch.empty_like(src)
@@ -270,6 +357,7 @@ def main():
         },
         "cpu_baseline": cpu,
         "decode_2erasure": dec_out,
+        "rs8_gf256": rs8,
     }
     print(json.dumps(out), flush=True)
 

@@ -62,6 +62,24 @@ int kvec_rdp_decode(void* const* shards, int k, int p, int64_t row_bytes, int e0
  * k*(p-1) row planes hold `stream_bytes` bytes.  Host-only arithmetic. */
 int64_t kvec_rdp_row_bytes(int64_t stream_bytes, int k, int p, int64_t granule);
 
+/* ================== spec family: RS over GF(2^8), Cauchy ================== */
+/* No reference counterpart (the reference RS works over GF(2^16), below); this
+ * is the code BASELINE's RS configurations name.  Polynomial 0x11D, systematic
+ * generator [I_k; C] with C[i][j] = 1 / ((k+i) ^ j).  Shards are separate
+ * 16-byte aligned buffers of shard_bytes (% 16 == 0) bytes.
+ * Limits: k <= 32, m <= 8, k*m <= 64. */
+
+/* The m x k block C, row-major, into host memory. */
+int kvec_rs8_cauchy(int k, int m, uint8_t* C);
+/* parity[i] = XOR_j C[i][j] * data[j]; host arrays of device pointers. */
+int kvec_rs8_encode(const void* const* data, int k, void* const* parity, int m,
+                    int64_t shard_bytes, void* stream);
+/* Rebuild the erased shards (host int32 array of shard indices in [0, k+m),
+ * at most m of them) in place from the first k surviving shards.  shards =
+ * host array of k+m device pointers (data..., parity...). */
+int kvec_rs8_decode(void* const* shards, int k, int m, int64_t shard_bytes,
+                    const int32_t* erased, int n_erased, void* stream);
+
 /* ============ gs family: XOR (benchmark/xor/kernel.cu, main.py) =========== */
 /* Byte shards, packed: shards = [(data_shards + 1), shard_size] bytes. */
 

@@ -66,3 +66,42 @@ def test_rdp_decode_inconsistent_input_matches_oracle(pkg, ora, gpu):
         torch.cuda.synchronize()
         for s in range(k + 2):
             assert np.array_equal(_host(dev[s], (p - 1, R)), want[s]), (e0, e1, s)
+
+
+# ------------------------------------------------------------------ RS GF(2^8)
+@pytest.mark.parametrize("k,m,S", [(6, 2, 4096), (5, 3, 1024 + 16), (4, 2, 16), (8, 2, 2048),
+                                   (10, 4, 512), (3, 1, 4096), (7, 3, 160), (12, 5, 64)])
+def test_rs8_encode_matches_oracle(pkg, ora, gpu, k, m, S):
+    assert np.array_equal(pkg.spec.rs8_cauchy(k, m), ora.rs8_cauchy(k, m))
+    rng = np.random.default_rng(k * 10 + m)
+    data = [rng.integers(0, 256, S, dtype=np.uint8) for _ in range(k)]
+    want = ora.rs8_encode(data, m)
+    d = _to_dev(data, gpu)
+    par = [torch.full((S,), 0x33, dtype=torch.uint8, device=gpu) for _ in range(m)]
+    pkg.spec.rs8_encode(d, par)
+    torch.cuda.synchronize()
+    for i in range(m):
+        assert np.array_equal(par[i].cpu().numpy(), want[i]), i
+
+
+@pytest.mark.parametrize("k,m", [(6, 2), (5, 3), (4, 2), (7, 3), (10, 4)])
+def test_rs8_decode_all_patterns(pkg, ora, gpu, k, m):
+    S = 2048 + 16
+    rng = np.random.default_rng(k * 31 + m)
+    data = [rng.integers(0, 256, S, dtype=np.uint8) for _ in range(k)]
+    full = data + ora.rs8_encode(data, m)
+    pats = [e for n in range(1, m + 1) for e in itertools.combinations(range(k + m), n)]
+    if len(pats) > 60:
+        pats = [pats[i] for i in rng.choice(len(pats), 60, replace=False)]
+    for er in pats:
+        sh = [x.copy() for x in full]
+        for e in er:
+            sh[e][:] = rng.integers(0, 256, S, dtype=np.uint8)
+        want = [x.copy() for x in sh]
+        ora.rs8_decode(want, k, m, er)
+        dev_sh = _to_dev(sh, gpu)
+        pkg.spec.rs8_decode(dev_sh, k, er)
+        torch.cuda.synchronize()
+        for s in range(k + m):
+            got = dev_sh[s].cpu().numpy()
+            assert np.array_equal(got, want[s]) and np.array_equal(got, full[s]), (er, s)
