@@ -9,10 +9,11 @@ signatures:
   rs          Reed-Solomon over GF(2^16)  (benchmark/rs/main.py)
   rdp_kv_ops  the serving plugin's inline extension (bench_ghostserve_rdp.py)
   spec        textbook RDP over a prime p, RS over GF(2^8) (stripe configs)
+  paged       paged KV pool <-> coding stream; fused gather + RDP encode
 
 Import the package with ``importlib.import_module("26mlsys-ae-ghostserve_amd")``
 (the directory name is not a Python identifier).
 """
-from . import _lib, rdp, rdp_kv_ops, rs, spec, xor  # noqa: F401
+from . import _lib, paged, rdp, rdp_kv_ops, rs, spec, xor  # noqa: F401
 
-__all__ = ["xor", "rdp", "rs", "rdp_kv_ops", "spec"]
+__all__ = ["xor", "rdp", "rs", "rdp_kv_ops", "spec", "paged"]

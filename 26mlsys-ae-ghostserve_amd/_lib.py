@@ -23,6 +23,24 @@ _i = C.c_int
 _i64 = C.c_int64
 _pp = C.POINTER(C.c_void_p)
 
+class PagedKV(C.Structure):
+    """struct kvec_paged_kv of include/kvec.h."""
+    _fields_ = [
+        ("pool", C.c_void_p),
+        ("pool_pages", C.c_int64),
+        ("layers", C.c_int),
+        ("token_bytes", C.c_int64),
+        ("page_tokens", C.c_int),
+        ("page_table", C.c_void_p),
+        ("batch", C.c_int),
+        ("pages_per_seq", C.c_int),
+        ("tok_off", C.c_int),
+        ("tokens", C.c_int),
+    ]
+
+
+_kvp = C.POINTER(PagedKV)
+
 # name -> (restype, argtypes); mirrors include/kvec.h
 SIGNATURES = {
     "kvec_version": (_i, []),
@@ -34,6 +52,10 @@ SIGNATURES = {
     "kvec_rs8_cauchy": (_i, [_i, _i, _vp]),
     "kvec_rs8_encode": (_i, [_pp, _i, _pp, _i, _i64, _vp]),
     "kvec_rs8_decode": (_i, [_pp, _i, _i, _i64, _vp, _i, _vp]),
+    "kvec_kv_stream_bytes": (_i64, [_kvp]),
+    "kvec_kv_gather": (_i, [_kvp, _vp, _vp]),
+    "kvec_kv_scatter": (_i, [_kvp, _vp, _vp, _vp]),
+    "kvec_rdp_encode_paged": (_i, [_kvp, _pp, _i, _vp, _vp, _i, _i64, _vp]),
     "kvec_xor_encode": (_i, [_vp, _vp, _i, _i64, _vp]),
     "kvec_xor_reconstruct": (_i, [_vp, _vp, _vp, _i64, _i, _vp, _i, _vp]),
     "kvec_pack_kv": (_i, [_vp, _vp, _vp, _i, _i, _vp]),

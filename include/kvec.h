@@ -80,6 +80,41 @@ int kvec_rs8_encode(const void* const* data, int k, void* const* parity, int m,
 int kvec_rs8_decode(void* const* shards, int k, int m, int64_t shard_bytes,
                     const int32_t* erased, int n_erased, void* stream);
 
+/* ============================ paged KV gather ============================ */
+/* The delta gather of the serving plugin, K = pool[slots, 0], V = pool[slots, 1]
+ * (bench_ghostserve_rdp.py:440-458), over a paged pool.  Pool layout:
+ * [layers][pool_pages][page_tokens][2 (K,V)][token_bytes]; page_table: device
+ * int32 [batch][pages_per_seq] of pool pages.  The coding stream of a chunk
+ * (positions tok_off .. tok_off+tokens-1 of every sequence) is
+ * [layers][2][batch][tokens][token_bytes]: per layer every K, then every V.
+ * token_bytes % 16 == 0, page_tokens a power of two.  Page-table entries
+ * outside [0, pool_pages) read as zero pages and are skipped by the scatter. */
+typedef struct kvec_paged_kv {
+    const void* pool;
+    int64_t pool_pages;
+    int layers;
+    int64_t token_bytes;        /* kv_heads * head_dim * element bytes */
+    int page_tokens;
+    const int32_t* page_table;  /* device */
+    int batch;
+    int pages_per_seq;
+    int tok_off;
+    int tokens;
+} kvec_paged_kv;
+
+/* Bytes of the coding stream of `kv` (host arithmetic). */
+int64_t kvec_kv_stream_bytes(const kvec_paged_kv* kv);
+/* out[0 .. stream bytes) = the chunk's stream gathered from the pool. */
+int kvec_kv_gather(const kvec_paged_kv* kv, void* out, void* stream);
+/* Inverse: write the stream `in` back into the pool pages (pool == kv->pool). */
+int kvec_kv_scatter(const kvec_paged_kv* kv, void* pool, const void* in, void* stream);
+/* Fused gather + spec RDP encode: the chunk's stream, cut into k data shards
+ * of (p-1)*row_bytes bytes (zero padded), is written to data[0..k-1] and its
+ * P, Q to P, Q, reading every pool byte once.  row_bytes must be a multiple of
+ * token_bytes and k*(p-1)*row_bytes >= the stream bytes. */
+int kvec_rdp_encode_paged(const kvec_paged_kv* kv, void* const* data, int k, void* P, void* Q,
+                          int p, int64_t row_bytes, void* stream);
+
 /* ============ gs family: XOR (benchmark/xor/kernel.cu, main.py) =========== */
 /* Byte shards, packed: shards = [(data_shards + 1), shard_size] bytes. */
 
