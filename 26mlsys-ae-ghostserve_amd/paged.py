@@ -5,8 +5,9 @@ gather + RDP encode that codes a prefill chunk straight out of the pool.
 Pool tensor: [layers, pool_pages, page_tokens, 2 (K,V), kv_heads, head_dim] of
 any dtype (coded as raw bytes).  Page table: int32 [batch, pages_per_seq] of
 pool page indices.  Stream of a chunk of ``tokens`` positions starting at
-``tok_off``: [layers, 2, batch, tokens, kv_heads, head_dim] -- per layer every
-K, then every V, as in the reference's K || V rows.
+``tok_off``: the chunk's token records in order,
+[layers, batch, tokens, 2 (K,V), kv_heads, head_dim], so each pool page
+contributes contiguous runs of records.
 """
 from __future__ import annotations
 
@@ -48,7 +49,7 @@ class PagedKV:
         return int(_lib.lib().kvec_kv_stream_bytes(self._c))
 
     def stream_shape(self):
-        return (self.layers, 2, self.batch, self.tokens, self.heads, self.dim)
+        return (self.layers, self.batch, self.tokens, 2, self.heads, self.dim)
 
     def gather(self, out: torch.Tensor | None = None) -> torch.Tensor:
         """The chunk's stream, as a uint8 tensor of stream_bytes() bytes."""
@@ -71,12 +72,9 @@ class PagedKV:
 
 
 def rdp_row_bytes_for(kv: PagedKV, k: int, p: int) -> int:
-    """Row-plane size for kv's stream: a multiple of the token bytes."""
+    """Row-plane size for kv's stream: a multiple of one token record (K and V)."""
     from .spec import rdp_row_bytes
-    g = kv.token_bytes
-    while g % 16:
-        g *= 2
-    return rdp_row_bytes(kv.stream_bytes(), k, p, g)
+    return rdp_row_bytes(kv.stream_bytes(), k, p, 2 * kv.token_bytes)
 
 
 def rdp_encode_paged(kv: PagedKV, data: Sequence[torch.Tensor], P: torch.Tensor, Q: torch.Tensor,

@@ -85,8 +85,8 @@ int kvec_rs8_decode(void* const* shards, int k, int m, int64_t shard_bytes,
  * (bench_ghostserve_rdp.py:440-458), over a paged pool.  Pool layout:
  * [layers][pool_pages][page_tokens][2 (K,V)][token_bytes]; page_table: device
  * int32 [batch][pages_per_seq] of pool pages.  The coding stream of a chunk
- * (positions tok_off .. tok_off+tokens-1 of every sequence) is
- * [layers][2][batch][tokens][token_bytes]: per layer every K, then every V.
+ * (positions tok_off .. tok_off+tokens-1 of every sequence) is the chunk's
+ * token records in order, [layers][batch][tokens][2 (K,V)][token_bytes].
  * token_bytes % 16 == 0, page_tokens a power of two.  Page-table entries
  * outside [0, pool_pages) read as zero pages and are skipped by the scatter. */
 typedef struct kvec_paged_kv {
@@ -111,7 +111,7 @@ int kvec_kv_scatter(const kvec_paged_kv* kv, void* pool, const void* in, void* s
 /* Fused gather + spec RDP encode: the chunk's stream, cut into k data shards
  * of (p-1)*row_bytes bytes (zero padded), is written to data[0..k-1] and its
  * P, Q to P, Q, reading every pool byte once.  row_bytes must be a multiple of
- * token_bytes and k*(p-1)*row_bytes >= the stream bytes. */
+ * 2*token_bytes (one token record) and k*(p-1)*row_bytes >= the stream bytes. */
 int kvec_rdp_encode_paged(const kvec_paged_kv* kv, void* const* data, int k, void* P, void* Q,
                           int p, int64_t row_bytes, void* stream);
 

@@ -602,7 +602,9 @@ int kvo_rs8_decode(uint8_t* const* sh, int k, int m, int64_t S, const int32_t* e
 /* Semantics of the delta gather K = pool[slots, 0], V = pool[slots, 1]
  * (bench_ghostserve_rdp.py:445-458), with slots taken from a page table of
  * page_tokens-token pages: slot(b, t) = table[b][t / page_tokens] * page_tokens
- * + t % page_tokens.  The stream is per layer K of every (b, t) then V. */
+ * + t % page_tokens.  The stream holds, per layer and sequence, the token
+ * records (K then V, as stored in the pool) of positions tok_off.. in order:
+ * [L][B][T][2][tok_bytes]. */
 int kvo_kv_gather(const uint8_t* pool, int64_t pool_pages, int L, int64_t tb,
                   int page_tokens, const int32_t* pt, int B, int pps, int tok_off, int T,
                   uint8_t* stream) {
@@ -615,17 +617,18 @@ int kvo_kv_gather(const uint8_t* pool, int64_t pool_pages, int L, int64_t tb,
     const int64_t layer_pool = pool_pages * page_tokens * 2 * tb;
 #pragma omp parallel for collapse(2) schedule(static)
     for (int l = 0; l < L; ++l)
-        for (int kv = 0; kv < 2; ++kv)
-            for (int b = 0; b < B; ++b)
-                for (int t = 0; t < T; ++t) {
-                    const int tt = tok_off + t;
-                    const int64_t slot =
-                        (int64_t)pt[(int64_t)b * pps + tt / page_tokens] * page_tokens +
-                        tt % page_tokens;
+        for (int b = 0; b < B; ++b)
+            for (int t = 0; t < T; ++t) {
+                const int tt = tok_off + t;
+                const int64_t slot =
+                    (int64_t)pt[(int64_t)b * pps + tt / page_tokens] * page_tokens +
+                    tt % page_tokens;
+                for (int kv = 0; kv < 2; ++kv) {
                     const uint8_t* src = pool + l * layer_pool + (slot * 2 + kv) * tb;
                     uint8_t* dst =
-                        stream + ((((int64_t)l * 2 + kv) * B + b) * (int64_t)T + t) * tb;
+                        stream + ((((int64_t)l * B + b) * (int64_t)T + t) * 2 + kv) * tb;
                     memcpy(dst, src, (size_t)tb);
                 }
+            }
     return 0;
 }

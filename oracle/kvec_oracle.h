@@ -80,7 +80,7 @@ int kvo_rs8_decode(uint8_t* const* shards, int k, int m, int64_t S,
 
 /* ---------------- paged KV gather ---------------- */
 /* pool: [L][pool_pages][page_tokens][2][tok_bytes]; page_table: [B][pps] int32.
- * stream: [L][2][B][T][tok_bytes] for tokens tok_off .. tok_off+T-1. */
+ * stream: [L][B][T][2][tok_bytes] for tokens tok_off .. tok_off+T-1. */
 int kvo_kv_gather(const uint8_t* pool, int64_t pool_pages, int L, int64_t tok_bytes,
                   int page_tokens, const int32_t* page_table, int B, int pps,
                   int tok_off, int T, uint8_t* stream);

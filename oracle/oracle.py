@@ -246,11 +246,11 @@ def rs8_decode(shards, k: int, m: int, erased):
 def kv_gather(pool: np.ndarray, page_table: np.ndarray, page_tokens: int, tok_off: int,
               T: int) -> np.ndarray:
     """pool: [L, pool_pages, page_tokens, 2, tok_bytes] uint8;
-    page_table: [B, pps] int32.  Returns stream [L, 2, B, T, tok_bytes]."""
+    page_table: [B, pps] int32.  Returns stream [L, B, T, 2, tok_bytes]."""
     L, pool_pages, pt_, two, tb = pool.shape
     assert pt_ == page_tokens and two == 2
     B, pps = page_table.shape
-    out = np.zeros((L, 2, B, T, tb), np.uint8)
+    out = np.zeros((L, B, T, 2, tb), np.uint8)
     pt = np.ascontiguousarray(page_table, np.int32)
     _check(lib().kvo_kv_gather(_p(pool), pool_pages, L, tb, page_tokens, _p(pt), B, pps,
                                tok_off, T, _p(out)), "kv_gather")

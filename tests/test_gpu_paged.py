@@ -38,13 +38,13 @@ def test_gather_scatter_match_oracle(pkg, ora, gpu, L, B, pps, pt, H, D, dtype, 
     kv.scatter(new.to(gpu))
     after = pool_bytes(kv.pool.cpu())
     exp = pool_bytes(pool).copy()
-    newv = new.numpy().reshape(L, 2, B, T, -1)
+    newv = new.numpy().reshape(L, B, T, 2, -1)
     for b in range(B):
         for t in range(T):
             tt = tok_off + t
             page = int(table[b, tt // pt])
             for kvi in range(2):
-                exp[:, page, tt % pt, kvi] = newv[:, kvi, b, t]
+                exp[:, page, tt % pt, kvi] = newv[:, b, t, kvi]
     assert np.array_equal(after, exp)
 
 
@@ -54,7 +54,7 @@ def test_fused_gather_rdp_encode(pkg, ora, gpu, p, k):
     pool, table = make_pool(gpu, L, B, pps, pt, H, D, torch.bfloat16, seed=p * k)
     kv = pkg.paged.PagedKV(pool.to(gpu), table.to(gpu), 0, pps * pt)
     R = pkg.paged.rdp_row_bytes_for(kv, k, p)
-    assert R % kv.token_bytes == 0
+    assert R % (2 * kv.token_bytes) == 0
     n = (p - 1) * R
     data = [torch.full((n,), 0x77, dtype=torch.uint8, device=gpu) for _ in range(k)]
     P = torch.empty(n, dtype=torch.uint8, device=gpu)
@@ -81,6 +81,6 @@ def test_invalid_page_reads_zero(pkg, gpu):
     pool, table = make_pool(gpu, L, B, pps, pt, H, D, torch.float16, seed=5)
     table[0, 1] = 10 ** 6
     kv = pkg.paged.PagedKV(pool.to(gpu), table.to(gpu), 0, 8)
-    s = kv.gather().cpu().numpy().reshape(L, 2, B, 8, -1)
-    assert not s[:, :, 0, 4:].any()
-    assert s[:, :, 0, :4].any()
+    s = kv.gather().cpu().numpy().reshape(L, B, 8, 2, -1)
+    assert not s[:, 0, 4:].any()
+    assert s[:, 0, :4].any()

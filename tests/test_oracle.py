@@ -421,4 +421,4 @@ def test_kv_gather_matches_indexing(ora, tb, page_tokens, tok_off, T):
     tokpool = pool.reshape(L, pool_pages * page_tokens, 2, tb)
     for kv in range(2):
         want = tokpool[:, slots.reshape(-1), kv].reshape(L, B, T, tb)
-        assert np.array_equal(got[:, kv], want)
+        assert np.array_equal(got[:, :, :, kv], want)
