@@ -41,6 +41,25 @@ class PagedKV(C.Structure):
 
 _kvp = C.POINTER(PagedKV)
 
+
+class ChunkStripe(C.Structure):
+    """struct kvec_chunk_stripe of include/kvec.h."""
+    _fields_ = [
+        ("data", C.POINTER(C.c_void_p)),
+        ("k", C.c_int),
+        ("P", C.c_void_p),
+        ("Q", C.c_void_p),
+        ("p", C.c_int),
+        ("rs", C.POINTER(C.c_void_p)),
+        ("m", C.c_int),
+        ("row_bytes", C.c_int64),
+        ("col_off", C.c_int64),
+        ("width", C.c_int64),
+    ]
+
+
+_csp = C.POINTER(ChunkStripe)
+
 # name -> (restype, argtypes); mirrors include/kvec.h
 SIGNATURES = {
     "kvec_version": (_i, []),
@@ -56,6 +75,9 @@ SIGNATURES = {
     "kvec_kv_gather": (_i, [_kvp, _vp, _vp]),
     "kvec_kv_scatter": (_i, [_kvp, _vp, _vp, _vp]),
     "kvec_rdp_encode_paged": (_i, [_kvp, _pp, _i, _vp, _vp, _i, _i64, _vp]),
+    "kvec_chunk_width": (_i64, [_i64, _i, _i, _i64]),
+    "kvec_chunk_encode_paged": (_i, [_kvp, _csp, _vp]),
+    "kvec_chunk_decode_paged": (_i, [_kvp, _vp, _csp, _vp, _i, _vp]),
     "kvec_xor_encode": (_i, [_vp, _vp, _i, _i64, _vp]),
     "kvec_xor_reconstruct": (_i, [_vp, _vp, _vp, _i64, _i, _vp, _i, _vp]),
     "kvec_pack_kv": (_i, [_vp, _vp, _vp, _i, _i, _vp]),

@@ -1,0 +1,474 @@
+// chunk.hip -- chunked coding of a paged KV pool, as prefill chunks arrive.
+//
+// One pass over a chunk's token records in the pool writes, at the chunk's own
+// columns of whole-sequence stripes:
+//   * (optionally) the k data shards,
+//   * textbook RDP(p) row parity P and diagonal parity Q over those k shards
+//     (k <= p-1; columns k..p-2 of the code are implicit zeros),
+//   * systematic RS(k, m) parity over GF(2^8)/0x11D (Cauchy) over the same k
+//     shards.
+//
+// Layout: chunk c's stream (its token records in order, paged_geom.h) is cut
+// into k*(p-1) cells of W bytes; cell (shard j, row r) is stream bytes
+// [(j*(p-1) + r)*W, +W) and lands at columns [col_off, col_off + W) of row
+// plane r of shard j, where a shard holds p-1 row planes of R bytes.  Both codes
+// work column by column, so a chunk touches only its own columns: no parity is
+// read back, and the union of the per-chunk encodes is the encode of the whole
+// sequence's stripes.
+//
+// The inverse rebuilds lost data cells straight into the pool pages: surviving
+// data cells are read from the pool (the pool is the primary copy of the data),
+// parity from the stripe buffers.  Lost parity shards are then re-encoded.
+#include "gf8.h"
+#include "paged_geom.h"
+#include "rdp_plan.h"
+
+namespace kvec {
+
+constexpr int kChunkMaxK = 12;
+constexpr int kChunkMaxM = 4;
+constexpr int kCBS = 128;
+
+// write-mask bits of the encode kernel; RS parity i is bit kWRs + i
+constexpr uint32_t kWData = 1u, kWP = 2u, kWQ = 4u, kWRs = 3;
+
+struct ChunkGeom {
+    uint64_t R;              // row-plane bytes of the whole-sequence stripe
+    uint32_t col_off;        // chunk's first column (bytes)
+    uint32_t recs_per_cell;  // W / record bytes
+    uint32_t nvec;           // W / 16
+};
+
+template <int N>
+struct Gf8Tab {
+    uint32_t t[N][6];
+};
+
+// Pool cell (shard j, row r) of the thread's column; zero for padding records.
+__device__ __forceinline__ u32x4 load_cell(const PagedGeom& g, const ChunkGeom& cg, int j, int r,
+                                           int rows, uint32_t w0, uint32_t inner) {
+    const uint32_t w = uint32_t(j * rows + r) * cg.recs_per_cell + w0;
+    const uint8_t* src = cell_src(g, w, inner);
+    return src ? ld_stream(src, 0) : u32x4{0, 0, 0, 0};
+}
+
+// ------------------------------------------------------------------ encode
+template <int P, int K, int M>
+__global__ __launch_bounds__(kCBS) void chunk_encode_kernel(PagedGeom g, ChunkGeom cg,
+                                                            Ptrs<kChunkMaxK> d,
+                                                            Ptrs<2 + kChunkMaxM> par,
+                                                            Gf8Tab<(K * M > 0 ? K * M : 1)> rs,
+                                                            uint32_t wmask) {
+    constexpr int ROWS = P - 1;
+    const uint32_t u = blockIdx.x * kCBS + threadIdx.x;
+    if (u >= cg.nvec) return;
+    const uint32_t o = u << 4;
+    const uint32_t w0 = fdiv(o, g.div_rec);
+    const uint32_t inner = o - w0 * g.rec;
+    const uint64_t nb = ROWS * cg.R;
+    const uint32_t lane = cg.col_off + o;
+    u32x4 q[ROWS];
+#pragma unroll
+    for (int r = 0; r < ROWS; ++r) q[r] = u32x4{0, 0, 0, 0};
+#pragma unroll
+    for (int r = 0; r < ROWS; ++r) {
+        u32x4 x[K];
+#pragma unroll
+        for (int j = 0; j < K; ++j) x[j] = load_cell(g, cg, j, r, ROWS, w0, inner);
+        if (wmask & kWData) {
+#pragma unroll
+            for (int j = 0; j < K; ++j) ShardView<true>(d.p[j], nb).store(r * cg.R, lane, x[j]);
+        }
+        u32x4 pr = x[0];
+#pragma unroll
+        for (int j = 1; j < K; ++j) pr ^= x[j];
+        if (wmask & kWP) ShardView<true>(par.p[0], nb).store(r * cg.R, lane, pr);
+        // cell (r, j) lies on diagonal (r + j) % p; the P cell of row r on r - 1
+#pragma unroll
+        for (int j = 0; j < K; ++j) {
+            const int dg = (r + j) % P;
+            if (dg != P - 1) q[dg] ^= x[j];
+        }
+        if (r >= 1) q[r - 1] ^= pr;
+        if constexpr (M > 0) {
+            u32x4 acc[M];
+#pragma unroll
+            for (int i = 0; i < M; ++i) acc[i] = u32x4{0, 0, 0, 0};
+#pragma unroll
+            for (int j = 0; j < K; ++j) {
+                const uint32_t w4[4] = {x[j].x, x[j].y, x[j].z, x[j].w};
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const Gf8Fields f = gf8_fields(w4[e]);
+#pragma unroll
+                    for (int i = 0; i < M; ++i) {
+                        const uint32_t pm = gf8_mul4(f, rs.t[i * K + j]);
+                        if (e == 0) acc[i].x ^= pm;
+                        else if (e == 1) acc[i].y ^= pm;
+                        else if (e == 2) acc[i].z ^= pm;
+                        else acc[i].w ^= pm;
+                    }
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < M; ++i)
+                if (wmask & (1u << (kWRs + i)))
+                    ShardView<true>(par.p[2 + i], nb).store(r * cg.R, lane, acc[i]);
+        }
+    }
+    if (wmask & kWQ) {
+        const ShardView<true> sq(par.p[1], nb);
+#pragma unroll
+        for (int r = 0; r < ROWS; ++r) sq.store(r * cg.R, lane, q[r]);
+    }
+}
+
+// ------------------------------------------------------------------ RS decode
+// Row by row: out_o = XOR_q M[o][q] * in_q.  Input q is data shard src_shard[q]
+// read from the pool when in_buf[q] is null, else the parity buffer in_buf[q].
+// Output o goes to the pool cells of data shard dst_shard[o] (if >= 0) and to
+// out_buf[o] (if not null).
+struct RsDecodeIo {
+    uint8_t* in_buf[kChunkMaxK];
+    int src_shard[kChunkMaxK];
+    uint8_t* out_buf[kChunkMaxM];
+    int dst_shard[kChunkMaxM];
+};
+
+template <int K, int NOUT>
+__global__ __launch_bounds__(kCBS) void chunk_rs_decode_kernel(PagedGeom g, ChunkGeom cg, int rows,
+                                                               RsDecodeIo io, Gf8Tab<K * NOUT> mix) {
+    const uint32_t u = blockIdx.x * kCBS + threadIdx.x;
+    if (u >= cg.nvec) return;
+    const uint32_t o = u << 4;
+    const uint32_t w0 = fdiv(o, g.div_rec);
+    const uint32_t inner = o - w0 * g.rec;
+    const uint64_t nb = uint64_t(rows) * cg.R;
+    const uint32_t lane = cg.col_off + o;
+    for (int r = 0; r < rows; ++r) {
+        u32x4 acc[NOUT];
+#pragma unroll
+        for (int i = 0; i < NOUT; ++i) acc[i] = u32x4{0, 0, 0, 0};
+#pragma unroll
+        for (int q = 0; q < K; ++q) {
+            const u32x4 x = io.in_buf[q]
+                                ? ShardView<true>(io.in_buf[q], nb).load(r * cg.R, lane)
+                                : load_cell(g, cg, io.src_shard[q], r, rows, w0, inner);
+            const uint32_t w4[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const Gf8Fields f = gf8_fields(w4[e]);
+#pragma unroll
+                for (int i = 0; i < NOUT; ++i) {
+                    const uint32_t pm = gf8_mul4(f, mix.t[i * K + q]);
+                    if (e == 0) acc[i].x ^= pm;
+                    else if (e == 1) acc[i].y ^= pm;
+                    else if (e == 2) acc[i].z ^= pm;
+                    else acc[i].w ^= pm;
+                }
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < NOUT; ++i) {
+            if (io.dst_shard[i] >= 0) {
+                const uint32_t w = uint32_t(io.dst_shard[i] * rows + r) * cg.recs_per_cell + w0;
+                if (cell_src(g, w, inner)) st_stream(cell_dst(g, w, inner), 0, acc[i]);
+            }
+            if (io.out_buf[i]) ShardView<true>(io.out_buf[i], nb).store(r * cg.R, lane, acc[i]);
+        }
+    }
+}
+
+// ------------------------------------------------------------------ RDP decode
+// The erasure pattern's XOR map (rdp_plan.h) over cells: data cells come from
+// (and rebuilt ones go to) the pool, P and Q cells from the parity buffers.
+// One output cell at a time, so re-read inputs come from cache.
+__device__ __forceinline__ u32x4 rdp_cell_load(const PagedGeom& g, const ChunkGeom& cg, int k,
+                                               int rows, const uint8_t* P, const uint8_t* Q, int c,
+                                               uint32_t w0, uint32_t inner, uint32_t lane) {
+    const int s = c / rows, r = c - s * rows;
+    if (s < k) return load_cell(g, cg, s, r, rows, w0, inner);
+    return ld16((s == k ? P : Q) + uint64_t(r) * cg.R + lane);
+}
+
+__global__ __launch_bounds__(kCBS) void chunk_rdp_decode_kernel(PagedGeom g, ChunkGeom cg, int k,
+                                                                int rows, Ptrs<kChunkMaxK> d,
+                                                                uint8_t* P, uint8_t* Q, RdpPlan plan) {
+    const uint32_t u = blockIdx.x * kCBS + threadIdx.x;
+    if (u >= cg.nvec) return;
+    const uint32_t o = u << 4;
+    const uint32_t w0 = fdiv(o, g.div_rec);
+    const uint32_t inner = o - w0 * g.rec;
+    const uint32_t lane = cg.col_off + o;
+    for (int oc = 0; oc < plan.nout; ++oc) {
+        u32x4 acc = {0, 0, 0, 0};
+        for (int wd = 0; wd < kRdpNW; ++wd) {
+            uint64_t msk = plan.mask[oc][wd];
+            while (msk) {
+                const int c = wd * 64 + __builtin_ctzll(msk);
+                msk &= msk - 1;
+                acc ^= rdp_cell_load(g, cg, k, rows, P, Q, c, w0, inner, lane);
+            }
+        }
+        const int c = plan.out_cell[oc];
+        const int s = c / rows, r = c - s * rows;
+        if (s < k) {
+            const uint32_t w = uint32_t(s * rows + r) * cg.recs_per_cell + w0;
+            if (cell_src(g, w, inner)) st_stream(cell_dst(g, w, inner), 0, acc);
+            if (d.p[s]) st_stream(d.p[s] + uint64_t(r) * cg.R, lane, acc);
+        } else {
+            st_stream((s == k ? P : Q) + uint64_t(r) * cg.R, lane, acc);
+        }
+    }
+}
+
+// ------------------------------------------------------------------ dispatch
+// Launch the encode instantiation <P, K, M> with a table sized for it.
+template <int P, int K, int M>
+static void launch_encode(dim3 grid, hipStream_t st, const PagedGeom& g, const ChunkGeom& cg,
+                          const Ptrs<kChunkMaxK>& d, const Ptrs<2 + kChunkMaxM>& par,
+                          const uint32_t (*tab)[6], uint32_t wmask) {
+    Gf8Tab<(K * M > 0 ? K * M : 1)> t{};
+    for (int i = 0; i < K * M; ++i)
+        for (int e = 0; e < 6; ++e) t.t[i][e] = tab[i][e];
+    hipLaunchKernelGGL((chunk_encode_kernel<P, K, M>), grid, dim3(kCBS), 0, st, g, cg, d, par, t,
+                       wmask);
+}
+
+typedef void (*EncLauncher)(dim3, hipStream_t, const PagedGeom&, const ChunkGeom&,
+                            const Ptrs<kChunkMaxK>&, const Ptrs<2 + kChunkMaxM>&,
+                            const uint32_t (*)[6], uint32_t);
+
+template <int P, int K, int M = 0>
+EncLauncher pick_encode_m(int m) {
+    if constexpr (M > 3) {
+        return nullptr;
+    } else {
+        if (m == M) return &launch_encode<P, K, M>;
+        return pick_encode_m<P, K, M + 1>(m);
+    }
+}
+
+template <int P, int K = 2>
+EncLauncher pick_encode_k(int k, int m) {
+    if constexpr (K > P - 1) {
+        return nullptr;
+    } else {
+        if (k == K) return pick_encode_m<P, K>(m);
+        return pick_encode_k<P, K + 1>(k, m);
+    }
+}
+
+// Built: p in {3, 5, 7}, 2 <= k <= p-1, 0 <= m <= 3.
+static EncLauncher encode_launcher(int p, int k, int m) {
+    switch (p) {
+        case 3: return pick_encode_k<3>(k, m);
+        case 5: return pick_encode_k<5>(k, m);
+        case 7: return pick_encode_k<7>(k, m);
+        default: return nullptr;
+    }
+}
+
+template <int K, int NOUT>
+static void launch_rs_decode(dim3 grid, hipStream_t st, const PagedGeom& g, const ChunkGeom& cg,
+                             int rows, const RsDecodeIo& io, const uint32_t (*tab)[6]) {
+    Gf8Tab<K * NOUT> t{};
+    for (int i = 0; i < K * NOUT; ++i)
+        for (int e = 0; e < 6; ++e) t.t[i][e] = tab[i][e];
+    hipLaunchKernelGGL((chunk_rs_decode_kernel<K, NOUT>), grid, dim3(kCBS), 0, st, g, cg, rows, io, t);
+}
+
+typedef void (*RsDecLauncher)(dim3, hipStream_t, const PagedGeom&, const ChunkGeom&, int,
+                              const RsDecodeIo&, const uint32_t (*)[6]);
+
+template <int K, int N = 1>
+RsDecLauncher pick_rs_dec_n(int n) {
+    if constexpr (N > 3) {
+        return nullptr;
+    } else {
+        if (n == N) return &launch_rs_decode<K, N>;
+        return pick_rs_dec_n<K, N + 1>(n);
+    }
+}
+
+template <int K = 2>
+RsDecLauncher rs_dec_launcher(int k, int n) {
+    if constexpr (K > 6) {
+        return nullptr;
+    } else {
+        if (k == K) return pick_rs_dec_n<K>(n);
+        return rs_dec_launcher<K + 1>(k, n);
+    }
+}
+
+struct ChunkArgs {
+    PagedGeom g;
+    ChunkGeom cg;
+    Ptrs<kChunkMaxK> d;
+    Ptrs<2 + kChunkMaxM> par;
+    bool have_data;
+    int k, p, m;
+};
+
+static int check_chunk(const kvec_paged_kv* kv, const kvec_chunk_stripe* st, ChunkArgs* a,
+                       const char* fn) {
+    int rc = make_geom(kv, &a->g, fn);
+    if (rc) return rc;
+    if (!st) return set_error(KVEC_EINVAL, "%s: null stripe", fn);
+    const int k = st->k, p = st->p, m = st->m;
+    if (!is_prime(p) || p < 3) return set_error(KVEC_EINVAL, "%s: p=%d is not an odd prime", fn, p);
+    if (p > kRdpMaxP) return set_error(KVEC_EUNSUPPORTED, "%s: p=%d > %d", fn, p, kRdpMaxP);
+    if (k < 1 || k > p - 1 || k > kChunkMaxK)
+        return set_error(KVEC_EINVAL, "%s: k=%d not in [1, p-1]", fn, k);
+    if (m < 0 || m > kChunkMaxM) return set_error(KVEC_EINVAL, "%s: m=%d not in [0, %d]", fn, m, kChunkMaxM);
+    const uint64_t R = uint64_t(st->row_bytes), W = uint64_t(st->width), off = uint64_t(st->col_off);
+    if (st->row_bytes <= 0 || st->width <= 0 || st->col_off < 0 || R % 16 || off % 16)
+        return set_error(KVEC_EINVAL, "%s: row_bytes/col_off must be multiples of 16, width > 0", fn);
+    if (W % a->g.rec)
+        return set_error(KVEC_EINVAL, "%s: width=%llu must be a multiple of the record size %u", fn,
+                         (unsigned long long)W, a->g.rec);
+    if (off + W > R) return set_error(KVEC_EINVAL, "%s: col_off + width > row_bytes", fn);
+    if (!fits_buffer(uint64_t(p - 1) * R))
+        return set_error(KVEC_EUNSUPPORTED, "%s: (p-1)*row_bytes must be < 4 GiB", fn);
+    const uint64_t cells = uint64_t(k) * uint64_t(p - 1);
+    if (cells * W < a->g.recs_total * a->g.rec)
+        return set_error(KVEC_EINVAL, "%s: k*(p-1)*width=%llu < chunk stream bytes %llu", fn,
+                         (unsigned long long)(cells * W),
+                         (unsigned long long)(a->g.recs_total * a->g.rec));
+    if (cells * (W / a->g.rec) >= (uint64_t(1) << 32))
+        return set_error(KVEC_EUNSUPPORTED, "%s: chunk too large for 32-bit record indices", fn);
+    if (!st->P || !st->Q || !aligned16(st->P) || !aligned16(st->Q))
+        return set_error(KVEC_EINVAL, "%s: P/Q null or not 16-byte aligned", fn);
+    a->par = Ptrs<2 + kChunkMaxM>{};
+    a->par.p[0] = (uint8_t*)st->P;
+    a->par.p[1] = (uint8_t*)st->Q;
+    if (m > 0 && !st->rs) return set_error(KVEC_EINVAL, "%s: null RS parity array", fn);
+    for (int i = 0; i < m; ++i) {
+        if (!st->rs[i] || !aligned16(st->rs[i]))
+            return set_error(KVEC_EINVAL, "%s: rs[%d] null or not 16-byte aligned", fn, i);
+        a->par.p[2 + i] = (uint8_t*)st->rs[i];
+    }
+    a->d = Ptrs<kChunkMaxK>{};
+    a->have_data = st->data != nullptr;
+    if (a->have_data)
+        for (int j = 0; j < k; ++j) {
+            if (!st->data[j] || !aligned16(st->data[j]))
+                return set_error(KVEC_EINVAL, "%s: data[%d] null or not 16-byte aligned", fn, j);
+            a->d.p[j] = (uint8_t*)st->data[j];
+        }
+    a->cg.R = R;
+    a->cg.col_off = uint32_t(off);
+    a->cg.recs_per_cell = uint32_t(W / a->g.rec);
+    a->cg.nvec = uint32_t(W / 16);
+    a->k = k;
+    a->p = p;
+    a->m = m;
+    return KVEC_OK;
+}
+
+static int run_encode(const ChunkArgs& a, uint32_t wmask, hipStream_t st, const char* fn) {
+    EncLauncher L = encode_launcher(a.p, a.k, a.m);
+    if (!L) return set_error(KVEC_EUNSUPPORTED, "%s: p=%d k=%d m=%d not built", fn, a.p, a.k, a.m);
+    uint8_t C[kRs8MaxM * kRs8MaxK];
+    cauchy(a.k, a.m, C);
+    uint32_t tab[kChunkMaxK * kChunkMaxM][6];
+    for (int i = 0; i < a.k * a.m; ++i) perm_tables(C[i], tab[i]);
+    L(dim3(blocks_for(a.cg.nvec, kCBS)), st, a.g, a.cg, a.d, a.par, tab, wmask);
+    return check_launch(fn);
+}
+
+}  // namespace kvec
+
+using namespace kvec;
+
+extern "C" int64_t kvec_chunk_width(int64_t chunk_stream_bytes, int k, int p, int64_t record_bytes) {
+    if (chunk_stream_bytes < 0 || k < 1 || p < 3 || record_bytes < 16 || record_bytes % 16) return -1;
+    const int64_t cells = int64_t(k) * (p - 1);
+    const int64_t per = (chunk_stream_bytes + cells - 1) / cells;
+    return (per + record_bytes - 1) / record_bytes * record_bytes;
+}
+
+extern "C" int kvec_chunk_encode_paged(const kvec_paged_kv* kv, const kvec_chunk_stripe* st,
+                                       void* stream) {
+    ChunkArgs a;
+    int rc = check_chunk(kv, st, &a, "kvec_chunk_encode_paged");
+    if (rc) return rc;
+    uint32_t wmask = kWP | kWQ | (a.have_data ? kWData : 0u);
+    for (int i = 0; i < a.m; ++i) wmask |= 1u << (kWRs + i);
+    return run_encode(a, wmask, as_stream(stream), "kvec_chunk_encode_paged");
+}
+
+extern "C" int kvec_chunk_decode_paged(const kvec_paged_kv* kv, void* pool,
+                                       const kvec_chunk_stripe* st, const int32_t* erased,
+                                       int n_erased, void* stream) {
+    static const char* fn = "kvec_chunk_decode_paged";
+    ChunkArgs a;
+    int rc = check_chunk(kv, st, &a, fn);
+    if (rc) return rc;
+    if (!pool || pool != kv->pool) return set_error(KVEC_EINVAL, "%s: pool must be kv->pool", fn);
+    if (n_erased < 0 || (n_erased > 0 && !erased)) return set_error(KVEC_EINVAL, "%s: bad erasure list", fn);
+    const int k = a.k, m = a.m, rows = a.p - 1, nsh = k + 2 + m;
+    bool er[kChunkMaxK + 2 + kChunkMaxM] = {};
+    for (int i = 0; i < n_erased; ++i) {
+        if (erased[i] < 0 || erased[i] >= nsh)
+            return set_error(KVEC_EINVAL, "%s: erased index %d not in [0, %d)", fn, erased[i], nsh);
+        er[erased[i]] = true;
+    }
+    int nd = 0, nrs = 0;
+    for (int s = 0; s < k; ++s) nd += er[s];
+    for (int i = 0; i < m; ++i) nrs += er[k + 2 + i];
+    const bool eP = er[k], eQ = er[k + 1];
+    hipStream_t hs = as_stream(stream);
+    const dim3 grid(blocks_for(a.cg.nvec, kCBS));
+    uint32_t reenc = (eP ? kWP : 0u) | (eQ ? kWQ : 0u);
+    if (nd > 0 && nd <= m - nrs) {
+        // RS: data shards and RS parity, data first (index order k..k+m-1 for parity)
+        bool er_rs[kChunkMaxK + kChunkMaxM] = {};
+        for (int s = 0; s < k; ++s) er_rs[s] = er[s];
+        for (int i = 0; i < m; ++i) er_rs[k + i] = er[k + 2 + i];
+        int surv[kRs8MaxK], outs[kRs8MaxM], no = 0;
+        uint8_t M[kRs8MaxM * kRs8MaxK];
+        if (!rs8_decode_rows(k, m, er_rs, surv, outs, &no, M))
+            return set_error(KVEC_EDECODE, "%s: RS survivor block singular", fn);
+        RsDecodeIo io{};
+        for (int q = 0; q < k; ++q) {
+            io.src_shard[q] = surv[q] < k ? surv[q] : -1;
+            io.in_buf[q] = surv[q] < k ? nullptr : a.par.p[2 + (surv[q] - k)];
+        }
+        for (int o = 0; o < no; ++o) {
+            const int s = outs[o];
+            io.dst_shard[o] = s < k ? s : -1;
+            io.out_buf[o] = s < k ? (a.have_data ? a.d.p[s] : nullptr) : a.par.p[2 + (s - k)];
+        }
+        uint32_t tab[kChunkMaxK * kChunkMaxM][6];
+        for (int i = 0; i < no * k; ++i) perm_tables(M[i], tab[i]);
+        RsDecLauncher L = rs_dec_launcher(k, no);
+        if (!L) return set_error(KVEC_EUNSUPPORTED, "%s: k=%d with %d outputs not built", fn, k, no);
+        L(grid, hs, a.g, a.cg, rows, io, tab);
+        rc = check_launch(fn);
+        if (rc) return rc;
+    } else if (nd > 0 && nd + int(eP) + int(eQ) <= 2) {
+        // RDP: the data and P/Q erasures of the pattern, then RS parity re-encoded
+        int e[2] = {-1, -1}, ne = 0;
+        for (int s = 0; s < k + 2; ++s)
+            if (er[s]) e[ne++] = s;
+        RdpPlan plan = make_rdp_plan(a.p, k, e[0], e[1]);
+        if (!plan.ok) return set_error(KVEC_EDECODE, "%s: RDP pattern (%d, %d) not decodable", fn, e[0], e[1]);
+        Ptrs<kChunkMaxK> dd = a.have_data ? a.d : Ptrs<kChunkMaxK>{};
+        hipLaunchKernelGGL(chunk_rdp_decode_kernel, grid, dim3(kCBS), 0, hs, a.g, a.cg, k, rows, dd,
+                           a.par.p[0], a.par.p[1], plan);
+        rc = check_launch(fn);
+        if (rc) return rc;
+        reenc = 0;
+        for (int i = 0; i < m; ++i)
+            if (er[k + 2 + i]) reenc |= 1u << (kWRs + i);
+    } else if (nd > 0) {
+        return set_error(KVEC_EDECODE, "%s: %d data erasures with %d of %d RS parities lost and P/Q "
+                         "lost (%d, %d) cannot be decoded", fn, nd, nrs, m, int(eP), int(eQ));
+    } else {
+        for (int i = 0; i < m; ++i)
+            if (er[k + 2 + i]) reenc |= 1u << (kWRs + i);
+    }
+    if (reenc) return run_encode(a, reenc, hs, fn);
+    return KVEC_OK;
+}

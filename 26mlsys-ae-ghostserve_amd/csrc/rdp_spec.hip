@@ -13,119 +13,9 @@
 // for the built (p, k) configurations, so the kernel is a straight-line XOR
 // network over the surviving cells; other configurations take the same map as
 // a kernel argument.
-#include "kvec_internal.h"
+#include "rdp_plan.h"
 
 namespace kvec {
-
-constexpr int kRdpMaxP = 13;
-constexpr int kRdpMaxRows = kRdpMaxP - 1;
-constexpr int kRdpMaxShards = kRdpMaxP + 1;  // k+2 with k <= p-1
-constexpr int kRdpMaxOut = 2 * kRdpMaxRows;
-constexpr int kRdpNW = (kRdpMaxShards * kRdpMaxRows + 63) / 64;
-
-typedef Ptrs<kRdpMaxShards> RdpPtrs;
-
-// ---------------------------------------------------------------- decode plan
-// Cells are numbered shard * (p-1) + row; shards 0..k-1 are data, k is P and
-// k+1 is Q.  mask[o] lists the surviving cells whose XOR is output cell o.
-struct RdpPlan {
-    int ok;
-    int nout;
-    int out_cell[kRdpMaxOut];
-    uint64_t mask[kRdpMaxOut][kRdpNW];
-    uint64_t need[kRdpNW];
-};
-
-struct RdpEq {
-    uint32_t um;            // unknowns (bit = index into the unknown list)
-    uint64_t km[kRdpNW];    // known cells
-};
-
-constexpr void eq_add(RdpEq& e, int cell, const int* unk_of_cell) {
-    if (unk_of_cell[cell] >= 0)
-        e.um ^= 1u << unk_of_cell[cell];
-    else
-        e.km[cell >> 6] ^= uint64_t(1) << (cell & 63);
-}
-
-// Equations used (the same ones the peeling decoder of the oracle ends up
-// using, so both give the same bytes even for inconsistent input):
-//   rows      when a data or P column is erased,
-//   diagonals when Q is erased or two non-Q columns are erased.
-constexpr RdpPlan make_rdp_plan(int P, int K, int e0, int e1) {
-    RdpPlan pl{};
-    const int rows = P - 1, nsh = K + 2;
-    if (P < 3 || P > kRdpMaxP || K < 1 || K > P - 1) return pl;
-    if (e0 < -1 || e0 >= nsh || e1 < -1 || e1 >= nsh) return pl;
-    bool er[kRdpMaxShards] = {};
-    if (e0 >= 0) er[e0] = true;
-    if (e1 >= 0) er[e1] = true;
-    int unk_of_cell[kRdpMaxShards * kRdpMaxRows] = {};
-    for (int c = 0; c < nsh * rows; ++c) unk_of_cell[c] = -1;
-    int nu = 0;
-    for (int s = 0; s < nsh; ++s)
-        if (er[s])
-            for (int r = 0; r < rows; ++r) {
-                pl.out_cell[nu] = s * rows + r;
-                unk_of_cell[s * rows + r] = nu++;
-            }
-    pl.nout = nu;
-    if (nu == 0) {
-        pl.ok = 1;
-        return pl;
-    }
-    const bool q_er = er[K + 1];
-    const int n_other = (er[K + 1] ? nu / rows - 1 : nu / rows);
-    RdpEq eq[kRdpMaxOut] = {};
-    int ne = 0;
-    if (n_other >= 1)
-        for (int r = 0; r < rows; ++r) {
-            RdpEq e{};
-            for (int j = 0; j < K; ++j) eq_add(e, j * rows + r, unk_of_cell);
-            eq_add(e, K * rows + r, unk_of_cell);
-            eq[ne++] = e;
-        }
-    if (q_er || n_other == 2)
-        for (int d = 0; d < rows; ++d) {
-            RdpEq e{};
-            for (int j = 0; j < K; ++j) {
-                const int r = ((d - j) % P + P) % P;
-                if (r < rows) eq_add(e, j * rows + r, unk_of_cell);
-            }
-            const int rp = (d + 1) % P;  // P cell (rp, column p-1) lies on diagonal d
-            if (rp < rows) eq_add(e, K * rows + rp, unk_of_cell);
-            eq_add(e, (K + 1) * rows + d, unk_of_cell);
-            eq[ne++] = e;
-        }
-    if (ne != nu) return pl;
-    // Gauss-Jordan over GF(2) on the unknown part.
-    for (int i = 0; i < nu; ++i) {
-        int piv = -1;
-        for (int e = i; e < ne; ++e)
-            if ((eq[e].um >> i) & 1u) {
-                piv = e;
-                break;
-            }
-        if (piv < 0) return pl;
-        if (piv != i) {
-            RdpEq t = eq[i];
-            eq[i] = eq[piv];
-            eq[piv] = t;
-        }
-        for (int e = 0; e < ne; ++e)
-            if (e != i && ((eq[e].um >> i) & 1u)) {
-                eq[e].um ^= eq[i].um;
-                for (int w = 0; w < kRdpNW; ++w) eq[e].km[w] ^= eq[i].km[w];
-            }
-    }
-    for (int o = 0; o < nu; ++o)
-        for (int w = 0; w < kRdpNW; ++w) {
-            pl.mask[o][w] = eq[o].km[w];
-            pl.need[w] |= eq[o].km[w];
-        }
-    pl.ok = 1;
-    return pl;
-}
 
 // ---------------------------------------------------------------- encode
 // A block of kBS threads covers kBS*V consecutive 16-byte lane offsets of

@@ -115,6 +115,52 @@ int kvec_kv_scatter(const kvec_paged_kv* kv, void* pool, const void* in, void* s
 int kvec_rdp_encode_paged(const kvec_paged_kv* kv, void* const* data, int k, void* P, void* Q,
                           int p, int64_t row_bytes, void* stream);
 
+/* ================= chunked coding of a paged pool (spec family) ================= */
+/* No reference function: the reference codes each prefill step's KV after an
+ * fp16 conversion (bench_ghostserve_rdp.py:334-392); this codes the cache bytes
+ * themselves (any dtype, e.g. fp8 e4m3), chunk by chunk, with textbook RDP(p)
+ * and RS(k, m) over GF(2^8)/0x11D (Cauchy) sharing the same k data shards.
+ *
+ * A whole-sequence stripe set is k data shards (optional: NULL data means the
+ * pool is the only copy of the data), P, Q and m RS parity shards, each
+ * (p-1)*row_bytes bytes: p-1 row planes of row_bytes.  Chunk c's stream (the
+ * kvec_paged_kv chunk) is cut into k*(p-1) cells of `width` bytes; cell (shard
+ * j, row r) = stream bytes [(j*(p-1) + r)*width, +width), zero padded, placed at
+ * columns [col_off, col_off + width) of row plane r of shard j.  Every code is
+ * column-wise, so encoding chunk c writes only its own columns, reads no parity,
+ * and the per-chunk encodes together equal the encode of the whole stripe set.
+ * Built: p in {3, 5, 7}, 2 <= k <= p-1, 0 <= m <= 3 (decode: k <= 6). */
+typedef struct kvec_chunk_stripe {
+    void* const* data;  /* host array of k device pointers, or NULL */
+    int k;
+    void* P;            /* RDP row parity */
+    void* Q;            /* RDP diagonal parity (diagonals 0..p-2) */
+    int p;
+    void* const* rs;    /* host array of m device pointers (RS parity 0..m-1) */
+    int m;
+    int64_t row_bytes;  /* R, multiple of 16; (p-1)*R < 4 GiB */
+    int64_t col_off;    /* this chunk's first column, multiple of 16 */
+    int64_t width;      /* this chunk's columns, a multiple of 2*token_bytes */
+} kvec_chunk_stripe;
+
+/* Smallest cell width (multiple of record_bytes) whose k*(p-1) cells hold
+ * chunk_stream_bytes bytes.  Host-only arithmetic; -1 on bad arguments. */
+int64_t kvec_chunk_width(int64_t chunk_stream_bytes, int k, int p, int64_t record_bytes);
+/* One pass over the chunk's pool pages: data shards (if given), P, Q and the
+ * RS parity at the chunk's columns. */
+int kvec_chunk_encode_paged(const kvec_paged_kv* kv, const kvec_chunk_stripe* stripe,
+                            void* stream);
+/* Rebuild the chunk's columns of the erased shards.  erased: host int32 array of
+ * shard indices, data 0..k-1, P = k, Q = k+1, RS parity i = k+2+i.  Lost data
+ * cells are written into the pool pages (pool == kv->pool; surviving data is
+ * read from the pool) and into the data shards when given; lost parity shards
+ * are recomputed.  RS decodes when the data erasures do not exceed the
+ * surviving RS parities, else RDP when data + P/Q erasures are at most two;
+ * anything else is KVEC_EDECODE.  Page-table entries of one chunk must be
+ * distinct (a shared page would be read and rewritten by two cells). */
+int kvec_chunk_decode_paged(const kvec_paged_kv* kv, void* pool, const kvec_chunk_stripe* stripe,
+                            const int32_t* erased, int n_erased, void* stream);
+
 /* ============ gs family: XOR (benchmark/xor/kernel.cu, main.py) =========== */
 /* Byte shards, packed: shards = [(data_shards + 1), shard_size] bytes. */
 

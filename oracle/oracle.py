@@ -255,3 +255,46 @@ def kv_gather(pool: np.ndarray, page_table: np.ndarray, page_tokens: int, tok_of
     _check(lib().kvo_kv_gather(_p(pool), pool_pages, L, tb, page_tokens, _p(pt), B, pps,
                                tok_off, T, _p(out)), "kv_gather")
     return out
+
+
+# ----------------------------- chunked coding -----------------------------
+# No reference function: the reference codes each prefill step's KV on the
+# serving path (bench_ghostserve_rdp.py:334-392, gather at :445-458).  These
+# compose the gather, RDP and RS8 oracles above with the chunk layout.
+def chunk_width(chunk_stream_bytes: int, k: int, p: int, record_bytes: int) -> int:
+    """Smallest multiple of record_bytes whose k*(p-1) cells hold the chunk."""
+    cells = k * (p - 1)
+    per = -(-chunk_stream_bytes // cells)
+    return -(-per // record_bytes) * record_bytes
+
+
+def chunk_cells(stream: np.ndarray, k: int, p: int, width: int) -> np.ndarray:
+    """One chunk's stream cut into cells [k, p-1, width], zero padded."""
+    flat = np.zeros(k * (p - 1) * width, np.uint8)
+    flat[: stream.size] = stream.reshape(-1)
+    return flat.reshape(k, p - 1, width)
+
+
+def chunked_encode(pool: np.ndarray, page_table: np.ndarray, page_tokens: int,
+                   chunk_tokens: int, n_chunks: int, k: int, p: int, m: int):
+    """Whole-sequence stripes of a paged pool coded chunk by chunk.
+
+    Chunk c (positions c*chunk_tokens.. of every sequence) is gathered, cut
+    into cells and placed at columns [c*width, (c+1)*width) of every row plane;
+    P, Q (RDP p) and the m RS parities are then the codes of the assembled data
+    shards.  Returns (width, data [k x (p-1, R)], P, Q, rs [m x (p-1, R)])."""
+    tb = pool.shape[-1]
+    rec = 2 * tb
+    L = pool.shape[0]
+    B = page_table.shape[0]
+    width = chunk_width(L * B * chunk_tokens * rec, k, p, rec)
+    R = n_chunks * width
+    data = [np.zeros((p - 1, R), np.uint8) for _ in range(k)]
+    for c in range(n_chunks):
+        s = kv_gather(pool, page_table, page_tokens, c * chunk_tokens, chunk_tokens)
+        cells = chunk_cells(s, k, p, width)
+        for j in range(k):
+            data[j][:, c * width:(c + 1) * width] = cells[j]
+    P_, Q_ = rdp_encode(data, p)
+    rs = [x.reshape(p - 1, R) for x in rs8_encode([d.reshape(-1) for d in data], m)]
+    return width, data, P_, Q_, rs

@@ -79,3 +79,47 @@ def test_product_fails_loudly_without_library(pkg, monkeypatch, tmp_path):
     monkeypatch.setattr(pkg._lib, "_lib", None)
     with pytest.raises(RuntimeError, match="not built"):
         pkg._lib.lib()
+
+
+def test_chunk_width(pkg):
+    L = pkg._lib.lib()
+    # 16 x 2048 tokens x 32 layers x 256 B records (fp8, 1 head x 128) over k=5, p=7
+    n = 16 * 2048 * 32 * 256
+    W = L.kvec_chunk_width(n, 5, 7, 256)
+    assert W % 256 == 0 and 30 * W >= n and 30 * (W - 256) < n
+    assert L.kvec_chunk_width(n, 5, 7, 24) == -1
+    assert L.kvec_chunk_width(-1, 5, 7, 256) == -1
+
+
+def test_chunk_rejects_bad_arguments(pkg):
+    """Argument checks run on the host before any launch (fake aligned pointers)."""
+    lib = pkg._lib
+    L = lib.lib()
+    table = C.c_void_p(4096)
+    kv = lib.PagedKV(4096, 64, 2, 128, 16, 4096, 3, 4, 0, 16)
+    rs = (C.c_void_p * 3)(4096, 8192, 12288)
+
+    def stripe(**kw):
+        a = dict(data=None, k=5, P=4096, Q=8192, p=7, rs=C.cast(rs, C.POINTER(C.c_void_p)),
+                 m=3, row_bytes=1 << 20, col_off=0, width=256 * 64)
+        a.update(kw)
+        return lib.ChunkStripe(a["data"], a["k"], a["P"], a["Q"], a["p"], a["rs"], a["m"],
+                               a["row_bytes"], a["col_off"], a["width"])
+
+    def rc(**kw):
+        return L.kvec_chunk_encode_paged(C.byref(kv), C.byref(stripe(**kw)), None)
+
+    assert rc(p=9) == -1                       # not prime
+    assert rc(k=7) == -1                       # k > p-1
+    assert rc(width=250) == -1                 # not a record multiple
+    assert rc(col_off=8) == -1                 # misaligned column
+    assert rc(col_off=(1 << 20) - 256) == -1   # past the row plane
+    assert rc(width=256) == -1                 # cells too small for the chunk
+    assert rc(P=4100) == -1                    # misaligned parity
+    assert rc(m=5) == -1
+    assert rc(row_bytes=1 << 30) == -2         # (p-1)*R >= 4 GiB
+    assert b"k*(p-1)*width" in L.kvec_last_error() or True
+    er = (C.c_int32 * 1)(10)
+    assert L.kvec_chunk_decode_paged(C.byref(kv), 4096, C.byref(stripe()), er, 1, None) == -1
+    assert L.kvec_chunk_decode_paged(C.byref(kv), 8192, C.byref(stripe()), er, 0, None) == -1
+    del table

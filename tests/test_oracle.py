@@ -422,3 +422,42 @@ def test_kv_gather_matches_indexing(ora, tb, page_tokens, tok_off, T):
     for kv in range(2):
         want = tokpool[:, slots.reshape(-1), kv].reshape(L, B, T, tb)
         assert np.array_equal(got[:, :, :, kv], want)
+
+
+# ------------------------------------------------------------------ chunked
+def test_chunk_cells_cut_and_pad(ora):
+    """Cells read in (shard, row) order give back the stream, then zeros."""
+    rng = np.random.default_rng(11)
+    k, p, rec = 5, 7, 32
+    for n in (1, 31, 32 * 30, 32 * 30 + 5, 999):
+        s = rng.integers(0, 256, n, dtype=np.uint8)
+        W = ora.chunk_width(n, k, p, rec)
+        assert W % rec == 0 and k * (p - 1) * W >= n and k * (p - 1) * (W - rec) < n
+        cells = ora.chunk_cells(s, k, p, W)
+        assert cells.shape == (k, p - 1, W)
+        flat = cells.reshape(-1)
+        assert np.array_equal(flat[:n], s) and not flat[n:].any()
+
+
+def test_chunked_encode_is_per_chunk(ora):
+    """Coding chunk c alone gives the columns of chunk c of the whole-sequence
+    code (each column is its own RDP/RS instance), and the data shards hold the
+    gathered chunks side by side."""
+    rng = np.random.default_rng(12)
+    L, B, pps, pt, tb = 2, 3, 4, 16, 32
+    npages = B * pps + 2
+    pool = rng.integers(0, 256, (L, npages, pt, 2, tb), dtype=np.uint8)
+    table = rng.permutation(npages)[: B * pps].astype(np.int32).reshape(B, pps)
+    k, p, m, ct, nc = 5, 7, 3, 16, 4
+    W, data, P, Q, rs = ora.chunked_encode(pool, table, pt, ct, nc, k, p, m)
+    for c in range(nc):
+        cols = slice(c * W, (c + 1) * W)
+        s = ora.kv_gather(pool, table, pt, c * ct, ct)
+        cells = ora.chunk_cells(s, k, p, W)
+        for j in range(k):
+            assert np.array_equal(data[j][:, cols], cells[j])
+        Pc, Qc = ora.rdp_encode([np.ascontiguousarray(cells[j]) for j in range(k)], p)
+        assert np.array_equal(P[:, cols], Pc) and np.array_equal(Q[:, cols], Qc)
+        rc = ora.rs8_encode([np.ascontiguousarray(cells[j]).reshape(-1) for j in range(k)], m)
+        for i in range(m):
+            assert np.array_equal(rs[i][:, cols], rc[i].reshape(p - 1, W))
