@@ -44,22 +44,38 @@ struct Gf8Tab {
     uint32_t t[N][6];
 };
 
+// Copy a coefficient table set from the kernel arguments to LDS.  Read back
+// from LDS, the v_perm tables land in VGPRs at their point of use instead of
+// holding up to 6*k*m SGPRs for the whole kernel (which overflow the SGPR file
+// next to the shard buffer resources and get spilled).
+template <int N>
+__device__ __forceinline__ void stage_tables(uint32_t (*lds)[6], const Gf8Tab<N>& tab) {
+    for (int i = threadIdx.x; i < N * 6; i += blockDim.x) lds[i / 6][i % 6] = tab.t[i / 6][i % 6];
+    __syncthreads();
+}
+
 // Pool cell (shard j, row r) of the thread's column; zero for padding records.
 __device__ __forceinline__ u32x4 load_cell(const PagedGeom& g, const ChunkGeom& cg, int j, int r,
                                            int rows, uint32_t w0, uint32_t inner) {
-    const uint32_t w = uint32_t(j * rows + r) * cg.recs_per_cell + w0;
-    const uint8_t* src = cell_src(g, w, inner);
-    return src ? ld_stream(src, 0) : u32x4{0, 0, 0, 0};
+    return cell_load(g, uint32_t(j * rows + r) * cg.recs_per_cell + w0, inner);
 }
 
 // ------------------------------------------------------------------ encode
+// All k*(p-1) cells of the thread's column are loaded before anything is
+// stored: stores to the shards could alias the pool as far as the compiler
+// knows, so loads issued after a store would wait for it.  Outputs switched off
+// by `wmask` get a buffer resource of size 0, whose stores the hardware drops,
+// so the kernel has no branches after the bounds check.
 template <int P, int K, int M>
-__global__ __launch_bounds__(kCBS) void chunk_encode_kernel(PagedGeom g, ChunkGeom cg,
+__global__ __launch_bounds__(kCBS) __attribute__((amdgpu_waves_per_eu(1, 2))) void chunk_encode_kernel(PagedGeom g, ChunkGeom cg,
                                                             Ptrs<kChunkMaxK> d,
                                                             Ptrs<2 + kChunkMaxM> par,
                                                             Gf8Tab<(K * M > 0 ? K * M : 1)> rs,
                                                             uint32_t wmask) {
     constexpr int ROWS = P - 1;
+    constexpr int NT = K * M > 0 ? K * M : 1;
+    __shared__ uint32_t tab[NT][6];
+    stage_tables<NT>(tab, rs);
     const uint32_t u = blockIdx.x * kCBS + threadIdx.x;
     if (u >= cg.nvec) return;
     const uint32_t o = u << 4;
@@ -67,27 +83,37 @@ __global__ __launch_bounds__(kCBS) void chunk_encode_kernel(PagedGeom g, ChunkGe
     const uint32_t inner = o - w0 * g.rec;
     const uint64_t nb = ROWS * cg.R;
     const uint32_t lane = cg.col_off + o;
+    uint32_t pg[ROWS][K];
+#pragma unroll
+    for (int r = 0; r < ROWS; ++r)
+#pragma unroll
+        for (int j = 0; j < K; ++j) pg[r][j] = cell_page(g, uint32_t(j * ROWS + r) * cg.recs_per_cell + w0);
+    __builtin_amdgcn_sched_barrier(0);
+    u32x4 x[ROWS][K];
+#pragma unroll
+    for (int r = 0; r < ROWS; ++r)
+#pragma unroll
+        for (int j = 0; j < K; ++j)
+            x[r][j] = cell_load_at(g, uint32_t(j * ROWS + r) * cg.recs_per_cell + w0, inner, pg[r][j]);
+    __builtin_amdgcn_sched_barrier(0);
+    const uint64_t nd = (wmask & kWData) ? nb : 0;
     u32x4 q[ROWS];
 #pragma unroll
     for (int r = 0; r < ROWS; ++r) q[r] = u32x4{0, 0, 0, 0};
+    const ShardView<true> sp(par.p[0], (wmask & kWP) ? nb : 0);
 #pragma unroll
     for (int r = 0; r < ROWS; ++r) {
-        u32x4 x[K];
 #pragma unroll
-        for (int j = 0; j < K; ++j) x[j] = load_cell(g, cg, j, r, ROWS, w0, inner);
-        if (wmask & kWData) {
+        for (int j = 0; j < K; ++j) ShardView<true>(d.p[j], nd).store(r * cg.R, lane, x[r][j]);
+        u32x4 pr = x[r][0];
 #pragma unroll
-            for (int j = 0; j < K; ++j) ShardView<true>(d.p[j], nb).store(r * cg.R, lane, x[j]);
-        }
-        u32x4 pr = x[0];
-#pragma unroll
-        for (int j = 1; j < K; ++j) pr ^= x[j];
-        if (wmask & kWP) ShardView<true>(par.p[0], nb).store(r * cg.R, lane, pr);
+        for (int j = 1; j < K; ++j) pr ^= x[r][j];
+        sp.store(r * cg.R, lane, pr);
         // cell (r, j) lies on diagonal (r + j) % p; the P cell of row r on r - 1
 #pragma unroll
         for (int j = 0; j < K; ++j) {
             const int dg = (r + j) % P;
-            if (dg != P - 1) q[dg] ^= x[j];
+            if (dg != P - 1) q[dg] ^= x[r][j];
         }
         if (r >= 1) q[r - 1] ^= pr;
         if constexpr (M > 0) {
@@ -96,13 +122,13 @@ __global__ __launch_bounds__(kCBS) void chunk_encode_kernel(PagedGeom g, ChunkGe
             for (int i = 0; i < M; ++i) acc[i] = u32x4{0, 0, 0, 0};
 #pragma unroll
             for (int j = 0; j < K; ++j) {
-                const uint32_t w4[4] = {x[j].x, x[j].y, x[j].z, x[j].w};
+                const uint32_t w4[4] = {x[r][j].x, x[r][j].y, x[r][j].z, x[r][j].w};
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
                     const Gf8Fields f = gf8_fields(w4[e]);
 #pragma unroll
                     for (int i = 0; i < M; ++i) {
-                        const uint32_t pm = gf8_mul4(f, rs.t[i * K + j]);
+                        const uint32_t pm = gf8_mul4(f, tab[i * K + j]);
                         if (e == 0) acc[i].x ^= pm;
                         else if (e == 1) acc[i].y ^= pm;
                         else if (e == 2) acc[i].z ^= pm;
@@ -112,15 +138,13 @@ __global__ __launch_bounds__(kCBS) void chunk_encode_kernel(PagedGeom g, ChunkGe
             }
 #pragma unroll
             for (int i = 0; i < M; ++i)
-                if (wmask & (1u << (kWRs + i)))
-                    ShardView<true>(par.p[2 + i], nb).store(r * cg.R, lane, acc[i]);
+                ShardView<true>(par.p[2 + i], (wmask & (1u << (kWRs + i))) ? nb : 0)
+                    .store(r * cg.R, lane, acc[i]);
         }
     }
-    if (wmask & kWQ) {
-        const ShardView<true> sq(par.p[1], nb);
+    const ShardView<true> sq(par.p[1], (wmask & kWQ) ? nb : 0);
 #pragma unroll
-        for (int r = 0; r < ROWS; ++r) sq.store(r * cg.R, lane, q[r]);
-    }
+    for (int r = 0; r < ROWS; ++r) sq.store(r * cg.R, lane, q[r]);
 }
 
 // ------------------------------------------------------------------ RS decode
@@ -138,6 +162,8 @@ struct RsDecodeIo {
 template <int K, int NOUT>
 __global__ __launch_bounds__(kCBS) void chunk_rs_decode_kernel(PagedGeom g, ChunkGeom cg, int rows,
                                                                RsDecodeIo io, Gf8Tab<K * NOUT> mix) {
+    __shared__ uint32_t tab[K * NOUT][6];
+    stage_tables<K * NOUT>(tab, mix);
     const uint32_t u = blockIdx.x * kCBS + threadIdx.x;
     if (u >= cg.nvec) return;
     const uint32_t o = u << 4;
@@ -160,7 +186,7 @@ __global__ __launch_bounds__(kCBS) void chunk_rs_decode_kernel(PagedGeom g, Chun
                 const Gf8Fields f = gf8_fields(w4[e]);
 #pragma unroll
                 for (int i = 0; i < NOUT; ++i) {
-                    const uint32_t pm = gf8_mul4(f, mix.t[i * K + q]);
+                    const uint32_t pm = gf8_mul4(f, tab[i * K + q]);
                     if (e == 0) acc[i].x ^= pm;
                     else if (e == 1) acc[i].y ^= pm;
                     else if (e == 2) acc[i].z ^= pm;
@@ -170,10 +196,9 @@ __global__ __launch_bounds__(kCBS) void chunk_rs_decode_kernel(PagedGeom g, Chun
         }
 #pragma unroll
         for (int i = 0; i < NOUT; ++i) {
-            if (io.dst_shard[i] >= 0) {
-                const uint32_t w = uint32_t(io.dst_shard[i] * rows + r) * cg.recs_per_cell + w0;
-                if (cell_src(g, w, inner)) st_stream(cell_dst(g, w, inner), 0, acc[i]);
-            }
+            if (io.dst_shard[i] >= 0)
+                cell_store(g, uint32_t(io.dst_shard[i] * rows + r) * cg.recs_per_cell + w0, inner,
+                           acc[i]);
             if (io.out_buf[i]) ShardView<true>(io.out_buf[i], nb).store(r * cg.R, lane, acc[i]);
         }
     }
@@ -213,8 +238,7 @@ __global__ __launch_bounds__(kCBS) void chunk_rdp_decode_kernel(PagedGeom g, Chu
         const int c = plan.out_cell[oc];
         const int s = c / rows, r = c - s * rows;
         if (s < k) {
-            const uint32_t w = uint32_t(s * rows + r) * cg.recs_per_cell + w0;
-            if (cell_src(g, w, inner)) st_stream(cell_dst(g, w, inner), 0, acc);
+            cell_store(g, uint32_t(s * rows + r) * cg.recs_per_cell + w0, inner, acc);
             if (d.p[s]) st_stream(d.p[s] + uint64_t(r) * cg.R, lane, acc);
         } else {
             st_stream((s == k ? P : Q) + uint64_t(r) * cg.R, lane, acc);

@@ -22,9 +22,7 @@ __global__ __launch_bounds__(kGBS) void kv_gather_kernel(PagedGeom g, uint8_t* _
     if (c >= ncells) return;
     const uint32_t w = fdiv(c, g.div_cells);
     const uint32_t inner = (c - w * g.div_cells.d) * 16;
-    const uint8_t* src = cell_src(g, w, inner);
-    const u32x4 v = src ? ld_stream(src, 0) : u32x4{0, 0, 0, 0};
-    st_stream(out, uint64_t(c) * 16, v);
+    st_stream(out, uint64_t(c) * 16, cell_load(g, w, inner));
 }
 
 // pool cell = stream[s] (inverse; padding slots and invalid pages are skipped)
@@ -34,8 +32,7 @@ __global__ __launch_bounds__(kGBS) void kv_scatter_kernel(PagedGeom g, const uin
     if (c >= ncells) return;
     const uint32_t w = fdiv(c, g.div_cells);
     const uint32_t inner = (c - w * g.div_cells.d) * 16;
-    if (!cell_src(g, w, inner)) return;
-    st_stream(cell_dst(g, w, inner), 0, ld_stream(in, uint64_t(c) * 16));
+    cell_store(g, w, inner, ld_stream(in, uint64_t(c) * 16));
 }
 
 // ------------------------------------------------- fused gather + RDP encode
@@ -46,7 +43,7 @@ __global__ __launch_bounds__(kGBS) void kv_scatter_kernel(PagedGeom g, const uin
 constexpr int kFBS = 128;
 
 template <int P, int K>
-__global__ __launch_bounds__(kFBS) void rdp_encode_paged_kernel(PagedGeom g, Ptrs<16> d,
+__global__ __launch_bounds__(kFBS) __attribute__((amdgpu_waves_per_eu(1, 2))) void rdp_encode_paged_kernel(PagedGeom g, Ptrs<16> d,
                                                                 uint8_t* __restrict__ Pp,
                                                                 uint8_t* __restrict__ Qp, uint64_t R,
                                                                 uint32_t recs_per_row, uint32_t nvec) {
@@ -57,6 +54,21 @@ __global__ __launch_bounds__(kFBS) void rdp_encode_paged_kernel(PagedGeom g, Ptr
     const uint32_t w0 = fdiv(off, g.div_rec);
     const uint32_t inner = off - w0 * g.rec;
     const uint64_t nb = ROWS * R;
+    // every cell is loaded before anything is stored (the shard stores could
+    // alias the pool as far as the compiler knows)
+    uint32_t pg[K][ROWS];
+#pragma unroll
+    for (int j = 0; j < K; ++j)
+#pragma unroll
+        for (int r = 0; r < ROWS; ++r) pg[j][r] = cell_page(g, (j * ROWS + r) * recs_per_row + w0);
+    __builtin_amdgcn_sched_barrier(0);
+    u32x4 x[K][ROWS];
+#pragma unroll
+    for (int j = 0; j < K; ++j)
+#pragma unroll
+        for (int r = 0; r < ROWS; ++r)
+            x[j][r] = cell_load_at(g, (j * ROWS + r) * recs_per_row + w0, inner, pg[j][r]);
+    __builtin_amdgcn_sched_barrier(0);
     u32x4 pr[ROWS], q[ROWS];
 #pragma unroll
     for (int r = 0; r < ROWS; ++r) {
@@ -68,13 +80,10 @@ __global__ __launch_bounds__(kFBS) void rdp_encode_paged_kernel(PagedGeom g, Ptr
         const ShardView<true> sv(d.p[j], nb);
 #pragma unroll
         for (int r = 0; r < ROWS; ++r) {
-            const uint32_t w = (j * ROWS + r) * recs_per_row + w0;
-            const uint8_t* src = cell_src(g, w, inner);
-            const u32x4 x = src ? ld_stream(src, 0) : u32x4{0, 0, 0, 0};
-            sv.store(r * R, off, x);
-            pr[r] ^= x;
+            sv.store(r * R, off, x[j][r]);
+            pr[r] ^= x[j][r];
             const int dg = (r + j) % P;
-            if (dg != P - 1) q[dg] ^= x;
+            if (dg != P - 1) q[dg] ^= x[j][r];
         }
     }
 #pragma unroll

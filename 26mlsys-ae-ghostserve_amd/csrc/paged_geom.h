@@ -25,22 +25,69 @@ struct PagedGeom {
     FastDiv div_rec, div_t, div_b, div_cells;  // div_cells: record_bytes / 16
 };
 
-// Source address of the 16-byte stream cell in record w at byte `inner`;
-// nullptr for padding records and invalid page-table entries.
-__device__ __forceinline__ const uint8_t* cell_src(const PagedGeom& g, uint32_t w, uint32_t inner) {
-    if (w >= g.recs_total) return nullptr;
-    const uint32_t lb = fdiv(w, g.div_t);
-    const uint32_t t = w - lb * g.div_t.d + g.tok_off;
+// Byte offset in the pool of the 16-byte stream cell in record w at byte
+// `inner`.  Branch-free, so that a thread's many cell loads can all be in
+// flight at once: a padding record (w >= recs_total) or an invalid page-table
+// entry yields the offset of a cell of pool page 0 and valid = false.
+__device__ __forceinline__ uint64_t cell_offset(const PagedGeom& g, uint32_t w, uint32_t inner,
+                                                bool& valid) {
+    valid = w < g.recs_total;
+    const uint32_t ww = valid ? w : 0u;
+    const uint32_t lb = fdiv(ww, g.div_t);
+    const uint32_t t = ww - lb * g.div_t.d + g.tok_off;
     const uint32_t layer = fdiv(lb, g.div_b);
     const uint32_t b = lb - layer * g.div_b.d;
-    const int32_t page = g.table[uint64_t(b) * g.pps + (t >> g.page_shift)];
-    if (page < 0 || uint32_t(page) >= g.pool_pages) return nullptr;
-    const uint64_t slot = (uint64_t(uint32_t(page)) << g.page_shift) | (t & ((1u << g.page_shift) - 1));
-    return g.pool + uint64_t(layer) * g.layer_stride + slot * g.rec + inner;
+    const uint32_t page = uint32_t(g.table[b * g.pps + (t >> g.page_shift)]);
+    valid = valid && page < g.pool_pages;
+    const uint32_t pg = valid ? page : 0u;
+    const uint64_t slot = (uint64_t(pg) << g.page_shift) | (t & ((1u << g.page_shift) - 1));
+    return uint64_t(layer) * g.layer_stride + slot * g.rec + inner;
 }
 
-__device__ __forceinline__ uint8_t* cell_dst(const PagedGeom& g, uint32_t w, uint32_t inner) {
-    return const_cast<uint8_t*>(cell_src(g, w, inner)) - g.pool + g.pool_w;
+// 16 zero bytes that invalid cells are read from: choosing the address before
+// the load (instead of zeroing the loaded value after it) keeps the validity
+// test off the load's critical path, so a thread's cell loads issue back to back.
+__device__ __attribute__((aligned(16))) uint32_t kZeroCell[4] = {0, 0, 0, 0};  // never written
+
+// The cell's 16 bytes (zero for padding records and invalid pages).
+__device__ __forceinline__ u32x4 cell_load(const PagedGeom& g, uint32_t w, uint32_t inner) {
+    bool valid;
+    const uint64_t off = cell_offset(g, w, inner, valid);
+    const uint8_t* a = valid ? g.pool + off : reinterpret_cast<const uint8_t*>(kZeroCell);
+    return ld_stream(a, 0);
+}
+
+// Two-phase access for kernels that load many cells per thread: first every
+// cell's page-table entry (cell_page), then every cell (cell_load_at), with a
+// scheduling barrier between the phases and before the arithmetic, so that
+// all table loads, and then all pool loads, are in flight together.
+__device__ __forceinline__ uint32_t cell_page(const PagedGeom& g, uint32_t w) {
+    const uint32_t ww = w < g.recs_total ? w : 0u;
+    const uint32_t lb = fdiv(ww, g.div_t);
+    const uint32_t t = ww - lb * g.div_t.d + g.tok_off;
+    const uint32_t b = lb - fdiv(lb, g.div_b) * g.div_b.d;
+    return uint32_t(g.table[b * g.pps + (t >> g.page_shift)]);
+}
+
+__device__ __forceinline__ u32x4 cell_load_at(const PagedGeom& g, uint32_t w, uint32_t inner,
+                                              uint32_t page) {
+    const bool valid = w < g.recs_total && page < g.pool_pages;
+    const uint32_t ww = valid ? w : 0u;
+    const uint32_t lb = fdiv(ww, g.div_t);
+    const uint32_t t = ww - lb * g.div_t.d + g.tok_off;
+    const uint32_t layer = fdiv(lb, g.div_b);
+    const uint64_t slot = (uint64_t(valid ? page : 0u) << g.page_shift) |
+                          (t & ((1u << g.page_shift) - 1));
+    const uint8_t* a = valid ? g.pool + (uint64_t(layer) * g.layer_stride + slot * g.rec + inner)
+                             : reinterpret_cast<const uint8_t*>(kZeroCell);
+    return ld_stream(a, 0);
+}
+
+// Write the cell (padding records and invalid pages are skipped).
+__device__ __forceinline__ void cell_store(const PagedGeom& g, uint32_t w, uint32_t inner, u32x4 v) {
+    bool valid;
+    const uint64_t off = cell_offset(g, w, inner, valid);
+    if (valid) st_stream(g.pool_w, off, v);
 }
 
 inline int make_geom(const kvec_paged_kv* kv, PagedGeom* g, const char* fn) {
@@ -60,7 +107,8 @@ inline int make_geom(const kvec_paged_kv* kv, PagedGeom* g, const char* fn) {
     const uint64_t rec = 2 * uint64_t(kv->token_bytes);
     const uint64_t recs = uint64_t(kv->layers) * kv->batch * uint64_t(kv->tokens);
     if (recs >= (uint64_t(1) << 32) || uint64_t(kv->layers) * kv->batch >= (uint64_t(1) << 32) ||
-        kv->pool_pages >= (int64_t(1) << 31) || recs * rec / 16 >= (uint64_t(1) << 32))
+        kv->pool_pages >= (int64_t(1) << 31) || recs * rec / 16 >= (uint64_t(1) << 32) ||
+        int64_t(kv->batch) * kv->pages_per_seq >= (int64_t(1) << 31))
         return set_error(KVEC_EUNSUPPORTED, "%s: chunk too large for 32-bit cell indices", fn);
     g->pool = (const uint8_t*)kv->pool;
     g->pool_w = (uint8_t*)kv->pool;

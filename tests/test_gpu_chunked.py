@@ -162,3 +162,31 @@ def test_chunked_decode_other_shapes(pkg, gpu, cfg):
         assert torch.equal(pool_d.view(torch.uint8), ref_pool.view(torch.uint8)), (cfg, er)
         for j, (t, r) in enumerate(zip(st.shards(), ref_sh)):
             assert torch.equal(t, r), (cfg, er, j)
+
+
+def test_chunked_encode_repeatable_at_scale(pkg, ora, gpu):
+    """A 64 MiB fp8 chunk (about 1,100 blocks): encoding it twice gives the same
+    bytes, which match the oracle on sampled stripe columns."""
+    L, B, pps, pt, H, D, k, p, m, ct = 8, 16, 128, 16, 1, 128, 5, 7, 3, 2048
+    pool, table, pool_d, table_d, nc, st = setup(pkg, gpu, L, B, pps, pt, H, D, k, p, m, ct,
+                                                 False, seed=21)
+    kv = pkg.chunked.chunk_kv(pool_d, table_d, 0, ct)
+    st.encode(kv, 0)
+    first = [t.clone() for t in st.shards()]
+    for _ in range(3):
+        st.encode(kv, 0)
+        torch.cuda.synchronize()
+        for i, (a, b) in enumerate(zip(st.shards(), first)):
+            assert torch.equal(a, b), f"shard {i} differs between two encodes"
+    W, R = st.width, st.row_bytes
+    s = kv.gather().cpu().numpy()
+    cells = ora.chunk_cells(s, k, p, W)
+    rng = np.random.default_rng(5)
+    cols = (np.sort(rng.choice(W // 16, 512, replace=False))[:, None] * 16 + np.arange(16)).reshape(-1)
+    sub = [np.ascontiguousarray(cells[j][:, cols]) for j in range(k)]
+    Pw, Qw = ora.rdp_encode(sub, p)
+    rsw = ora.rs8_encode([x.reshape(-1) for x in sub], m)
+    got = [t.view(p - 1, R)[:, torch.from_numpy(cols).to(gpu)].cpu().numpy() for t in st.shards()]
+    assert np.array_equal(got[0], Pw) and np.array_equal(got[1], Qw)
+    for i in range(m):
+        assert np.array_equal(got[2 + i].reshape(-1), rsw[i]), i
