@@ -61,13 +61,18 @@ __device__ __forceinline__ u32x4 load_cell(const PagedGeom& g, const ChunkGeom& 
 }
 
 // ------------------------------------------------------------------ encode
-// All k*(p-1) cells of the thread's column are loaded before anything is
-// stored: stores to the shards could alias the pool as far as the compiler
-// knows, so loads issued after a store would wait for it.  Outputs switched off
-// by `wmask` get a buffer resource of size 0, whose stores the hardware drops,
-// so the kernel has no branches after the bounds check.
+// Every cell's page-table entry is loaded first.  Then rows are double
+// buffered: row r+1's k cells are loaded before row r is coded and stored, so
+// a wave always has a row of loads in flight while it computes, and a thread
+// holds two rows (not all p-1) in registers.  Program order is what keeps the
+// loads early: stores to the shards could alias the pool as far as the
+// compiler knows, and the compiler barrier after each row also keeps the GF
+// tables from being hoisted out of the row loop (they are re-read from LDS per
+// row instead of pinning 6*k*m registers).  Outputs switched off by `wmask` get
+// a buffer resource of size 0, whose stores the hardware drops, so the kernel
+// has no branches after the bounds check.
 template <int P, int K, int M>
-__global__ __launch_bounds__(kCBS) __attribute__((amdgpu_waves_per_eu(1, 2))) void chunk_encode_kernel(PagedGeom g, ChunkGeom cg,
+__global__ __launch_bounds__(kCBS) void chunk_encode_kernel(PagedGeom g, ChunkGeom cg,
                                                             Ptrs<kChunkMaxK> d,
                                                             Ptrs<2 + kChunkMaxM> par,
                                                             Gf8Tab<(K * M > 0 ? K * M : 1)> rs,
@@ -88,14 +93,10 @@ __global__ __launch_bounds__(kCBS) __attribute__((amdgpu_waves_per_eu(1, 2))) vo
     for (int r = 0; r < ROWS; ++r)
 #pragma unroll
         for (int j = 0; j < K; ++j) pg[r][j] = cell_page(g, uint32_t(j * ROWS + r) * cg.recs_per_cell + w0);
-    __builtin_amdgcn_sched_barrier(0);
-    u32x4 x[ROWS][K];
+    u32x4 x[2][K];
 #pragma unroll
-    for (int r = 0; r < ROWS; ++r)
-#pragma unroll
-        for (int j = 0; j < K; ++j)
-            x[r][j] = cell_load_at(g, uint32_t(j * ROWS + r) * cg.recs_per_cell + w0, inner, pg[r][j]);
-    __builtin_amdgcn_sched_barrier(0);
+    for (int j = 0; j < K; ++j)
+        x[0][j] = cell_load_at(g, uint32_t(j * ROWS) * cg.recs_per_cell + w0, inner, pg[0][j]);
     const uint64_t nd = (wmask & kWData) ? nb : 0;
     u32x4 q[ROWS];
 #pragma unroll
@@ -103,17 +104,24 @@ __global__ __launch_bounds__(kCBS) __attribute__((amdgpu_waves_per_eu(1, 2))) vo
     const ShardView<true> sp(par.p[0], (wmask & kWP) ? nb : 0);
 #pragma unroll
     for (int r = 0; r < ROWS; ++r) {
+        const int c = r & 1;
+        if (r + 1 < ROWS) {
 #pragma unroll
-        for (int j = 0; j < K; ++j) ShardView<true>(d.p[j], nd).store(r * cg.R, lane, x[r][j]);
-        u32x4 pr = x[r][0];
+            for (int j = 0; j < K; ++j)
+                x[c ^ 1][j] = cell_load_at(g, uint32_t(j * ROWS + r + 1) * cg.recs_per_cell + w0, inner,
+                                           pg[r + 1][j]);
+        }
 #pragma unroll
-        for (int j = 1; j < K; ++j) pr ^= x[r][j];
+        for (int j = 0; j < K; ++j) ShardView<true>(d.p[j], nd).store(r * cg.R, lane, x[c][j]);
+        u32x4 pr = x[c][0];
+#pragma unroll
+        for (int j = 1; j < K; ++j) pr ^= x[c][j];
         sp.store(r * cg.R, lane, pr);
         // cell (r, j) lies on diagonal (r + j) % p; the P cell of row r on r - 1
 #pragma unroll
         for (int j = 0; j < K; ++j) {
             const int dg = (r + j) % P;
-            if (dg != P - 1) q[dg] ^= x[r][j];
+            if (dg != P - 1) q[dg] ^= x[c][j];
         }
         if (r >= 1) q[r - 1] ^= pr;
         if constexpr (M > 0) {
@@ -122,7 +130,7 @@ __global__ __launch_bounds__(kCBS) __attribute__((amdgpu_waves_per_eu(1, 2))) vo
             for (int i = 0; i < M; ++i) acc[i] = u32x4{0, 0, 0, 0};
 #pragma unroll
             for (int j = 0; j < K; ++j) {
-                const uint32_t w4[4] = {x[r][j].x, x[r][j].y, x[r][j].z, x[r][j].w};
+                const uint32_t w4[4] = {x[c][j].x, x[c][j].y, x[c][j].z, x[c][j].w};
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
                     const Gf8Fields f = gf8_fields(w4[e]);
@@ -141,6 +149,7 @@ __global__ __launch_bounds__(kCBS) __attribute__((amdgpu_waves_per_eu(1, 2))) vo
                 ShardView<true>(par.p[2 + i], (wmask & (1u << (kWRs + i))) ? nb : 0)
                     .store(r * cg.R, lane, acc[i]);
         }
+        asm volatile("" ::: "memory");
     }
     const ShardView<true> sq(par.p[1], (wmask & kWQ) ? nb : 0);
 #pragma unroll
