@@ -11,10 +11,11 @@ signatures:
   spec        textbook RDP over a prime p, RS over GF(2^8) (stripe configs)
   paged       paged KV pool <-> coding stream; fused gather + RDP encode
   chunked     per-prefill-chunk RDP + RS coding of a paged (e.g. fp8) cache
+  offload     parity copies to pinned host memory on a side stream
 
 Import the package with ``importlib.import_module("26mlsys-ae-ghostserve_amd")``
 (the directory name is not a Python identifier).
 """
-from . import _lib, chunked, paged, rdp, rdp_kv_ops, rs, spec, xor  # noqa: F401
+from . import _lib, chunked, offload, paged, rdp, rdp_kv_ops, rs, spec, xor  # noqa: F401
 
-__all__ = ["xor", "rdp", "rs", "rdp_kv_ops", "spec", "paged", "chunked"]
+__all__ = ["xor", "rdp", "rs", "rdp_kv_ops", "spec", "paged", "chunked", "offload"]

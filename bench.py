@@ -14,9 +14,10 @@ byte-compared against the originals at full size) is reported alongside.
 Algorithmic bytes per step = 536,870,912 read + 178,956,971 written
 = 715,827,883 B; `value` is that over the wall time of the timed steps, and
 `roofline.achieved` is that over the average launch duration: one HIP event
-pair on the launch stream around the K back-to-back launches, divided by K.  Before any number is printed, the outputs are checked
-byte-exact against the CPU oracle on a sample of stripe columns (each column
-offset is an independent RDP instance).
+pair on the launch stream around the K back-to-back launches, divided by K.
+Before any number is printed, the outputs are checked byte-exact against the
+CPU oracle on a sample of stripe columns (each column offset is an
+independent RDP instance).
 
     python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-cpu-baseline]
 """
@@ -364,6 +365,37 @@ def bench_chunked(pkg, torch, oracle, dev, seed, warmup):
     wall = time.perf_counter() - t0
     enc_us = e0.elapsed_time(e1) * 1e3 / NCH
 
+    # parity offload to pinned host memory (PCIe), overlapped with the next
+    # chunk's encode: the 16 chunks pipelined (which also touches every host
+    # page once), then one chunk's copies alone
+    par = [st.P, st.Q] + list(st.rs)
+    off = pkg.offload.ParityOffload(par, p - 1, R)
+    torch.cuda.synchronize()
+    tp = time.perf_counter()
+    evs_off = []
+    for c in range(NCH):
+        st.encode(kvs[c], c)
+        evs_off.append(off.to_host(c * W, W))
+    for e in evs_off:
+        e.synchronize()
+    torch.cuda.synchronize()
+    pipe_us = (time.perf_counter() - tp) * 1e6 / NCH
+    t1 = torch.cuda.Event(enable_timing=True)
+    t2 = torch.cuda.Event(enable_timing=True)
+    t1.record(off.stream)
+    off.to_host(W, W)
+    t2.record(off.stream)
+    t2.synchronize()
+    d2h_ms = t1.elapsed_time(t2)
+    offload = {
+        "parity_bytes_per_chunk": parity_w,
+        "d2h_ms_per_chunk": round(d2h_ms, 3),
+        "d2h_gbs": round(parity_w / d2h_ms / 1e6, 2),
+        "pipelined_encode_plus_d2h_us_per_chunk": round(pipe_us, 1),
+        "host_buffers": "pinned",
+    }
+    del off, par
+
     # decode into the pool at full size: RS path (3 data shards) and RDP path
     # (2 data shards with the RS parities lost), byte-compared with the pool
     dec = {}
@@ -406,6 +438,7 @@ def bench_chunked(pkg, torch, oracle, dev, seed, warmup):
         "wall_us_per_chunk": round(wall * 1e6 / NCH, 2),
         "decode_us": dec,
         "decode_byte_exact": True,
+        "parity_offload": offload,
     }
 
 

@@ -1,0 +1,42 @@
+"""Parity offload to pinned host memory on a side stream, ordered after the
+encode, and the restore of lost device parity from the host copy."""
+import numpy as np
+import pytest
+import torch
+
+from test_gpu_chunked import setup
+
+pytestmark = pytest.mark.gpu
+
+
+def test_offload_and_restore(pkg, gpu):
+    L, B, pps, pt, H, D, k, p, m, ct = 2, 3, 8, 16, 1, 128, 5, 7, 3, 32
+    _, _, pool_d, table_d, nc, st = setup(pkg, gpu, L, B, pps, pt, H, D, k, p, m, ct, False, seed=8)
+    par = [st.P, st.Q] + list(st.rs)
+    off = pkg.offload.ParityOffload(par, p - 1, st.row_bytes)
+    W = st.width
+    evs = []
+    for c in range(nc):
+        st.encode(pkg.chunked.chunk_kv(pool_d, table_d, c, ct), c)
+        evs.append(off.to_host(c * W, W))      # copy of chunk c overlaps encode of c+1
+    for e in evs:
+        e.synchronize()
+    torch.cuda.synchronize()
+    for d, h in zip(par, off.host):
+        assert np.array_equal(d.view(p - 1, -1).cpu().numpy(), h.numpy())
+    want = [t.clone() for t in par]
+    for t in par:
+        t.view(p - 1, -1)[:, W:2 * W] = 0xEE      # chunk 1's device parity lost
+    off.to_device(W, W)
+    torch.cuda.synchronize()
+    for t, w in zip(par, want):
+        assert torch.equal(t, w)
+
+
+def test_offload_rejects_bad_ranges(pkg, gpu):
+    t = [torch.zeros(6 * 64, dtype=torch.uint8, device=gpu)]
+    off = pkg.offload.ParityOffload(t, 6, 64)
+    with pytest.raises(ValueError):
+        off.to_host(48, 32)
+    with pytest.raises(ValueError):
+        pkg.offload.ParityOffload([torch.zeros(100, dtype=torch.uint8, device=gpu)], 6, 64)
