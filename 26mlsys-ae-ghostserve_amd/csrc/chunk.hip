@@ -168,8 +168,10 @@ struct RsDecodeIo {
     int dst_shard[kChunkMaxM];
 };
 
-template <int K, int NOUT>
-__global__ __launch_bounds__(kCBS) void chunk_rs_decode_kernel(PagedGeom g, ChunkGeom cg, int rows,
+// Page-table entries of the pool-side inputs and outputs first, then rows
+// double buffered as in the encode.
+template <int ROWS, int K, int NOUT>
+__global__ __launch_bounds__(kCBS) void chunk_rs_decode_kernel(PagedGeom g, ChunkGeom cg,
                                                                RsDecodeIo io, Gf8Tab<K * NOUT> mix) {
     __shared__ uint32_t tab[K * NOUT][6];
     stage_tables<K * NOUT>(tab, mix);
@@ -178,18 +180,38 @@ __global__ __launch_bounds__(kCBS) void chunk_rs_decode_kernel(PagedGeom g, Chun
     const uint32_t o = u << 4;
     const uint32_t w0 = fdiv(o, g.div_rec);
     const uint32_t inner = o - w0 * g.rec;
-    const uint64_t nb = uint64_t(rows) * cg.R;
+    const uint64_t nb = uint64_t(ROWS) * cg.R;
     const uint32_t lane = cg.col_off + o;
-    for (int r = 0; r < rows; ++r) {
+    auto rec = [&](int shard, int r) { return uint32_t(shard * ROWS + r) * cg.recs_per_cell + w0; };
+    uint32_t pin[ROWS][K], pout[ROWS][NOUT];
+#pragma unroll
+    for (int r = 0; r < ROWS; ++r) {
+#pragma unroll
+        for (int q = 0; q < K; ++q) pin[r][q] = io.in_buf[q] ? 0u : cell_page(g, rec(io.src_shard[q], r));
+#pragma unroll
+        for (int i = 0; i < NOUT; ++i)
+            pout[r][i] = io.dst_shard[i] >= 0 ? cell_page(g, rec(io.dst_shard[i], r)) : 0u;
+    }
+    auto load_in = [&](int q, int r) {
+        return io.in_buf[q] ? ShardView<true>(io.in_buf[q], nb).load(r * cg.R, lane)
+                            : cell_load_at(g, rec(io.src_shard[q], r), inner, pin[r][q]);
+    };
+    u32x4 x[2][K];
+#pragma unroll
+    for (int q = 0; q < K; ++q) x[0][q] = load_in(q, 0);
+#pragma unroll
+    for (int r = 0; r < ROWS; ++r) {
+        const int c = r & 1;
+        if (r + 1 < ROWS) {
+#pragma unroll
+            for (int q = 0; q < K; ++q) x[c ^ 1][q] = load_in(q, r + 1);
+        }
         u32x4 acc[NOUT];
 #pragma unroll
         for (int i = 0; i < NOUT; ++i) acc[i] = u32x4{0, 0, 0, 0};
 #pragma unroll
         for (int q = 0; q < K; ++q) {
-            const u32x4 x = io.in_buf[q]
-                                ? ShardView<true>(io.in_buf[q], nb).load(r * cg.R, lane)
-                                : load_cell(g, cg, io.src_shard[q], r, rows, w0, inner);
-            const uint32_t w4[4] = {x.x, x.y, x.z, x.w};
+            const uint32_t w4[4] = {x[c][q].x, x[c][q].y, x[c][q].z, x[c][q].w};
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 const Gf8Fields f = gf8_fields(w4[e]);
@@ -205,11 +227,10 @@ __global__ __launch_bounds__(kCBS) void chunk_rs_decode_kernel(PagedGeom g, Chun
         }
 #pragma unroll
         for (int i = 0; i < NOUT; ++i) {
-            if (io.dst_shard[i] >= 0)
-                cell_store(g, uint32_t(io.dst_shard[i] * rows + r) * cg.recs_per_cell + w0, inner,
-                           acc[i]);
+            if (io.dst_shard[i] >= 0) cell_store_at(g, rec(io.dst_shard[i], r), inner, pout[r][i], acc[i]);
             if (io.out_buf[i]) ShardView<true>(io.out_buf[i], nb).store(r * cg.R, lane, acc[i]);
         }
+        asm volatile("" ::: "memory");
     }
 }
 
@@ -251,6 +272,57 @@ __global__ __launch_bounds__(kCBS) void chunk_rdp_decode_kernel(PagedGeom g, Chu
             if (d.p[s]) st_stream(d.p[s] + uint64_t(r) * cg.R, lane, acc);
         } else {
             st_stream((s == k ? P : Q) + uint64_t(r) * cg.R, lane, acc);
+        }
+    }
+}
+
+// The same map solved at compile time (p = 7, k = 5, the chunked shape): every
+// needed cell is loaded once (page-table entries first), then the erased
+// cells are straight-line XORs of registers.
+template <int P, int K, int E0, int E1>
+__global__ __launch_bounds__(kCBS) void chunk_rdp_decode_fixed(PagedGeom g, ChunkGeom cg,
+                                                               Ptrs<kChunkMaxK> d, uint8_t* Pp,
+                                                               uint8_t* Qp) {
+    constexpr int ROWS = P - 1, NC = (K + 2) * ROWS;
+    constexpr RdpPlan plan = make_rdp_plan(P, K, E0, E1);
+    static_assert(plan.ok, "RDP erasure pattern not decodable");
+    const uint32_t u = blockIdx.x * kCBS + threadIdx.x;
+    if (u >= cg.nvec) return;
+    const uint32_t o = u << 4;
+    const uint32_t w0 = fdiv(o, g.div_rec);
+    const uint32_t inner = o - w0 * g.rec;
+    const uint64_t nb = uint64_t(ROWS) * cg.R;
+    const uint32_t lane = cg.col_off + o;
+    auto rec = [&](int c) { return uint32_t(c) * cg.recs_per_cell + w0; };  // cell c = shard*ROWS + r
+    auto needed = [&](int c) { return (plan.need[c >> 6] >> (c & 63)) & 1; };
+    uint32_t pg[NC], pgo[plan.nout];
+#pragma unroll
+    for (int c = 0; c < NC; ++c) pg[c] = (c < K * ROWS && needed(c)) ? cell_page(g, rec(c)) : 0u;
+#pragma unroll
+    for (int i = 0; i < plan.nout; ++i)
+        pgo[i] = plan.out_cell[i] < K * ROWS ? cell_page(g, rec(plan.out_cell[i])) : 0u;
+    __builtin_amdgcn_sched_barrier(0);
+    const ShardView<true> sp(Pp, nb), sq(Qp, nb);
+    u32x4 x[NC];
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+        if (!needed(c)) continue;
+        const int s = c / ROWS, r = c % ROWS;
+        x[c] = s < K ? cell_load_at(g, rec(c), inner, pg[c]) : (s == K ? sp : sq).load(r * cg.R, lane);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = 0; i < plan.nout; ++i) {
+        u32x4 acc = {0, 0, 0, 0};
+#pragma unroll
+        for (int c = 0; c < NC; ++c)
+            if ((plan.mask[i][c >> 6] >> (c & 63)) & 1) acc ^= x[c];
+        const int c = plan.out_cell[i], s = c / ROWS, r = c % ROWS;
+        if (s < K) {
+            cell_store_at(g, rec(c), inner, pgo[i], acc);
+            if (d.p[s]) st_stream(d.p[s] + uint64_t(r) * cg.R, lane, acc);
+        } else {
+            (s == K ? sp : sq).store(r * cg.R, lane, acc);
         }
     }
 }
@@ -302,35 +374,71 @@ static EncLauncher encode_launcher(int p, int k, int m) {
     }
 }
 
-template <int K, int NOUT>
+template <int ROWS, int K, int NOUT>
 static void launch_rs_decode(dim3 grid, hipStream_t st, const PagedGeom& g, const ChunkGeom& cg,
-                             int rows, const RsDecodeIo& io, const uint32_t (*tab)[6]) {
+                             const RsDecodeIo& io, const uint32_t (*tab)[6]) {
     Gf8Tab<K * NOUT> t{};
     for (int i = 0; i < K * NOUT; ++i)
         for (int e = 0; e < 6; ++e) t.t[i][e] = tab[i][e];
-    hipLaunchKernelGGL((chunk_rs_decode_kernel<K, NOUT>), grid, dim3(kCBS), 0, st, g, cg, rows, io, t);
+    hipLaunchKernelGGL((chunk_rs_decode_kernel<ROWS, K, NOUT>), grid, dim3(kCBS), 0, st, g, cg, io, t);
 }
 
-typedef void (*RsDecLauncher)(dim3, hipStream_t, const PagedGeom&, const ChunkGeom&, int,
+typedef void (*RsDecLauncher)(dim3, hipStream_t, const PagedGeom&, const ChunkGeom&,
                               const RsDecodeIo&, const uint32_t (*)[6]);
 
-template <int K, int N = 1>
+template <int ROWS, int K, int N = 1>
 RsDecLauncher pick_rs_dec_n(int n) {
     if constexpr (N > 3) {
         return nullptr;
     } else {
-        if (n == N) return &launch_rs_decode<K, N>;
-        return pick_rs_dec_n<K, N + 1>(n);
+        if (n == N) return &launch_rs_decode<ROWS, K, N>;
+        return pick_rs_dec_n<ROWS, K, N + 1>(n);
     }
 }
 
-template <int K = 2>
-RsDecLauncher rs_dec_launcher(int k, int n) {
-    if constexpr (K > 6) {
+template <int ROWS, int K = 2>
+RsDecLauncher pick_rs_dec_k(int k, int n) {
+    if constexpr (K > ROWS) {
         return nullptr;
     } else {
-        if (k == K) return pick_rs_dec_n<K>(n);
-        return rs_dec_launcher<K + 1>(k, n);
+        if (k == K) return pick_rs_dec_n<ROWS, K>(n);
+        return pick_rs_dec_k<ROWS, K + 1>(k, n);
+    }
+}
+
+// Built: p in {3, 5, 7} (rows 2, 4, 6), 2 <= k <= p-1, 1..3 outputs.
+static RsDecLauncher rs_dec_launcher(int p, int k, int n) {
+    switch (p) {
+        case 3: return pick_rs_dec_k<2>(k, n);
+        case 5: return pick_rs_dec_k<4>(k, n);
+        case 7: return pick_rs_dec_k<6>(k, n);
+        default: return nullptr;
+    }
+}
+
+typedef void (*RdpFixedFn)(PagedGeom, ChunkGeom, Ptrs<kChunkMaxK>, uint8_t*, uint8_t*);
+
+template <int P, int K, int E0, int E1 = E0 + 1>
+RdpFixedFn pick_rdp_fixed_pair(int e1) {
+    if constexpr (E1 > K + 1) {
+        return nullptr;
+    } else {
+        if (e1 == E1) return &chunk_rdp_decode_fixed<P, K, E0, E1>;
+        return pick_rdp_fixed_pair<P, K, E0, E1 + 1>(e1);
+    }
+}
+
+// Patterns with at least one data shard (the only ones that reach the RDP path).
+template <int P, int K, int E0 = 0>
+RdpFixedFn pick_rdp_fixed(int e0, int e1) {
+    if constexpr (E0 >= K) {
+        return nullptr;
+    } else {
+        if (e0 == E0) {
+            if (e1 < 0) return &chunk_rdp_decode_fixed<P, K, E0, -1>;
+            return pick_rdp_fixed_pair<P, K, E0>(e1);
+        }
+        return pick_rdp_fixed<P, K, E0 + 1>(e0, e1);
     }
 }
 
@@ -475,9 +583,9 @@ extern "C" int kvec_chunk_decode_paged(const kvec_paged_kv* kv, void* pool,
         }
         uint32_t tab[kChunkMaxK * kChunkMaxM][6];
         for (int i = 0; i < no * k; ++i) perm_tables(M[i], tab[i]);
-        RsDecLauncher L = rs_dec_launcher(k, no);
-        if (!L) return set_error(KVEC_EUNSUPPORTED, "%s: k=%d with %d outputs not built", fn, k, no);
-        L(grid, hs, a.g, a.cg, rows, io, tab);
+        RsDecLauncher L = rs_dec_launcher(a.p, k, no);
+        if (!L) return set_error(KVEC_EUNSUPPORTED, "%s: p=%d k=%d with %d outputs not built", fn, a.p, k, no);
+        L(grid, hs, a.g, a.cg, io, tab);
         rc = check_launch(fn);
         if (rc) return rc;
     } else if (nd > 0 && nd + int(eP) + int(eQ) <= 2) {
@@ -488,8 +596,12 @@ extern "C" int kvec_chunk_decode_paged(const kvec_paged_kv* kv, void* pool,
         RdpPlan plan = make_rdp_plan(a.p, k, e[0], e[1]);
         if (!plan.ok) return set_error(KVEC_EDECODE, "%s: RDP pattern (%d, %d) not decodable", fn, e[0], e[1]);
         Ptrs<kChunkMaxK> dd = a.have_data ? a.d : Ptrs<kChunkMaxK>{};
-        hipLaunchKernelGGL(chunk_rdp_decode_kernel, grid, dim3(kCBS), 0, hs, a.g, a.cg, k, rows, dd,
-                           a.par.p[0], a.par.p[1], plan);
+        RdpFixedFn fx = (a.p == 7 && k == 5) ? pick_rdp_fixed<7, 5>(e[0], e[1]) : nullptr;
+        if (fx)
+            hipLaunchKernelGGL(fx, grid, dim3(kCBS), 0, hs, a.g, a.cg, dd, a.par.p[0], a.par.p[1]);
+        else
+            hipLaunchKernelGGL(chunk_rdp_decode_kernel, grid, dim3(kCBS), 0, hs, a.g, a.cg, k, rows, dd,
+                               a.par.p[0], a.par.p[1], plan);
         rc = check_launch(fn);
         if (rc) return rc;
         reenc = 0;

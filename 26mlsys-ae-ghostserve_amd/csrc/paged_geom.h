@@ -83,6 +83,17 @@ __device__ __forceinline__ u32x4 cell_load_at(const PagedGeom& g, uint32_t w, ui
     return ld_stream(a, 0);
 }
 
+// Store counterpart of cell_load_at (padding records and invalid pages skipped).
+__device__ __forceinline__ void cell_store_at(const PagedGeom& g, uint32_t w, uint32_t inner,
+                                              uint32_t page, u32x4 v) {
+    if (w >= g.recs_total || page >= g.pool_pages) return;
+    const uint32_t lb = fdiv(w, g.div_t);
+    const uint32_t t = w - lb * g.div_t.d + g.tok_off;
+    const uint32_t layer = fdiv(lb, g.div_b);
+    const uint64_t slot = (uint64_t(page) << g.page_shift) | (t & ((1u << g.page_shift) - 1));
+    st_stream(g.pool_w, uint64_t(layer) * g.layer_stride + slot * g.rec + inner, v);
+}
+
 // Write the cell (padding records and invalid pages are skipped).
 __device__ __forceinline__ void cell_store(const PagedGeom& g, uint32_t w, uint32_t inner, u32x4 v) {
     bool valid;
