@@ -8,6 +8,7 @@ from __future__ import annotations
 import concurrent.futures as cf
 import glob
 import os
+import re
 import shutil
 import subprocess
 
@@ -41,12 +42,32 @@ def hipcc() -> str:
     return cand
 
 
+def sgpr_spills(remarks: str) -> list:
+    """(kernel, count) for every kernel the resource-usage remarks report with
+    spilled SGPRs.  Kernels here that spilled SGPRs to VGPR lanes produced
+    run-to-run different bytes on gfx950, so the build rejects them."""
+    out, name = [], None
+    for line in remarks.splitlines():
+        m = re.search(r"Function Name: (\S+)", line)
+        if m:
+            name = m.group(1)
+            continue
+        m = re.search(r"SGPRs Spill: (\d+)", line)
+        if m and int(m.group(1)) > 0:
+            out.append((name, int(m.group(1))))
+    return out
+
+
 def _compile(src: str) -> str:
     obj = os.path.join(OBJDIR, os.path.basename(src)[:-4] + ".o")
-    cmd = [hipcc(), *FLAGS, "-c", src, "-o", obj]
+    cmd = [hipcc(), *FLAGS, "-Rpass-analysis=kernel-resource-usage", "-c", src, "-o", obj]
     r = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"hipcc failed on {os.path.basename(src)}:\n{r.stdout}")
+    spills = sgpr_spills(r.stdout)
+    if spills:
+        names = "\n  ".join(f"{n}: {c}" for n, c in spills)
+        raise RuntimeError(f"{os.path.basename(src)}: kernels spill SGPRs:\n  {names}")
     return obj
 
 

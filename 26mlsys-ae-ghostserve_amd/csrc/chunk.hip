@@ -61,16 +61,15 @@ __device__ __forceinline__ u32x4 load_cell(const PagedGeom& g, const ChunkGeom& 
 }
 
 // ------------------------------------------------------------------ encode
-// Every cell's page-table entry is loaded first.  Then rows are double
-// buffered: row r+1's k cells are loaded before row r is coded and stored, so
-// a wave always has a row of loads in flight while it computes, and a thread
-// holds two rows (not all p-1) in registers.  Program order is what keeps the
-// loads early: stores to the shards could alias the pool as far as the
-// compiler knows, and the compiler barrier after each row also keeps the GF
-// tables from being hoisted out of the row loop (they are re-read from LDS per
-// row instead of pinning 6*k*m registers).  Outputs switched off by `wmask` get
-// a buffer resource of size 0, whose stores the hardware drops, so the kernel
-// has no branches after the bounds check.
+// Rows are software pipelined two deep: while row r is coded and stored, row
+// r+1's cells are in flight and row r+2's page-table entries are being
+// fetched, so a thread holds two rows of cells and two rows of references.
+// Program order is what keeps the loads early: stores to the shards could
+// alias the pool as far as the compiler knows, and the compiler barrier after
+// each row also keeps the GF tables from being hoisted out of the row loop
+// (they are re-read from LDS per row instead of pinning 6*k*m registers).
+// Outputs switched off by `wmask` get a buffer resource of size 0, whose stores
+// the hardware drops, so the kernel has no branches after the bounds check.
 template <int P, int K, int M>
 __global__ __launch_bounds__(kCBS) void chunk_encode_kernel(PagedGeom g, ChunkGeom cg,
                                                             Ptrs<kChunkMaxK> d,
@@ -88,15 +87,17 @@ __global__ __launch_bounds__(kCBS) void chunk_encode_kernel(PagedGeom g, ChunkGe
     const uint32_t inner = o - w0 * g.rec;
     const uint64_t nb = ROWS * cg.R;
     const uint32_t lane = cg.col_off + o;
-    uint32_t pg[ROWS][K];
-#pragma unroll
-    for (int r = 0; r < ROWS; ++r)
-#pragma unroll
-        for (int j = 0; j < K; ++j) pg[r][j] = cell_page(g, uint32_t(j * ROWS + r) * cg.recs_per_cell + w0);
+    auto rec = [&](int j, int r) { return uint32_t(j * ROWS + r) * cg.recs_per_cell + w0; };
+    CellRef ref[2][K];
     u32x4 x[2][K];
 #pragma unroll
-    for (int j = 0; j < K; ++j)
-        x[0][j] = cell_load_at(g, uint32_t(j * ROWS) * cg.recs_per_cell + w0, inner, pg[0][j]);
+    for (int j = 0; j < K; ++j) ref[0][j] = cell_ref(g, rec(j, 0));
+    if constexpr (ROWS > 1) {
+#pragma unroll
+        for (int j = 0; j < K; ++j) ref[1][j] = cell_ref(g, rec(j, 1));
+    }
+#pragma unroll
+    for (int j = 0; j < K; ++j) x[0][j] = cell_load_ref(g, ref[0][j], inner);
     const uint64_t nd = (wmask & kWData) ? nb : 0;
     u32x4 q[ROWS];
 #pragma unroll
@@ -107,15 +108,15 @@ __global__ __launch_bounds__(kCBS) void chunk_encode_kernel(PagedGeom g, ChunkGe
         const int c = r & 1;
         if (r + 1 < ROWS) {
 #pragma unroll
-            for (int j = 0; j < K; ++j)
-                x[c ^ 1][j] = cell_load_at(g, uint32_t(j * ROWS + r + 1) * cg.recs_per_cell + w0, inner,
-                                           pg[r + 1][j]);
+            for (int j = 0; j < K; ++j) x[c ^ 1][j] = cell_load_ref(g, ref[c ^ 1][j], inner);
+        }
+        if (r + 2 < ROWS) {
+#pragma unroll
+            for (int j = 0; j < K; ++j) ref[c][j] = cell_ref(g, rec(j, r + 2));
         }
 #pragma unroll
         for (int j = 0; j < K; ++j) ShardView<true>(d.p[j], nd).store(r * cg.R, lane, x[c][j]);
-        u32x4 pr = x[c][0];
-#pragma unroll
-        for (int j = 1; j < K; ++j) pr ^= x[c][j];
+        const u32x4 pr = xor_all<K>(x[c]);
         sp.store(r * cg.R, lane, pr);
         // cell (r, j) lies on diagonal (r + j) % p; the P cell of row r on r - 1
 #pragma unroll
@@ -130,19 +131,10 @@ __global__ __launch_bounds__(kCBS) void chunk_encode_kernel(PagedGeom g, ChunkGe
             for (int i = 0; i < M; ++i) acc[i] = u32x4{0, 0, 0, 0};
 #pragma unroll
             for (int j = 0; j < K; ++j) {
-                const uint32_t w4[4] = {x[c][j].x, x[c][j].y, x[c][j].z, x[c][j].w};
+                Gf8Fields f[4];
+                gf8_fields16(x[c][j], f);
 #pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const Gf8Fields f = gf8_fields(w4[e]);
-#pragma unroll
-                    for (int i = 0; i < M; ++i) {
-                        const uint32_t pm = gf8_mul4(f, tab[i * K + j]);
-                        if (e == 0) acc[i].x ^= pm;
-                        else if (e == 1) acc[i].y ^= pm;
-                        else if (e == 2) acc[i].z ^= pm;
-                        else acc[i].w ^= pm;
-                    }
-                }
+                for (int i = 0; i < M; ++i) acc[i] = gf8_fma16(acc[i], f, tab[i * K + j]);
             }
 #pragma unroll
             for (int i = 0; i < M; ++i)
@@ -168,8 +160,8 @@ struct RsDecodeIo {
     int dst_shard[kChunkMaxM];
 };
 
-// Page-table entries of the pool-side inputs and outputs first, then rows
-// double buffered as in the encode.
+// Rows pipelined as in the encode, with a ring of three rows of references
+// (a row's output references are still needed when its stores issue).
 template <int ROWS, int K, int NOUT>
 __global__ __launch_bounds__(kCBS) void chunk_rs_decode_kernel(PagedGeom g, ChunkGeom cg,
                                                                RsDecodeIo io, Gf8Tab<K * NOUT> mix) {
@@ -183,20 +175,22 @@ __global__ __launch_bounds__(kCBS) void chunk_rs_decode_kernel(PagedGeom g, Chun
     const uint64_t nb = uint64_t(ROWS) * cg.R;
     const uint32_t lane = cg.col_off + o;
     auto rec = [&](int shard, int r) { return uint32_t(shard * ROWS + r) * cg.recs_per_cell + w0; };
-    uint32_t pin[ROWS][K], pout[ROWS][NOUT];
+    CellRef rin[3][K], rout[3][NOUT];
+    auto refs = [&](int r) {
 #pragma unroll
-    for (int r = 0; r < ROWS; ++r) {
-#pragma unroll
-        for (int q = 0; q < K; ++q) pin[r][q] = io.in_buf[q] ? 0u : cell_page(g, rec(io.src_shard[q], r));
+        for (int q = 0; q < K; ++q)
+            if (!io.in_buf[q]) rin[r % 3][q] = cell_ref(g, rec(io.src_shard[q], r));
 #pragma unroll
         for (int i = 0; i < NOUT; ++i)
-            pout[r][i] = io.dst_shard[i] >= 0 ? cell_page(g, rec(io.dst_shard[i], r)) : 0u;
-    }
+            if (io.dst_shard[i] >= 0) rout[r % 3][i] = cell_ref(g, rec(io.dst_shard[i], r));
+    };
     auto load_in = [&](int q, int r) {
         return io.in_buf[q] ? ShardView<true>(io.in_buf[q], nb).load(r * cg.R, lane)
-                            : cell_load_at(g, rec(io.src_shard[q], r), inner, pin[r][q]);
+                            : cell_load_ref(g, rin[r % 3][q], inner);
     };
     u32x4 x[2][K];
+    refs(0);
+    if constexpr (ROWS > 1) refs(1);
 #pragma unroll
     for (int q = 0; q < K; ++q) x[0][q] = load_in(q, 0);
 #pragma unroll
@@ -206,28 +200,20 @@ __global__ __launch_bounds__(kCBS) void chunk_rs_decode_kernel(PagedGeom g, Chun
 #pragma unroll
             for (int q = 0; q < K; ++q) x[c ^ 1][q] = load_in(q, r + 1);
         }
+        if (r + 2 < ROWS) refs(r + 2);
         u32x4 acc[NOUT];
 #pragma unroll
         for (int i = 0; i < NOUT; ++i) acc[i] = u32x4{0, 0, 0, 0};
 #pragma unroll
         for (int q = 0; q < K; ++q) {
-            const uint32_t w4[4] = {x[c][q].x, x[c][q].y, x[c][q].z, x[c][q].w};
+            Gf8Fields f[4];
+            gf8_fields16(x[c][q], f);
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const Gf8Fields f = gf8_fields(w4[e]);
-#pragma unroll
-                for (int i = 0; i < NOUT; ++i) {
-                    const uint32_t pm = gf8_mul4(f, tab[i * K + q]);
-                    if (e == 0) acc[i].x ^= pm;
-                    else if (e == 1) acc[i].y ^= pm;
-                    else if (e == 2) acc[i].z ^= pm;
-                    else acc[i].w ^= pm;
-                }
-            }
+            for (int i = 0; i < NOUT; ++i) acc[i] = gf8_fma16(acc[i], f, tab[i * K + q]);
         }
 #pragma unroll
         for (int i = 0; i < NOUT; ++i) {
-            if (io.dst_shard[i] >= 0) cell_store_at(g, rec(io.dst_shard[i], r), inner, pout[r][i], acc[i]);
+            if (io.dst_shard[i] >= 0) cell_store_ref(g, rout[r % 3][i], inner, acc[i]);
             if (io.out_buf[i]) ShardView<true>(io.out_buf[i], nb).store(r * cg.R, lane, acc[i]);
         }
         asm volatile("" ::: "memory");
@@ -293,14 +279,15 @@ __global__ __launch_bounds__(kCBS) void chunk_rdp_decode_fixed(PagedGeom g, Chun
     const uint32_t inner = o - w0 * g.rec;
     const uint64_t nb = uint64_t(ROWS) * cg.R;
     const uint32_t lane = cg.col_off + o;
-    auto rec = [&](int c) { return uint32_t(c) * cg.recs_per_cell + w0; };  // cell c = shard*ROWS + r
     auto needed = [&](int c) { return (plan.need[c >> 6] >> (c & 63)) & 1; };
-    uint32_t pg[NC], pgo[plan.nout];
+    CellRef ref[NC], refo[plan.nout];   // c = shard * ROWS + row
 #pragma unroll
-    for (int c = 0; c < NC; ++c) pg[c] = (c < K * ROWS && needed(c)) ? cell_page(g, rec(c)) : 0u;
+    for (int c = 0; c < NC; ++c)
+        if (c < K * ROWS && needed(c)) ref[c] = cell_ref(g, uint32_t(c) * cg.recs_per_cell + w0);
 #pragma unroll
     for (int i = 0; i < plan.nout; ++i)
-        pgo[i] = plan.out_cell[i] < K * ROWS ? cell_page(g, rec(plan.out_cell[i])) : 0u;
+        if (plan.out_cell[i] < K * ROWS)
+            refo[i] = cell_ref(g, uint32_t(plan.out_cell[i]) * cg.recs_per_cell + w0);
     __builtin_amdgcn_sched_barrier(0);
     const ShardView<true> sp(Pp, nb), sq(Qp, nb);
     u32x4 x[NC];
@@ -308,7 +295,7 @@ __global__ __launch_bounds__(kCBS) void chunk_rdp_decode_fixed(PagedGeom g, Chun
     for (int c = 0; c < NC; ++c) {
         if (!needed(c)) continue;
         const int s = c / ROWS, r = c % ROWS;
-        x[c] = s < K ? cell_load_at(g, rec(c), inner, pg[c]) : (s == K ? sp : sq).load(r * cg.R, lane);
+        x[c] = s < K ? cell_load_ref(g, ref[c], inner) : (s == K ? sp : sq).load(r * cg.R, lane);
     }
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
@@ -319,7 +306,7 @@ __global__ __launch_bounds__(kCBS) void chunk_rdp_decode_fixed(PagedGeom g, Chun
             if ((plan.mask[i][c >> 6] >> (c & 63)) & 1) acc ^= x[c];
         const int c = plan.out_cell[i], s = c / ROWS, r = c % ROWS;
         if (s < K) {
-            cell_store_at(g, rec(c), inner, pgo[i], acc);
+            cell_store_ref(g, refo[i], inner, acc);
             if (d.p[s]) st_stream(d.p[s] + uint64_t(r) * cg.R, lane, acc);
         } else {
             (s == K ? sp : sq).store(r * cg.R, lane, acc);

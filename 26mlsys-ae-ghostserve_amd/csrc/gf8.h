@@ -146,4 +146,25 @@ __device__ __forceinline__ uint32_t gf8_mul4(const Gf8Fields& f, const uint32_t*
     return gf8_mul4(f.f0, f.f1, f.f2, t);
 }
 
+// acc ^ x*c for four bytes: three v_perm_b32 and two 3-input XORs.
+__device__ __forceinline__ uint32_t gf8_fma4(uint32_t acc, const Gf8Fields& f, const uint32_t* t) {
+    const uint32_t p0 = __builtin_amdgcn_perm(t[1], t[0], f.f0);
+    const uint32_t p1 = __builtin_amdgcn_perm(t[3], t[2], f.f1);
+    const uint32_t p2 = __builtin_amdgcn_perm(t[5], t[4], f.f2);
+    return xor3(xor3(acc, p0, p1), p2, 0u);
+}
+
+// acc ^ x*c for a 16-byte cell.
+__device__ __forceinline__ u32x4 gf8_fma16(u32x4 acc, const Gf8Fields* f, const uint32_t* t) {
+    return u32x4{gf8_fma4(acc.x, f[0], t), gf8_fma4(acc.y, f[1], t), gf8_fma4(acc.z, f[2], t),
+                 gf8_fma4(acc.w, f[3], t)};
+}
+
+__device__ __forceinline__ void gf8_fields16(u32x4 x, Gf8Fields* f) {
+    f[0] = gf8_fields(x.x);
+    f[1] = gf8_fields(x.y);
+    f[2] = gf8_fields(x.z);
+    f[3] = gf8_fields(x.w);
+}
+
 }  // namespace kvec

@@ -36,6 +36,26 @@ __device__ __forceinline__ void st16(uint8_t* p, u32x4 v) {
     *reinterpret_cast<u32x4*>(p) = v;
 }
 
+// Three-input XOR in one VALU op (v_bitop3_b32 with truth table 0x96); the
+// compiler does not form it from a ^ b ^ c by itself.
+__device__ __forceinline__ uint32_t xor3(uint32_t a, uint32_t b, uint32_t c) {
+    return __builtin_amdgcn_bitop3_b32(a, b, c, 0x96);
+}
+__device__ __forceinline__ u32x4 xor3(u32x4 a, u32x4 b, u32x4 c) {
+    return u32x4{xor3(a.x, b.x, c.x), xor3(a.y, b.y, c.y), xor3(a.z, b.z, c.z), xor3(a.w, b.w, c.w)};
+}
+
+// XOR of N cells with 3-input XORs.
+template <int N>
+__device__ __forceinline__ u32x4 xor_all(const u32x4* v) {
+    u32x4 a = v[0];
+    int i = 1;
+#pragma unroll
+    for (; i + 1 < N; i += 2) a = xor3(a, v[i], v[i + 1]);
+    if (i < N) a ^= v[i];
+    return a;
+}
+
 // ------------------------------------------------------------- shard views
 // One shard buffer seen by a kernel.  Shards below 4 GiB use a buffer
 // resource: the row-plane offset rides in an SGPR (soffset), the lane offset

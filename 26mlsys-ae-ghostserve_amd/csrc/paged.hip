@@ -38,12 +38,14 @@ __global__ __launch_bounds__(kGBS) void kv_scatter_kernel(PagedGeom g, const uin
 // ------------------------------------------------- fused gather + RDP encode
 // Stream cell (shard j, row r, lane offset o) is stream byte (j*(p-1) + r)*R + o;
 // with R a multiple of the record size its record is (j*(p-1) + r)*(R/rec) + o/rec.
-// The cell is loaded from the pool once, stored to its data shard and folded
-// into P and Q in registers.
+// Each cell is loaded from the pool once, stored to its data shard and folded
+// into P and Q in registers.  Shards are software pipelined two deep: while
+// shard j is folded in and stored, shard j+1's cells are in flight and shard
+// j+2's page-table entries are being fetched.
 constexpr int kFBS = 128;
 
 template <int P, int K>
-__global__ __launch_bounds__(kFBS) __attribute__((amdgpu_waves_per_eu(1, 2))) void rdp_encode_paged_kernel(PagedGeom g, Ptrs<16> d,
+__global__ __launch_bounds__(kFBS) void rdp_encode_paged_kernel(PagedGeom g, Ptrs<16> d,
                                                                 uint8_t* __restrict__ Pp,
                                                                 uint8_t* __restrict__ Qp, uint64_t R,
                                                                 uint32_t recs_per_row, uint32_t nvec) {
@@ -54,21 +56,17 @@ __global__ __launch_bounds__(kFBS) __attribute__((amdgpu_waves_per_eu(1, 2))) vo
     const uint32_t w0 = fdiv(off, g.div_rec);
     const uint32_t inner = off - w0 * g.rec;
     const uint64_t nb = ROWS * R;
-    // every cell is loaded before anything is stored (the shard stores could
-    // alias the pool as far as the compiler knows)
-    uint32_t pg[K][ROWS];
+    auto rec = [&](int j, int r) { return uint32_t(j * ROWS + r) * recs_per_row + w0; };
+    CellRef ref[2][ROWS];
+    u32x4 x[2][ROWS];
 #pragma unroll
-    for (int j = 0; j < K; ++j)
+    for (int r = 0; r < ROWS; ++r) ref[0][r] = cell_ref(g, rec(0, r));
+    if constexpr (K > 1) {
 #pragma unroll
-        for (int r = 0; r < ROWS; ++r) pg[j][r] = cell_page(g, (j * ROWS + r) * recs_per_row + w0);
-    __builtin_amdgcn_sched_barrier(0);
-    u32x4 x[K][ROWS];
+        for (int r = 0; r < ROWS; ++r) ref[1][r] = cell_ref(g, rec(1, r));
+    }
 #pragma unroll
-    for (int j = 0; j < K; ++j)
-#pragma unroll
-        for (int r = 0; r < ROWS; ++r)
-            x[j][r] = cell_load_at(g, (j * ROWS + r) * recs_per_row + w0, inner, pg[j][r]);
-    __builtin_amdgcn_sched_barrier(0);
+    for (int r = 0; r < ROWS; ++r) x[0][r] = cell_load_ref(g, ref[0][r], inner);
     u32x4 pr[ROWS], q[ROWS];
 #pragma unroll
     for (int r = 0; r < ROWS; ++r) {
@@ -77,14 +75,24 @@ __global__ __launch_bounds__(kFBS) __attribute__((amdgpu_waves_per_eu(1, 2))) vo
     }
 #pragma unroll
     for (int j = 0; j < K; ++j) {
+        const int c = j & 1;
+        if (j + 1 < K) {
+#pragma unroll
+            for (int r = 0; r < ROWS; ++r) x[c ^ 1][r] = cell_load_ref(g, ref[c ^ 1][r], inner);
+        }
+        if (j + 2 < K) {
+#pragma unroll
+            for (int r = 0; r < ROWS; ++r) ref[c][r] = cell_ref(g, rec(j + 2, r));
+        }
         const ShardView<true> sv(d.p[j], nb);
 #pragma unroll
         for (int r = 0; r < ROWS; ++r) {
-            sv.store(r * R, off, x[j][r]);
-            pr[r] ^= x[j][r];
+            sv.store(r * R, off, x[c][r]);
+            pr[r] ^= x[c][r];
             const int dg = (r + j) % P;
-            if (dg != P - 1) q[dg] ^= x[j][r];
+            if (dg != P - 1) q[dg] ^= x[c][r];
         }
+        asm volatile("" ::: "memory");
     }
 #pragma unroll
     for (int r = 1; r < ROWS; ++r) q[r - 1] ^= pr[r];

@@ -20,6 +20,7 @@ struct PagedGeom {
     uint8_t* pool_w;            // same pool, for the scatter
     const int32_t* table;       // [batch][pps]
     uint64_t layer_stride;      // pool_pages * page_tokens * record bytes
+    uint32_t layer_recs;        // pool_pages * page_tokens
     uint64_t recs_total;        // layers * batch * tokens
     uint32_t rec, pps, tok_off, page_shift, pool_pages;
     FastDiv div_rec, div_t, div_b, div_cells;  // div_cells: record_bytes / 16
@@ -57,41 +58,49 @@ __device__ __forceinline__ u32x4 cell_load(const PagedGeom& g, uint32_t w, uint3
     return ld_stream(a, 0);
 }
 
-// Two-phase access for kernels that load many cells per thread: first every
-// cell's page-table entry (cell_page), then every cell (cell_load_at), with a
-// scheduling barrier between the phases and before the arithmetic, so that
-// all table loads, and then all pool loads, are in flight together.
-__device__ __forceinline__ uint32_t cell_page(const PagedGeom& g, uint32_t w) {
-    const uint32_t ww = w < g.recs_total ? w : 0u;
-    const uint32_t lb = fdiv(ww, g.div_t);
-    const uint32_t t = ww - lb * g.div_t.d + g.tok_off;
-    const uint32_t b = lb - fdiv(lb, g.div_b) * g.div_b.d;
-    return uint32_t(g.table[b * g.pps + (t >> g.page_shift)]);
-}
+// Split access for kernels that keep several cells in flight per thread:
+// cell_ref issues the page-table load of a cell and keeps, in two VGPRs, the
+// entry and the cell's record index with page 0 (its layer and in-page token),
+// kNoCell for padding records; cell_load_ref / cell_store_ref finish the access.
+// Issuing the refs of a later row before the cells of an earlier one keeps both
+// kinds of load in flight.  Everything stays per lane: no wave-uniform values
+// are held across the phases (spilled SGPRs have given run-to-run different
+// results in these kernels).
+constexpr uint32_t kNoCell = 0xFFFFFFFFu;
 
-__device__ __forceinline__ u32x4 cell_load_at(const PagedGeom& g, uint32_t w, uint32_t inner,
-                                              uint32_t page) {
-    const bool valid = w < g.recs_total && page < g.pool_pages;
+struct CellRef {
+    uint32_t base;  // layer * layer_recs + in-page token, or kNoCell
+    uint32_t page;  // page-table entry (any value; checked on use)
+};
+
+__device__ __forceinline__ CellRef cell_ref(const PagedGeom& g, uint32_t w) {
+    const bool valid = w < g.recs_total;
     const uint32_t ww = valid ? w : 0u;
     const uint32_t lb = fdiv(ww, g.div_t);
     const uint32_t t = ww - lb * g.div_t.d + g.tok_off;
     const uint32_t layer = fdiv(lb, g.div_b);
-    const uint64_t slot = (uint64_t(valid ? page : 0u) << g.page_shift) |
-                          (t & ((1u << g.page_shift) - 1));
-    const uint8_t* a = valid ? g.pool + (uint64_t(layer) * g.layer_stride + slot * g.rec + inner)
-                             : reinterpret_cast<const uint8_t*>(kZeroCell);
+    const uint32_t b = lb - layer * g.div_b.d;
+    const uint32_t page = uint32_t(g.table[b * g.pps + (t >> g.page_shift)]);
+    return CellRef{valid ? layer * g.layer_recs + (t & ((1u << g.page_shift) - 1)) : kNoCell, page};
+}
+
+__device__ __forceinline__ bool cell_valid(const PagedGeom& g, const CellRef& c) {
+    return c.base != kNoCell && c.page < g.pool_pages;
+}
+
+__device__ __forceinline__ uint64_t cell_ref_offset(const PagedGeom& g, const CellRef& c, uint32_t inner) {
+    return uint64_t(c.base + (c.page << g.page_shift)) * g.rec + inner;
+}
+
+__device__ __forceinline__ u32x4 cell_load_ref(const PagedGeom& g, const CellRef& c, uint32_t inner) {
+    const uint8_t* a = cell_valid(g, c) ? g.pool + cell_ref_offset(g, c, inner)
+                                        : reinterpret_cast<const uint8_t*>(kZeroCell);
     return ld_stream(a, 0);
 }
 
-// Store counterpart of cell_load_at (padding records and invalid pages skipped).
-__device__ __forceinline__ void cell_store_at(const PagedGeom& g, uint32_t w, uint32_t inner,
-                                              uint32_t page, u32x4 v) {
-    if (w >= g.recs_total || page >= g.pool_pages) return;
-    const uint32_t lb = fdiv(w, g.div_t);
-    const uint32_t t = w - lb * g.div_t.d + g.tok_off;
-    const uint32_t layer = fdiv(lb, g.div_b);
-    const uint64_t slot = (uint64_t(page) << g.page_shift) | (t & ((1u << g.page_shift) - 1));
-    st_stream(g.pool_w, uint64_t(layer) * g.layer_stride + slot * g.rec + inner, v);
+__device__ __forceinline__ void cell_store_ref(const PagedGeom& g, const CellRef& c, uint32_t inner,
+                                               u32x4 v) {
+    if (cell_valid(g, c)) st_stream(g.pool_w, cell_ref_offset(g, c, inner), v);
 }
 
 // Write the cell (padding records and invalid pages are skipped).
@@ -119,12 +128,14 @@ inline int make_geom(const kvec_paged_kv* kv, PagedGeom* g, const char* fn) {
     const uint64_t recs = uint64_t(kv->layers) * kv->batch * uint64_t(kv->tokens);
     if (recs >= (uint64_t(1) << 32) || uint64_t(kv->layers) * kv->batch >= (uint64_t(1) << 32) ||
         kv->pool_pages >= (int64_t(1) << 31) || recs * rec / 16 >= (uint64_t(1) << 32) ||
-        int64_t(kv->batch) * kv->pages_per_seq >= (int64_t(1) << 31))
+        int64_t(kv->batch) * kv->pages_per_seq >= (int64_t(1) << 31) ||
+        uint64_t(kv->layers) * uint64_t(kv->pool_pages) * uint64_t(kv->page_tokens) >= kNoCell)
         return set_error(KVEC_EUNSUPPORTED, "%s: chunk too large for 32-bit cell indices", fn);
     g->pool = (const uint8_t*)kv->pool;
     g->pool_w = (uint8_t*)kv->pool;
     g->table = kv->page_table;
     g->layer_stride = uint64_t(kv->pool_pages) * kv->page_tokens * rec;
+    g->layer_recs = uint32_t(uint64_t(kv->pool_pages) * kv->page_tokens);
     g->recs_total = recs;
     g->rec = uint32_t(rec);
     g->pps = uint32_t(kv->pages_per_seq);

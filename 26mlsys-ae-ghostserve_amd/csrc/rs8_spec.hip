@@ -14,9 +14,17 @@
 
 namespace kvec {
 
+// The coefficient tables are staged in LDS and read at their point of use:
+// held in SGPRs from the kernel arguments, 6*k*m dwords next to the shard
+// buffer resources overflow the SGPR file and get spilled (and kernels that
+// spilled SGPRs have given run-to-run different results).
 template <int NIN, int NOUT, int V>
 __global__ __launch_bounds__(kRs8BS) void gf8_mix_kernel(Ptrs<kRs8MaxK> in, Ptrs<kRs8MaxM> out,
                                                          Gf8Mix mix, uint32_t S, uint32_t nvec) {
+    __shared__ uint32_t lds_tab[NIN * NOUT][6];
+    for (int i = threadIdx.x; i < NIN * NOUT * 6; i += kRs8BS) lds_tab[i / 6][i % 6] = mix.t[i / 6][i % 6];
+    __syncthreads();
+    auto tab = [&](int c) -> const uint32_t* { return lds_tab[c]; };
     const uint32_t u0 = blockIdx.x * (kRs8BS * V) + threadIdx.x;
     u32x4 acc[V][NOUT];
 #pragma unroll
@@ -34,21 +42,10 @@ __global__ __launch_bounds__(kRs8BS) void gf8_mix_kernel(Ptrs<kRs8MaxK> in, Ptrs
         }
 #pragma unroll
         for (int v = 0; v < V; ++v) {
-            const uint32_t w[4] = {x[v].x, x[v].y, x[v].z, x[v].w};
+            Gf8Fields f[4];
+            gf8_fields16(x[v], f);
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const uint32_t f0 = w[q] & 0x07070707u;
-                const uint32_t f1 = (w[q] >> 3) & 0x07070707u;
-                const uint32_t f2 = (w[q] >> 6) & 0x03030303u;
-#pragma unroll
-                for (int o = 0; o < NOUT; ++o) {
-                    const uint32_t pr = gf8_mul4(f0, f1, f2, mix.t[o * NIN + j]);
-                    if (q == 0) acc[v][o].x ^= pr;
-                    else if (q == 1) acc[v][o].y ^= pr;
-                    else if (q == 2) acc[v][o].z ^= pr;
-                    else acc[v][o].w ^= pr;
-                }
-            }
+            for (int o = 0; o < NOUT; ++o) acc[v][o] = gf8_fma16(acc[v][o], f, tab(o * NIN + j));
         }
     }
 #pragma unroll
