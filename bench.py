@@ -442,6 +442,108 @@ def bench_chunked(pkg, torch, oracle, dev, seed, warmup):
     }
 
 
+def bench_gs(pkg, torch, oracle, dev, seed, steps, warmup):
+    """The reference's own codes (bit-exact family) on the same 512 MiB
+    Llama-3.1-8B stream, in the reference's packed layouts:
+      star-diagonal P/Q  compute_rdp_parity on rows [(6+2), S] u16 (nd = 6),
+      XOR                encode_xor of data_padded into [(6+1), S] u8,
+      RS GF(2^16)        encode_rs_u16 of data_padded into [(6+2), S] u16.
+    Each output is checked on sampled columns (P, XOR and RS against the
+    oracle on the gathered columns, Q against its definition) before timing."""
+    import numpy as np
+    rng = np.random.default_rng(seed + 400)
+    nd, sb = 6, 0
+    words = STREAM_BYTES // 2
+    S = -(-words // nd)
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed + 401)
+    out = {}
+
+    # star-diagonal P/Q (bench_ghostserve_rdp.py:121-150, benchmark/rdp/kernel.cu:76-107)
+    rows = [torch.zeros((nd + 2, S), dtype=torch.uint16, device=dev) for _ in range(2)]
+    for r in rows:
+        r[:nd].view(torch.int16).copy_(torch.randint(-32768, 32767, (nd, S), generator=g, device=dev,
+                                                     dtype=torch.int16))
+
+    def par(rw):
+        pkg.rdp_kv_ops.compute_rdp_parity(rw, nd, S, sb)
+
+    par(rows[0])
+    torch.cuda.synchronize()
+    cols = np.sort(rng.choice(S, 4096, replace=False))
+    h = rows[0].cpu().numpy()
+    if not np.array_equal(h[nd, cols], np.bitwise_xor.reduce(h[:nd, cols], axis=0)):
+        raise RuntimeError("gs P mismatch")
+    q = np.zeros(cols.size, np.uint16)
+    for r in range(nd):
+        c = (cols - r) % S
+        q ^= np.where(c != (sb + r) % S, h[r, c], 0).astype(np.uint16)
+    if not np.array_equal(h[nd + 1, cols], q):
+        raise RuntimeError("gs Q mismatch")
+    del h
+    wall, kms = time_kernel(torch, par, [(r,) for r in rows], steps, warmup)
+    alg = nd * S * 2 + 2 * S * 2
+    out["star_diagonal_pq"] = {"us": round(kms * 1e3, 2), "alg_bytes": alg,
+                               "gbs": round(alg / kms / 1e6, 2),
+                               "frac_hbm_peak": round(alg / kms / 1e6 / HBM_PEAK_GBS, 4)}
+    del rows
+
+    # XOR (benchmark/xor/kernel.cu:17-41): copy of the data rows + P
+    Sb = -(-STREAM_BYTES // nd)
+    sets = []
+    for _ in range(2):
+        dp = torch.randint(0, 256, (nd * Sb,), generator=g, device=dev, dtype=torch.uint8)
+        sets.append((dp, torch.empty((nd + 1, Sb), dtype=torch.uint8, device=dev)))
+
+    def xenc(dp, sh):
+        pkg.xor.xor_kernel.encode_xor(dp, sh, nd, Sb)
+
+    xenc(*sets[0])
+    torch.cuda.synchronize()
+    cb = np.sort(rng.choice(Sb, 4096, replace=False))
+    dsub = np.ascontiguousarray(sets[0][0].view(nd, Sb)[:, torch.from_numpy(cb).to(dev)].cpu().numpy())
+    want = oracle.xor_encode(dsub.reshape(-1), nd, cb.size)
+    if not np.array_equal(sets[0][1][:, torch.from_numpy(cb).to(dev)].cpu().numpy(), want):
+        raise RuntimeError("gs XOR mismatch")
+    wall, kms = time_kernel(torch, xenc, sets, steps, warmup)
+    alg = 2 * nd * Sb + nd * Sb + Sb   # copy (read + write) and the XOR pass (read + P write)
+    out["xor_encode"] = {"us": round(kms * 1e3, 2), "alg_bytes": alg,
+                         "gbs": round(alg / kms / 1e6, 2),
+                         "frac_hbm_peak": round(alg / kms / 1e6 / HBM_PEAK_GBS, 4)}
+    del sets
+
+    # RS over GF(2^16) (benchmark/rs/kernel.cu:67-102): copy of the data rows + 2 parities
+    m = 2
+    ex, lg = pkg.rs.device_gf_tables(dev)
+    sets = []
+    for _ in range(2):
+        dp = torch.randint(-32768, 32767, (nd * S,), generator=g, device=dev,
+                           dtype=torch.int16).view(torch.uint16)
+        sets.append((dp, torch.empty((nd + m, S), dtype=torch.uint16, device=dev)))
+
+    def renc(dp, sh):
+        pkg.rs.rs_kernel.encode_rs_u16(dp, sh, nd, m, S, ex, lg)
+
+    renc(*sets[0])
+    torch.cuda.synchronize()
+    cw = torch.from_numpy(np.sort(rng.choice(S, 2048, replace=False))).to(dev)
+    dsub = np.ascontiguousarray(sets[0][0].view(torch.int16).view(nd, S)[:, cw].cpu().numpy()
+                                .view(np.uint16))
+    exh, lgh = oracle.gf16_tables()
+    want = oracle.rs16_encode(dsub.reshape(-1), nd, m, cw.numel(), exh, lgh)
+    if not np.array_equal(sets[0][1].view(torch.int16)[:, cw].cpu().numpy().view(np.uint16), want):
+        raise RuntimeError("gs RS16 mismatch")
+    wall, kms = time_kernel(torch, renc, sets, steps, warmup)
+    alg = 2 * nd * S * 2 + nd * S * 2 + m * S * 2
+    out["rs16_encode"] = {"us": round(kms * 1e3, 2), "alg_bytes": alg,
+                          "gbs": round(alg / kms / 1e6, 2),
+                          "frac_hbm_peak": round(alg / kms / 1e6 / HBM_PEAK_GBS, 4)}
+    del sets
+    out["workload"] = "gs_family_nd6_llama3.1-8b_16x2048tok_512MiB"
+    out["byte_exact_sampled"] = True
+    return out
+
+
 def cpu_baseline(oracle, torch, data, R, budget_s=10.0):
     import numpy as np
     host = [np.ascontiguousarray(d.cpu().numpy().reshape(P_RDP - 1, R)) for d in data]
@@ -473,6 +575,7 @@ def main():
     ap.add_argument("--no-rs8", action="store_true")
     ap.add_argument("--no-paged", action="store_true")
     ap.add_argument("--no-chunked", action="store_true")
+    ap.add_argument("--no-gs", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run three 256 MiB device copies (reference kernel of known "
                          "size for HBM byte counters)")
@@ -548,6 +651,13 @@ def main():
         log(f"[bench] rs8: encode {rs8['encode_us']:.1f} us ({rs8['encode_gbs']:.0f} GB/s), "
             f"decode {rs8['decode_mean_us']:.1f} us ({rs8['decode_gbs']:.0f} GB/s)")
 
+    gs = None
+    if not args.no_gs:
+        log("[bench] gs family (reference codes, packed layouts) on the 512 MiB stream")
+        gs = bench_gs(pkg, torch, oracle, dev, args.seed, args.steps, args.warmup)
+        log(f"[bench] gs: P/Q {gs['star_diagonal_pq']['us']:.1f} us, XOR {gs['xor_encode']['us']:.1f} us, "
+            f"RS16 {gs['rs16_encode']['us']:.1f} us")
+
     if args.copy_calibration:
         src = torch.empty(1 << 28, dtype=torch.uint8, device=dev)
         dst = torch.empty_like(src)
@@ -595,6 +705,7 @@ def main():
         "rs8_gf256": rs8,
         "paged_gather_rdp_encode": fused,
         "chunked_fp8_rdp_rs": chunked,
+        "gs_family": gs,
     }
     print(json.dumps(out), flush=True)
 
