@@ -84,36 +84,81 @@ __global__ __launch_bounds__(kTB) void xor_reconstruct_kernel(const uint8_t* enc
 
 // ----------------------------------------------------------------- gs RDP P/Q
 // Words (u16).  P[c] = XOR_r D_r[c]; Qfull[d] = XOR_r D_r[(d - r) mod S].
-__global__ __launch_bounds__(kTB) void gs_rdp_parity_kernel(uint16_t* sh, int nd, int64_t S) {
+// Row r starts at byte r*S*2, so its tile is misaligned by mr bytes, and the
+// diagonal term of row r is the same row shifted by r words.  Each thread loads
+// one aligned 16-byte chunk of each row; the P window (offset mr) and the Q
+// window (offset mr - 2r) are byte funnels of that chunk and a neighbour's,
+// taken from the adjacent lane by a DPP wave shift (lanes at a wave edge load
+// the neighbouring chunk themselves).  Every load is bounded by the tensor,
+// whatever the shifts deliver.  Columns whose diagonal wraps (w < nd - 1) and
+// the row tail take a per-word path.
+//
+// The star skip: row r leaves its word at column star_r = (star_base + r) % S
+// (C remainder: negative means no skip) out of the diagonal it lies on,
+// d = star_r + r (mod S).  That word is the one at position d - w0 of the
+// thread's row-r diagonal window, so it is masked there.
+// x % S with C semantics (the sign of x), dividing only when x is outside [0, S).
+__device__ __forceinline__ int64_t cmod(int64_t x, int64_t S) {
+    return (x >= 0 && x < S) ? x : x % S;
+}
+
+__device__ __forceinline__ u32x4 drop_word(u32x4 v, int64_t k) {
+    if (k < 0 || k >= 8) return v;
+    const uint32_t m = (k & 1) ? 0x0000FFFFu : 0xFFFF0000u;
+    switch (k >> 1) {
+        case 0: v.x &= m; break;
+        case 1: v.y &= m; break;
+        case 2: v.z &= m; break;
+        default: v.w &= m; break;
+    }
+    return v;
+}
+
+__global__ __launch_bounds__(kTB) void gs_rdp_parity_kernel(uint16_t* sh, int nd, int64_t S,
+                                                            int star_base) {
     __shared__ __attribute__((aligned(16))) uint8_t tp[kTileBytes + 16];
     __shared__ __attribute__((aligned(16))) uint8_t tq[kTileBytes + 16];
     const uint8_t* base = reinterpret_cast<const uint8_t*>(sh);
+    const uint8_t* end = base + uint64_t(nd + 2) * uint64_t(S) * 2;
     const uint64_t Sb = uint64_t(S) * 2;
     const int64_t w0 = int64_t(blockIdx.x) * (kTileBytes / 2) + 8 * threadIdx.x;
     const uint64_t t0b = uint64_t(blockIdx.x) * kTileBytes;
     const uint32_t nbytes = uint32_t(Sb - t0b < uint64_t(kTileBytes) ? Sb - t0b : kTileBytes);
+    const uint32_t lane = threadIdx.x & 63;
+    const bool fast = w0 + 8 <= S && w0 >= nd - 1;
     u32x4 p = {0, 0, 0, 0}, q = {0, 0, 0, 0};
-    if (w0 + 8 <= S) {
-        for (int r = 0; r < nd; ++r) p ^= load_window16(base + (uint64_t(r) * S + w0) * 2);
-    } else if (w0 < S) {
-        for (int i = 0; i < int(S - w0); ++i) {
-            uint16_t a = 0;
-            for (int r = 0; r < nd; ++r) a ^= sh[uint64_t(r) * S + w0 + i];
-            p = set_byte(set_byte(p, 2 * i, uint8_t(a)), 2 * i + 1, uint8_t(a >> 8));
+    for (int r = 0; r < nd; ++r) {
+        const uint8_t* A0 = base + uint64_t(r) * Sb + t0b;
+        const uint32_t mr = uint32_t(reinterpret_cast<uintptr_t>(A0) & 15);
+        const uint8_t* my = A0 - mr + 16 * threadIdx.x;
+        const u32x4 z = {0, 0, 0, 0};
+        const u32x4 c0 = my < end ? ld16(my) : z;
+        // the shifts run with every lane active (a lane reading a disabled lane
+        // gets nothing); lanes at a wave edge then load their neighbour chunk
+        u32x4 c1 = from_next_lane(c0), cm = from_prev_lane(c0);
+        const int s = int(mr) - 2 * r;   // Q window offset in [-2(nd-1), 15]
+        if (lane == 63 && fast && (mr > 0 || s > 0)) c1 = ld16(my + 16);
+        if (lane == 0 && fast && s < 0) cm = ld16(my - 16);
+        if (fast) {
+            p ^= mr ? funnel16(c0, c1, mr) : c0;
+            const u32x4 qw = s > 0 ? funnel16(c0, c1, uint32_t(s))
+                                   : (s == 0 ? c0 : funnel16(cm, c0, uint32_t(s + 16)));
+            const int64_t star = cmod(int64_t(star_base) + r, S);
+            q ^= star < 0 ? qw : drop_word(qw, cmod(star + r, S) - w0);
         }
     }
-    if (w0 + 8 <= S && w0 >= nd - 1) {
-        for (int r = 0; r < nd; ++r) q ^= load_window16(base + (uint64_t(r) * S + w0 - r) * 2);
-    } else if (w0 < S) {
+    if (!fast && w0 < S) {
         const int n = int(S - w0 < 8 ? S - w0 : 8);
         for (int i = 0; i < n; ++i) {
-            uint16_t a = 0;
+            uint16_t a = 0, b = 0;
             for (int r = 0; r < nd; ++r) {
+                a ^= sh[uint64_t(r) * S + w0 + i];
                 int64_t c = (w0 + i - r) % S;
                 if (c < 0) c += S;
-                a ^= sh[uint64_t(r) * S + c];
+                if (c != cmod(int64_t(star_base) + r, S)) b ^= sh[uint64_t(r) * S + c];
             }
-            q = set_byte(set_byte(q, 2 * i, uint8_t(a)), 2 * i + 1, uint8_t(a >> 8));
+            p = set_byte(set_byte(p, 2 * i, uint8_t(a)), 2 * i + 1, uint8_t(a >> 8));
+            q = set_byte(set_byte(q, 2 * i, uint8_t(b)), 2 * i + 1, uint8_t(b >> 8));
         }
     }
     *reinterpret_cast<u32x4*>(tp + 16 * threadIdx.x) = p;
@@ -122,20 +167,6 @@ __global__ __launch_bounds__(kTB) void gs_rdp_parity_kernel(uint16_t* sh, int nd
     uint8_t* out = reinterpret_cast<uint8_t*>(sh);
     tile_store(out + uint64_t(nd) * Sb + t0b, tp, nbytes);
     tile_store(out + uint64_t(nd + 1) * Sb + t0b, tq, nbytes);
-}
-
-// Remove each row's star word from its diagonal: the reference skips column
-// (star_base + r) % S of row r (C remainder: negative means no skip).  One
-// thread, rows in order, so coinciding diagonals compose exactly.
-__global__ void gs_rdp_star_fixup_kernel(uint16_t* sh, int nd, int64_t S, int star_base) {
-    if (threadIdx.x != 0 || blockIdx.x != 0) return;
-    uint16_t* Q = sh + uint64_t(nd + 1) * S;
-    for (int r = 0; r < nd; ++r) {
-        const int64_t star = (int64_t(star_base) + r) % S;
-        if (star < 0) continue;
-        const int64_t d = (star + r) % S;
-        Q[d] ^= sh[uint64_t(r) * S + star];
-    }
 }
 
 // ----------------------------------------------------------------- host side
@@ -158,10 +189,7 @@ static int gs_rdp_parity(uint16_t* sh, int nd, int64_t S, int star_base, hipStre
                          const char* what) {
     if (nd <= 0 || S <= 0) return KVEC_OK;  // the reference kernel returns at once
     hipLaunchKernelGGL(gs_rdp_parity_kernel, dim3(blocks_for(S * 2, kTileBytes)), dim3(kTB), 0, st, sh,
-                       nd, S);
-    int rc = check_launch(what);
-    if (rc) return rc;
-    hipLaunchKernelGGL(gs_rdp_star_fixup_kernel, dim3(1), dim3(64), 0, st, sh, nd, S, star_base);
+                       nd, S, star_base);
     return check_launch(what);
 }
 

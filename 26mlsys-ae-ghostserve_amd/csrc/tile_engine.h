@@ -32,6 +32,22 @@ __device__ __forceinline__ u32x4 funnel16(u32x4 a, u32x4 b, uint32_t sh) {
                  __builtin_amdgcn_alignbyte(s3, s2, r), __builtin_amdgcn_alignbyte(s4, s3, r)};
 }
 
+// Wave-wide lane shifts (DPP wave_shl:1 / wave_shr:1, one VALU op per dword):
+// from_next_lane gives lane i the value of lane i+1 (lane 63 gets 0),
+// from_prev_lane gives lane i the value of lane i-1 (lane 0 gets 0).
+__device__ __forceinline__ u32x4 from_next_lane(u32x4 v) {
+    return u32x4{uint32_t(__builtin_amdgcn_update_dpp(0, int(v.x), 0x130, 0xF, 0xF, false)),
+                 uint32_t(__builtin_amdgcn_update_dpp(0, int(v.y), 0x130, 0xF, 0xF, false)),
+                 uint32_t(__builtin_amdgcn_update_dpp(0, int(v.z), 0x130, 0xF, 0xF, false)),
+                 uint32_t(__builtin_amdgcn_update_dpp(0, int(v.w), 0x130, 0xF, 0xF, false))};
+}
+__device__ __forceinline__ u32x4 from_prev_lane(u32x4 v) {
+    return u32x4{uint32_t(__builtin_amdgcn_update_dpp(0, int(v.x), 0x138, 0xF, 0xF, false)),
+                 uint32_t(__builtin_amdgcn_update_dpp(0, int(v.y), 0x138, 0xF, 0xF, false)),
+                 uint32_t(__builtin_amdgcn_update_dpp(0, int(v.z), 0x138, 0xF, 0xF, false)),
+                 uint32_t(__builtin_amdgcn_update_dpp(0, int(v.w), 0x138, 0xF, 0xF, false))};
+}
+
 // 16 bytes at any address.  The caller guarantees the 16 bytes belong to the
 // tensor; the aligned chunks read around them then hold at least one of its
 // bytes each and cannot cross into an unmapped page.
