@@ -1,26 +1,33 @@
 // gs_rs16.hip -- the reference's Reed-Solomon code over GF(2^16), bit-exact
 // (benchmark/rs/kernel.cu:16-222), on its packed [(k+m), S] u16 tensors.
 //
-// Multiplication uses the caller's log/exp tables exactly as the reference's
-// gf_mul does, but only to build per-block lookup tables: for a constant c,
-// x*c = T_lo[x & 0xFF] ^ T_hi[x >> 8] with T_lo[v] = gf_mul(v, c) and
-// T_hi[v] = gf_mul(v << 8, c) (the field product is GF(2)-bilinear), so the
-// streaming loop does two LDS lookups per symbol and coefficient instead of
-// three dependent global-table gathers.
+// Multiplication by a constant c is GF(2)-linear in the symbol x.  Each block
+// asks the caller's log/exp tables (exactly the reference's gf_mul) only for
+// the sixteen basis products c * 2^b, and builds from them, by linearity, four
+// byte-to-byte maps per coefficient:
+//     x * c = (lo(x) -> lo, hi(x) -> lo) in the low byte, (lo -> hi, hi -> hi) in the high byte.
+// Each byte map is applied with the 3/3/2-bit field split of the GF(2^8)
+// kernels: three v_perm_b32 byte-permutes of 8-entry tables, four bytes at a
+// time.  The streaming loop therefore holds words byte-transposed: one
+// register carries the low bytes of four words and one the high bytes, so a
+// coefficient costs 12 v_perm_b32 per four words and no memory lookup.
 //
 // Reconstruction folds the reference's two steps (right-hand side b, then
 // x = V^-1 b) into one coefficient per (output, input) pair: exact in the
 // field, so the bytes are those of the two-step computation.  The inverse is
 // computed per block with the reference's Gauss-Jordan (pivot order and
 // zero-pivot skip included), from indices read on the device.
+#include "gf8.h"
 #include "tile_engine.h"
 
 namespace kvec {
 
 constexpr int kGfOrder = 65535;
 constexpr int kRsMaxM = 16;           // reference limit (benchmark/rs/kernel.cu:118)
-constexpr int kRsMaxTables = 48;      // coefficient tables held in LDS (48 KiB)
-constexpr int kRsGrid = 2048;         // persistent blocks: tables are built once per block
+constexpr int kRsMaxTables = 48;      // coefficients held in LDS
+constexpr int kRs16Tab = 24;          // dwords per coefficient: 4 byte maps x 6
+constexpr int kRsGroup = 2;           // outputs accumulated per pass over the inputs
+constexpr int kRsGrid = 1024;         // persistent blocks (4 per CU): tables are built once per block
 
 __device__ __forceinline__ uint16_t gf16_mul_tab(uint16_t a, uint16_t b, const uint16_t* ex,
                                                  const uint16_t* lg) {
@@ -45,81 +52,228 @@ struct RsJob {
     int64_t S;                              // words per row
 };
 
-// Products of the input symbols with the coefficient table set `tab`
-// ([nout][nin][2][256] u16 in LDS) for 8 logical words of output o.
-__device__ __forceinline__ u32x4 rs_mix_window(const RsJob& j, const uint16_t* tab, int o,
-                                               int64_t w0) {
-    uint32_t acc[4] = {0, 0, 0, 0};
-    for (int i = 0; i < j.nin; ++i) {
-        const u32x4 x = load_window16(reinterpret_cast<const uint8_t*>(j.in_rows[i] + w0));
-        const uint16_t* tl = tab + (size_t(o) * j.nin + i) * 512;
-        const uint16_t* th = tl + 256;
-        const uint32_t xs[4] = {x.x, x.y, x.z, x.w};
-#pragma unroll
+// Byte maps of coefficient t, ptab[t][24]: dwords 0-5 lo->lo, 6-11 hi->lo,
+// 12-17 lo->hi, 18-23 hi->hi; within a map, the two dwords of field f (bits
+// 3f.. of the source byte) hold the images of the field values 0-3 and 4-7.
+// All threads call it.
+__device__ __forceinline__ void rs_build_perm_tables(uint32_t (*ptab)[kRs16Tab], uint16_t (*basis)[16],
+                                     const uint16_t* coef, int ncoef, const uint16_t* ex,
+                                     const uint16_t* lg) {
+    for (int e = threadIdx.x; e < ncoef * 16; e += kTB)
+        basis[e >> 4][e & 15] = gf16_mul_tab(uint16_t(1u << (e & 15)), coef[e >> 4], ex, lg);
+    __syncthreads();
+    for (int e = threadIdx.x; e < ncoef * kRs16Tab; e += kTB) {
+        const int t = e / kRs16Tab, d = e % kRs16Tab;
+        const int map = d / 6, f = (d % 6) >> 1, half = d & 1;
+        const int src = map & 1, dst = map >> 1;   // 0 = low byte, 1 = high byte
+        uint32_t dw = 0;
         for (int q = 0; q < 4; ++q) {
-            const uint32_t v = xs[q];
-            const uint32_t lo = tl[v & 0xFF] ^ th[(v >> 8) & 0xFF];
-            const uint32_t hi = tl[(v >> 16) & 0xFF] ^ th[v >> 24];
-            acc[q] ^= lo | (hi << 16);
+            const int v = half * 4 + q;
+            if (f == 2 && v >= 4) continue;
+            const uint32_t x = uint32_t(v) << (3 * f);   // source byte value
+            uint32_t y = 0;
+            for (int b = 0; b < 8; ++b)
+                if (x & (1u << b)) y ^= basis[t][b + 8 * src];
+            dw |= ((y >> (8 * dst)) & 0xFFu) << (8 * q);
+        }
+        ptab[t][d] = dw;
+    }
+}
+
+// Four words' low bytes into one register and their high bytes into another:
+// b[0], b[1] for words 0-3 of the window, b[2], b[3] for words 4-7.
+__device__ __forceinline__ void split_bytes(u32x4 x, uint32_t b[4]) {
+    b[0] = __builtin_amdgcn_perm(x.y, x.x, 0x06040200u);
+    b[1] = __builtin_amdgcn_perm(x.y, x.x, 0x07050301u);
+    b[2] = __builtin_amdgcn_perm(x.w, x.z, 0x06040200u);
+    b[3] = __builtin_amdgcn_perm(x.w, x.z, 0x07050301u);
+}
+
+__device__ __forceinline__ u32x4 join_bytes(const uint32_t a[4]) {
+    return u32x4{__builtin_amdgcn_perm(a[1], a[0], 0x05010400u),
+                 __builtin_amdgcn_perm(a[1], a[0], 0x07030602u),
+                 __builtin_amdgcn_perm(a[3], a[2], 0x05010400u),
+                 __builtin_amdgcn_perm(a[3], a[2], 0x07030602u)};
+}
+
+// acc ^ map_a(bytes of fa) ^ map_b(bytes of fb): six v_perm_b32, three 3-input XORs.
+__device__ __forceinline__ uint32_t gf16_fma2(uint32_t acc, const Gf8Fields& fa, const uint32_t* ta,
+                                              const Gf8Fields& fb, const uint32_t* tb) {
+    const uint32_t p0 = __builtin_amdgcn_perm(ta[1], ta[0], fa.f0);
+    const uint32_t p1 = __builtin_amdgcn_perm(ta[3], ta[2], fa.f1);
+    const uint32_t p2 = __builtin_amdgcn_perm(ta[5], ta[4], fa.f2);
+    const uint32_t p3 = __builtin_amdgcn_perm(tb[1], tb[0], fb.f0);
+    const uint32_t p4 = __builtin_amdgcn_perm(tb[3], tb[2], fb.f1);
+    const uint32_t p5 = __builtin_amdgcn_perm(tb[5], tb[4], fb.f2);
+    return xor3(xor3(xor3(acc, p0, p1), p2, p3), p4, p5);
+}
+
+// Words w0 .. w0+7 of a row, zero past its end S.
+__device__ __forceinline__ u32x4 rs_window(const uint16_t* row, int64_t w0, int64_t S) {
+    if (w0 + 8 <= S) return load_window16(reinterpret_cast<const uint8_t*>(row + w0));
+    const gptr<const uint16_t> r = as_global(row) + (w0 < S ? w0 : 0);
+    const int nq = w0 < S ? int(S - w0) : 0;   // < 8 here
+    uint32_t v[4] = {0, 0, 0, 0};
+    for (int q = 0; q < nq; ++q) v[q >> 1] |= uint32_t(r[q]) << (16 * (q & 1));
+    return u32x4{v[0], v[1], v[2], v[3]};
+}
+
+// A row seen from one tile: the 16-byte-aligned address below the tile's
+// first byte and the row's misalignment, both wave-uniform.
+struct RowWin {
+    const uint8_t* al;
+    uint32_t sh;
+};
+
+__device__ __forceinline__ RowWin row_win(const uint16_t* row, uint64_t t0b) {
+    const uint8_t* p = wave_uniform(reinterpret_cast<const uint8_t*>(row)) + t0b;
+    const uint32_t sh = uint32_t(reinterpret_cast<uintptr_t>(p) & 15);
+    return RowWin{p - sh, sh};
+}
+
+// The 16 bytes at tile offset `off` (a multiple of 16) of a tile that lies
+// wholly inside the row: one aligned load, two when the row is misaligned (the
+// second chunk then holds at least one byte of the row).
+__device__ __forceinline__ u32x4 win_load(const RowWin& r, uint32_t off) {
+    const u32x4 lo = ld16(r.al + off);
+    if (r.sh == 0) return lo;
+    return funnel16(lo, ld16(r.al + off + 16), r.sh);
+}
+
+// Fold input i's NW windows x[] into outputs og .. og+G-1: acc[n][g] holds
+// them byte-transposed (split_bytes order).  Each coefficient's tables are
+// read from LDS once and applied to all NW windows.
+template <int G, int NW>
+__device__ __forceinline__ void rs_mix_input(const uint32_t (*ptab)[kRs16Tab], int og, int nin,
+                                             int i, const u32x4* x, uint32_t (*acc)[kRsGroup][4]) {
+    Gf8Fields f[NW][4];
+#pragma unroll
+    for (int n = 0; n < NW; ++n) {
+        uint32_t by[4];
+        split_bytes(x[n], by);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) f[n][q] = gf8_fields(by[q]);
+    }
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+        const uint32_t* T = ptab[(og + g) * nin + i];
+#pragma unroll
+        for (int n = 0; n < NW; ++n) {
+            acc[n][g][0] = gf16_fma2(acc[n][g][0], f[n][0], T + 0, f[n][1], T + 6);
+            acc[n][g][1] = gf16_fma2(acc[n][g][1], f[n][0], T + 12, f[n][1], T + 18);
+            acc[n][g][2] = gf16_fma2(acc[n][g][2], f[n][2], T + 0, f[n][3], T + 6);
+            acc[n][g][3] = gf16_fma2(acc[n][g][3], f[n][2], T + 12, f[n][3], T + 18);
         }
     }
-    return u32x4{acc[0], acc[1], acc[2], acc[3]};
 }
 
-__device__ __forceinline__ uint16_t rs_mix_word(const RsJob& j, const uint16_t* tab, int o,
-                                                int64_t w) {
-    uint16_t a = 0;
-    for (int i = 0; i < j.nin; ++i) {
-        const uint16_t x = j.in_rows[i][w];
-        const uint16_t* tl = tab + (size_t(o) * j.nin + i) * 512;
-        a ^= tl[x & 0xFF] ^ tl[256 + (x >> 8)];
+template <int G, int NW>
+__device__ __forceinline__ void rs_zero(uint32_t (*acc)[kRsGroup][4]) {
+#pragma unroll
+    for (int n = 0; n < NW; ++n)
+#pragma unroll
+        for (int g = 0; g < G; ++g) acc[n][g][0] = acc[n][g][1] = acc[n][g][2] = acc[n][g][3] = 0;
+}
+
+// A tile wholly inside the rows, software pipelined over the inputs: input
+// i+1's aligned chunks are in flight while input i is folded in.
+template <int G, int NW>
+__device__ __forceinline__ void rs_mix_full(const RsJob& j, const uint32_t (*ptab)[kRs16Tab],
+                                            int og, uint64_t t0b, uint32_t (*acc)[kRsGroup][4]) {
+    rs_zero<G, NW>(acc);
+    const int nin = j.nin;
+    u32x4 lo[NW], hi[NW];
+    RowWin rw = row_win(j.in_rows[0], t0b);
+#pragma unroll
+    for (int n = 0; n < NW; ++n) {
+        const uint32_t off = 16 * (threadIdx.x + n * kTB);
+        lo[n] = ld16(rw.al + off);
+        hi[n] = rw.sh ? ld16(rw.al + off + 16) : lo[n];
     }
-    return a;
-}
-
-// Stream every tile of the job through the tables already in LDS.
-__device__ void rs_run_tiles(const RsJob& j, const uint16_t* tab, uint8_t* tile) {
-    const uint64_t Sb = uint64_t(j.S) * 2;
-    const uint64_t ntiles = (Sb + kTileBytes - 1) / kTileBytes;
-    for (uint64_t tt = blockIdx.x; tt < ntiles; tt += gridDim.x) {
-        const uint64_t t0b = tt * kTileBytes;
-        const uint32_t nbytes = uint32_t(Sb - t0b < uint64_t(kTileBytes) ? Sb - t0b : kTileBytes);
-        const int64_t w0 = int64_t(t0b / 2) + 8 * threadIdx.x;
-        for (int o = 0; o < j.nout; ++o) {
-            u32x4 acc = {0, 0, 0, 0};
-            if (w0 + 8 <= j.S) {
-                acc = rs_mix_window(j, tab, o, w0);
-            } else if (w0 < j.S) {
-                for (int q = 0; q < int(j.S - w0); ++q) {
-                    const uint16_t a = rs_mix_word(j, tab, o, w0 + q);
-                    acc = set_byte(set_byte(acc, 2 * q, uint8_t(a)), 2 * q + 1, uint8_t(a >> 8));
-                }
+    for (int i = 0; i < nin; ++i) {
+        u32x4 x[NW];
+#pragma unroll
+        for (int n = 0; n < NW; ++n) x[n] = rw.sh ? funnel16(lo[n], hi[n], rw.sh) : lo[n];
+        if (i + 1 < nin) {
+            rw = row_win(j.in_rows[i + 1], t0b);
+#pragma unroll
+            for (int n = 0; n < NW; ++n) {
+                const uint32_t off = 16 * (threadIdx.x + n * kTB);
+                lo[n] = ld16(rw.al + off);
+                hi[n] = rw.sh ? ld16(rw.al + off + 16) : lo[n];
             }
-            *reinterpret_cast<u32x4*>(tile + 16 * threadIdx.x) = acc;
-            __syncthreads();
-            tile_store(reinterpret_cast<uint8_t*>(j.out_rows[o]) + t0b, tile, nbytes);
-            __syncthreads();
         }
+        rs_mix_input<G, NW>(ptab, og, nin, i, x, acc);
     }
 }
 
-// Fill the [nout][nin] byte-split tables for coefficient matrix `coef` (LDS).
-__device__ void rs_build_tables(uint16_t* tab, const uint16_t* coef, int nout, int nin,
-                                const uint16_t* ex, const uint16_t* lg) {
-    const int n = nout * nin * 512;
-    for (int e = threadIdx.x; e < n; e += kTB) {
-        const int t = e >> 9, half = (e >> 8) & 1, v = e & 0xFF;
-        const uint16_t x = half ? uint16_t(v << 8) : uint16_t(v);
-        tab[e] = gf16_mul_tab(x, coef[t], ex, lg);
+// The last, partial tile: word loads guarded by the row length.
+template <int G, int NW>
+__device__ __forceinline__ void rs_mix_tail(const RsJob& j, const uint32_t (*ptab)[kRs16Tab],
+                                            int og, const int64_t* w0,
+                                            uint32_t (*acc)[kRsGroup][4]) {
+    rs_zero<G, NW>(acc);
+    for (int i = 0; i < j.nin; ++i) {
+        u32x4 x[NW];
+#pragma unroll
+        for (int n = 0; n < NW; ++n) x[n] = rs_window(j.in_rows[i], w0[n], j.S);
+        rs_mix_input<G, NW>(ptab, og, j.nin, i, x, acc);
+    }
+}
+
+constexpr int kRsNW = 2;                              // windows per thread
+constexpr uint32_t kRsTile = kTileBytes * kRsNW;      // logical bytes per row per tile
+constexpr uint32_t kRsStage = kRsTile + 16;           // LDS staging row
+
+// Stream every tile of the job through the tables already in LDS; `tile`
+// holds kRsGroup staging rows of kRsStage bytes.  Window n of thread t covers
+// logical bytes 16 (t + n kTB) .. +15 of the tile, so each window's loads are
+// contiguous across the block.
+__device__ __forceinline__ void rs_run_tiles(const RsJob& j, const uint32_t (*ptab)[kRs16Tab],
+                                             uint8_t* tile) {
+    const uint64_t Sb = uint64_t(j.S) * 2;
+    const uint64_t ntiles = (Sb + kRsTile - 1) / kRsTile;
+    for (uint64_t tt = blockIdx.x; tt < ntiles; tt += gridDim.x) {
+        const uint64_t t0b = tt * kRsTile;
+        const uint32_t nbytes = uint32_t(Sb - t0b < uint64_t(kRsTile) ? Sb - t0b : kRsTile);
+        int64_t w0[kRsNW];
+#pragma unroll
+        for (int n = 0; n < kRsNW; ++n) w0[n] = int64_t(t0b / 2) + 8 * (threadIdx.x + n * kTB);
+        for (int og = 0; og < j.nout; og += kRsGroup) {
+            const int G = j.nout - og < kRsGroup ? j.nout - og : kRsGroup;
+            uint32_t acc[kRsNW][kRsGroup][4];
+            static_assert(kRsGroup == 2, "one instantiation per group size");
+            if (nbytes == kRsTile) {
+                if (G == 1) rs_mix_full<1, kRsNW>(j, ptab, og, t0b, acc);
+                else rs_mix_full<2, kRsNW>(j, ptab, og, t0b, acc);
+            } else if (w0[0] < j.S) {
+                if (G == 1) rs_mix_tail<1, kRsNW>(j, ptab, og, w0, acc);
+                else rs_mix_tail<2, kRsNW>(j, ptab, og, w0, acc);
+            } else {
+                for (int n = 0; n < kRsNW; ++n)
+                    for (int g = 0; g < kRsGroup; ++g)
+                        acc[n][g][0] = acc[n][g][1] = acc[n][g][2] = acc[n][g][3] = 0;
+            }
+            for (int g = 0; g < G; ++g)
+                for (int n = 0; n < kRsNW; ++n)
+                    *reinterpret_cast<u32x4*>(tile + g * kRsStage + 16 * (threadIdx.x + n * kTB)) =
+                        join_bytes(acc[n][g]);
+            __syncthreads();
+            for (int g = 0; g < G; ++g)
+                tile_store(reinterpret_cast<uint8_t*>(j.out_rows[og + g]) + t0b, tile + g * kRsStage,
+                           nbytes);
+            __syncthreads();
+        }
     }
 }
 
 // benchmark/rs/kernel.cu:67-102 parity: Par_p = XOR_i D_i * alpha^((p+1) i mod 65535).
-__global__ __launch_bounds__(kTB) void rs16_encode_kernel(RsJob job, const uint16_t* ex,
+__global__ __launch_bounds__(kTB) __attribute__((amdgpu_waves_per_eu(4))) void rs16_encode_kernel(RsJob job, const uint16_t* ex,
                                                           const uint16_t* lg) {
-    __shared__ __attribute__((aligned(16))) uint16_t tab[kRsMaxTables * 512];
+    __shared__ __attribute__((aligned(16))) uint32_t ptab[kRsMaxTables][kRs16Tab];
+    __shared__ uint16_t basis[kRsMaxTables][16];
     __shared__ uint16_t coef[kRsMaxTables];
-    __shared__ __attribute__((aligned(16))) uint8_t tile[kTileBytes + 16];
+    __shared__ __attribute__((aligned(16))) uint8_t tile[kRsGroup * kRsStage];
     __shared__ RsJob j;
     if (threadIdx.x == 0) j = job;
     __syncthreads();
@@ -128,26 +282,27 @@ __global__ __launch_bounds__(kTB) void rs16_encode_kernel(RsJob job, const uint1
         coef[t] = ex[((p + 1) * i) % kGfOrder];
     }
     __syncthreads();
-    rs_build_tables(tab, coef, j.nout, j.nin, ex, lg);
+    rs_build_perm_tables(ptab, basis, coef, j.nout * j.nin, ex, lg);
     __syncthreads();
-    rs_run_tiles(j, tab, tile);
+    rs_run_tiles(j, ptab, tile);
 }
 
 // benchmark/rs/kernel.cu:105-222 with the right-hand side folded into the
 // coefficients.  Inputs: the k - m surviving data rows, then the m parity rows
 // of parity_used; outputs: the m missing data rows.
-__global__ __launch_bounds__(kTB) void rs16_reconstruct_kernel(uint16_t* sh, int64_t S, int k,
+__global__ __launch_bounds__(kTB) __attribute__((amdgpu_waves_per_eu(4))) void rs16_reconstruct_kernel(uint16_t* sh, int64_t S, int k,
                                                                int mpar, int m,
                                                                const int32_t* missing,
                                                                const int32_t* pused,
                                                                const uint16_t* ex,
                                                                const uint16_t* lg) {
-    __shared__ __attribute__((aligned(16))) uint16_t tab[kRsMaxTables * 512];
+    __shared__ __attribute__((aligned(16))) uint32_t ptab[kRsMaxTables][kRs16Tab];
+    __shared__ uint16_t basis[kRsMaxTables][16];
     __shared__ uint16_t coef[kRsMaxTables];
     __shared__ uint16_t inv[kRsMaxM * kRsMaxM];
     __shared__ int s_miss[kRsMaxM], s_pu[kRsMaxM];
     __shared__ int s_ok;
-    __shared__ __attribute__((aligned(16))) uint8_t tile[kTileBytes + 16];
+    __shared__ __attribute__((aligned(16))) uint8_t tile[kRsGroup * kRsStage];
     __shared__ RsJob j;
     if (threadIdx.x < m) {
         s_miss[threadIdx.x] = missing[threadIdx.x];
@@ -240,13 +395,13 @@ __global__ __launch_bounds__(kTB) void rs16_reconstruct_kernel(uint16_t* sh, int
         coef[t] = v;
     }
     __syncthreads();
-    rs_build_tables(tab, coef, m, nin, ex, lg);
+    rs_build_perm_tables(ptab, basis, coef, m * nin, ex, lg);
     __syncthreads();
-    rs_run_tiles(j, tab, tile);
+    rs_run_tiles(j, ptab, tile);
 }
 
 static int rs_grid(int64_t S) {
-    const int64_t tiles = (S * 2 + kTileBytes - 1) / kTileBytes;
+    const int64_t tiles = (S * 2 + kRsTile - 1) / kRsTile;
     return int(tiles < kRsGrid ? tiles : kRsGrid);
 }
 

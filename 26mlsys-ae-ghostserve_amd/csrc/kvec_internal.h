@@ -28,12 +28,23 @@ __device__ __forceinline__ u32x4 ld_stream(const uint8_t* base, uint64_t off) {
 __device__ __forceinline__ void st_stream(uint8_t* base, uint64_t off, u32x4 v) {
     __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(base + off));
 }
+// Global-memory views of a generic pointer.  Row pointers that a kernel reads
+// out of LDS or a table have no provable address space, and generic (flat)
+// accesses count against both the memory and the LDS wait counters, so a wait
+// for an LDS read would also wait for every load in flight.
+template <class T>
+using gptr = __attribute__((address_space(1))) T*;
+template <class T>
+__device__ __forceinline__ gptr<T> as_global(T* p) {
+    return (gptr<T>)p;
+}
+
 // Ordinary (cached) 16-byte load, for data that neighbouring lanes re-read.
 __device__ __forceinline__ u32x4 ld16(const uint8_t* p) {
-    return *reinterpret_cast<const u32x4*>(p);
+    return *as_global(reinterpret_cast<const u32x4*>(p));
 }
 __device__ __forceinline__ void st16(uint8_t* p, u32x4 v) {
-    *reinterpret_cast<u32x4*>(p) = v;
+    *as_global(reinterpret_cast<u32x4*>(p)) = v;
 }
 
 // Three-input XOR in one VALU op (v_bitop3_b32 with truth table 0x96); the

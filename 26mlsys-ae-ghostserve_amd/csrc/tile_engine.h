@@ -48,6 +48,17 @@ __device__ __forceinline__ u32x4 from_prev_lane(u32x4 v) {
                  uint32_t(__builtin_amdgcn_update_dpp(0, int(v.w), 0x138, 0xF, 0xF, false))};
 }
 
+// A pointer that every lane holds the same value of, moved to scalar
+// registers: offsets and shifts derived from it are then wave-uniform, so a
+// switch on them is a scalar branch rather than per-lane selects.
+template <class T>
+__device__ __forceinline__ T* wave_uniform(T* p) {
+    const uint64_t v = reinterpret_cast<uint64_t>(p);
+    const uint32_t lo = uint32_t(__builtin_amdgcn_readfirstlane(int(uint32_t(v))));
+    const uint32_t hi = uint32_t(__builtin_amdgcn_readfirstlane(int(uint32_t(v >> 32))));
+    return reinterpret_cast<T*>((uint64_t(hi) << 32) | lo);
+}
+
 // 16 bytes at any address.  The caller guarantees the 16 bytes belong to the
 // tensor; the aligned chunks read around them then hold at least one of its
 // bytes each and cannot cross into an unmapped page.
@@ -76,27 +87,31 @@ __device__ __forceinline__ u32x4 set_byte(u32x4 v, int i, uint8_t b) {
 // Write logical bytes [0, nbytes) of the LDS tile `t` (16-byte aligned, with 16
 // bytes of slack after nbytes) to dst, any alignment.  All threads call it.
 __device__ __forceinline__ void tile_store(uint8_t* dst, const uint8_t* t, uint32_t nbytes) {
+    dst = wave_uniform(dst);
+    nbytes = uint32_t(__builtin_amdgcn_readfirstlane(int(nbytes)));
     const uintptr_t D0 = reinterpret_cast<uintptr_t>(dst);
     const uintptr_t E = D0 + nbytes;
     const uintptr_t A0 = (D0 + 15) & ~uintptr_t(15);
     const uintptr_t A1 = E & ~uintptr_t(15);
     if (A0 < A1) {
         const uint32_t delta = uint32_t(A0 - D0);
+        const uint32_t dsh = delta & 15, dal = delta - dsh;   // uniform
         const uint32_t nch = uint32_t((A1 - A0) >> 4);
         for (uint32_t k = threadIdx.x; k < nch; k += kTB) {
-            const uint32_t so = delta + 16 * k;
-            const uint32_t al = so & ~15u;
+            const uint32_t al = dal + 16 * k;
             u32x4 v = *reinterpret_cast<const u32x4*>(t + al);
-            if (so != al) v = funnel16(v, *reinterpret_cast<const u32x4*>(t + al + 16), so - al);
-            *reinterpret_cast<u32x4*>(A0 + 16 * uintptr_t(k)) = v;
+            if (dsh) v = funnel16(v, *reinterpret_cast<const u32x4*>(t + al + 16), dsh);
+            st16(reinterpret_cast<uint8_t*>(A0 + 16 * uintptr_t(k)), v);
         }
         // head [D0, A0) and tail [A1, E): at most 15 bytes each
         const uint32_t nh = uint32_t(A0 - D0), nt = uint32_t(E - A1);
         const uint32_t i = threadIdx.x;
-        if (i < nh) dst[i] = t[i];
-        else if (i >= 16 && i - 16 < nt) dst[(A1 - D0) + (i - 16)] = t[(A1 - D0) + (i - 16)];
+        const gptr<uint8_t> g = as_global(dst);
+        if (i < nh) g[i] = t[i];
+        else if (i >= 16 && i - 16 < nt) g[(A1 - D0) + (i - 16)] = t[(A1 - D0) + (i - 16)];
     } else {
-        for (uint32_t i = threadIdx.x; i < nbytes; i += kTB) dst[i] = t[i];
+        const gptr<uint8_t> g = as_global(dst);
+        for (uint32_t i = threadIdx.x; i < nbytes; i += kTB) g[i] = t[i];
     }
 }
 

@@ -183,7 +183,8 @@ def test_gs_pack_row(pkg, ora, gpu):
 
 # ------------------------------------------------------------------ gs RS16
 @pytest.mark.parametrize("k,m,S", [(8, 2, 4096), (6, 2, 44741), (5, 3, 1000), (4, 1, 3),
-                                   (8, 0, 100), (10, 4, 2049), (1, 1, 77), (16, 3, 8)])
+                                   (8, 0, 100), (10, 4, 2049), (1, 1, 77), (16, 3, 8),
+                                   (6, 7, 1001), (3, 16, 513), (48, 1, 300)])
 def test_rs16_encode_matches_oracle(pkg, ora, gpu, k, m, S):
     ex, lg = ora.gf16_tables()
     rng = np.random.default_rng(k * 100 + m)
@@ -196,7 +197,7 @@ def test_rs16_encode_matches_oracle(pkg, ora, gpu, k, m, S):
     assert np.array_equal(host(shards), want)
 
 
-@pytest.mark.parametrize("k,m,S", [(8, 2, 4099), (6, 3, 1000), (5, 3, 9)])
+@pytest.mark.parametrize("k,m,S", [(8, 2, 4099), (6, 3, 1000), (5, 3, 9), (9, 5, 2051)])
 def test_rs16_reconstruct_matches_oracle(pkg, ora, gpu, k, m, S):
     ex, lg = ora.gf16_tables()
     rng = np.random.default_rng(S)
