@@ -50,6 +50,7 @@ struct RsJob {
     uint16_t* out_rows[kRsMaxM];            // output rows
     int nin, nout;
     int64_t S;                              // words per row
+    FlatCopy copy;                          // data rows -> shard rows (encode), or none
 };
 
 // Byte maps of coefficient t, ptab[t][24]: dwords 0-5 lo->lo, 6-11 hi->lo,
@@ -118,28 +119,6 @@ __device__ __forceinline__ u32x4 rs_window(const uint16_t* row, int64_t w0, int6
     return u32x4{v[0], v[1], v[2], v[3]};
 }
 
-// A row seen from one tile: the 16-byte-aligned address below the tile's
-// first byte and the row's misalignment, both wave-uniform.
-struct RowWin {
-    const uint8_t* al;
-    uint32_t sh;
-};
-
-__device__ __forceinline__ RowWin row_win(const uint16_t* row, uint64_t t0b) {
-    const uint8_t* p = wave_uniform(reinterpret_cast<const uint8_t*>(row)) + t0b;
-    const uint32_t sh = uint32_t(reinterpret_cast<uintptr_t>(p) & 15);
-    return RowWin{p - sh, sh};
-}
-
-// The 16 bytes at tile offset `off` (a multiple of 16) of a tile that lies
-// wholly inside the row: one aligned load, two when the row is misaligned (the
-// second chunk then holds at least one byte of the row).
-__device__ __forceinline__ u32x4 win_load(const RowWin& r, uint32_t off) {
-    const u32x4 lo = ld16(r.al + off);
-    if (r.sh == 0) return lo;
-    return funnel16(lo, ld16(r.al + off + 16), r.sh);
-}
-
 // Fold input i's NW windows x[] into outputs og .. og+G-1: acc[n][g] holds
 // them byte-transposed (split_bytes order).  Each coefficient's tables are
 // read from LDS once and applied to all NW windows.
@@ -177,31 +156,29 @@ __device__ __forceinline__ void rs_zero(uint32_t (*acc)[kRsGroup][4]) {
 
 // A tile wholly inside the rows, software pipelined over the inputs: input
 // i+1's aligned chunks are in flight while input i is folded in.
+// With `copy`, the loaded chunks of every input also go to the copy's
+// destination (the data rows of an encode are the inputs, in order).
 template <int G, int NW>
 __device__ __forceinline__ void rs_mix_full(const RsJob& j, const uint32_t (*ptab)[kRs16Tab],
-                                            int og, uint64_t t0b, uint32_t (*acc)[kRsGroup][4]) {
+                                            int og, uint64_t t0b, bool copy,
+                                            uint32_t (*acc)[kRsGroup][4]) {
     rs_zero<G, NW>(acc);
     const int nin = j.nin;
     u32x4 lo[NW], hi[NW];
-    RowWin rw = row_win(j.in_rows[0], t0b);
+    RowWin rw = row_win(reinterpret_cast<const uint8_t*>(j.in_rows[0]) + t0b);
 #pragma unroll
-    for (int n = 0; n < NW; ++n) {
-        const uint32_t off = 16 * (threadIdx.x + n * kTB);
-        lo[n] = ld16(rw.al + off);
-        hi[n] = rw.sh ? ld16(rw.al + off + 16) : lo[n];
-    }
+    for (int n = 0; n < NW; ++n) win_chunks(rw, 16 * (threadIdx.x + n * kTB), lo[n], hi[n]);
     for (int i = 0; i < nin; ++i) {
         u32x4 x[NW];
 #pragma unroll
-        for (int n = 0; n < NW; ++n) x[n] = rw.sh ? funnel16(lo[n], hi[n], rw.sh) : lo[n];
+        for (int n = 0; n < NW; ++n) {
+            x[n] = win_join(rw, lo[n], hi[n]);
+            if (copy) copy_owned(j.copy, rw, 16 * (threadIdx.x + n * kTB), lo[n], hi[n]);
+        }
         if (i + 1 < nin) {
-            rw = row_win(j.in_rows[i + 1], t0b);
+            rw = row_win(reinterpret_cast<const uint8_t*>(j.in_rows[i + 1]) + t0b);
 #pragma unroll
-            for (int n = 0; n < NW; ++n) {
-                const uint32_t off = 16 * (threadIdx.x + n * kTB);
-                lo[n] = ld16(rw.al + off);
-                hi[n] = rw.sh ? ld16(rw.al + off + 16) : lo[n];
-            }
+            for (int n = 0; n < NW; ++n) win_chunks(rw, 16 * (threadIdx.x + n * kTB), lo[n], hi[n]);
         }
         rs_mix_input<G, NW>(ptab, og, nin, i, x, acc);
     }
@@ -210,13 +187,21 @@ __device__ __forceinline__ void rs_mix_full(const RsJob& j, const uint32_t (*pta
 // The last, partial tile: word loads guarded by the row length.
 template <int G, int NW>
 __device__ __forceinline__ void rs_mix_tail(const RsJob& j, const uint32_t (*ptab)[kRs16Tab],
-                                            int og, const int64_t* w0,
+                                            int og, const int64_t* w0, bool copy,
                                             uint32_t (*acc)[kRsGroup][4]) {
     rs_zero<G, NW>(acc);
     for (int i = 0; i < j.nin; ++i) {
         u32x4 x[NW];
 #pragma unroll
-        for (int n = 0; n < NW; ++n) x[n] = rs_window(j.in_rows[i], w0[n], j.S);
+        for (int n = 0; n < NW; ++n) {
+            x[n] = rs_window(j.in_rows[i], w0[n], j.S);
+            if (copy && w0[n] < j.S) {
+                const uint64_t o = uint64_t(reinterpret_cast<const uint8_t*>(j.in_rows[i] + w0[n]) -
+                                            j.copy.src);
+                const int64_t nw = j.S - w0[n] < 8 ? j.S - w0[n] : 8;
+                copy_bytes(j.copy, o, o + 2 * uint64_t(nw));
+            }
+        }
         rs_mix_input<G, NW>(ptab, og, j.nin, i, x, acc);
     }
 }
@@ -239,16 +224,21 @@ __device__ __forceinline__ void rs_run_tiles(const RsJob& j, const uint32_t (*pt
         int64_t w0[kRsNW];
 #pragma unroll
         for (int n = 0; n < kRsNW; ++n) w0[n] = int64_t(t0b / 2) + 8 * (threadIdx.x + n * kTB);
+        if (j.copy.dst && tt == 0 && threadIdx.x == 0)
+            for (int i = 0; i < j.nin; ++i)
+                copy_row_head(j.copy,
+                              uint64_t(reinterpret_cast<const uint8_t*>(j.in_rows[i]) - j.copy.src), Sb);
         for (int og = 0; og < j.nout; og += kRsGroup) {
+            const bool copy = j.copy.dst != nullptr && og == 0;
             const int G = j.nout - og < kRsGroup ? j.nout - og : kRsGroup;
             uint32_t acc[kRsNW][kRsGroup][4];
             static_assert(kRsGroup == 2, "one instantiation per group size");
             if (nbytes == kRsTile) {
-                if (G == 1) rs_mix_full<1, kRsNW>(j, ptab, og, t0b, acc);
-                else rs_mix_full<2, kRsNW>(j, ptab, og, t0b, acc);
+                if (G == 1) rs_mix_full<1, kRsNW>(j, ptab, og, t0b, copy, acc);
+                else rs_mix_full<2, kRsNW>(j, ptab, og, t0b, copy, acc);
             } else if (w0[0] < j.S) {
-                if (G == 1) rs_mix_tail<1, kRsNW>(j, ptab, og, w0, acc);
-                else rs_mix_tail<2, kRsNW>(j, ptab, og, w0, acc);
+                if (G == 1) rs_mix_tail<1, kRsNW>(j, ptab, og, w0, copy, acc);
+                else rs_mix_tail<2, kRsNW>(j, ptab, og, w0, copy, acc);
             } else {
                 for (int n = 0; n < kRsNW; ++n)
                     for (int g = 0; g < kRsGroup; ++g)
@@ -364,6 +354,7 @@ __global__ __launch_bounds__(kTB) __attribute__((amdgpu_waves_per_eu(4))) void r
     if (threadIdx.x == 0) {
         j.S = S;
         j.nout = m;
+        j.copy = FlatCopy{nullptr, nullptr, 0};
         int n = 0;
         for (int i = 0; i < k; ++i) {
             bool miss = false;
@@ -455,11 +446,19 @@ extern "C" int kvec_rs16_encode(const void* data_padded, void* shards, int data_
     hipStream_t st = as_stream(stream);
     const int64_t S = shard_size;
     if (S == 0) return KVEC_OK;
-    hipError_t e = hipMemcpyAsync(shards, data_padded, uint64_t(data_shards) * S * 2,
-                                  hipMemcpyDeviceToDevice, st);
-    if (e != hipSuccess) return set_error(KVEC_EHIP, "kvec_rs16_encode: %s", hipGetErrorString(e));
+    const uint64_t data_bytes = uint64_t(data_shards) * S * 2;
+    // The data rows are copied by the coding kernel itself when the two
+    // buffers are disjoint and equally aligned modulo 16 bytes; otherwise (or
+    // with no parity to code) by a separate stream-ordered copy.
+    const bool fuse = parity_shards > 0 && fused_copy_ok(data_padded, shards, data_bytes);
+    if (!fuse && shards != data_padded) {
+        hipError_t e = hipMemcpyAsync(shards, data_padded, data_bytes, hipMemcpyDeviceToDevice, st);
+        if (e != hipSuccess) return set_error(KVEC_EHIP, "kvec_rs16_encode: %s", hipGetErrorString(e));
+    }
     if (parity_shards == 0) return KVEC_OK;
     RsJob j{};
+    j.copy = fuse ? FlatCopy{(const uint8_t*)data_padded, (uint8_t*)shards, data_bytes}
+                  : FlatCopy{nullptr, nullptr, 0};
     j.S = S;
     j.nin = data_shards;
     j.nout = parity_shards;

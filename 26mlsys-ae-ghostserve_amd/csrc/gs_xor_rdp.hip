@@ -42,16 +42,39 @@ __device__ __forceinline__ u32x4 xor_rows_partial(const uint8_t* in, uint64_t Sb
 }
 
 // One tile of XOR-of-rows, written to up to two outputs (row base addresses).
+// With fc.dst set, rows lo..hi-1 of `in` (the whole flat range of fc, no
+// skip) are also copied to fc.dst by the same loads.
 __device__ __forceinline__ void xor_rows_tile(const uint8_t* in, uint64_t Sb, RowSet rs,
-                                              uint8_t* out0, uint8_t* out1, uint8_t* tile) {
+                                              uint8_t* out0, uint8_t* out1, const FlatCopy& fc,
+                                              uint8_t* tile) {
     const uint64_t t0 = uint64_t(blockIdx.x) * kTileBytes;
     const uint32_t nbytes = uint32_t(Sb - t0 < uint64_t(kTileBytes) ? Sb - t0 : kTileBytes);
     const uint64_t c0 = t0 + 16 * threadIdx.x;
     u32x4 acc = {0, 0, 0, 0};
-    if (c0 + 16 <= Sb)
+    if (t0 + kTileBytes <= Sb) {
+        // whole tile inside the rows: uniform row windows, loads carry the copy
+        const uint32_t off = 16 * threadIdx.x;
+        for (int r = rs.lo; r < rs.hi; ++r) {
+            if (r == rs.skip) continue;
+            const RowWin rw = row_win(in + uint64_t(r) * Sb + t0);
+            u32x4 lo, hi;
+            win_chunks(rw, off, lo, hi);
+            acc ^= win_join(rw, lo, hi);
+            if (fc.dst) copy_owned(fc, rw, off, lo, hi);
+        }
+        if (rs.extra >= 0) acc ^= load_window16(in + uint64_t(rs.extra) * Sb + c0);
+    } else if (c0 + 16 <= Sb) {
         acc = xor_rows_window(in, Sb, rs, c0);
-    else if (c0 < Sb)
+    } else if (c0 < Sb) {
         acc = xor_rows_partial(in, Sb, rs, c0, uint32_t(Sb - c0));
+    }
+    if (fc.dst) {
+        if (t0 + kTileBytes > Sb && c0 < Sb)
+            for (int r = rs.lo; r < rs.hi; ++r)
+                copy_bytes(fc, uint64_t(r) * Sb + c0, uint64_t(r) * Sb + (c0 + 16 < Sb ? c0 + 16 : Sb));
+        if (t0 == 0 && threadIdx.x == 0)
+            for (int r = rs.lo; r < rs.hi; ++r) copy_row_head(fc, uint64_t(r) * Sb, Sb);
+    }
     *reinterpret_cast<u32x4*>(tile + 16 * threadIdx.x) = acc;
     __syncthreads();
     if (out0) tile_store(out0 + t0, tile, nbytes);
@@ -59,9 +82,9 @@ __device__ __forceinline__ void xor_rows_tile(const uint8_t* in, uint64_t Sb, Ro
 }
 
 __global__ __launch_bounds__(kTB) void xor_rows_kernel(const uint8_t* in, uint64_t Sb, RowSet rs,
-                                                       uint8_t* out0, uint8_t* out1) {
+                                                       uint8_t* out0, uint8_t* out1, FlatCopy fc) {
     __shared__ __attribute__((aligned(16))) uint8_t tile[kTileBytes + 16];
-    xor_rows_tile(in, Sb, rs, out0, out1, tile);
+    xor_rows_tile(in, Sb, rs, out0, out1, fc, tile);
 }
 
 // benchmark/xor/kernel.cu:47-88 with the missing index read on the device:
@@ -79,7 +102,8 @@ __global__ __launch_bounds__(kTB) void xor_reconstruct_kernel(const uint8_t* enc
         rs = RowSet{0, nd, -1, -1};
     else
         return;
-    xor_rows_tile(enc, Sb, rs, rec + uint64_t(m) * Sb, rec_missing, tile);
+    xor_rows_tile(enc, Sb, rs, rec + uint64_t(m) * Sb, rec_missing, FlatCopy{nullptr, nullptr, 0},
+                  tile);
 }
 
 // ----------------------------------------------------------------- gs RDP P/Q
@@ -171,10 +195,10 @@ __global__ __launch_bounds__(kTB) void gs_rdp_parity_kernel(uint16_t* sh, int nd
 
 // ----------------------------------------------------------------- host side
 static int xor_rows(const uint8_t* in, uint64_t Sb, RowSet rs, uint8_t* out0, uint8_t* out1,
-                    hipStream_t st, const char* what) {
+                    hipStream_t st, const char* what, FlatCopy fc = FlatCopy{nullptr, nullptr, 0}) {
     if (Sb == 0) return KVEC_OK;
     hipLaunchKernelGGL(xor_rows_kernel, dim3(blocks_for(int64_t(Sb), kTileBytes)), dim3(kTB), 0, st,
-                       in, Sb, rs, out0, out1);
+                       in, Sb, rs, out0, out1, fc);
     return check_launch(what);
 }
 
@@ -208,6 +232,12 @@ extern "C" int kvec_xor_encode(const void* data_padded, void* shards, int data_s
                          (long long)shard_size);
     hipStream_t st = as_stream(stream);
     const uint64_t Sb = uint64_t(shard_size);
+    // The data rows are copied by the parity kernel's own loads when the two
+    // buffers are disjoint and equally aligned modulo 16 bytes.
+    if (Sb && fused_copy_ok(data_padded, shards, Sb * data_shards))
+        return xor_rows((const uint8_t*)data_padded, Sb, RowSet{0, data_shards, -1, -1},
+                        (uint8_t*)shards + Sb * data_shards, nullptr, st, "kvec_xor_encode",
+                        FlatCopy{(const uint8_t*)data_padded, (uint8_t*)shards, Sb * data_shards});
     int rc = copy_d2d(shards, data_padded, Sb * data_shards, st, "kvec_xor_encode");
     if (rc) return rc;
     return xor_rows((const uint8_t*)data_padded, Sb, RowSet{0, data_shards, -1, -1},

@@ -70,6 +70,31 @@ __device__ __forceinline__ u32x4 load_window16(const uint8_t* p) {
     return funnel16(lo, ld16(al + 16), sh);
 }
 
+// A row seen from one tile: the 16-byte-aligned address at or below the
+// tile's first byte `p` and the misalignment, both wave-uniform.
+struct RowWin {
+    const uint8_t* al;
+    uint32_t sh;
+};
+
+__device__ __forceinline__ RowWin row_win(const uint8_t* p) {
+    p = wave_uniform(p);
+    const uint32_t sh = uint32_t(reinterpret_cast<uintptr_t>(p) & 15);
+    return RowWin{p - sh, sh};
+}
+
+// The aligned chunks under the 16 bytes at tile offset `off` (a multiple of
+// 16) of a tile that lies wholly inside its row: lo, and hi when the row is
+// misaligned (hi then holds at least one byte of the row).
+__device__ __forceinline__ void win_chunks(const RowWin& r, uint32_t off, u32x4& lo, u32x4& hi) {
+    lo = ld16(r.al + off);
+    hi = r.sh ? ld16(r.al + off + 16) : lo;
+}
+
+__device__ __forceinline__ u32x4 win_join(const RowWin& r, u32x4 lo, u32x4 hi) {
+    return r.sh ? funnel16(lo, hi, r.sh) : lo;
+}
+
 __device__ __forceinline__ uint8_t byte_of(u32x4 v, int i) {
     const uint32_t w = i < 4 ? v.x : i < 8 ? v.y : i < 12 ? v.z : v.w;
     return uint8_t(w >> (8 * (i & 3)));
@@ -82,6 +107,66 @@ __device__ __forceinline__ u32x4 set_byte(u32x4 v, int i, uint8_t b) {
     else if (i < 12) v.z = (v.z & m) | x;
     else v.w = (v.w & m) | x;
     return v;
+}
+
+// ------------------------------------------------------------- fused copy
+// A flat device-to-device copy of [src, src+len) to dst carried by a coding
+// kernel's own tile loads, so the copied bytes are read from HBM once (the
+// reference's encode kernels copy the data rows into the shard tensor while
+// coding them: benchmark/xor/kernel.cu:17-41, benchmark/rs/kernel.cu:67-102).
+// dst - src is a multiple of 16, so an aligned source chunk is an aligned
+// destination chunk.  Ownership, for rows laid end to end in the range:
+//   - in a tile wholly inside its row, each lane stores the aligned chunk
+//     starting inside its window (hi when the row is misaligned, else lo);
+//     over the tile these are disjoint and continue where the previous tile's
+//     stopped;
+//   - the first tile stores each row's head bytes up to its first aligned
+//     address, and the row's partial last tile stores its bytes one by one.
+// Chunks that reach into the next row store bytes that row also stores,
+// with the same values; nothing past src+len is written.
+struct FlatCopy {
+    const uint8_t* src;
+    uint8_t* dst;   // null: no copy
+    uint64_t len;
+};
+
+// Host side: whether a copy of `len` bytes from src to dst can ride on the
+// coding kernel (disjoint ranges, equal alignment modulo 16).
+inline bool fused_copy_ok(const void* src, const void* dst, uint64_t len) {
+    const uintptr_t s = reinterpret_cast<uintptr_t>(src), d = reinterpret_cast<uintptr_t>(dst);
+    return ((s ^ d) & 15) == 0 && (d >= s + len || s >= d + len);
+}
+
+// Store the source chunk at `c` (16-byte aligned, value v) at its place in dst.
+__device__ __forceinline__ void copy_chunk(const FlatCopy& fc, const uint8_t* c, u32x4 v) {
+    const uint64_t o = uint64_t(c - fc.src);
+    if (o + 16 <= fc.len) {
+        st16(fc.dst + o, v);
+        return;
+    }
+    const gptr<uint8_t> d = as_global(fc.dst);
+    for (int i = 0; i < 16 && o + i < fc.len; ++i) d[o + i] = byte_of(v, i);
+}
+
+__device__ __forceinline__ void copy_owned(const FlatCopy& fc, const RowWin& r, uint32_t off,
+                                           u32x4 lo, u32x4 hi) {
+    if (r.sh) copy_chunk(fc, r.al + off + 16, hi);
+    else copy_chunk(fc, r.al + off, lo);
+}
+
+// Bytes [a, b) of the range, one by one.
+__device__ __forceinline__ void copy_bytes(const FlatCopy& fc, uint64_t a, uint64_t b) {
+    const gptr<const uint8_t> s = as_global(fc.src);
+    const gptr<uint8_t> d = as_global(fc.dst);
+    for (uint64_t i = a; i < b; ++i) d[i] = s[i];
+}
+
+// Head bytes of the row starting at range offset `o`: up to its first
+// 16-byte-aligned address (at most 15, no further than `row_len`).
+__device__ __forceinline__ void copy_row_head(const FlatCopy& fc, uint64_t o, uint64_t row_len) {
+    const uint32_t mis = uint32_t(reinterpret_cast<uintptr_t>(fc.src + o) & 15);
+    const uint64_t n = mis ? 16 - mis : 0;
+    copy_bytes(fc, o, o + (n < row_len ? n : row_len));
 }
 
 // Write logical bytes [0, nbytes) of the LDS tile `t` (16-byte aligned, with 16

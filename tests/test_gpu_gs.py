@@ -30,6 +30,26 @@ def test_xor_encode_matches_oracle(pkg, ora, gpu, nd, S):
     assert np.array_equal(host(shards), want)
 
 
+# The data rows ride on the parity kernel's loads when data and shards are
+# disjoint and equally aligned modulo 16 bytes (else a separate copy): offsets
+# into guard-filled buffers cover both paths, misaligned row starts, whole
+# tiles and partial tails, and nothing outside the shard tensor may change.
+@pytest.mark.parametrize("nd,S", [(6, 8192), (3, 4096 * 2 + 10), (4, 1000), (2, 17), (1, 4096)])
+@pytest.mark.parametrize("doff,soff", [(0, 0), (5, 5), (3, 7), (0, 16), (11, 27)])
+def test_xor_encode_fused_copy_offsets(pkg, ora, gpu, nd, S, doff, soff):
+    rng = np.random.default_rng(nd * 1000 + S + doff)
+    data = rng.integers(0, 256, nd * S, dtype=np.uint8)
+    want = ora.xor_encode(data, nd, S)
+    dbuf = torch.zeros(nd * S + 64, dtype=torch.uint8, device=gpu)
+    dbuf[doff:doff + nd * S] = dev(data, gpu)
+    sbuf = torch.full(((nd + 1) * S + 64,), 0xA5, dtype=torch.uint8, device=gpu)
+    shards = sbuf[soff:soff + (nd + 1) * S].view(nd + 1, S)
+    pkg.xor.xor_kernel.encode_xor(dbuf[doff:doff + nd * S], shards, nd, S)
+    assert np.array_equal(host(shards), want)
+    rest = torch.cat([sbuf[:soff], sbuf[soff + (nd + 1) * S:]])
+    assert bool((rest == 0xA5).all())
+
+
 @pytest.mark.parametrize("nd,S", [(4, 262144), (8, 999), (3, 17), (5, 3)])
 def test_xor_reconstruct_matches_oracle(pkg, ora, gpu, nd, S):
     rng = np.random.default_rng(S)
@@ -195,6 +215,26 @@ def test_rs16_encode_matches_oracle(pkg, ora, gpu, k, m, S):
     gex, glg = pkg.rs.device_gf_tables(gpu)
     pkg.rs.rs_kernel.encode_rs_u16(dev(data, gpu), shards, k, m, S, gex, glg)
     assert np.array_equal(host(shards), want)
+
+
+@pytest.mark.parametrize("k,m,S", [(6, 2, 4096), (3, 3, 4096 * 2 + 5), (4, 1, 1000), (2, 2, 9)])
+@pytest.mark.parametrize("doff,soff", [(0, 0), (3, 3), (1, 5), (0, 8), (7, 15)])
+def test_rs16_encode_fused_copy_offsets(pkg, ora, gpu, k, m, S, doff, soff):
+    """Offsets in u16 words: equal offsets modulo 8 words take the fused copy."""
+    ex, lg = ora.gf16_tables()
+    rng = np.random.default_rng(k * 100 + S + doff)
+    data = rng.integers(0, 65536, k * S, dtype=np.uint16)
+    want = ora.rs16_encode(data, k, m, S, ex, lg)
+    dbuf = torch.zeros(k * S + 32, dtype=torch.int16, device=gpu)
+    dbuf[doff:doff + k * S] = dev(data.view(np.int16), gpu)
+    sbuf = torch.full(((k + m) * S + 32,), 0x1234, dtype=torch.int16, device=gpu)
+    shards = sbuf[soff:soff + (k + m) * S].view(k + m, S)
+    gex, glg = pkg.rs.device_gf_tables(gpu)
+    pkg.rs.rs_kernel.encode_rs_u16(dbuf[doff:doff + k * S].view(torch.uint16),
+                                   shards.view(torch.uint16), k, m, S, gex, glg)
+    assert np.array_equal(host(shards).view(np.uint16), want)
+    rest = torch.cat([sbuf[:soff], sbuf[soff + (k + m) * S:]])
+    assert bool((rest == 0x1234).all())
 
 
 @pytest.mark.parametrize("k,m,S", [(8, 2, 4099), (6, 3, 1000), (5, 3, 9), (9, 5, 2051)])
