@@ -85,10 +85,13 @@ __device__ __forceinline__ RowWin row_win(const uint8_t* p) {
 
 // The aligned chunks under the 16 bytes at tile offset `off` (a multiple of
 // 16) of a tile that lies wholly inside its row: lo, and hi when the row is
-// misaligned (hi then holds at least one byte of the row).
+// misaligned (hi then holds at least one byte of the row).  Both loads are
+// always issued (hi re-reads lo's chunk, a cache hit, when the row is
+// aligned and hi is unused): a branch around the second load would make the
+// compiler wait for the first at the join, serializing the rows' loads.
 __device__ __forceinline__ void win_chunks(const RowWin& r, uint32_t off, u32x4& lo, u32x4& hi) {
     lo = ld16(r.al + off);
-    hi = r.sh ? ld16(r.al + off + 16) : lo;
+    hi = ld16(r.al + off + (r.sh ? 16 : 0));
 }
 
 __device__ __forceinline__ u32x4 win_join(const RowWin& r, u32x4 lo, u32x4 hi) {
