@@ -138,8 +138,60 @@ __device__ __forceinline__ u32x4 drop_word(u32x4 v, int64_t k) {
     return v;
 }
 
+// Where the data rows' bytes come from.  Without K/V (FUSED false) they are
+// the shard rows themselves.  For the fused backup (the pack of
+// benchmark/rdp/kernel.cu:32-72, then the parity of :76-107) data-row bytes
+// [0, kb) are K_TN, [kb, 2 kb) are V_TN and the rest is the row tensor's own
+// padding, which the caller zero-fills and nothing here writes; the kernel
+// stores the K/V bytes into the data rows (bytes [0, copy_end)) from the same
+// loads.  K and V are equally aligned modulo 16 with their place in the rows,
+// so an aligned row chunk is an aligned K or V chunk.
+struct GsSource {
+    const uint8_t* K;
+    const uint8_t* V;
+    int64_t kb;         // bytes of K (and of V)
+    int64_t copy_end;   // data-row bytes that come from K||V: min(2 kb, nd Sb)
+    int64_t rows_end;   // bytes of the whole row tensor, (nd + 2) Sb
+};
+
+__device__ __forceinline__ uint8_t gs_src_byte(const GsSource& g, const uint8_t* base, int64_t x) {
+    if (x < g.kb) return as_global(g.K)[x];
+    if (x < 2 * g.kb) return as_global(g.V)[x - g.kb];
+    return x < g.rows_end ? as_global(base)[x] : uint8_t(0);
+}
+
+__device__ __forceinline__ uint16_t gs_src_word(const GsSource& g, const uint16_t* sh, int64_t w) {
+    const int64_t kw = g.kb / 2;
+    if (w < kw) return as_global(reinterpret_cast<const uint16_t*>(g.K))[w];
+    if (w < 2 * kw) return as_global(reinterpret_cast<const uint16_t*>(g.V))[w - kw];
+    return as_global(sh)[w];
+}
+
+// The aligned 16-byte chunk at row offset X assembled byte by byte: only for
+// the few chunks next to a K/V/padding boundary.  Bytes before the tensor
+// (X < 0) are never used and read as 0.
+__device__ __forceinline__ u32x4 gs_src_chunk_bytes(const GsSource& g, const uint8_t* base,
+                                                    int64_t X) {
+    u32x4 v = {0, 0, 0, 0};
+    for (int i = 0; i < 16; ++i)
+        if (X + i >= 0) v = set_byte(v, i, gs_src_byte(g, base, X + i));
+    return v;
+}
+
+// Store the parts of the chunk at row offset X that lie in [0, lim).
+__device__ __forceinline__ void gs_store_chunk(uint8_t* base, int64_t X, u32x4 v, int64_t lim) {
+    if (X >= 0 && X + 16 <= lim) {
+        st16(base + X, v);
+        return;
+    }
+    const gptr<uint8_t> d = as_global(base);
+    for (int i = 0; i < 16; ++i)
+        if (X + i >= 0 && X + i < lim) d[X + i] = byte_of(v, i);
+}
+
+template <bool FUSED>
 __global__ __launch_bounds__(kTB) void gs_rdp_parity_kernel(uint16_t* sh, int nd, int64_t S,
-                                                            int star_base) {
+                                                            int star_base, GsSource g) {
     __shared__ __attribute__((aligned(16))) uint8_t tp[kTileBytes + 16];
     __shared__ __attribute__((aligned(16))) uint8_t tq[kTileBytes + 16];
     const uint8_t* base = reinterpret_cast<const uint8_t*>(sh);
@@ -154,19 +206,68 @@ __global__ __launch_bounds__(kTB) void gs_rdp_parity_kernel(uint16_t* sh, int nd
     for (int r = 0; r < nd; ++r) {
         const uint8_t* A0 = base + uint64_t(r) * Sb + t0b;
         const uint32_t mr = uint32_t(reinterpret_cast<uintptr_t>(A0) & 15);
-        const uint8_t* my = A0 - mr + 16 * threadIdx.x;
-        const u32x4 z = {0, 0, 0, 0};
-        const u32x4 c0 = my < end ? ld16(my) : z;
+        const int s = int(mr) - 2 * r;   // Q window offset from my, in [-2(nd-1), 15]
+        // lane 0's aligned chunk: at row offset X0, read from rp (uniform)
+        const int64_t X0 = int64_t(uint64_t(r) * Sb + t0b) - int64_t(mr);
+        const uint8_t* rp = A0 - mr;
+        bool mixed = false, from_kv = false;
+        if (FUSED) {
+            // every chunk any lane loads for this row: its own, the edge lanes'
+            // neighbours, and the Q window's chunks when it starts more than
+            // one chunk back (s < -16)
+            const int64_t lo = X0 - 48 - 2 * int64_t(nd), hi = X0 + kTileBytes + 32;
+            if (hi <= g.kb) {
+                rp = g.K + X0;
+                from_kv = true;
+            } else if (lo >= g.kb && hi <= 2 * g.kb) {
+                rp = g.V + (X0 - g.kb);
+                from_kv = true;
+            } else if (lo < 2 * g.kb) {
+                mixed = true;
+            }
+        }
+        const uint8_t* my = rp + 16 * threadIdx.x;
+        const int64_t X = X0 + 16 * int64_t(threadIdx.x);
+        // K/V chunks lie inside K/V by the classification above; row chunks
+        // past the tensor's end (lanes past the last word) read as zero
+        u32x4 c0;
+        if (FUSED && mixed) c0 = gs_src_chunk_bytes(g, base, X);
+        else c0 = (from_kv || my < end) ? ld16(my) : u32x4{0, 0, 0, 0};
         // the shifts run with every lane active (a lane reading a disabled lane
         // gets nothing); lanes at a wave edge then load their neighbour chunk
         u32x4 c1 = from_next_lane(c0), cm = from_prev_lane(c0);
-        const int s = int(mr) - 2 * r;   // Q window offset in [-2(nd-1), 15]
-        if (lane == 63 && fast && (mr > 0 || s > 0)) c1 = ld16(my + 16);
-        if (lane == 0 && fast && s < 0) cm = ld16(my - 16);
+        if (lane == 63 && fast && (mr > 0 || s > 0))
+            c1 = (FUSED && mixed) ? gs_src_chunk_bytes(g, base, X + 16) : ld16(my + 16);
+        if (lane == 0 && fast && s < 0)
+            cm = (FUSED && mixed) ? gs_src_chunk_bytes(g, base, X - 16) : ld16(my - 16);
         if (fast) {
+            if (FUSED && (from_kv || mixed)) {
+                // This lane's chunk into the data rows.  The window's last mr
+                // bytes are in the next chunk: the next lane stores it, unless
+                // that lane is past the block or is a word-by-word lane (the
+                // row's last words), whose copy covers only its own words.
+                gs_store_chunk(reinterpret_cast<uint8_t*>(sh), X, c0, g.copy_end);
+                if (mr > 0 && (threadIdx.x == kTB - 1 || w0 + 16 > S))
+                    gs_store_chunk(reinterpret_cast<uint8_t*>(sh), X + 16, c1, g.copy_end);
+            }
             p ^= mr ? funnel16(c0, c1, mr) : c0;
-            const u32x4 qw = s > 0 ? funnel16(c0, c1, uint32_t(s))
-                                   : (s == 0 ? c0 : funnel16(cm, c0, uint32_t(s + 16)));
+            u32x4 qw;
+            if (s > 0) {
+                qw = funnel16(c0, c1, uint32_t(s));
+            } else if (s == 0) {
+                qw = c0;
+            } else if (s >= -16) {
+                qw = funnel16(cm, c0, uint32_t(s + 16));
+            } else {
+                // rows r >= 9 of wide stripes: the window starts k chunks
+                // back (k = floor(s / 16) <= -2), past the neighbour lane
+                const int k = (s - 15) / 16;
+                const int64_t Xq = X + 16 * k;
+                const u32x4 a = (FUSED && mixed) ? gs_src_chunk_bytes(g, base, Xq) : ld16(my + 16 * k);
+                const u32x4 b = (FUSED && mixed) ? gs_src_chunk_bytes(g, base, Xq + 16)
+                                                 : ld16(my + 16 * k + 16);
+                qw = funnel16(a, b, uint32_t(s - 16 * k));
+            }
             const int64_t star = cmod(int64_t(star_base) + r, S);
             q ^= star < 0 ? qw : drop_word(qw, cmod(star + r, S) - w0);
         }
@@ -176,10 +277,14 @@ __global__ __launch_bounds__(kTB) void gs_rdp_parity_kernel(uint16_t* sh, int nd
         for (int i = 0; i < n; ++i) {
             uint16_t a = 0, b = 0;
             for (int r = 0; r < nd; ++r) {
-                a ^= sh[uint64_t(r) * S + w0 + i];
+                const int64_t x = int64_t(r) * S + w0 + i;
+                const uint16_t v = FUSED ? gs_src_word(g, sh, x) : sh[x];
+                if (FUSED && 2 * x < g.copy_end) as_global(sh)[x] = v;
+                a ^= v;
                 int64_t c = (w0 + i - r) % S;
                 if (c < 0) c += S;
-                if (c != cmod(int64_t(star_base) + r, S)) b ^= sh[uint64_t(r) * S + c];
+                if (c != cmod(int64_t(star_base) + r, S))
+                    b ^= FUSED ? gs_src_word(g, sh, int64_t(r) * S + c) : sh[uint64_t(r) * S + c];
             }
             p = set_byte(set_byte(p, 2 * i, uint8_t(a)), 2 * i + 1, uint8_t(a >> 8));
             q = set_byte(set_byte(q, 2 * i, uint8_t(b)), 2 * i + 1, uint8_t(b >> 8));
@@ -210,10 +315,15 @@ static int copy_d2d(void* dst, const void* src, uint64_t n, hipStream_t st, cons
 }
 
 static int gs_rdp_parity(uint16_t* sh, int nd, int64_t S, int star_base, hipStream_t st,
-                         const char* what) {
+                         const char* what, const GsSource* fused = nullptr) {
     if (nd <= 0 || S <= 0) return KVEC_OK;  // the reference kernel returns at once
-    hipLaunchKernelGGL(gs_rdp_parity_kernel, dim3(blocks_for(S * 2, kTileBytes)), dim3(kTB), 0, st, sh,
-                       nd, S, star_base);
+    const dim3 grid(blocks_for(S * 2, kTileBytes));
+    if (fused)
+        hipLaunchKernelGGL(gs_rdp_parity_kernel<true>, grid, dim3(kTB), 0, st, sh, nd, S, star_base,
+                           *fused);
+    else
+        hipLaunchKernelGGL(gs_rdp_parity_kernel<false>, grid, dim3(kTB), 0, st, sh, nd, S, star_base,
+                           GsSource{nullptr, nullptr, 0, 0, 0});
     return check_launch(what);
 }
 
@@ -299,6 +409,17 @@ extern "C" int kvec_gs_rdp_backup(const void* K_TN, const void* V_TN, void* shar
     if (T > 0 && n > 0 && nd > 0 && S > 0) {
         if (!K_TN || !V_TN) return set_error(KVEC_EINVAL, "kvec_gs_rdp_backup: null K/V");
         const uint64_t tn = uint64_t(T) * uint64_t(n), cap = uint64_t(nd) * uint64_t(S);
+        // The pack rides on the parity kernel when K and V are equally aligned
+        // modulo 16 with their place in the rows and overlap nothing there.
+        const uintptr_t R0 = uintptr_t(shards), Rend = R0 + (cap + 2 * uint64_t(S)) * 2;
+        const uintptr_t Kp = uintptr_t(K_TN), Vp = uintptr_t(V_TN);
+        const bool apart = (Kp + tn * 2 <= R0 || Kp >= Rend) && (Vp + tn * 2 <= R0 || Vp >= Rend);
+        if (apart && ((Kp ^ R0) & 15) == 0 && ((Vp ^ (R0 + tn * 2)) & 15) == 0) {
+            const uint64_t kv = 4 * tn, rows = 2 * cap;
+            const GsSource g{(const uint8_t*)K_TN, (const uint8_t*)V_TN, int64_t(2 * tn),
+                             int64_t(kv < rows ? kv : rows), int64_t(Rend - R0)};
+            return gs_rdp_parity((uint16_t*)shards, nd, S, star_base, st, "kvec_gs_rdp_backup", &g);
+        }
         const uint64_t nk = tn < cap ? tn : cap;
         const uint64_t nv = 2 * tn < cap ? tn : (cap > tn ? cap - tn : 0);
         int rc = copy_d2d(shards, K_TN, nk * 2, st, "kvec_gs_rdp_backup");

@@ -488,6 +488,45 @@ def bench_gs(pkg, torch, oracle, dev, seed, steps, warmup):
                                "frac_hbm_peak": round(alg / kms / 1e6 / HBM_PEAK_GBS, 4)}
     del rows
 
+    # fused_backup_full_kv (benchmark/rdp/kernel.cu:366-395): K_TN || V_TN packed
+    # into the data rows and P/Q, one pass.  K/V are the stream's two halves,
+    # [16 x 2048 tokens, 32 layers x 128] each.
+    T_tok, n_w = 16 * 2048, 32 * 128
+    assert 2 * T_tok * n_w == words
+    bsets = []
+    for _ in range(2):
+        kv = torch.randint(-32768, 32767, (2, T_tok, n_w), generator=g, device=dev, dtype=torch.int16)
+        shb = torch.empty((nd + 2, S), dtype=torch.int16, device=dev)
+        shb.view(-1)[words:nd * S].zero_()   # the caller zero-fills the padding
+        bsets.append((kv[0].view(torch.uint16), kv[1].view(torch.uint16), shb.view(torch.uint16)))
+
+    def backup(K, V, shb):
+        pkg.rdp.rdp_kernel.fused_backup_full_kv(K, V, shb, nd, S, T_tok, n_w, sb)
+
+    backup(*bsets[0])
+    torch.cuda.synchronize()
+    K, V, shb = bsets[0]
+    flat = shb.view(torch.int16).view(-1)
+    if not (torch.equal(flat[:words // 2], K.view(torch.int16).reshape(-1)) and
+            torch.equal(flat[words // 2:words], V.view(torch.int16).reshape(-1))):
+        raise RuntimeError("gs backup data rows differ from K || V")
+    hc = shb.view(torch.int16).cpu().numpy().view(np.uint16)
+    if not np.array_equal(hc[nd, cols], np.bitwise_xor.reduce(hc[:nd, cols], axis=0)):
+        raise RuntimeError("gs backup P mismatch")
+    q = np.zeros(cols.size, np.uint16)
+    for r in range(nd):
+        c = (cols - r) % S
+        q ^= np.where(c != (sb + r) % S, hc[r, c], 0).astype(np.uint16)
+    if not np.array_equal(hc[nd + 1, cols], q):
+        raise RuntimeError("gs backup Q mismatch")
+    del hc
+    wall, kms = time_kernel(torch, backup, bsets, steps, warmup)
+    alg = words * 2 + nd * S * 2 + 2 * S * 2   # K/V read once; data rows + P/Q written
+    out["rdp_backup"] = {"us": round(kms * 1e3, 2), "alg_bytes": alg,
+                         "gbs": round(alg / kms / 1e6, 2),
+                         "frac_hbm_peak": round(alg / kms / 1e6 / HBM_PEAK_GBS, 4)}
+    del bsets, K, V, shb, flat
+
     # XOR (benchmark/xor/kernel.cu:17-41): the data rows copied into the shard
     # tensor and P, in one pass
     Sb = -(-STREAM_BYTES // nd)
@@ -657,7 +696,8 @@ def main():
     if not args.no_gs:
         log("[bench] gs family (reference codes, packed layouts) on the 512 MiB stream")
         gs = bench_gs(pkg, torch, oracle, dev, args.seed, args.steps, args.warmup)
-        log(f"[bench] gs: P/Q {gs['star_diagonal_pq']['us']:.1f} us, XOR {gs['xor_encode']['us']:.1f} us, "
+        log(f"[bench] gs: P/Q {gs['star_diagonal_pq']['us']:.1f} us, backup (pack + P/Q) "
+            f"{gs['rdp_backup']['us']:.1f} us, XOR {gs['xor_encode']['us']:.1f} us, "
             f"RS16 {gs['rs16_encode']['us']:.1f} us")
 
     if args.copy_calibration:

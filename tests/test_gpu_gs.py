@@ -106,7 +106,10 @@ def test_xor_forward_backward_round_trip(pkg, ora, gpu, dtype, nd):
 
 # ------------------------------------------------------------------ gs RDP
 @pytest.mark.parametrize("nd,S", [(8, 5000), (6, 101), (1, 9), (3, 2), (2, 1), (13, 4103),
-                                  (8, 2048), (8, 2049), (4, 16), (5, 24577), (8, 7)])
+                                  (8, 2048), (8, 2049), (4, 16), (5, 24577), (8, 7),
+                                  # rows whose Q window starts more than one chunk
+                                  # back (misalignment - 2 r < -16)
+                                  (13, 4096), (11, 4100), (20, 4105), (16, 2000)])
 @pytest.mark.parametrize("star_base", [0, 3, -1, -5, 10 ** 6])
 def test_gs_rdp_parity_matches_oracle(pkg, ora, gpu, nd, S, star_base):
     rng = np.random.default_rng(nd * 1000 + S)
@@ -133,6 +136,46 @@ def test_gs_rdp_parity_row_stride_is_S(pkg, ora, gpu):
     got = host(d).reshape(-1)
     assert np.array_equal(got[: (nd + 2) * S], want.reshape(-1))
     assert np.array_equal(got[(nd + 2) * S:], rows.reshape(-1)[(nd + 2) * S:])
+
+
+# The pack (K_TN || V_TN into the data rows) rides on the parity kernel when
+# K and V are equally aligned modulo 16 with their place in the rows; offsets
+# (in u16 words) pick that path or the copy-then-parity one.  The rows'
+# padding keeps the caller's bytes (here a guard pattern) and enters P/Q as
+# is; nothing outside the row tensor changes.
+@pytest.mark.parametrize("T,n,nd,S_extra,koff,voff,soff,sb", [
+    (64, 128, 6, 0, 0, 0, 0, 0),          # 2Tn multiple of 16: fused
+    (3, 5, 4, 2, 1, 0, 1, 3),             # K/V boundary inside a chunk: fused
+    (3, 5, 4, 2, 2, 0, 1, 0),             # K misaligned with its rows: copies
+    (256, 1024, 6, 0, 5, 5, 5, -1),       # many tiles, misaligned rows: fused
+    (256, 1024, 6, -900, 0, 0, 0, 2),     # K/V larger than the rows: truncated
+    (100, 77, 13, 37, 3, 7, 3, 1000000),  # padding words, odd sizes: fused
+    (2048, 9, 1, 0, 0, 0, 0, 0),          # one data row: fused
+    (40, 50, 3, 5, 7, 7, 7, -5),          # fused
+    (40, 50, 3, 5, 7, 3, 7, -5),          # V misaligned with its rows: copies
+])
+def test_gs_fused_backup_layouts(pkg, ora, gpu, T, n, nd, S_extra, koff, voff, soff, sb):
+    tn = T * n
+    S = -(-2 * tn // nd) + S_extra
+    rng = np.random.default_rng(T * 31 + n + nd)
+    K = rng.integers(0, 65536, tn, dtype=np.uint16)
+    V = rng.integers(0, 65536, tn, dtype=np.uint16)
+    init = rng.integers(0, 65536, (nd + 2) * S, dtype=np.uint16).reshape(nd + 2, S)
+    want = init.copy()
+    ora.gs_pack(K.reshape(T, n), V.reshape(T, n), want, nd, S, T, n)
+    ora.gs_parity(want, nd, S, sb)
+    kb = torch.zeros(tn + 16, dtype=torch.int16, device=gpu)
+    vb = torch.zeros(tn + 16, dtype=torch.int16, device=gpu)
+    kb[koff:koff + tn] = dev(K.view(np.int16), gpu)
+    vb[voff:voff + tn] = dev(V.view(np.int16), gpu)
+    sbuf = torch.full(((nd + 2) * S + 32,), 0x3C3C, dtype=torch.int16, device=gpu)
+    sbuf[soff:soff + (nd + 2) * S] = dev(init.reshape(-1).view(np.int16), gpu)
+    shards = sbuf[soff:soff + (nd + 2) * S].view(nd + 2, S)
+    pkg.rdp.rdp_kernel.fused_backup_full_kv(kb[koff:koff + tn].view(T, n),
+                                            vb[voff:voff + tn].view(T, n), shards, nd, S, T, n, sb)
+    assert np.array_equal(host(shards).view(np.uint16), want)
+    rest = torch.cat([sbuf[:soff], sbuf[soff + (nd + 2) * S:]])
+    assert bool((rest == 0x3C3C).all())
 
 
 @pytest.mark.parametrize("B,H,T,D,nd", [(1, 8, 512, 128, 8), (2, 1, 33, 128, 6), (1, 2, 5, 64, 3),
