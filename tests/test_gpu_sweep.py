@@ -96,3 +96,53 @@ def test_sweep_rs16_encode(pkg, ora, gpu, k, m, S, doff, soff):
                                    k, m, S, gex, glg)
     assert np.array_equal(sh.cpu().numpy().view(np.uint16), want)
     assert bool((torch.cat([sbuf[:soff], sbuf[soff + (k + m) * S:]]) == 0x2468).all())
+
+
+# ------------------------------------------------------------------ spec codes
+RDP = _draw(20, lambda i: (lambda p: (p, int(_R.integers(1, p)), 16 * int(_R.integers(1, 3000)),
+                                      sorted(_R.choice(int(_R.integers(1, p)) + 2, 2, replace=False).tolist())))(
+    int(_R.choice([3, 5, 7, 11, 13]))))
+RS8 = _draw(16, lambda i: (lambda k: (k, int(_R.integers(1, min(8, 64 // k) + 1)), 16 * int(_R.integers(1, 4000))))(
+    int(_R.integers(1, 33))))
+
+
+@pytest.mark.parametrize("p,k,R,er", RDP)
+def test_sweep_rdp_encode_decode(pkg, ora, gpu, p, k, R, er):
+    er = [e for e in er if e < k + 2]
+    rng = np.random.default_rng(p * 1000 + k * 10 + R)
+    data = [rng.integers(0, 256, (p - 1, R), dtype=np.uint8) for _ in range(k)]
+    P, Q = ora.rdp_encode(data, p)
+    d = [dev(x.reshape(-1), gpu) for x in data]
+    Pg = torch.empty_like(d[0])
+    Qg = torch.empty_like(d[0])
+    pkg.spec.rdp_encode(d, Pg, Qg, p)
+    assert np.array_equal(Pg.cpu().numpy().reshape(p - 1, R), P)
+    assert np.array_equal(Qg.cpu().numpy().reshape(p - 1, R), Q)
+    sh = d + [Pg, Qg]
+    want = [t.clone() for t in sh]
+    for e in er:
+        sh[e].fill_(0xEE)
+    pkg.spec.rdp_decode(sh, p, er)
+    for a, b in zip(sh, want):
+        assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("k,m,S", RS8)
+def test_sweep_rs8_encode_decode(pkg, ora, gpu, k, m, S):
+    rng = np.random.default_rng(k * 100 + m + S)
+    data = [rng.integers(0, 256, S, dtype=np.uint8) for _ in range(k)]
+    par = ora.rs8_encode(data, m)
+    d = [dev(x, gpu) for x in data]
+    pg = [torch.empty_like(d[0]) for _ in range(m)]
+    pkg.spec.rs8_encode(d, pg)
+    for a, b in zip(pg, par):
+        assert np.array_equal(a.cpu().numpy(), b)
+    sh = d + pg
+    want = [t.clone() for t in sh]
+    ne = int(rng.integers(1, m + 1))
+    er = sorted(rng.choice(k + m, ne, replace=False).tolist())
+    for e in er:
+        sh[e].fill_(0x11)
+    pkg.spec.rs8_decode(sh, k, er)
+    for a, b in zip(sh, want):
+        assert torch.equal(a, b)
