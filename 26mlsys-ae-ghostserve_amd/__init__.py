@@ -12,10 +12,11 @@ signatures:
   paged       paged KV pool <-> coding stream; fused gather + RDP encode
   chunked     per-prefill-chunk RDP + RS coding of a paged (e.g. fp8) cache
   offload     parity copies to pinned host memory on a side stream
+  serving     forward_extend hook: per-step KV delta parity, JSONL metrics
 
 Import the package with ``importlib.import_module("26mlsys-ae-ghostserve_amd")``
 (the directory name is not a Python identifier).
 """
-from . import _lib, chunked, offload, paged, rdp, rdp_kv_ops, rs, spec, xor  # noqa: F401
+from . import _lib, chunked, offload, paged, rdp, rdp_kv_ops, rs, serving, spec, xor  # noqa: F401
 
-__all__ = ["xor", "rdp", "rs", "rdp_kv_ops", "spec", "paged", "chunked", "offload"]
+__all__ = ["xor", "rdp", "rs", "rdp_kv_ops", "spec", "paged", "chunked", "offload", "serving"]

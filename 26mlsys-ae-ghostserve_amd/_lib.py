@@ -73,6 +73,7 @@ SIGNATURES = {
     "kvec_rs8_decode": (_i, [_pp, _i, _i, _i64, _vp, _i, _vp]),
     "kvec_kv_stream_bytes": (_i64, [_kvp]),
     "kvec_kv_gather": (_i, [_kvp, _vp, _vp]),
+    "kvec_kv_gather_split": (_i, [_kvp, _vp, _vp, _vp]),
     "kvec_kv_scatter": (_i, [_kvp, _vp, _vp, _vp]),
     "kvec_rdp_encode_paged": (_i, [_kvp, _pp, _i, _vp, _vp, _i, _i64, _vp]),
     "kvec_chunk_width": (_i64, [_i64, _i, _i, _i64]),

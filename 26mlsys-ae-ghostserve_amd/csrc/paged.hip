@@ -25,6 +25,22 @@ __global__ __launch_bounds__(kGBS) void kv_gather_kernel(PagedGeom g, uint8_t* _
     st_stream(out, uint64_t(c) * 16, cell_load(g, w, inner));
 }
 
+// The K halves of the chunk's records to outK and the V halves to outV, each
+// in record order (the delta gather kv_pool[slots, 0] / kv_pool[slots, 1] of
+// bench_ghostserve_rdp.py:445-458, laid out as the [K | V] parity row of
+// pack_row_from_block, :105-118).  tb = token_bytes, a multiple of 16, so no
+// cell straddles the halves; the destination is selected without a branch.
+__global__ __launch_bounds__(kGBS) void kv_gather_split_kernel(PagedGeom g, uint8_t* __restrict__ outK,
+                                                               uint8_t* __restrict__ outV,
+                                                               uint32_t ncells, uint32_t tb) {
+    const uint32_t c = blockIdx.x * kGBS + threadIdx.x;
+    if (c >= ncells) return;
+    const uint32_t w = fdiv(c, g.div_cells);
+    const uint32_t inner = (c - w * g.div_cells.d) * 16;
+    const bool v = inner >= tb;
+    st_stream(v ? outV : outK, uint64_t(w) * tb + (v ? inner - tb : inner), cell_load(g, w, inner));
+}
+
 // pool cell = stream[s] (inverse; padding slots and invalid pages are skipped)
 __global__ __launch_bounds__(kGBS) void kv_scatter_kernel(PagedGeom g, const uint8_t* __restrict__ in,
                                                           uint32_t ncells) {
@@ -146,6 +162,20 @@ extern "C" int kvec_kv_gather(const kvec_paged_kv* kv, void* out, void* stream) 
     hipLaunchKernelGGL(kv_gather_kernel, dim3(blocks_for(ncells, kGBS)), dim3(kGBS), 0,
                        as_stream(stream), g, (uint8_t*)out, ncells);
     return check_launch("kvec_kv_gather");
+}
+
+extern "C" int kvec_kv_gather_split(const kvec_paged_kv* kv, void* out_k, void* out_v, void* stream) {
+    PagedGeom g;
+    int rc = make_geom(kv, &g, "kvec_kv_gather_split");
+    if (rc) return rc;
+    if (!out_k || !out_v || !aligned16(out_k) || !aligned16(out_v))
+        return set_error(KVEC_EINVAL, "kvec_kv_gather_split: output null or misaligned");
+    const uint32_t ncells = uint32_t(g.recs_total * g.rec / 16);
+    if (ncells == 0) return KVEC_OK;
+    hipLaunchKernelGGL(kv_gather_split_kernel, dim3(blocks_for(ncells, kGBS)), dim3(kGBS), 0,
+                       as_stream(stream), g, (uint8_t*)out_k, (uint8_t*)out_v, ncells,
+                       uint32_t(kv->token_bytes));
+    return check_launch("kvec_kv_gather_split");
 }
 
 extern "C" int kvec_kv_scatter(const kvec_paged_kv* kv, void* pool, const void* in, void* stream) {

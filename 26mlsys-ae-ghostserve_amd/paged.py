@@ -62,6 +62,17 @@ class PagedKV:
         _lib.call("kvec_kv_gather", self._c, out.data_ptr(), _lib.stream_handle(out.device))
         return out
 
+    def gather_split(self, out_k: torch.Tensor, out_v: torch.Tensor) -> None:
+        """The chunk's K halves into out_k and V halves into out_v, each in
+        record order (stream_bytes() / 2 bytes each, 16-byte aligned)."""
+        half = self.stream_bytes() // 2
+        for t in (out_k, out_v):
+            if t.numel() * t.element_size() < half:
+                raise ValueError("output smaller than half the stream")
+        _lib.require_cuda(out_k, out_v, what="gather output")
+        _lib.call("kvec_kv_gather_split", self._c, out_k.data_ptr(), out_v.data_ptr(),
+                  _lib.stream_handle(out_k.device))
+
     def scatter(self, stream: torch.Tensor) -> None:
         """Write a stream (e.g. a recovered one) back into the pool pages."""
         if stream.numel() * stream.element_size() < self.stream_bytes():

@@ -106,6 +106,13 @@ typedef struct kvec_paged_kv {
 int64_t kvec_kv_stream_bytes(const kvec_paged_kv* kv);
 /* out[0 .. stream bytes) = the chunk's stream gathered from the pool. */
 int kvec_kv_gather(const kvec_paged_kv* kv, void* out, void* stream);
+/* The chunk's K halves to out_k and V halves to out_v, each in record order
+ * (layer, sequence, token): with one layer and one sequence this is the
+ * serving plugin's delta gather kv_pool[slots, 0] and kv_pool[slots, 1]
+ * (bench_ghostserve_rdp.py:445-458) written straight into the [K | V] parity
+ * row that pack_row_from_block assembles (:105-118).  Both outputs 16-byte
+ * aligned; each receives stream_bytes / 2 bytes. */
+int kvec_kv_gather_split(const kvec_paged_kv* kv, void* out_k, void* out_v, void* stream);
 /* Inverse: write the stream `in` back into the pool pages (pool == kv->pool). */
 int kvec_kv_scatter(const kvec_paged_kv* kv, void* pool, const void* in, void* stream);
 /* Fused gather + spec RDP encode: the chunk's stream, cut into k data shards

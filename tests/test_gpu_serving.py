@@ -1,0 +1,83 @@
+"""Serving hook on the GPU: the split delta gather, and whole steps through
+the forward_extend wrapper checked against the oracle's star-diagonal parity
+of the reference's [K | V] row (bench_ghostserve_rdp.py:105-150, :340-389)."""
+import json
+
+import numpy as np
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+
+def _pool(gpu, T=300, H=2, D=64, seed=0):
+    g = torch.Generator(device="cpu").manual_seed(seed)
+    return torch.randn(T, 2, H, D, generator=g).to(torch.bfloat16).to(gpu)
+
+
+def test_gather_split_matches_indexing(pkg, gpu):
+    pool = _pool(gpu)
+    T, _, H, D = pool.shape
+    slots = torch.tensor([5, 17, 3, 299, 0, 42], dtype=torch.int32, device=gpu)
+    n = slots.numel()
+    kv = pkg.paged.PagedKV(pool.view(1, T, 1, 2, H, D), slots.view(1, n), 0, n)
+    k = torch.empty(n * H * D, dtype=torch.bfloat16, device=gpu)
+    v = torch.empty_like(k)
+    kv.gather_split(k, v)
+    idx = slots.long()
+    assert torch.equal(k.view(torch.int16), pool[idx, 0].reshape(-1).view(torch.int16))
+    assert torch.equal(v.view(torch.int16), pool[idx, 1].reshape(-1).view(torch.int16))
+
+
+class _Batch:
+    def __init__(self, slots):
+        self.slot_mapping = slots
+
+
+class _Backend:
+    def __init__(self, pool):
+        self.kv_buffer = pool
+
+    def forward_extend(self, q, batch=None):
+        return q
+
+
+class _Runner:
+    def __init__(self, be):
+        self.attn_backend = be
+
+
+@pytest.mark.parametrize("star_base", [0, 5])
+def test_hook_steps_match_oracle(pkg, ora, gpu, tmp_path, star_base):
+    pool = _pool(gpu, seed=star_base)
+    be = _Backend(pool)
+    path = tmp_path / "metrics.jsonl"
+    hook = pkg.serving.install(_Runner(be), pkg.serving.KVParityHook(
+        star_base=star_base, metrics_file=str(path), prog_start_mono=0.0, probe_h2d=True),
+        on_error=lambda e: (_ for _ in ()).throw(e))
+    steps = [[7, 8, 9, -1, 10], [-1, -1], [100, 3, 250, 251, 252, 253, 11, 12]]
+    got = []
+    for st in steps:
+        be.forward_extend("q", batch=_Batch(torch.tensor(st, device=gpu)))
+        hook.flush()
+        got.append(hook.last_parity)
+    recs = [json.loads(x) for x in path.read_text().splitlines()]
+    assert [r["chunk_id"] for r in recs] == [1, 2]   # the empty step codes nothing
+    for r in recs:
+        assert r["dst_rank"] == 0 and r["first_chunk_wall_ms"] is not None
+        t = r["timings"]
+        assert set(t) == {"rdp_encode_ms", "rdp_decode_ms", "gpu_to_cpu_ms", "cpu_to_gpu_ms",
+                          "parity_bytes"}
+        assert t["rdp_encode_ms"] >= 0 and t["gpu_to_cpu_ms"] >= 0 and t["cpu_to_gpu_ms"] >= 0
+        assert t["rdp_decode_ms"] is None
+    host = pool.cpu().view(torch.int16).numpy().view(np.uint16)
+    for st, (P, Q), rec in zip([steps[0], steps[2]], [got[0], got[2]], recs):
+        act = [s for s in st if s != -1]
+        row = np.concatenate([host[act, 0].reshape(-1), host[act, 1].reshape(-1)])
+        S = row.size
+        rows = np.zeros((3, S), np.uint16)
+        rows[0] = row
+        ora.gs_parity(rows, 1, S, star_base)
+        assert np.array_equal(P.numpy().view(np.uint16), rows[1])
+        assert np.array_equal(Q.numpy().view(np.uint16), rows[2])
+        assert rec["timings"]["parity_bytes"] == 2 * S * 2
