@@ -43,7 +43,8 @@ const char* kvec_last_error(void);
 
 /* ======================= spec family: textbook RDP ======================= */
 /* No reference counterpart (the reference "RDP" is the gs star-diagonal code
- * below); this is the code BASELINE's RDP configurations name.
+ * below); this is Row-Diagonal Parity as Corbett et al. define it (FAST 2004),
+ * the double-parity code of the p = 7, k = 6 KV chunk stripes.
  * Stripe: p prime (3..13), k data shards (1 <= k <= p-1; data columns k..p-2
  * are implicit zeros), each shard buffer holds p-1 row planes of `row_bytes`
  * bytes (row r at offset r*row_bytes); row_bytes % 16 == 0.  Column p-1 is
@@ -64,7 +65,8 @@ int64_t kvec_rdp_row_bytes(int64_t stream_bytes, int k, int p, int64_t granule);
 
 /* ================== spec family: RS over GF(2^8), Cauchy ================== */
 /* No reference counterpart (the reference RS works over GF(2^16), below); this
- * is the code BASELINE's RS configurations name.  Polynomial 0x11D, systematic
+ * is Reed-Solomon over GF(2^8), the code of the RS(6,2) and RS(5,3) KV stripes.
+ * Polynomial 0x11D, systematic
  * generator [I_k; C] with C[i][j] = 1 / ((k+i) ^ j).  Shards are separate
  * 16-byte aligned buffers of shard_bytes (% 16 == 0) bytes.
  * Limits: k <= 32, m <= 8, k*m <= 64. */
