@@ -56,6 +56,22 @@ __device__ __forceinline__ u32x4 xor3(u32x4 a, u32x4 b, u32x4 c) {
     return u32x4{xor3(a.x, b.x, c.x), xor3(a.y, b.y, c.y), xor3(a.z, b.z, c.z), xor3(a.w, b.w, c.w)};
 }
 
+// XOR accumulator that folds its inputs two at a time with the 3-input XOR.
+// Whether an input is held is known at compile time once the loops that feed
+// it are unrolled, so `held` costs nothing.
+struct Xor3Acc {
+    u32x4 a, pend;
+    bool held;
+    __device__ __forceinline__ explicit Xor3Acc(u32x4 init = u32x4{0, 0, 0, 0})
+        : a(init), pend{0, 0, 0, 0}, held(false) {}
+    __device__ __forceinline__ void add(u32x4 x) {
+        if (held) a = xor3(a, pend, x);
+        else pend = x;
+        held = !held;
+    }
+    __device__ __forceinline__ u32x4 get() const { return held ? a ^ pend : a; }
+};
+
 // XOR of N cells with 3-input XORs.
 template <int N>
 __device__ __forceinline__ u32x4 xor_all(const u32x4* v) {
@@ -71,11 +87,10 @@ __device__ __forceinline__ u32x4 xor_all(const u32x4* v) {
 // One shard buffer seen by a kernel.  Shards below 4 GiB use a buffer
 // resource: the row-plane offset rides in an SGPR (soffset), the lane offset
 // in one VGPR, and there is no 64-bit address arithmetic per access.  Larger
-// shards use 64-bit global addressing.  Loads are non-temporal (every byte is
-// read once per launch); stores carry sc0 sc1, which measured fastest for the
-// write streams of these kernels on MI355X.
+// shards use 64-bit global addressing.  Loads and stores are non-temporal:
+// every byte is read or written once per launch.
 constexpr int kAuxLoadNT = 2;        // nt
-constexpr int kAuxStoreSC01 = 17;    // sc0 | sc1
+constexpr int kAuxStoreNT = 2;       // nt
 constexpr uint32_t kBufWord3 = 0x00020000;
 
 template <bool BUF>
@@ -92,7 +107,7 @@ struct ShardView<true> {
             u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, lane_off, (uint32_t)row_off, kAuxLoadNT));
     }
     __device__ __forceinline__ void store(uint64_t row_off, uint32_t lane_off, u32x4 v) const {
-        __builtin_amdgcn_raw_buffer_store_b128(v, rs, lane_off, (uint32_t)row_off, kAuxStoreSC01);
+        __builtin_amdgcn_raw_buffer_store_b128(v, rs, lane_off, (uint32_t)row_off, kAuxStoreNT);
     }
 };
 

@@ -124,4 +124,59 @@ constexpr RdpPlan make_rdp_plan(int P, int K, int e0, int e1) {
     return pl;
 }
 
+// ---------------------------------------------------------------- XOR schedule
+// The outputs of one pattern share most of their inputs (a decode chain
+// rebuilds each cell from a neighbour's equation), so an output is cheapest as
+// an earlier output XOR the cells where the two masks differ.  The order and
+// bases form a minimum spanning tree (Prim) over the outputs plus a zero root,
+// with edge weight = XORs needed: popcount(mask) - 1 from the root,
+// popcount(mask_a ^ mask_b) between outputs.  For the p = 7 data pairs this
+// takes the expanded map's ~200 cell terms per lane down to about a third.
+struct RdpSched {
+    int order[kRdpMaxOut];              // outputs in computation order
+    int base[kRdpMaxOut];               // per output: the earlier output it extends, or -1
+    uint64_t dmask[kRdpMaxOut][kRdpNW]; // per output: cells XORed onto its base
+};
+
+constexpr int mask_pop(const uint64_t* m) {
+    int n = 0;
+    for (int w = 0; w < kRdpNW; ++w) n += __builtin_popcountll(m[w]);
+    return n;
+}
+
+constexpr int mask_dist(const uint64_t* a, const uint64_t* b) {
+    int n = 0;
+    for (int w = 0; w < kRdpNW; ++w) n += __builtin_popcountll(a[w] ^ b[w]);
+    return n;
+}
+
+constexpr RdpSched make_rdp_sched(const RdpPlan& pl) {
+    RdpSched s{};
+    bool done[kRdpMaxOut] = {};
+    int cost[kRdpMaxOut] = {}, par[kRdpMaxOut] = {};
+    for (int o = 0; o < pl.nout; ++o) {
+        cost[o] = mask_pop(pl.mask[o]) - 1;
+        par[o] = -1;
+    }
+    for (int step = 0; step < pl.nout; ++step) {
+        int o = -1;
+        for (int i = 0; i < pl.nout; ++i)
+            if (!done[i] && (o < 0 || cost[i] < cost[o])) o = i;
+        done[o] = true;
+        s.order[step] = o;
+        s.base[o] = par[o];
+        for (int w = 0; w < kRdpNW; ++w)
+            s.dmask[o][w] = par[o] < 0 ? pl.mask[o][w] : pl.mask[o][w] ^ pl.mask[par[o]][w];
+        for (int i = 0; i < pl.nout; ++i)
+            if (!done[i]) {
+                const int c = mask_dist(pl.mask[i], pl.mask[o]);
+                if (c < cost[i]) {
+                    cost[i] = c;
+                    par[i] = o;
+                }
+            }
+    }
+    return s;
+}
+
 }  // namespace kvec

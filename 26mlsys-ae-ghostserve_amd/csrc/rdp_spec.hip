@@ -18,95 +18,107 @@
 namespace kvec {
 
 // ---------------------------------------------------------------- encode
-// A block of kBS threads covers kBS*V consecutive 16-byte lane offsets of
-// every row plane (V = 2 for p <= 7, 1 above to bound register use); each
-// load instruction of a wave reads 1 KiB contiguous from one row plane.
-constexpr int kBS = 128;
-constexpr int rdp_vec(int P) { return P <= 7 ? 2 : 1; }
+// A thread owns one 16-byte lane offset; a block is one wave, so each load
+// instruction reads 1 KiB contiguous from one row plane.  Memory-level
+// parallelism comes from each thread requesting many cells before folding any
+// of them in: the cells of rdp_group(p, k) shards (all k*(p-1) cells for p <= 7) are
+// issued back to back, and a scheduling barrier keeps the compiler from
+// interleaving the XORs with them, which it otherwise does to lower register
+// use, waiting on each load in turn.  Two waves per SIMD leave room for the
+// 36 in-flight cells of p = 7 (144 VGPRs) beside the 12 accumulators.
+constexpr int kBS = 64;
+
+// Shards whose cells are requested together: every shard while their cells
+// and the 2(p-1) accumulators fit in about 200 VGPRs.
+constexpr int rdp_group(int P, int K) {
+    const int g = (50 - 2 * (P - 1)) / (P - 1);
+    return g < 1 ? 1 : (g > K ? K : g);
+}
 
 template <int P, int K, bool BUF>
-__global__ __launch_bounds__(kBS) void rdp_encode_kernel(RdpPtrs d, uint8_t* __restrict__ Pp,
-                                                         uint8_t* __restrict__ Qp, uint64_t R,
-                                                         uint32_t nvec) {
-    constexpr int ROWS = P - 1, V = rdp_vec(P);
+__global__ __launch_bounds__(kBS) __attribute__((amdgpu_waves_per_eu(1, 2))) void rdp_encode_kernel(
+        RdpPtrs d, uint8_t* __restrict__ Pp, uint8_t* __restrict__ Qp, uint64_t R, uint32_t nvec) {
+    constexpr int ROWS = P - 1, G = rdp_group(P, K);
     const uint64_t nb = ROWS * R;
-    const uint32_t u0 = blockIdx.x * (kBS * V) + threadIdx.x;
-    u32x4 pr[V][ROWS], q[V][ROWS];
+    const uint32_t u = blockIdx.x * kBS + threadIdx.x;
+    if (u >= nvec) return;
+    const uint32_t off = u << 4;
+    Xor3Acc pr[ROWS], q[ROWS];
 #pragma unroll
-    for (int v = 0; v < V; ++v)
+    for (int j0 = 0; j0 < K; j0 += G) {
+        u32x4 x[G][ROWS];
 #pragma unroll
-        for (int r = 0; r < ROWS; ++r) {
-            pr[v][r] = u32x4{0, 0, 0, 0};
-            q[v][r] = u32x4{0, 0, 0, 0};
+        for (int g = 0; g < G; ++g) {
+            if (j0 + g >= K) break;
+            const ShardView<BUF> sv(d.p[j0 + g], nb);
+#pragma unroll
+            for (int r = 0; r < ROWS; ++r) x[g][r] = sv.load(r * R, off);
         }
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int j = 0; j < K; ++j) {
-        const ShardView<BUF> sv(d.p[j], nb);
+        for (int g = 0; g < G; ++g) {
+            const int j = j0 + g;
+            if (j >= K) break;
 #pragma unroll
-        for (int r = 0; r < ROWS; ++r)
-#pragma unroll
-            for (int v = 0; v < V; ++v) {
-                const uint32_t u = u0 + v * kBS;
-                // lanes past the end read the plane start; their sums are dropped
-                const u32x4 x = sv.load(r * R, (u < nvec ? u : 0u) << 4);
-                pr[v][r] ^= x;
+            for (int r = 0; r < ROWS; ++r) {
+                pr[r].add(x[g][r]);
                 const int dg = (r + j) % P;
-                if (dg != P - 1) q[v][dg] ^= x;
+                if (dg != P - 1) q[dg].add(x[g][r]);
             }
+        }
+        // keep the next group's loads behind this fold (bounds register use)
+        if constexpr (G < K) __builtin_amdgcn_sched_barrier(0);
     }
     const ShardView<BUF> sp(Pp, nb), sq(Qp, nb);
 #pragma unroll
-    for (int v = 0; v < V; ++v) {
-        const uint32_t u = u0 + v * kBS;
-        if (u >= nvec) continue;
-        // P cell of row r lies on diagonal (r + p - 1) % p = r - 1.
-#pragma unroll
-        for (int r = 1; r < ROWS; ++r) q[v][r - 1] ^= pr[v][r];
-#pragma unroll
-        for (int r = 0; r < ROWS; ++r) {
-            sp.store(r * R, u << 4, pr[v][r]);
-            sq.store(r * R, u << 4, q[v][r]);
-        }
+    for (int r = 0; r < ROWS; ++r) {
+        const u32x4 pv = pr[r].get();
+        sp.store(r * R, off, pv);
+        // The P cell of row r lies on diagonal (r + p - 1) % p = r - 1.
+        if (r >= 1) q[r - 1].add(pv);
     }
+#pragma unroll
+    for (int r = 0; r < ROWS; ++r) sq.store(r * R, off, q[r].get());
 }
 
 // ---------------------------------------------------------------- decode
+// Same shape as the encode: every surviving cell the plan needs (36 for a
+// p = 7 pair) is requested before the XOR network runs.  The network follows
+// the pattern's schedule (rdp_plan.h): each output extends an earlier one by
+// the cells where their maps differ.
 template <int P, int K, int E0, int E1, bool BUF>
-__global__ __launch_bounds__(kBS) void rdp_decode_kernel(RdpPtrs sh, uint64_t R, uint32_t nvec) {
-    constexpr int ROWS = P - 1, V = rdp_vec(P);
+__global__ __launch_bounds__(kBS) __attribute__((amdgpu_waves_per_eu(1, 2))) void rdp_decode_kernel(
+        RdpPtrs sh, uint64_t R, uint32_t nvec) {
+    constexpr int ROWS = P - 1;
     constexpr int NC = (K + 2) * ROWS;
     constexpr RdpPlan plan = make_rdp_plan(P, K, E0, E1);
     static_assert(plan.ok, "RDP erasure pattern not decodable");
     const uint64_t nb = ROWS * R;
-    const uint32_t u0 = blockIdx.x * (kBS * V) + threadIdx.x;
-    u32x4 acc[V][plan.nout];
-#pragma unroll
-    for (int v = 0; v < V; ++v)
-#pragma unroll
-        for (int o = 0; o < plan.nout; ++o) acc[v][o] = u32x4{0, 0, 0, 0};
+    const uint32_t u = blockIdx.x * kBS + threadIdx.x;
+    if (u >= nvec) return;
+    const uint32_t off = u << 4;
+    u32x4 x[NC];
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
         if (!((plan.need[c >> 6] >> (c & 63)) & 1)) continue;
-        const ShardView<BUF> sv(sh.p[c / ROWS], nb);
+        x[c] = ShardView<BUF>(sh.p[c / ROWS], nb).load((c % ROWS) * R, off);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    constexpr RdpSched sch = make_rdp_sched(plan);
+    u32x4 acc[plan.nout];
 #pragma unroll
-        for (int v = 0; v < V; ++v) {
-            const uint32_t u = u0 + v * kBS;
-            const u32x4 x = sv.load((c % ROWS) * R, (u < nvec ? u : 0u) << 4);
+    for (int i = 0; i < plan.nout; ++i) {
+        const int o = sch.order[i];
+        Xor3Acc a(sch.base[o] < 0 ? u32x4{0, 0, 0, 0} : acc[sch.base[o]]);
 #pragma unroll
-            for (int o = 0; o < plan.nout; ++o)
-                if ((plan.mask[o][c >> 6] >> (c & 63)) & 1) acc[v][o] ^= x;
-        }
+        for (int c = 0; c < NC; ++c)
+            if ((sch.dmask[o][c >> 6] >> (c & 63)) & 1) a.add(x[c]);
+        acc[o] = a.get();
     }
 #pragma unroll
-    for (int v = 0; v < V; ++v) {
-        const uint32_t u = u0 + v * kBS;
-        if (u >= nvec) continue;
-#pragma unroll
-        for (int o = 0; o < plan.nout; ++o) {
-            const int c = plan.out_cell[o];
-            const ShardView<BUF> sv(sh.p[c / ROWS], nb);
-            sv.store((c % ROWS) * R, u << 4, acc[v][o]);
-        }
+    for (int o = 0; o < plan.nout; ++o) {
+        const int c = plan.out_cell[o];
+        ShardView<BUF>(sh.p[c / ROWS], nb).store((c % ROWS) * R, off, acc[o]);
     }
 }
 
@@ -190,9 +202,7 @@ static DecFn decode_fn(int p, int k, int e0, int e1) {
     return nullptr;
 }
 
-static unsigned rdp_grid(uint32_t nvec, int p) {
-    return blocks_for(nvec, kBS * rdp_vec(p));
-}
+static unsigned rdp_grid(uint32_t nvec) { return blocks_for(nvec, kBS); }
 
 static int check_geom(int k, int p, int64_t row_bytes, const char* fn) {
     if (!is_prime(p) || p < 3) return set_error(KVEC_EINVAL, "%s: p=%d is not an odd prime", fn, p);
@@ -228,7 +238,7 @@ extern "C" int kvec_rdp_encode(const void* const* data, int k, void* P, void* Q,
     EncFn fn = buf ? encode_fn<true>(p, k) : encode_fn<false>(p, k);
     if (!fn) return set_error(KVEC_EUNSUPPORTED, "kvec_rdp_encode: p=%d k=%d not built", p, k);
     const uint32_t nvec = uint32_t(row_bytes / 16);
-    hipLaunchKernelGGL(fn, dim3(rdp_grid(nvec, p)), dim3(kBS), 0, as_stream(stream), d,
+    hipLaunchKernelGGL(fn, dim3(rdp_grid(nvec)), dim3(kBS), 0, as_stream(stream), d,
                        (uint8_t*)P, (uint8_t*)Q, uint64_t(row_bytes), nvec);
     return check_launch("kvec_rdp_encode");
 }
@@ -256,7 +266,7 @@ extern "C" int kvec_rdp_decode(void* const* shards, int k, int p, int64_t row_by
     const bool buf = fits_buffer(uint64_t(p - 1) * uint64_t(row_bytes));
     DecFn fn = buf ? decode_fn(p, k, a, b) : nullptr;
     if (fn) {
-        hipLaunchKernelGGL(fn, dim3(rdp_grid(nvec, p)), dim3(kBS), 0, as_stream(stream), s,
+        hipLaunchKernelGGL(fn, dim3(rdp_grid(nvec)), dim3(kBS), 0, as_stream(stream), s,
                            uint64_t(row_bytes), nvec);
     } else {
         const dim3 grid(blocks_for(nvec, kBS)), block(kBS);

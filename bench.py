@@ -136,15 +136,22 @@ def decode_all_pairs(pkg, torch, sets, R, seed):
             if not (torch.equal(shards[a], keep[0]) and torch.equal(shards[b], keep[1])):
                 raise RuntimeError(f"RDP decode of pair ({a}, {b}) is not byte-exact")
             del keep
+        # decoding a consistent stripe set rewrites the same bytes, so the
+        # launches can repeat; two untimed ones first let the write-back of
+        # the clones and fills above drain before the timed ones
+        for i in range(2):
+            data, P, Q = sets[i % 2]
+            pkg.spec.rdp_decode(list(data) + [P, Q], P_RDP, [a, b], R)
+        torch.cuda.synchronize()
         e0 = torch.cuda.Event(enable_timing=True)
         e1 = torch.cuda.Event(enable_timing=True)
         e0.record(stream)
-        for i in range(4):
+        for i in range(8):
             data, P, Q = sets[i % 2]
             pkg.spec.rdp_decode(list(data) + [P, Q], P_RDP, [a, b], R)
         e1.record(stream)
         torch.cuda.synchronize()
-        times[(a, b)] = e0.elapsed_time(e1) * 1e3 / 4
+        times[(a, b)] = e0.elapsed_time(e1) * 1e3 / 8
     return times
 
 
@@ -201,15 +208,19 @@ def bench_rs8(pkg, torch, oracle, dev, seed, steps, warmup):
             if not all(torch.equal(sh[e], kp) for e, kp in zip(er, keep)):
                 raise RuntimeError(f"RS8 decode of {er} is not byte-exact")
             del keep
+        for i in range(2):      # untimed: drain the write-back of the fills above
+            data, par = sets[i % 2]
+            pkg.spec.rs8_decode(list(data) + list(par), k, er)
+        torch.cuda.synchronize()
         e0 = torch.cuda.Event(enable_timing=True)
         e1 = torch.cuda.Event(enable_timing=True)
         e0.record(stream)
-        for i in range(4):
+        for i in range(8):
             data, par = sets[i % 2]
             pkg.spec.rs8_decode(list(data) + list(par), k, er)
         e1.record(stream)
         torch.cuda.synchronize()
-        dec_us.append(e0.elapsed_time(e1) * 1e3 / 4)
+        dec_us.append(e0.elapsed_time(e1) * 1e3 / 8)
     del sets
     dmean = sum(dec_us) / len(dec_us)
     return {
@@ -669,6 +680,7 @@ def main():
             "frac_hbm_peak": round(ALG_BYTES / dec_us / 1e3 / HBM_PEAK_GBS, 4),
             "slowest_pair": list(worst),
             "slowest_us": round(dec[worst], 2),
+            "per_pair_us": {f"{a},{b}": round(t, 2) for (a, b), t in sorted(dec.items())},
         }
 
     fused = None
