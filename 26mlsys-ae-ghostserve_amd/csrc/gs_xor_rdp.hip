@@ -5,10 +5,8 @@
 //   RDP  benchmark/rdp/kernel.cu:32-345 and bench_ghostserve_rdp.py:105-150
 //
 // The column work runs on the tile engine (tile_engine.h).  The diagonal
-// parity Q[d] = XOR_r D_r[(d - r) mod S] is formed without the per-row star
-// skip; a one-thread fix-up then XORs each row's star word back out of its
-// diagonal, which gives the reference's skip exactly (XOR is its own inverse)
-// without a per-word test in the streaming kernel.
+// parity Q[d] = XOR_r D_r[(d - r) mod S] skips each row's star word in the
+// same pass: the lane whose window holds it masks it before the XOR.
 #include "tile_engine.h"
 
 namespace kvec {
@@ -189,9 +187,125 @@ __device__ __forceinline__ void gs_store_chunk(uint8_t* base, int64_t X, u32x4 v
         if (X + i >= 0 && X + i < lim) d[X + i] = byte_of(v, i);
 }
 
-template <bool FUSED>
+// gs_store_chunk with 32-bit offsets, X >= 0 (row tensors below 2 GiB).
+__device__ __forceinline__ void gs_store_chunk32(uint8_t* base, uint32_t X, u32x4 v, uint32_t lim) {
+    if (X + 16 <= lim) {
+        st16(base + X, v);
+        return;
+    }
+    const gptr<uint8_t> d = as_global(base);
+    for (int i = 0; i < 16; ++i)
+        if (X + i < lim) d[X + i] = byte_of(v, i);
+}
+
+// Buffer-resource view of one source of data-row bytes for the batched path.
+// A voffset at or past 2^31 is out of range (the resources hold < 2^31
+// bytes): such a load returns 0 without touching memory, which lets the wave
+// edge lanes alone fetch their neighbour chunks with no branch around loads.
+constexpr uint32_t kNoLoad = 0x80000000u;
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t gs_rsrc(const void* p, uint32_t n) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)n, (int)kBufWord3);
+}
+
+__device__ __forceinline__ u32x4 gs_load(__amdgpu_buffer_rsrc_t rs, uint32_t voff) {
+    return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, voff, 0, kAuxLoadNT));
+}
+
+// Per data row r < 8: the diagonal its star word lies on, (star_r + r) mod S
+// with star_r = (star_base + r) % S, or -1 when the row skips nothing (C
+// remainder: a negative star_base gives a negative star_r).  The same for
+// every tile, so the host computes it once; the batched path runs only on
+// row tensors below 2 GiB, so it fits 32 bits.
+struct GsStar {
+    int32_t d[8];
+};
+
+// P/Q of one interior tile (not the first, so no diagonal wraps and every
+// chunk offset is positive, and wholly inside the rows) with ND = nd <= 8
+// data rows: each row's chunk, and the edge
+// lanes' neighbour chunks, are all requested before the first is used, so a
+// thread has every row in flight at once.  With nd <= 8 the Q window starts
+// at most 14 bytes before the lane's chunk (mr - 2r >= -14), so the previous
+// lane's chunk always covers it.  Returns false, having loaded nothing, when
+// the tile needs the general path: a fused tile whose K/V/padding boundary
+// falls inside some row's loads.
+template <bool FUSED, int ND>
+__device__ __forceinline__ bool gs_pq_batched(uint16_t* sh, uint32_t Sb, uint32_t t0b, int32_t w0,
+                                              const GsStar& star, const GsSource& g,
+                                              uint32_t rows_bytes, u32x4& p, u32x4& q) {
+    const uint8_t* base = reinterpret_cast<const uint8_t*>(sh);
+    const uint32_t lane = threadIdx.x & 63;
+    const uint32_t b15 = uint32_t(reinterpret_cast<uintptr_t>(base)) & 15;
+    const uint32_t kb = uint32_t(g.kb), copy_end = uint32_t(g.copy_end);
+    // misalignment of row r's tile start, and its lane-0 chunk offset in the rows
+    // (positive: the path does not run on tile 0)
+    auto row_mr = [&](int r) { return (b15 + uint32_t(r) * Sb + t0b) & 15; };
+    auto row_x0 = [&](int r) { return uint32_t(r) * Sb + t0b - row_mr(r); };
+    // source of row r's chunks: 0 the rows, 1 K, 2 V, -1 mixed
+    auto row_src = [&](int r) {
+        if (!FUSED) return 0;
+        const int64_t x0 = row_x0(r), lo = x0 - 16, hi = x0 + kTileBytes + 32;
+        if (hi <= int64_t(kb)) return 1;
+        if (lo >= int64_t(kb) && hi <= 2 * int64_t(kb)) return 2;
+        return lo < 2 * int64_t(kb) ? -1 : 0;
+    };
+    if (FUSED) {
+        bool mixed = false;
+#pragma unroll
+        for (int r = 0; r < ND; ++r) mixed |= row_src(r) < 0;
+        if (mixed) return false;
+    }
+    const __amdgpu_buffer_rsrc_t rrows = gs_rsrc(base, rows_bytes);
+    u32x4 c0[ND], e1[ND], em[ND];
+#pragma unroll
+    for (int r = 0; r < ND; ++r) {
+        const int src = row_src(r);
+        const __amdgpu_buffer_rsrc_t rs =
+            src == 1 ? gs_rsrc(g.K, kb) : (src == 2 ? gs_rsrc(g.V, kb) : rrows);
+        const uint32_t mr = row_mr(r);
+        const int s = int(mr) - 2 * r;
+        const uint32_t my = row_x0(r) - (src == 2 ? kb : 0) + 16 * threadIdx.x;
+        c0[r] = gs_load(rs, my);
+        e1[r] = gs_load(rs, lane == 63 && (mr > 0 || s > 0) ? my + 16 : kNoLoad);
+        em[r] = gs_load(rs, lane == 0 && s < 0 ? my - 16 : kNoLoad);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int r = 0; r < ND; ++r) {
+        const uint32_t mr = row_mr(r);
+        const int s = int(mr) - 2 * r;
+        // the shifts run with every lane active; the edge lanes keep the
+        // chunks they loaded themselves (a per-lane select here was
+        // miscompiled: one funnel case read the shifted value from before
+        // the select, so lane 0 lost its previous chunk)
+        const u32x4 c1 = from_next_lane_or(c0[r], e1[r]), cm = from_prev_lane_or(c0[r], em[r]);
+        if (FUSED) {
+            // this lane's chunk into the data rows (rows read from the row
+            // tensor itself lie past K||V, so their chunks fail the test); the
+            // last thread also stores the chunk past the block, which the
+            // window's last mr bytes fall in
+            const uint32_t X = row_x0(r) + 16 * threadIdx.x;
+            if (X < copy_end) {
+                gs_store_chunk32(reinterpret_cast<uint8_t*>(sh), X, c0[r], copy_end);
+                if (mr > 0 && threadIdx.x == kTB - 1)
+                    gs_store_chunk32(reinterpret_cast<uint8_t*>(sh), X + 16, c1, copy_end);
+            }
+        }
+        p ^= mr ? funnel16(c0[r], c1, mr) : c0[r];
+        u32x4 qw;
+        if (s > 0) qw = funnel16(c0[r], c1, uint32_t(s));
+        else if (s == 0) qw = c0[r];
+        else qw = funnel16(cm, c0[r], uint32_t(s + 16));
+        q ^= star.d[r] < 0 ? qw : drop_word(qw, int64_t(star.d[r]) - w0);
+    }
+    return true;
+}
+
+template <bool FUSED, int ND>
 __global__ __launch_bounds__(kTB) void gs_rdp_parity_kernel(uint16_t* sh, int nd, int64_t S,
-                                                            int star_base, GsSource g) {
+                                                            int star_base, GsSource g,
+                                                            uint64_t rows_bytes, GsStar star) {
     __shared__ __attribute__((aligned(16))) uint8_t tp[kTileBytes + 16];
     __shared__ __attribute__((aligned(16))) uint8_t tq[kTileBytes + 16];
     const uint8_t* base = reinterpret_cast<const uint8_t*>(sh);
@@ -203,7 +317,17 @@ __global__ __launch_bounds__(kTB) void gs_rdp_parity_kernel(uint16_t* sh, int nd
     const uint32_t lane = threadIdx.x & 63;
     const bool fast = w0 + 8 <= S && w0 >= nd - 1;
     u32x4 p = {0, 0, 0, 0}, q = {0, 0, 0, 0};
-    for (int r = 0; r < nd; ++r) {
+    // Interior tiles of small stripes: every row requested at once.  The
+    // general loop below handles the two end tiles, nd > 8, rows tensors of
+    // 2 GiB or more and fused tiles next to a K/V boundary.
+    bool batched = false;
+    if constexpr (ND > 0) {
+        const int64_t t0w = int64_t(blockIdx.x) * (kTileBytes / 2);
+        if (rows_bytes && blockIdx.x > 0 && t0w + kTileBytes / 2 <= S)
+            batched = gs_pq_batched<FUSED, ND>(sh, uint32_t(Sb), uint32_t(t0b), int32_t(w0), star, g,
+                                               uint32_t(rows_bytes), p, q);
+    }
+    for (int r = 0; r < (batched ? 0 : nd); ++r) {
         const uint8_t* A0 = base + uint64_t(r) * Sb + t0b;
         const uint32_t mr = uint32_t(reinterpret_cast<uintptr_t>(A0) & 15);
         const int s = int(mr) - 2 * r;   // Q window offset from my, in [-2(nd-1), 15]
@@ -272,7 +396,7 @@ __global__ __launch_bounds__(kTB) void gs_rdp_parity_kernel(uint16_t* sh, int nd
             q ^= star < 0 ? qw : drop_word(qw, cmod(star + r, S) - w0);
         }
     }
-    if (!fast && w0 < S) {
+    if (!batched && !fast && w0 < S) {
         const int n = int(S - w0 < 8 ? S - w0 : 8);
         for (int i = 0; i < n; ++i) {
             uint16_t a = 0, b = 0;
@@ -314,16 +438,38 @@ static int copy_d2d(void* dst, const void* src, uint64_t n, hipStream_t st, cons
     return KVEC_OK;
 }
 
+typedef void (*GsParityFn)(uint16_t*, int, int64_t, int, GsSource, uint64_t, GsStar);
+
+template <bool FUSED, int ND = 1>
+GsParityFn gs_parity_fn(int nd) {
+    if constexpr (ND > 8) {
+        return &gs_rdp_parity_kernel<FUSED, 0>;
+    } else {
+        if (nd == ND) return &gs_rdp_parity_kernel<FUSED, ND>;
+        return gs_parity_fn<FUSED, ND + 1>(nd);
+    }
+}
+
 static int gs_rdp_parity(uint16_t* sh, int nd, int64_t S, int star_base, hipStream_t st,
                          const char* what, const GsSource* fused = nullptr) {
     if (nd <= 0 || S <= 0) return KVEC_OK;  // the reference kernel returns at once
     const dim3 grid(blocks_for(S * 2, kTileBytes));
+    // The batched path addresses the rows (and K, V) through buffer resources
+    // whose out-of-range loads must start at 2^31: 0 switches it off.
+    const uint64_t rows_bytes = uint64_t(nd + 2) * uint64_t(S) * 2;
+    const bool small = rows_bytes < (uint64_t(1) << 31) && (!fused || fused->kb < (int64_t(1) << 31));
+    const uint64_t rb = small ? rows_bytes : 0;
+    GsStar star{};
+    for (int r = 0; r < 8; ++r) {
+        const int64_t sr = (int64_t(star_base) + r) % S;
+        star.d[r] = sr < 0 ? -1 : int32_t((sr + r) % S);
+    }
     if (fused)
-        hipLaunchKernelGGL(gs_rdp_parity_kernel<true>, grid, dim3(kTB), 0, st, sh, nd, S, star_base,
-                           *fused);
+        hipLaunchKernelGGL(gs_parity_fn<true>(nd), grid, dim3(kTB), 0, st, sh, nd, S, star_base, *fused, rb,
+                           star);
     else
-        hipLaunchKernelGGL(gs_rdp_parity_kernel<false>, grid, dim3(kTB), 0, st, sh, nd, S, star_base,
-                           GsSource{nullptr, nullptr, 0, 0, 0});
+        hipLaunchKernelGGL(gs_parity_fn<false>(nd), grid, dim3(kTB), 0, st, sh, nd, S, star_base,
+                           GsSource{nullptr, nullptr, 0, 0, 0}, rb, star);
     return check_launch(what);
 }
 

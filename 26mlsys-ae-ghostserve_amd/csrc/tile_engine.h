@@ -48,6 +48,23 @@ __device__ __forceinline__ u32x4 from_prev_lane(u32x4 v) {
                  uint32_t(__builtin_amdgcn_update_dpp(0, int(v.w), 0x138, 0xF, 0xF, false))};
 }
 
+// The same shifts with the lane whose source is outside the wave (63 for
+// from_next_lane_or, 0 for from_prev_lane_or) taking `edge` instead of 0: DPP
+// leaves the destination's old value in a lane with no source lane, and the
+// old value is `edge`.  One instruction per dword and no per-lane select.
+__device__ __forceinline__ u32x4 from_next_lane_or(u32x4 v, u32x4 edge) {
+    return u32x4{uint32_t(__builtin_amdgcn_update_dpp(int(edge.x), int(v.x), 0x130, 0xF, 0xF, false)),
+                 uint32_t(__builtin_amdgcn_update_dpp(int(edge.y), int(v.y), 0x130, 0xF, 0xF, false)),
+                 uint32_t(__builtin_amdgcn_update_dpp(int(edge.z), int(v.z), 0x130, 0xF, 0xF, false)),
+                 uint32_t(__builtin_amdgcn_update_dpp(int(edge.w), int(v.w), 0x130, 0xF, 0xF, false))};
+}
+__device__ __forceinline__ u32x4 from_prev_lane_or(u32x4 v, u32x4 edge) {
+    return u32x4{uint32_t(__builtin_amdgcn_update_dpp(int(edge.x), int(v.x), 0x138, 0xF, 0xF, false)),
+                 uint32_t(__builtin_amdgcn_update_dpp(int(edge.y), int(v.y), 0x138, 0xF, 0xF, false)),
+                 uint32_t(__builtin_amdgcn_update_dpp(int(edge.z), int(v.z), 0x138, 0xF, 0xF, false)),
+                 uint32_t(__builtin_amdgcn_update_dpp(int(edge.w), int(v.w), 0x138, 0xF, 0xF, false))};
+}
+
 // A pointer that every lane holds the same value of, moved to scalar
 // registers: offsets and shifts derived from it are then wave-uniform, so a
 // switch on them is a scalar branch rather than per-lane selects.

@@ -338,3 +338,52 @@ def test_rs16_forward_backward_round_trip(pkg, ora, gpu, k, m):
         assert torch.equal(vr.view(torch.int16), V.view(torch.int16)), missing
     with pytest.raises(RuntimeError):
         pkg.rs.backwards_decode_kv(shards.clone(), meta, list(range(m + 1)))
+
+
+# ---------------------------------------------------- P/Q interior tiles
+# Interior tiles of stripes with nd <= 8 data rows take a path that requests
+# every row's chunk at once: cover every nd there, row tensors whose start is
+# 0 or 6 bytes past a 16-byte boundary, rows of odd length (every row
+# misaligned differently), star words inside interior tiles, no star skip,
+# and fused backups whose K/V and V/padding boundaries cross interior tiles.
+@pytest.mark.parametrize("nd", range(1, 9))
+@pytest.mark.parametrize("soff", [0, 3])
+@pytest.mark.parametrize("S,sb", [(12295, 4100), (10000, -1), (4096 * 4, 9000)])
+def test_gs_parity_interior_tiles(pkg, ora, gpu, nd, soff, S, sb):
+    rng = np.random.default_rng(nd * 131 + soff * 7 + S)
+    rows = rng.integers(0, 65536, (nd + 2, S), dtype=np.uint16)
+    want = rows.copy()
+    ora.gs_parity(want, nd, S, sb)
+    buf = torch.full(((nd + 2) * S + 16,), 0x3C3C, dtype=torch.int16, device=gpu)
+    buf[soff:soff + (nd + 2) * S] = dev(rows.reshape(-1).view(np.int16), gpu)
+    d = buf[soff:soff + (nd + 2) * S].view(nd + 2, S)
+    pkg.rdp_kv_ops.compute_rdp_parity(d.view(torch.uint16), nd, S, sb)
+    assert np.array_equal(d.cpu().numpy().view(np.uint16), want)
+    assert bool((torch.cat([buf[:soff], buf[soff + (nd + 2) * S:]]) == 0x3C3C).all())
+
+
+@pytest.mark.parametrize("nd", range(1, 9))
+@pytest.mark.parametrize("soff,S_extra", [(0, 0), (5, 2500), (3, 7000)])
+def test_gs_backup_interior_tiles(pkg, ora, gpu, nd, soff, S_extra):
+    T, n, sb = 96, 211, 2050
+    tn = T * n
+    S = -(-2 * tn // nd) + S_extra
+    koff, voff = soff, (soff + tn) % 8      # the alignment the fused pack needs
+    rng = np.random.default_rng(nd * 17 + soff)
+    K = rng.integers(0, 65536, tn, dtype=np.uint16)
+    V = rng.integers(0, 65536, tn, dtype=np.uint16)
+    init = np.zeros((nd + 2, S), dtype=np.uint16)
+    want = init.copy()
+    ora.gs_pack(K.reshape(T, n), V.reshape(T, n), want, nd, S, T, n)
+    ora.gs_parity(want, nd, S, sb)
+    kb = torch.zeros(tn + 16, dtype=torch.int16, device=gpu)
+    vb = torch.zeros(tn + 16, dtype=torch.int16, device=gpu)
+    kb[koff:koff + tn] = dev(K.view(np.int16), gpu)
+    vb[voff:voff + tn] = dev(V.view(np.int16), gpu)
+    sbuf = torch.full(((nd + 2) * S + 16,), 0x5A5A, dtype=torch.int16, device=gpu)
+    sbuf[soff:soff + (nd + 2) * S] = 0
+    sh = sbuf[soff:soff + (nd + 2) * S].view(nd + 2, S)
+    pkg.rdp.rdp_kernel.fused_backup_full_kv(kb[koff:koff + tn].view(T, n), vb[voff:voff + tn].view(T, n),
+                                            sh.view(torch.uint16), nd, S, T, n, sb)
+    assert np.array_equal(sh.cpu().numpy().view(np.uint16), want)
+    assert bool((torch.cat([sbuf[:soff], sbuf[soff + (nd + 2) * S:]]) == 0x5A5A).all())
