@@ -173,7 +173,7 @@ __device__ __forceinline__ void rs_mix_full(const RsJob& j, const uint32_t (*pta
 #pragma unroll
         for (int n = 0; n < NW; ++n) {
             x[n] = win_join(rw, lo[n], hi[n]);
-            if (copy) copy_owned(j.copy, rw, 16 * (threadIdx.x + n * kTB), lo[n], hi[n]);
+            if (copy) copy_owned<false>(j.copy, rw, 16 * (threadIdx.x + n * kTB), lo[n], hi[n]);
         }
         if (i + 1 < nin) {
             rw = row_win(reinterpret_cast<const uint8_t*>(j.in_rows[i + 1]) + t0b);

@@ -39,17 +39,74 @@ __device__ __forceinline__ u32x4 xor_rows_partial(const uint8_t* in, uint64_t Sb
     return acc;
 }
 
+// Whether a whole tile of `rs` can take the batched path with ND rows: rows
+// 0..ND-1 (encode, or P recomputed), or rows 0..ND minus one data row (a data
+// row rebuilt from P), in an `in` tensor of in_bytes < 2^31 (0: never).
+template <int ND>
+__device__ __forceinline__ bool xor_rows_batchable(RowSet rs, uint32_t in_bytes) {
+    if (ND == 0 || in_bytes == 0 || rs.lo != 0 || rs.hi != ND) return false;
+    return (rs.skip < 0 && rs.extra < 0) || (rs.skip >= 0 && rs.skip < ND && rs.extra == ND);
+}
+
+// XOR of the ND rows of one whole tile with every row's chunk requested at
+// once.  Row i of the batch is row i of `in`, or i + 1 from the skipped row
+// on.  Each lane loads its aligned chunk of the row; the next chunk, which a
+// misaligned window reaches into, is the next lane's (DPP), and lane 63 loads
+// it itself (other lanes' edge loads are out of range and read nothing).
+// Offsets are taken from `in` rounded down to 16 bytes, so they are never
+// negative, and the resource reaches to the end of the last 16-byte chunk
+// holding a byte of `in`.  With fc.dst set, the owned chunks are copied as in
+// the general path.
+template <int ND>
+__device__ __forceinline__ u32x4 xor_rows_batched(const uint8_t* in, uint32_t Sb, uint32_t in_bytes,
+                                                  RowSet rs, const FlatCopy& fc) {
+    const uint32_t b15 = uint32_t(reinterpret_cast<uintptr_t>(in)) & 15;
+    const uint8_t* in_al = in - b15;
+    const __amdgpu_buffer_rsrc_t rsin = chunk_rsrc(in_al, (b15 + in_bytes + 15) & ~15u);
+    const uint32_t t0 = blockIdx.x * uint32_t(kTileBytes);
+    const uint32_t lane = threadIdx.x & 63;
+    auto row_a = [&](int i) {   // tile start of batch row i, from in_al
+        const uint32_t j = uint32_t(i + (rs.skip >= 0 && i >= rs.skip ? 1 : 0));
+        return b15 + j * Sb + t0;
+    };
+    u32x4 lo[ND], e1[ND];
+#pragma unroll
+    for (int i = 0; i < ND; ++i) {
+        const uint32_t A = row_a(i), sh = A & 15;
+        const uint32_t my = A - sh + 16 * threadIdx.x;
+        lo[i] = chunk_load(rsin, my);
+        e1[i] = chunk_load(rsin, lane == 63 && sh ? my + 16 : kNoLoad);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    u32x4 acc = {0, 0, 0, 0};
+#pragma unroll
+    for (int i = 0; i < ND; ++i) {
+        const uint32_t A = row_a(i), sh = A & 15;
+        const u32x4 hi = from_next_lane_or(lo[i], e1[i]);
+        acc ^= sh ? funnel16(lo[i], hi, sh) : lo[i];
+        if (fc.dst) {
+            const uint8_t* c = in_al + (A - sh) + 16 * threadIdx.x;
+            if (sh) copy_chunk(fc, c + 16, hi);
+            else copy_chunk(fc, c, lo[i]);
+        }
+    }
+    return acc;
+}
+
 // One tile of XOR-of-rows, written to up to two outputs (row base addresses).
 // With fc.dst set, rows lo..hi-1 of `in` (the whole flat range of fc, no
 // skip) are also copied to fc.dst by the same loads.
-__device__ __forceinline__ void xor_rows_tile(const uint8_t* in, uint64_t Sb, RowSet rs,
-                                              uint8_t* out0, uint8_t* out1, const FlatCopy& fc,
-                                              uint8_t* tile) {
+template <int ND>
+__device__ __forceinline__ void xor_rows_tile(const uint8_t* in, uint64_t Sb, uint32_t in_bytes,
+                                              RowSet rs, uint8_t* out0, uint8_t* out1,
+                                              const FlatCopy& fc, uint8_t* tile) {
     const uint64_t t0 = uint64_t(blockIdx.x) * kTileBytes;
     const uint32_t nbytes = uint32_t(Sb - t0 < uint64_t(kTileBytes) ? Sb - t0 : kTileBytes);
     const uint64_t c0 = t0 + 16 * threadIdx.x;
     u32x4 acc = {0, 0, 0, 0};
-    if (t0 + kTileBytes <= Sb) {
+    if (t0 + kTileBytes <= Sb && xor_rows_batchable<ND>(rs, in_bytes)) {
+        if constexpr (ND > 0) acc = xor_rows_batched<ND>(in, uint32_t(Sb), in_bytes, rs, fc);
+    } else if (t0 + kTileBytes <= Sb) {
         // whole tile inside the rows: uniform row windows, loads carry the copy
         const uint32_t off = 16 * threadIdx.x;
         for (int r = rs.lo; r < rs.hi; ++r) {
@@ -79,18 +136,22 @@ __device__ __forceinline__ void xor_rows_tile(const uint8_t* in, uint64_t Sb, Ro
     if (out1) tile_store(out1 + t0, tile, nbytes);
 }
 
-__global__ __launch_bounds__(kTB) void xor_rows_kernel(const uint8_t* in, uint64_t Sb, RowSet rs,
-                                                       uint8_t* out0, uint8_t* out1, FlatCopy fc) {
+template <int ND>
+__global__ __launch_bounds__(kTB) void xor_rows_kernel(const uint8_t* in, uint64_t Sb, uint32_t in_bytes,
+                                                       RowSet rs, uint8_t* out0, uint8_t* out1,
+                                                       FlatCopy fc) {
     __shared__ __attribute__((aligned(16))) uint8_t tile[kTileBytes + 16];
-    xor_rows_tile(in, Sb, rs, out0, out1, fc, tile);
+    xor_rows_tile<ND>(in, Sb, in_bytes, rs, out0, out1, fc, tile);
 }
 
 // benchmark/xor/kernel.cu:47-88 with the missing index read on the device:
 // data row m < nd is P ^ the other data rows; m == nd recomputes P; anything
 // else leaves every buffer untouched.
+template <int ND>
 __global__ __launch_bounds__(kTB) void xor_reconstruct_kernel(const uint8_t* enc, uint8_t* rec,
                                                               uint8_t* rec_missing, uint64_t Sb,
-                                                              int nd, const int32_t* missing_idx) {
+                                                              uint32_t in_bytes, int nd,
+                                                              const int32_t* missing_idx) {
     __shared__ __attribute__((aligned(16))) uint8_t tile[kTileBytes + 16];
     const int m = __builtin_amdgcn_readfirstlane(missing_idx[0]);
     RowSet rs;
@@ -100,8 +161,8 @@ __global__ __launch_bounds__(kTB) void xor_reconstruct_kernel(const uint8_t* enc
         rs = RowSet{0, nd, -1, -1};
     else
         return;
-    xor_rows_tile(enc, Sb, rs, rec + uint64_t(m) * Sb, rec_missing, FlatCopy{nullptr, nullptr, 0},
-                  tile);
+    xor_rows_tile<ND>(enc, Sb, in_bytes, rs, rec + uint64_t(m) * Sb, rec_missing,
+                      FlatCopy{nullptr, nullptr, 0}, tile);
 }
 
 // ----------------------------------------------------------------- gs RDP P/Q
@@ -179,7 +240,7 @@ __device__ __forceinline__ u32x4 gs_src_chunk_bytes(const GsSource& g, const uin
 // Store the parts of the chunk at row offset X that lie in [0, lim).
 __device__ __forceinline__ void gs_store_chunk(uint8_t* base, int64_t X, u32x4 v, int64_t lim) {
     if (X >= 0 && X + 16 <= lim) {
-        st16(base + X, v);
+        st_stream(base, X, v);
         return;
     }
     const gptr<uint8_t> d = as_global(base);
@@ -190,26 +251,12 @@ __device__ __forceinline__ void gs_store_chunk(uint8_t* base, int64_t X, u32x4 v
 // gs_store_chunk with 32-bit offsets, X >= 0 (row tensors below 2 GiB).
 __device__ __forceinline__ void gs_store_chunk32(uint8_t* base, uint32_t X, u32x4 v, uint32_t lim) {
     if (X + 16 <= lim) {
-        st16(base + X, v);
+        st_stream(base, X, v);
         return;
     }
     const gptr<uint8_t> d = as_global(base);
     for (int i = 0; i < 16; ++i)
         if (X + i < lim) d[X + i] = byte_of(v, i);
-}
-
-// Buffer-resource view of one source of data-row bytes for the batched path.
-// A voffset at or past 2^31 is out of range (the resources hold < 2^31
-// bytes): such a load returns 0 without touching memory, which lets the wave
-// edge lanes alone fetch their neighbour chunks with no branch around loads.
-constexpr uint32_t kNoLoad = 0x80000000u;
-
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t gs_rsrc(const void* p, uint32_t n) {
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)n, (int)kBufWord3);
-}
-
-__device__ __forceinline__ u32x4 gs_load(__amdgpu_buffer_rsrc_t rs, uint32_t voff) {
-    return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, voff, 0, kAuxLoadNT));
 }
 
 // Per data row r < 8: the diagonal its star word lies on, (star_r + r) mod S
@@ -256,19 +303,19 @@ __device__ __forceinline__ bool gs_pq_batched(uint16_t* sh, uint32_t Sb, uint32_
         for (int r = 0; r < ND; ++r) mixed |= row_src(r) < 0;
         if (mixed) return false;
     }
-    const __amdgpu_buffer_rsrc_t rrows = gs_rsrc(base, rows_bytes);
+    const __amdgpu_buffer_rsrc_t rrows = chunk_rsrc(base, rows_bytes);
     u32x4 c0[ND], e1[ND], em[ND];
 #pragma unroll
     for (int r = 0; r < ND; ++r) {
         const int src = row_src(r);
         const __amdgpu_buffer_rsrc_t rs =
-            src == 1 ? gs_rsrc(g.K, kb) : (src == 2 ? gs_rsrc(g.V, kb) : rrows);
+            src == 1 ? chunk_rsrc(g.K, kb) : (src == 2 ? chunk_rsrc(g.V, kb) : rrows);
         const uint32_t mr = row_mr(r);
         const int s = int(mr) - 2 * r;
         const uint32_t my = row_x0(r) - (src == 2 ? kb : 0) + 16 * threadIdx.x;
-        c0[r] = gs_load(rs, my);
-        e1[r] = gs_load(rs, lane == 63 && (mr > 0 || s > 0) ? my + 16 : kNoLoad);
-        em[r] = gs_load(rs, lane == 0 && s < 0 ? my - 16 : kNoLoad);
+        c0[r] = chunk_load(rs, my);
+        e1[r] = chunk_load(rs, lane == 63 && (mr > 0 || s > 0) ? my + 16 : kNoLoad);
+        em[r] = chunk_load(rs, lane == 0 && s < 0 ? my - 16 : kNoLoad);
     }
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
@@ -418,16 +465,46 @@ __global__ __launch_bounds__(kTB) void gs_rdp_parity_kernel(uint16_t* sh, int nd
     *reinterpret_cast<u32x4*>(tq + 16 * threadIdx.x) = q;
     __syncthreads();
     uint8_t* out = reinterpret_cast<uint8_t*>(sh);
-    tile_store(out + uint64_t(nd) * Sb + t0b, tp, nbytes);
-    tile_store(out + uint64_t(nd + 1) * Sb + t0b, tq, nbytes);
+    tile_store<true>(out + uint64_t(nd) * Sb + t0b, tp, nbytes);
+    tile_store<true>(out + uint64_t(nd + 1) * Sb + t0b, tq, nbytes);
 }
 
 // ----------------------------------------------------------------- host side
+// The batched tile paths take 1..8 rows (ND = the row count; 0: general path
+// only) in tensors below 2 GiB, whose out-of-range buffer loads then start
+// at 2^31.
+typedef void (*XorRowsFn)(const uint8_t*, uint64_t, uint32_t, RowSet, uint8_t*, uint8_t*, FlatCopy);
+typedef void (*XorRecFn)(const uint8_t*, uint8_t*, uint8_t*, uint64_t, uint32_t, int, const int32_t*);
+
+template <int ND = 1>
+XorRowsFn xor_rows_fn(int rows) {
+    if constexpr (ND > 8) {
+        return &xor_rows_kernel<0>;
+    } else {
+        if (rows == ND) return &xor_rows_kernel<ND>;
+        return xor_rows_fn<ND + 1>(rows);
+    }
+}
+
+template <int ND = 1>
+XorRecFn xor_rec_fn(int rows) {
+    if constexpr (ND > 8) {
+        return &xor_reconstruct_kernel<0>;
+    } else {
+        if (rows == ND) return &xor_reconstruct_kernel<ND>;
+        return xor_rec_fn<ND + 1>(rows);
+    }
+}
+
+inline uint32_t small_bytes(uint64_t n) { return n < (uint64_t(1) << 31) ? uint32_t(n) : 0; }
+
 static int xor_rows(const uint8_t* in, uint64_t Sb, RowSet rs, uint8_t* out0, uint8_t* out1,
                     hipStream_t st, const char* what, FlatCopy fc = FlatCopy{nullptr, nullptr, 0}) {
     if (Sb == 0) return KVEC_OK;
-    hipLaunchKernelGGL(xor_rows_kernel, dim3(blocks_for(int64_t(Sb), kTileBytes)), dim3(kTB), 0, st,
-                       in, Sb, rs, out0, out1, fc);
+    // rows of `in` the tile reads: lo..hi-1 and extra
+    const int top = rs.extra >= rs.hi ? rs.extra + 1 : rs.hi;
+    hipLaunchKernelGGL(xor_rows_fn(rs.hi - rs.lo), dim3(blocks_for(int64_t(Sb), kTileBytes)), dim3(kTB),
+                       0, st, in, Sb, small_bytes(uint64_t(top) * Sb), rs, out0, out1, fc);
     return check_launch(what);
 }
 
@@ -513,9 +590,10 @@ extern "C" int kvec_xor_reconstruct(const void* encoded_data, void* recovered_da
                          data_shards, (long long)shard_size);
     if (shard_size == 0) return KVEC_OK;
     const uint64_t Sb = uint64_t(shard_size);
-    hipLaunchKernelGGL(xor_reconstruct_kernel, dim3(blocks_for(int64_t(Sb), kTileBytes)), dim3(kTB), 0,
+    hipLaunchKernelGGL(xor_rec_fn(data_shards), dim3(blocks_for(int64_t(Sb), kTileBytes)), dim3(kTB), 0,
                        as_stream(stream), (const uint8_t*)encoded_data, (uint8_t*)recovered_data,
-                       (uint8_t*)recovered_missing, Sb, data_shards, missing_indices);
+                       (uint8_t*)recovered_missing, Sb, small_bytes(uint64_t(data_shards + 1) * Sb),
+                       data_shards, missing_indices);
     return check_launch("kvec_xor_reconstruct");
 }
 

@@ -65,6 +65,20 @@ __device__ __forceinline__ u32x4 from_prev_lane_or(u32x4 v, u32x4 edge) {
                  uint32_t(__builtin_amdgcn_update_dpp(int(edge.w), int(v.w), 0x138, 0xF, 0xF, false))};
 }
 
+// 16-byte loads through a buffer resource of fewer than 2^31 bytes.  A
+// voffset at or past 2^31 is then out of range: the load returns 0 without
+// touching memory, which lets only some lanes (a wave's edge lanes) fetch a
+// chunk with no branch around the load.
+constexpr uint32_t kNoLoad = 0x80000000u;
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t chunk_rsrc(const void* p, uint32_t n) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)n, (int)kBufWord3);
+}
+
+__device__ __forceinline__ u32x4 chunk_load(__amdgpu_buffer_rsrc_t rs, uint32_t voff) {
+    return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, voff, 0, kAuxLoadNT));
+}
+
 // A pointer that every lane holds the same value of, moved to scalar
 // registers: offsets and shifts derived from it are then wave-uniform, so a
 // switch on them is a scalar branch rather than per-lane selects.
@@ -158,20 +172,25 @@ inline bool fused_copy_ok(const void* src, const void* dst, uint64_t len) {
 }
 
 // Store the source chunk at `c` (16-byte aligned, value v) at its place in dst.
+// NT: non-temporal stores, faster for the XOR encode's copy (measured on
+// MI355X), slower for the RS GF(2^16) encode's.
+template <bool NT = true>
 __device__ __forceinline__ void copy_chunk(const FlatCopy& fc, const uint8_t* c, u32x4 v) {
     const uint64_t o = uint64_t(c - fc.src);
     if (o + 16 <= fc.len) {
-        st16(fc.dst + o, v);
+        if (NT) st_stream(fc.dst, o, v);
+        else st16(fc.dst + o, v);
         return;
     }
     const gptr<uint8_t> d = as_global(fc.dst);
     for (int i = 0; i < 16 && o + i < fc.len; ++i) d[o + i] = byte_of(v, i);
 }
 
+template <bool NT = true>
 __device__ __forceinline__ void copy_owned(const FlatCopy& fc, const RowWin& r, uint32_t off,
                                            u32x4 lo, u32x4 hi) {
-    if (r.sh) copy_chunk(fc, r.al + off + 16, hi);
-    else copy_chunk(fc, r.al + off, lo);
+    if (r.sh) copy_chunk<NT>(fc, r.al + off + 16, hi);
+    else copy_chunk<NT>(fc, r.al + off, lo);
 }
 
 // Bytes [a, b) of the range, one by one.
@@ -191,6 +210,11 @@ __device__ __forceinline__ void copy_row_head(const FlatCopy& fc, uint64_t o, ui
 
 // Write logical bytes [0, nbytes) of the LDS tile `t` (16-byte aligned, with 16
 // bytes of slack after nbytes) to dst, any alignment.  All threads call it.
+// NT: the aligned 16-byte stores are non-temporal.  Which is faster depends on
+// the kernel's other traffic (measured per kernel on MI355X): the P/Q rows of
+// the star-diagonal code write 12 % faster with it, the XOR parity row next
+// to the fused data-row copy 7 % slower.
+template <bool NT = false>
 __device__ __forceinline__ void tile_store(uint8_t* dst, const uint8_t* t, uint32_t nbytes) {
     dst = wave_uniform(dst);
     nbytes = uint32_t(__builtin_amdgcn_readfirstlane(int(nbytes)));
@@ -206,7 +230,8 @@ __device__ __forceinline__ void tile_store(uint8_t* dst, const uint8_t* t, uint3
             const uint32_t al = dal + 16 * k;
             u32x4 v = *reinterpret_cast<const u32x4*>(t + al);
             if (dsh) v = funnel16(v, *reinterpret_cast<const u32x4*>(t + al + 16), dsh);
-            st16(reinterpret_cast<uint8_t*>(A0 + 16 * uintptr_t(k)), v);
+            if (NT) st_stream(reinterpret_cast<uint8_t*>(A0 + 16 * uintptr_t(k)), 0, v);
+            else st16(reinterpret_cast<uint8_t*>(A0 + 16 * uintptr_t(k)), v);
         }
         // head [D0, A0) and tail [A1, E): at most 15 bytes each
         const uint32_t nh = uint32_t(A0 - D0), nt = uint32_t(E - A1);
