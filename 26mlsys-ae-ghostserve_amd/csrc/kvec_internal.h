@@ -4,6 +4,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 #include "kvec.h"
 
 namespace kvec {
@@ -71,6 +73,21 @@ struct Xor3Acc {
     }
     __device__ __forceinline__ u32x4 get() const { return held ? a ^ pend : a; }
 };
+
+// The same interface with 2-input XORs and one register per accumulator, for
+// kernels whose accumulators alone would otherwise crowd the register file
+// (RDP over p >= 11 keeps 2(p-1) of them).
+struct XorAcc {
+    u32x4 a;
+    __device__ __forceinline__ explicit XorAcc(u32x4 init = u32x4{0, 0, 0, 0}) : a(init) {}
+    __device__ __forceinline__ void add(u32x4 x) { a ^= x; }
+    __device__ __forceinline__ u32x4 get() const { return a; }
+};
+
+// Accumulator for an RDP kernel over prime p: 3-input XORs while the 2(p-1)
+// accumulators' held inputs fit beside the cells in flight.
+template <int P>
+using RdpAcc = typename std::conditional<(P <= 7), Xor3Acc, XorAcc>::type;
 
 // XOR of N cells with 3-input XORs.
 template <int N>

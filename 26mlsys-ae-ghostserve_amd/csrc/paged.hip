@@ -55,69 +55,82 @@ __global__ __launch_bounds__(kGBS) void kv_scatter_kernel(PagedGeom g, const uin
 // Stream cell (shard j, row r, lane offset o) is stream byte (j*(p-1) + r)*R + o;
 // with R a multiple of the record size its record is (j*(p-1) + r)*(R/rec) + o/rec.
 // Each cell is loaded from the pool once, stored to its data shard and folded
-// into P and Q in registers.  Shards are software pipelined two deep: while
-// shard j is folded in and stored, shard j+1's cells are in flight and shard
-// j+2's page-table entries are being fetched.
-constexpr int kFBS = 128;
+// into P and Q in registers.  A thread owns one lane offset and a block is one
+// wave.  Shards go in groups of paged_group(p, k) (18 cells for p = 7): the
+// group's page-table entries are all requested, then all its cells, then the
+// cells are stored and folded; scheduling barriers keep each phase's loads
+// together (left to itself the compiler interleaves them with their uses and
+// waits on each in turn).  Groups of 3 shards measured fastest for p = 7
+// (whole-stripe groups, 2-shard groups and groups whose page-table loads ride
+// with the previous group's cells were 1-3 % slower).
+constexpr int kFBS = 64;
+
+constexpr int paged_group(int P, int K) {
+    const int g = 18 / (P - 1);
+    return g < 1 ? 1 : (g > K ? K : g);
+}
 
 template <int P, int K>
-__global__ __launch_bounds__(kFBS) void rdp_encode_paged_kernel(PagedGeom g, Ptrs<16> d,
-                                                                uint8_t* __restrict__ Pp,
-                                                                uint8_t* __restrict__ Qp, uint64_t R,
-                                                                uint32_t recs_per_row, uint32_t nvec) {
-    constexpr int ROWS = P - 1;
+__global__ __launch_bounds__(kFBS) __attribute__((amdgpu_waves_per_eu(1, P <= 7 ? 2 : 4))) void rdp_encode_paged_kernel(
+        PagedGeom g, Ptrs<16> d, uint8_t* __restrict__ Pp, uint8_t* __restrict__ Qp, uint64_t R,
+        uint32_t recs_per_row, uint32_t nvec) {
+    constexpr int ROWS = P - 1, G = paged_group(P, K);
     const uint32_t u = blockIdx.x * kFBS + threadIdx.x;
     if (u >= nvec) return;
     const uint32_t off = u << 4;
     const uint32_t w0 = fdiv(off, g.div_rec);
-    const uint32_t inner = off - w0 * g.rec;
+    const uint32_t inner = off - w0 * g.div_rec.d;
     const uint64_t nb = ROWS * R;
     auto rec = [&](int j, int r) { return uint32_t(j * ROWS + r) * recs_per_row + w0; };
-    CellRef ref[2][ROWS];
-    u32x4 x[2][ROWS];
+    RdpAcc<P> pr[ROWS], q[ROWS];
 #pragma unroll
-    for (int r = 0; r < ROWS; ++r) ref[0][r] = cell_ref(g, rec(0, r));
-    if constexpr (K > 1) {
+    for (int j0 = 0; j0 < K; j0 += G) {
+        CellRef ref[G][ROWS];
 #pragma unroll
-        for (int r = 0; r < ROWS; ++r) ref[1][r] = cell_ref(g, rec(1, r));
-    }
+        for (int gg = 0; gg < G; ++gg)
 #pragma unroll
-    for (int r = 0; r < ROWS; ++r) x[0][r] = cell_load_ref(g, ref[0][r], inner);
-    u32x4 pr[ROWS], q[ROWS];
+            for (int r = 0; r < ROWS; ++r)
+                if (j0 + gg < K) ref[gg][r] = cell_ref(g, rec(j0 + gg, r));
+        __builtin_amdgcn_sched_barrier(0);
+        u32x4 x[G][ROWS];
 #pragma unroll
-    for (int r = 0; r < ROWS; ++r) {
-        pr[r] = u32x4{0, 0, 0, 0};
-        q[r] = u32x4{0, 0, 0, 0};
-    }
+        for (int gg = 0; gg < G; ++gg)
 #pragma unroll
-    for (int j = 0; j < K; ++j) {
-        const int c = j & 1;
-        if (j + 1 < K) {
+            for (int r = 0; r < ROWS; ++r)
+                if (j0 + gg < K) x[gg][r] = cell_load_ref(g, ref[gg][r], inner);
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-            for (int r = 0; r < ROWS; ++r) x[c ^ 1][r] = cell_load_ref(g, ref[c ^ 1][r], inner);
+        for (int gg = 0; gg < G; ++gg) {
+            const int j = j0 + gg;
+            if (j >= K) break;
+            const ShardView<true> sv(d.p[j], nb);
+#pragma unroll
+            for (int r = 0; r < ROWS; ++r) {
+                sv.store(r * R, off, x[gg][r]);
+                pr[r].add(x[gg][r]);
+                const int dg = (r + j) % P;
+                if (dg != P - 1) q[dg].add(x[gg][r]);
+            }
         }
-        if (j + 2 < K) {
-#pragma unroll
-            for (int r = 0; r < ROWS; ++r) ref[c][r] = cell_ref(g, rec(j + 2, r));
+        // Keep the next group's loads (page-table entries included) behind
+        // this fold: a compiler memory barrier for the IR passes, which would
+        // otherwise hoist every group's page-table loads to the top, and a
+        // scheduling barrier for the machine scheduler.
+        if constexpr (G < K) {
+            asm volatile("" ::: "memory");
+            __builtin_amdgcn_sched_barrier(0);
         }
-        const ShardView<true> sv(d.p[j], nb);
-#pragma unroll
-        for (int r = 0; r < ROWS; ++r) {
-            sv.store(r * R, off, x[c][r]);
-            pr[r] ^= x[c][r];
-            const int dg = (r + j) % P;
-            if (dg != P - 1) q[dg] ^= x[c][r];
-        }
-        asm volatile("" ::: "memory");
     }
-#pragma unroll
-    for (int r = 1; r < ROWS; ++r) q[r - 1] ^= pr[r];
+    // The P cell of row r lies on diagonal (r + p - 1) % p = r - 1.
     const ShardView<true> sp(Pp, nb), sq(Qp, nb);
 #pragma unroll
     for (int r = 0; r < ROWS; ++r) {
-        sp.store(r * R, off, pr[r]);
-        sq.store(r * R, off, q[r]);
+        const u32x4 pv = pr[r].get();
+        sp.store(r * R, off, pv);
+        if (r >= 1) q[r - 1].add(pv);
     }
+#pragma unroll
+    for (int r = 0; r < ROWS; ++r) sq.store(r * R, off, q[r].get());
 }
 
 typedef void (*PagedEncFn)(PagedGeom, Ptrs<16>, uint8_t*, uint8_t*, uint64_t, uint32_t, uint32_t);

@@ -43,7 +43,7 @@ __global__ __launch_bounds__(kBS) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
     const uint32_t u = blockIdx.x * kBS + threadIdx.x;
     if (u >= nvec) return;
     const uint32_t off = u << 4;
-    Xor3Acc pr[ROWS], q[ROWS];
+    RdpAcc<P> pr[ROWS], q[ROWS];
 #pragma unroll
     for (int j0 = 0; j0 < K; j0 += G) {
         u32x4 x[G][ROWS];
@@ -66,8 +66,13 @@ __global__ __launch_bounds__(kBS) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
                 if (dg != P - 1) q[dg].add(x[g][r]);
             }
         }
-        // keep the next group's loads behind this fold (bounds register use)
-        if constexpr (G < K) __builtin_amdgcn_sched_barrier(0);
+        // keep the next group's loads behind this fold (bounds register use):
+        // a compiler memory barrier for the IR passes, a scheduling barrier
+        // for the machine scheduler
+        if constexpr (G < K) {
+            asm volatile("" ::: "memory");
+            __builtin_amdgcn_sched_barrier(0);
+        }
     }
     const ShardView<BUF> sp(Pp, nb), sq(Qp, nb);
 #pragma unroll
