@@ -42,19 +42,21 @@ def hipcc() -> str:
     return cand
 
 
-def sgpr_spills(remarks: str) -> list:
-    """(kernel, count) for every kernel the resource-usage remarks report with
-    spilled SGPRs.  Kernels here that spilled SGPRs to VGPR lanes produced
-    run-to-run different bytes on gfx950, so the build rejects them."""
+def register_spills(remarks: str) -> list:
+    """(kernel, kind, count) for every kernel the resource-usage remarks report
+    with spilled SGPRs or VGPRs.  Kernels here that spilled SGPRs to VGPR lanes
+    produced run-to-run different bytes on gfx950, and a build variant that
+    spilled VGPRs to scratch produced wrong bytes, so the build rejects both.
+    (Scratch that holds a small array indexed at run time is not a spill.)"""
     out, name = [], None
     for line in remarks.splitlines():
         m = re.search(r"Function Name: (\S+)", line)
         if m:
             name = m.group(1)
             continue
-        m = re.search(r"SGPRs Spill: (\d+)", line)
-        if m and int(m.group(1)) > 0:
-            out.append((name, int(m.group(1))))
+        m = re.search(r"([SV]GPRs) Spill: (\d+)", line)
+        if m and int(m.group(2)) > 0:
+            out.append((name, m.group(1), int(m.group(2))))
     return out
 
 
@@ -64,10 +66,10 @@ def _compile(src: str) -> str:
     r = subprocess.run(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"hipcc failed on {os.path.basename(src)}:\n{r.stdout}")
-    spills = sgpr_spills(r.stdout)
+    spills = register_spills(r.stdout)
     if spills:
-        names = "\n  ".join(f"{n}: {c}" for n, c in spills)
-        raise RuntimeError(f"{os.path.basename(src)}: kernels spill SGPRs:\n  {names}")
+        names = "\n  ".join(f"{n}: {c} {kind}" for n, kind, c in spills)
+        raise RuntimeError(f"{os.path.basename(src)}: kernels spill registers:\n  {names}")
     return obj
 
 

@@ -71,7 +71,7 @@ constexpr int paged_group(int P, int K) {
 }
 
 template <int P, int K>
-__global__ __launch_bounds__(kFBS) __attribute__((amdgpu_waves_per_eu(1, P <= 7 ? 2 : 4))) void rdp_encode_paged_kernel(
+__global__ __launch_bounds__(kFBS) __attribute__((amdgpu_waves_per_eu(1, 2))) void rdp_encode_paged_kernel(
         PagedGeom g, Ptrs<16> d, uint8_t* __restrict__ Pp, uint8_t* __restrict__ Qp, uint64_t R,
         uint32_t recs_per_row, uint32_t nvec) {
     constexpr int ROWS = P - 1, G = paged_group(P, K);
@@ -137,7 +137,10 @@ typedef void (*PagedEncFn)(PagedGeom, Ptrs<16>, uint8_t*, uint8_t*, uint64_t, ui
 
 template <int P, int K = 1>
 PagedEncFn pick_paged(int k) {
-    if constexpr (K > P - 1) {
+    // p = 13 with k >= 10 would need more registers than a wave has and spill
+    // to scratch (spilled code has produced wrong bytes on this hardware), so
+    // those codes are not built here.
+    if constexpr (K > P - 1 || (P == 13 && K >= 10)) {
         return nullptr;
     } else {
         if (k == K) return &rdp_encode_paged_kernel<P, K>;
@@ -231,6 +234,7 @@ extern "C" int kvec_rdp_encode_paged(const kvec_paged_kv* kv, void* const* data,
         d.p[j] = (uint8_t*)data[j];
     }
     PagedEncFn fn = paged_fn(p, k);
+    if (!fn) return set_error(KVEC_EUNSUPPORTED, "kvec_rdp_encode_paged: p=%d k=%d not built", p, k);
     const uint32_t nvec = uint32_t(row_bytes / 16);
     const uint32_t spr = uint32_t(row_bytes / g.rec);
     hipLaunchKernelGGL(fn, dim3(blocks_for(nvec, kFBS)), dim3(kFBS), 0, as_stream(stream), g, d,

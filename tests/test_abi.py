@@ -123,3 +123,26 @@ def test_chunk_rejects_bad_arguments(pkg):
     assert L.kvec_chunk_decode_paged(C.byref(kv), 4096, C.byref(stripe()), er, 1, None) == -1
     assert L.kvec_chunk_decode_paged(C.byref(kv), 8192, C.byref(stripe()), er, 0, None) == -1
     del table
+
+
+def test_build_rejects_register_spills():
+    """The build refuses kernels whose resource-usage remarks report spilled
+    SGPRs or VGPRs; scratch without spills (a run-time indexed array) passes."""
+    import importlib.util
+    spec = importlib.util.spec_from_file_location(
+        "_kvec_build_t", os.path.join(ROOT, "26mlsys-ae-ghostserve_amd", "_build.py"))
+    b = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(b)
+    rem = "\n".join([
+        "x.hip:1:1: remark: Function Name: k_ok [-Rpass-analysis=kernel-resource-usage]",
+        "x.hip:1:1: remark:     SGPRs Spill: 0 [-Rpass-analysis=kernel-resource-usage]",
+        "x.hip:1:1: remark:     VGPRs Spill: 0 [-Rpass-analysis=kernel-resource-usage]",
+        "x.hip:1:1: remark:     ScratchSize [bytes/lane]: 528 [-Rpass-analysis=kernel-resource-usage]",
+        "x.hip:2:1: remark: Function Name: k_s [-Rpass-analysis=kernel-resource-usage]",
+        "x.hip:2:1: remark:     SGPRs Spill: 3 [-Rpass-analysis=kernel-resource-usage]",
+        "x.hip:2:1: remark:     VGPRs Spill: 0 [-Rpass-analysis=kernel-resource-usage]",
+        "x.hip:3:1: remark: Function Name: k_v [-Rpass-analysis=kernel-resource-usage]",
+        "x.hip:3:1: remark:     SGPRs Spill: 0 [-Rpass-analysis=kernel-resource-usage]",
+        "x.hip:3:1: remark:     VGPRs Spill: 68 [-Rpass-analysis=kernel-resource-usage]",
+    ])
+    assert b.register_spills(rem) == [("k_s", "SGPRs", 3), ("k_v", "VGPRs", 68)]

@@ -48,7 +48,7 @@ def test_gather_scatter_match_oracle(pkg, ora, gpu, L, B, pps, pt, H, D, dtype, 
     assert np.array_equal(after, exp)
 
 
-@pytest.mark.parametrize("p,k", [(7, 6), (5, 4), (7, 3)])
+@pytest.mark.parametrize("p,k", [(7, 6), (5, 4), (7, 3), (3, 2), (11, 10), (13, 9)])
 def test_fused_gather_rdp_encode(pkg, ora, gpu, p, k):
     L, B, pps, pt, H, D = 4, 3, 5, 16, 1, 128
     pool, table = make_pool(gpu, L, B, pps, pt, H, D, torch.bfloat16, seed=p * k)
@@ -84,3 +84,22 @@ def test_invalid_page_reads_zero(pkg, gpu):
     s = kv.gather().cpu().numpy().reshape(L, B, 8, 2, -1)
     assert not s[:, 0, 4:].any()
     assert s[:, 0, :4].any()
+
+
+# p = 13 with k >= 10 is not built (its kernel would spill registers): the
+# call fails with an error and writes nothing.
+def test_paged_encode_unbuilt_config_raises(pkg, gpu):
+    L, B, pps, pt, H, D = 2, 2, 4, 16, 1, 128
+    pool, table = make_pool(gpu, L, B, pps, pt, H, D, torch.bfloat16, seed=3)
+    kv = pkg.paged.PagedKV(pool.to(gpu), table.to(gpu), 0, pps * pt)
+    p, k = 13, 10
+    R = pkg.paged.rdp_row_bytes_for(kv, k, p)
+    n = (p - 1) * R
+    data = [torch.full((n,), 0x77, dtype=torch.uint8, device=gpu) for _ in range(k)]
+    P = torch.full((n,), 0x55, dtype=torch.uint8, device=gpu)
+    Q = torch.full((n,), 0x55, dtype=torch.uint8, device=gpu)
+    with pytest.raises(RuntimeError, match="not built"):
+        pkg.paged.rdp_encode_paged(kv, data, P, Q, p, R)
+    torch.cuda.synchronize()
+    assert bool((P == 0x55).all()) and bool((Q == 0x55).all())
+    assert all(bool((d == 0x77).all()) for d in data)
