@@ -68,9 +68,12 @@ __device__ __forceinline__ u32x4 load_cell(const PagedGeom& g, const ChunkGeom& 
 // alias the pool as far as the compiler knows, and the compiler barrier after
 // each row also keeps the GF tables from being hoisted out of the row loop
 // (they are re-read from LDS per row instead of pinning 6*k*m registers).
-// Outputs switched off by `wmask` get a buffer resource of size 0, whose stores
-// the hardware drops, so the kernel has no branches after the bounds check.
-template <int P, int K, int M>
+// Parity outputs switched off by `wmask` get a buffer resource of size 0,
+// whose stores the hardware drops, so the kernel has no branches after the
+// bounds check.  Whether the data shards are written is a template parameter
+// instead: dropped stores still occupy the memory pipeline, and the
+// parity-only encode would issue k(p-1) of them per thread.
+template <int P, int K, int M, bool DATA>
 __global__ __launch_bounds__(kCBS) void chunk_encode_kernel(PagedGeom g, ChunkGeom cg,
                                                             Ptrs<kChunkMaxK> d,
                                                             Ptrs<2 + kChunkMaxM> par,
@@ -98,7 +101,6 @@ __global__ __launch_bounds__(kCBS) void chunk_encode_kernel(PagedGeom g, ChunkGe
     }
 #pragma unroll
     for (int j = 0; j < K; ++j) x[0][j] = cell_load_ref(g, ref[0][j], inner);
-    const uint64_t nd = (wmask & kWData) ? nb : 0;
     u32x4 q[ROWS];
 #pragma unroll
     for (int r = 0; r < ROWS; ++r) q[r] = u32x4{0, 0, 0, 0};
@@ -114,8 +116,10 @@ __global__ __launch_bounds__(kCBS) void chunk_encode_kernel(PagedGeom g, ChunkGe
 #pragma unroll
             for (int j = 0; j < K; ++j) ref[c][j] = cell_ref(g, rec(j, r + 2));
         }
+        if constexpr (DATA) {
 #pragma unroll
-        for (int j = 0; j < K; ++j) ShardView<true>(d.p[j], nd).store(r * cg.R, lane, x[c][j]);
+            for (int j = 0; j < K; ++j) ShardView<true>(d.p[j], nb).store(r * cg.R, lane, x[c][j]);
+        }
         const u32x4 pr = xor_all<K>(x[c]);
         sp.store(r * cg.R, lane, pr);
         // cell (r, j) lies on diagonal (r + j) % p; the P cell of row r on r - 1
@@ -323,8 +327,12 @@ static void launch_encode(dim3 grid, hipStream_t st, const PagedGeom& g, const C
     Gf8Tab<(K * M > 0 ? K * M : 1)> t{};
     for (int i = 0; i < K * M; ++i)
         for (int e = 0; e < 6; ++e) t.t[i][e] = tab[i][e];
-    hipLaunchKernelGGL((chunk_encode_kernel<P, K, M>), grid, dim3(kCBS), 0, st, g, cg, d, par, t,
-                       wmask);
+    if (wmask & kWData)
+        hipLaunchKernelGGL((chunk_encode_kernel<P, K, M, true>), grid, dim3(kCBS), 0, st, g, cg, d, par,
+                           t, wmask);
+    else
+        hipLaunchKernelGGL((chunk_encode_kernel<P, K, M, false>), grid, dim3(kCBS), 0, st, g, cg, d, par,
+                           t, wmask);
 }
 
 typedef void (*EncLauncher)(dim3, hipStream_t, const PagedGeom&, const ChunkGeom&,
