@@ -185,6 +185,15 @@ __device__ __forceinline__ int64_t cmod(int64_t x, int64_t S) {
     return (x >= 0 && x < S) ? x : x % S;
 }
 
+// v with its bytes 0..n-1 zeroed (n <= 0: v).
+__device__ __forceinline__ u32x4 drop_low_bytes(u32x4 v, int n) {
+    auto m = [&](int d) {
+        const int k = n - 4 * d;   // bytes of dword d to clear
+        return k <= 0 ? 0xFFFFFFFFu : (k >= 4 ? 0u : 0xFFFFFFFFu << (8 * k));
+    };
+    return u32x4{v.x & m(0), v.y & m(1), v.z & m(2), v.w & m(3)};
+}
+
 __device__ __forceinline__ u32x4 drop_word(u32x4 v, int64_t k) {
     if (k < 0 || k >= 8) return v;
     const uint32_t m = (k & 1) ? 0x0000FFFFu : 0xFFFF0000u;
@@ -268,15 +277,21 @@ struct GsStar {
     int32_t d[8];
 };
 
-// P/Q of one interior tile (not the first, so no diagonal wraps and every
-// chunk offset is positive, and wholly inside the rows) with ND = nd <= 8
-// data rows: each row's chunk, and the edge
-// lanes' neighbour chunks, are all requested before the first is used, so a
-// thread has every row in flight at once.  With nd <= 8 the Q window starts
-// at most 14 bytes before the lane's chunk (mr - 2r >= -14), so the previous
-// lane's chunk always covers it.  Returns false, having loaded nothing, when
-// the tile needs the general path: a fused tile whose K/V/padding boundary
-// falls inside some row's loads.
+// P/Q of one full tile wholly inside the rows with ND = nd <= 8 data rows:
+// each row's chunk, and the edge lanes' neighbour chunks, are all requested
+// before the first is used, so a thread has every row in flight at once.
+// With nd <= 8 the Q window starts at most 14 bytes before the lane's chunk
+// (mr - 2r >= -14), so the previous lane's chunk always covers it.  Without
+// K/V the row resource starts at the 16-aligned address at or below the row
+// tensor, so every chunk offset is >= 0, the first tile's included.  In the
+// first tile only thread 0's Q words wrap: word i < r of row r is row r's word
+// S + i - r, and the window read the flat word before the row (row r-1's word
+// S + i - r) in its place.  Lanes 1..ND of wave 0 fetch the rows' last 16
+// bytes along with their own loads, and thread 0 adds the difference of
+// consecutive rows' tails from them.  Returns false, having loaded nothing,
+// when the tile needs the general path: a fused tile whose K/V/padding
+// boundary falls inside some row's loads, and the fused first tile of a row
+// tensor that is not 16-byte aligned (row 0's first chunk would start before K).
 template <bool FUSED, int ND>
 __device__ __forceinline__ bool gs_pq_batched(uint16_t* sh, uint32_t Sb, uint32_t t0b, int32_t w0,
                                               const GsStar& star, const GsSource& g,
@@ -285,37 +300,78 @@ __device__ __forceinline__ bool gs_pq_batched(uint16_t* sh, uint32_t Sb, uint32_
     const uint32_t lane = threadIdx.x & 63;
     const uint32_t b15 = uint32_t(reinterpret_cast<uintptr_t>(base)) & 15;
     const uint32_t kb = uint32_t(g.kb), copy_end = uint32_t(g.copy_end);
-    // misalignment of row r's tile start, and its lane-0 chunk offset in the rows
-    // (positive: the path does not run on tile 0)
+    if (FUSED && t0b == 0 && b15 != 0) return false;
+    // misalignment of row r's tile start, and its lane-0 chunk offset in the
+    // rows (-b15 for row 0 of the first tile: the chunk holding byte 0)
     auto row_mr = [&](int r) { return (b15 + uint32_t(r) * Sb + t0b) & 15; };
     auto row_x0 = [&](int r) { return uint32_t(r) * Sb + t0b - row_mr(r); };
     // source of row r's chunks: 0 the rows, 1 K, 2 V, -1 mixed
+    // every byte row r's loads cover: the lanes' chunks, lane 0's previous
+    // chunk (a window starting before its chunk, not in the first tile) and
+    // the last lane's next chunk (a window reaching past its chunk)
     auto row_src = [&](int r) {
         if (!FUSED) return 0;
-        const int64_t x0 = row_x0(r), lo = x0 - 16, hi = x0 + kTileBytes + 32;
+        const int32_t mr = int32_t(row_mr(r)), sq = mr - 2 * r;
+        const int64_t x0 = row_x0(r);
+        const int64_t lo = x0 - (sq < 0 && t0b != 0 ? 16 : 0);
+        const int64_t hi = x0 + kTileBytes + (mr > 0 || sq > 0 ? 16 : 0);
         if (hi <= int64_t(kb)) return 1;
         if (lo >= int64_t(kb) && hi <= 2 * int64_t(kb)) return 2;
         return lo < 2 * int64_t(kb) ? -1 : 0;
     };
+    uint32_t srcs = 0;   // row r's source in bits 2r, 2r+1
     if (FUSED) {
         bool mixed = false;
 #pragma unroll
-        for (int r = 0; r < ND; ++r) mixed |= row_src(r) < 0;
+        for (int r = 0; r < ND; ++r) {
+            const int sr = row_src(r);
+            mixed |= sr < 0;
+            srcs |= uint32_t(sr & 3) << (2 * r);
+        }
         if (mixed) return false;
     }
-    const __amdgpu_buffer_rsrc_t rrows = chunk_rsrc(base, rows_bytes);
+    // without K/V the rows from their aligned-down start (offsets + rb)
+    const uint32_t rb = FUSED ? 0 : b15;
+    const __amdgpu_buffer_rsrc_t rrows = chunk_rsrc(base - rb, rows_bytes + rb);
+    // first tile: lane j + 1 of wave 0 fetches the two aligned chunks over the
+    // 16 bytes before row j's end (flat offset tx), from the rows or from K or
+    // V; a pair across a K/V/padding boundary is read byte by byte.  Without
+    // K/V along with the lane's own loads; the fused kernel, which has no
+    // scalar registers to spare there, after them.
+    const bool tail_lane = ND > 1 && t0b == 0 && threadIdx.x >= 1 && threadIdx.x <= ND;
+    const uint32_t tx = threadIdx.x * Sb - 16, tm = (b15 + tx) & 15, ta = tx - tm;
+    auto tail_of = [&]() {
+        u32x4 t = {0, 0, 0, 0};
+        if (tail_lane) {
+            const uint8_t* c = base + ta;
+            const uint32_t te = ta + (tm ? 32 : 16);
+            bool bytes = false;
+            if (FUSED && te <= kb) c = g.K + ta;
+            else if (FUSED && ta >= kb && te <= 2 * kb) c = g.V + (ta - kb);
+            else if (FUSED && ta < 2 * kb) bytes = true;
+            if (bytes) {
+                t = gs_src_chunk_bytes(g, base, tx);
+            } else {
+                const u32x4 lo = ld16(c);
+                t = tm ? funnel16(lo, ld16(c + 16), tm) : lo;
+            }
+        }
+        return t;
+    };
+    u32x4 tail = {0, 0, 0, 0};
+    if (!FUSED) tail = tail_of();
     u32x4 c0[ND], e1[ND], em[ND];
 #pragma unroll
     for (int r = 0; r < ND; ++r) {
-        const int src = row_src(r);
+        const int src = int(srcs >> (2 * r)) & 3;
         const __amdgpu_buffer_rsrc_t rs =
             src == 1 ? chunk_rsrc(g.K, kb) : (src == 2 ? chunk_rsrc(g.V, kb) : rrows);
         const uint32_t mr = row_mr(r);
         const int s = int(mr) - 2 * r;
-        const uint32_t my = row_x0(r) - (src == 2 ? kb : 0) + 16 * threadIdx.x;
+        const uint32_t my = row_x0(r) + (src == 2 ? 0u - kb : rb) + 16 * threadIdx.x;
         c0[r] = chunk_load(rs, my);
         e1[r] = chunk_load(rs, lane == 63 && (mr > 0 || s > 0) ? my + 16 : kNoLoad);
-        em[r] = chunk_load(rs, lane == 0 && s < 0 ? my - 16 : kNoLoad);
+        em[r] = chunk_load(rs, lane == 0 && s < 0 && (t0b | threadIdx.x) != 0 ? my - 16 : kNoLoad);
     }
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
@@ -346,6 +402,26 @@ __device__ __forceinline__ bool gs_pq_batched(uint16_t* sh, uint32_t Sb, uint32_
         else qw = funnel16(cm, c0[r], uint32_t(s + 16));
         q ^= star.d[r] < 0 ? qw : drop_word(qw, int64_t(star.d[r]) - w0);
     }
+    if constexpr (ND > 1) {
+        if (t0b == 0 && threadIdx.x < 64) {
+            const u32x4 t = FUSED ? tail_of() : tail;
+            // Words 0..r-1 of row r's window are the 2r bytes before the row:
+            // its first chunk's first mr bytes (flat bytes of row r-1's end)
+            // after zeros (lane 0 loads no previous chunk here).  In their
+            // place go row r's last r words.
+            u32x4 fix = {0, 0, 0, 0}, prev = lane_value(t, 1);
+#pragma unroll
+            for (int r = 1; r < ND; ++r) {
+                const u32x4 cur = lane_value(t, r + 1);
+                const int mr = int(row_mr(r)), z = 2 * r - mr;   // leading zero bytes
+                const u32x4 was = drop_low_bytes(funnel16(prev, u32x4{0, 0, 0, 0}, 16 - 2 * r), z);
+                const u32x4 f = was ^ funnel16(cur, u32x4{0, 0, 0, 0}, 16 - 2 * r);
+                fix ^= star.d[r] < 0 ? f : drop_word(f, int64_t(star.d[r]) - w0);
+                prev = cur;
+            }
+            if (threadIdx.x == 0) q ^= fix;
+        }
+    }
     return true;
 }
 
@@ -364,13 +440,13 @@ __global__ __launch_bounds__(kTB) void gs_rdp_parity_kernel(uint16_t* sh, int nd
     const uint32_t lane = threadIdx.x & 63;
     const bool fast = w0 + 8 <= S && w0 >= nd - 1;
     u32x4 p = {0, 0, 0, 0}, q = {0, 0, 0, 0};
-    // Interior tiles of small stripes: every row requested at once.  The
-    // general loop below handles the two end tiles, nd > 8, rows tensors of
-    // 2 GiB or more and fused tiles next to a K/V boundary.
+    // Full tiles of small stripes: every row requested at once.  The general
+    // loop below handles a last partial tile, nd > 8, rows tensors of 2 GiB or
+    // more and fused tiles next to a K/V boundary.
     bool batched = false;
     if constexpr (ND > 0) {
         const int64_t t0w = int64_t(blockIdx.x) * (kTileBytes / 2);
-        if (rows_bytes && blockIdx.x > 0 && t0w + kTileBytes / 2 <= S)
+        if (rows_bytes && t0w + kTileBytes / 2 <= S)
             batched = gs_pq_batched<FUSED, ND>(sh, uint32_t(Sb), uint32_t(t0b), int32_t(w0), star, g,
                                                uint32_t(rows_bytes), p, q);
     }
@@ -532,9 +608,11 @@ static int gs_rdp_parity(uint16_t* sh, int nd, int64_t S, int star_base, hipStre
     if (nd <= 0 || S <= 0) return KVEC_OK;  // the reference kernel returns at once
     const dim3 grid(blocks_for(S * 2, kTileBytes));
     // The batched path addresses the rows (and K, V) through buffer resources
-    // whose out-of-range loads must start at 2^31: 0 switches it off.
+    // of up to 15 bytes more than the tensor, whose out-of-range loads must
+    // start at 2^31: 0 switches it off.
     const uint64_t rows_bytes = uint64_t(nd + 2) * uint64_t(S) * 2;
-    const bool small = rows_bytes < (uint64_t(1) << 31) && (!fused || fused->kb < (int64_t(1) << 31));
+    const uint64_t lim = (uint64_t(1) << 31) - 16;
+    const bool small = rows_bytes <= lim && (!fused || uint64_t(fused->kb) <= lim);
     const uint64_t rb = small ? rows_bytes : 0;
     GsStar star{};
     for (int r = 0; r < 8; ++r) {

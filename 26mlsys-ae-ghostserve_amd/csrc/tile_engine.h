@@ -65,6 +65,15 @@ __device__ __forceinline__ u32x4 from_prev_lane_or(u32x4 v, u32x4 edge) {
                  uint32_t(__builtin_amdgcn_update_dpp(int(edge.w), int(v.w), 0x138, 0xF, 0xF, false))};
 }
 
+// Lane j's value of v, in every lane (ds_bpermute; j in [0, 64)).
+__device__ __forceinline__ u32x4 lane_value(u32x4 v, int j) {
+    const int a = 4 * j;
+    return u32x4{uint32_t(__builtin_amdgcn_ds_bpermute(a, int(v.x))),
+                 uint32_t(__builtin_amdgcn_ds_bpermute(a, int(v.y))),
+                 uint32_t(__builtin_amdgcn_ds_bpermute(a, int(v.z))),
+                 uint32_t(__builtin_amdgcn_ds_bpermute(a, int(v.w)))};
+}
+
 // 16-byte loads through a buffer resource of fewer than 2^31 bytes.  A
 // voffset at or past 2^31 is then out of range: the load returns 0 without
 // touching memory, which lets only some lanes (a wave's edge lanes) fetch a

@@ -591,6 +591,46 @@ def bench_gs(pkg, torch, oracle, dev, seed, steps, warmup):
                           "gbs": round(alg / kms / 1e6, 2),
                           "frac_hbm_peak": round(alg / kms / 1e6 / HBM_PEAK_GBS, 4)}
     del sets
+    # The serving plugin's per-step parity (bench_ghostserve_rdp.py:334-360):
+    # Llama-3.1-8B at TP8, a 2048-token prefill step, one [K | V] row per rank
+    # of w = 2048 x 1 KV head x 128 words each, so rows [(8+2), 2w] u16.  A small
+    # launch: reported as us per launch, back to back and one at a time with a
+    # host synchronization (as the plugin makes it).
+    nd8, w = 8, 2048 * 128
+    S8 = 2 * w
+    rows8 = [torch.zeros((nd8 + 2, S8), dtype=torch.uint16, device=dev) for _ in range(2)]
+    for r in rows8:
+        r[:nd8].view(torch.int16).copy_(torch.randint(-32768, 32767, (nd8, S8), generator=g,
+                                                      device=dev, dtype=torch.int16))
+
+    def par8(rw):
+        pkg.rdp_kv_ops.compute_rdp_parity(rw, nd8, S8, 0)
+
+    par8(rows8[0])
+    torch.cuda.synchronize()
+    h = rows8[0].cpu().numpy()
+    cs = np.sort(rng.choice(S8, 2048, replace=False))
+    if not np.array_equal(h[nd8, cs], np.bitwise_xor.reduce(h[:nd8, cs], axis=0)):
+        raise RuntimeError("gs P mismatch (plugin step)")
+    q = np.zeros(cs.size, np.uint16)
+    for r in range(nd8):
+        c = (cs - r) % S8
+        q ^= np.where(c != r % S8, h[r, c], 0).astype(np.uint16)
+    if not np.array_equal(h[nd8 + 1, cs], q):
+        raise RuntimeError("gs Q mismatch (plugin step)")
+    del h
+    _, kms = time_kernel(torch, par8, [(r,) for r in rows8], 50, 5)
+    one = []
+    for i in range(20):
+        t0 = time.perf_counter()
+        par8(rows8[i % 2])
+        torch.cuda.synchronize()
+        one.append((time.perf_counter() - t0) * 1e6)
+    alg8 = nd8 * S8 * 2 + 2 * S8 * 2
+    out["plugin_step_pq_tp8"] = {"rows": [nd8 + 2, S8], "alg_bytes": alg8,
+                                 "us_back_to_back": round(kms * 1e3, 2),
+                                 "us_launch_and_sync_median": round(sorted(one)[len(one) // 2], 2)}
+    del rows8
     out["workload"] = "gs_family_nd6_llama3.1-8b_16x2048tok_512MiB"
     out["byte_exact_sampled"] = True
     return out

@@ -362,6 +362,41 @@ def test_gs_parity_interior_tiles(pkg, ora, gpu, nd, soff, S, sb):
     assert bool((torch.cat([buf[:soff], buf[soff + (nd + 2) * S:]]) == 0x3C3C).all())
 
 
+# The first tile of a stripe without K/V takes the same path; there thread 0's
+# Q words i < r of row r wrap to row r's last words.  star_base S - 6 puts the
+# skipped word of rows 3, 4 and 5 on a wrapped word (diagonals 0, 2 and 4),
+# star_base 0 puts it on unwrapped words of thread 0, -1 skips nothing in row
+# 0.  S = 2048 is a one-tile stripe; 524288 words is a Llama-3.1-8B TP8 prefill
+# step's [K | V] rows (2048 tokens x 128 words).
+@pytest.mark.parametrize("nd", range(1, 9))
+@pytest.mark.parametrize("soff", [0, 3])
+@pytest.mark.parametrize("S,sb", [(2048, 2042), (2048 * 3 + 5, 0), (6000, -1), (4096, 4095)])
+def test_gs_parity_first_tile(pkg, ora, gpu, nd, soff, S, sb):
+    rng = np.random.default_rng(nd * 29 + soff * 3 + S + sb)
+    rows = rng.integers(0, 65536, (nd + 2, S), dtype=np.uint16)
+    want = rows.copy()
+    ora.gs_parity(want, nd, S, sb)
+    buf = torch.full(((nd + 2) * S + 16,), 0x3C3C, dtype=torch.int16, device=gpu)
+    buf[soff:soff + (nd + 2) * S] = dev(rows.reshape(-1).view(np.int16), gpu)
+    d = buf[soff:soff + (nd + 2) * S].view(nd + 2, S)
+    pkg.rdp_kv_ops.compute_rdp_parity(d.view(torch.uint16), nd, S, sb)
+    assert np.array_equal(d.cpu().numpy().view(np.uint16), want)
+    assert bool((torch.cat([buf[:soff], buf[soff + (nd + 2) * S:]]) == 0x3C3C).all())
+
+
+@pytest.mark.parametrize("sb", [0, 524288 - 6])
+def test_gs_parity_plugin_step_shape(pkg, ora, gpu, sb):
+    nd, S = 8, 2 * 2048 * 128
+    rng = np.random.default_rng(sb + 1)
+    rows = np.zeros((nd + 2, S), dtype=np.uint16)
+    rows[:nd] = rng.integers(0, 65536, (nd, S), dtype=np.uint16)
+    want = rows.copy()
+    ora.gs_parity(want, nd, S, sb)
+    d = dev(rows, gpu)
+    pkg.rdp_kv_ops.compute_rdp_parity(d, nd, S, sb)
+    assert np.array_equal(d.cpu().numpy(), want)
+
+
 @pytest.mark.parametrize("nd", range(1, 9))
 @pytest.mark.parametrize("soff,S_extra", [(0, 0), (5, 2500), (3, 7000)])
 def test_gs_backup_interior_tiles(pkg, ora, gpu, nd, soff, S_extra):
@@ -387,3 +422,40 @@ def test_gs_backup_interior_tiles(pkg, ora, gpu, nd, soff, S_extra):
                                             sh.view(torch.uint16), nd, S, T, n, sb)
     assert np.array_equal(sh.cpu().numpy().view(np.uint16), want)
     assert bool((torch.cat([sbuf[:soff], sbuf[soff + (nd + 2) * S:]]) == 0x5A5A).all())
+
+
+# The fused first tile of an aligned row tensor takes the batched path too:
+# star words on thread 0's wrapped words (star_base S - 6), and rows whose last
+# 16 bytes lie in K, in V, in the padding or across the K/V or V/padding
+# boundary (nd = 2 with no padding ends row 0 exactly at the K/V boundary).
+@pytest.mark.parametrize("nd", range(1, 9))
+@pytest.mark.parametrize("T,n,S_extra,sb_back", [(96, 211, 0, 6), (64, 128, 0, None), (50, 77, 1000, 6)])
+def test_gs_backup_first_tile(pkg, ora, gpu, nd, T, n, S_extra, sb_back):
+    tn = T * n
+    S = -(-2 * tn // nd) + S_extra
+    sb = 0 if sb_back is None else S - sb_back
+    rng = np.random.default_rng(nd * 41 + T + n)
+    K = rng.integers(0, 65536, tn, dtype=np.uint16)
+    V = rng.integers(0, 65536, tn, dtype=np.uint16)
+    want = np.zeros((nd + 2, S), dtype=np.uint16)
+    ora.gs_pack(K.reshape(T, n), V.reshape(T, n), want, nd, S, T, n)
+    ora.gs_parity(want, nd, S, sb)
+    voff = tn % 8                           # V aligned like its place in the rows
+    kb = dev(K.view(np.int16), gpu)
+    vb = torch.zeros(tn + 16, dtype=torch.int16, device=gpu)
+    vb[voff:voff + tn] = dev(V.view(np.int16), gpu)
+    sh = torch.zeros((nd + 2, S), dtype=torch.uint16, device=gpu)
+    pkg.rdp.rdp_kernel.fused_backup_full_kv(kb.view(T, n), vb[voff:voff + tn].view(T, n), sh, nd, S, T,
+                                            n, sb)
+    assert np.array_equal(sh.cpu().numpy(), want)
+
+
+def test_gs_backup_reference_demo_shape(pkg, ora, gpu):
+    """benchmark/rdp/main.py defaults: B=1, 8 heads, T=512, head_dim 128, 8 shards."""
+    torch.manual_seed(0)
+    keys = torch.randn(1, 8, 512, 128, device=gpu, dtype=torch.float16)
+    values = torch.randn(1, 8, 512, 128, device=gpu, dtype=torch.float16)
+    out = pkg.rdp.fused_backup_full_kv(keys, values, 8, star_base=0)
+    K_TN = keys.permute(2, 0, 1, 3).reshape(512, -1).cpu().numpy().view(np.uint16)
+    V_TN = values.permute(2, 0, 1, 3).reshape(512, -1).cpu().numpy().view(np.uint16)
+    assert np.array_equal(out["shards_KV"].cpu().numpy(), ora.gs_backup(K_TN, V_TN, 8, 0))
