@@ -277,9 +277,13 @@ struct GsStar {
     int32_t d[8];
 };
 
-// P/Q of one full tile wholly inside the rows with ND = nd <= 8 data rows:
-// each row's chunk, and the edge lanes' neighbour chunks, are all requested
-// before the first is used, so a thread has every row in flight at once.
+// P/Q of one tile of a stripe of at least one full tile with ND = nd <= 8
+// data rows: each row's chunk, and the edge lanes' neighbour chunks, are all
+// requested before the first is used, so a thread has every row in flight at
+// once.  In a partial last tile the lanes past the row's end compute words
+// that are not stored (their loads read the next row, or zeros past the
+// resource); a fused copy from them stores the next row's bytes from the same
+// source the owning tile reads them from.
 // With nd <= 8 the Q window starts at most 14 bytes before the lane's chunk
 // (mr - 2r >= -14), so the previous lane's chunk always covers it.  Without
 // K/V the row resource starts at the 16-aligned address at or below the row
@@ -440,13 +444,12 @@ __global__ __launch_bounds__(kTB) void gs_rdp_parity_kernel(uint16_t* sh, int nd
     const uint32_t lane = threadIdx.x & 63;
     const bool fast = w0 + 8 <= S && w0 >= nd - 1;
     u32x4 p = {0, 0, 0, 0}, q = {0, 0, 0, 0};
-    // Full tiles of small stripes: every row requested at once.  The general
-    // loop below handles a last partial tile, nd > 8, rows tensors of 2 GiB or
-    // more and fused tiles next to a K/V boundary.
+    // Stripes of at least one full tile: every row requested at once.  The
+    // general loop below handles shorter stripes, nd > 8, rows tensors of
+    // 2 GiB or more and fused tiles next to a K/V boundary.
     bool batched = false;
     if constexpr (ND > 0) {
-        const int64_t t0w = int64_t(blockIdx.x) * (kTileBytes / 2);
-        if (rows_bytes && t0w + kTileBytes / 2 <= S)
+        if (rows_bytes && S >= kTileBytes / 2)
             batched = gs_pq_batched<FUSED, ND>(sh, uint32_t(Sb), uint32_t(t0b), int32_t(w0), star, g,
                                                uint32_t(rows_bytes), p, q);
     }
