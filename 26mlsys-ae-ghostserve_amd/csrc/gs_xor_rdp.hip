@@ -548,6 +548,93 @@ __global__ __launch_bounds__(kTB) void gs_rdp_parity_kernel(uint16_t* sh, int nd
     tile_store<true>(out + uint64_t(nd + 1) * Sb + t0b, tq, nbytes);
 }
 
+// ------------------------------------------------------------- gs recovery
+// fused_recovery_full_kv in one pass: row t (t >= 0) rebuilt as P ^ the other
+// data rows and written back into the shards, and every data row's tile (row
+// t's the rebuilt one) written to out, the flat copy-out of the data rows
+// clipped to out_len bytes (load_full_kernel, benchmark/rdp/kernel.cu:305-345).
+// A block owns one column tile of every row.  Each data row's window is staged
+// in an LDS tile and written with tile_store, so every output byte has exactly
+// one writer whatever the alignment of out.  Full tiles of stripes with
+// nd = ND <= 8 in shards below 2 GiB request every surviving row's chunk at
+// once (the loads of xor_rows_batched, one LDS tile per row); otherwise the
+// rows go one at a time through one LDS tile.  Row t itself is never read.
+// Stores, as measured on the 512 MiB stream: the copy-out non-temporal (232
+// -> 209 us), the rebuilt row plain (non-temporal: 226 us).
+template <int ND>
+__global__ __launch_bounds__(kTB) void gs_recover_kernel(uint8_t* sh, uint64_t Sb, uint32_t in_bytes,
+                                                         int nd, int t, uint8_t* out,
+                                                         uint64_t out_len) {
+    constexpr int NT = ND > 0 ? ND : 1;
+    __shared__ __attribute__((aligned(16))) uint8_t tiles[NT][kTileBytes + 16];
+    const uint64_t t0 = uint64_t(blockIdx.x) * kTileBytes;
+    const uint32_t nbytes = uint32_t(Sb - t0 < uint64_t(kTileBytes) ? Sb - t0 : kTileBytes);
+    const uint64_t c0 = t0 + 16 * threadIdx.x;
+    // data row r's tile into out, up to out_len
+    auto store_row = [&](int r, const uint8_t* tile) {
+        const uint64_t o = uint64_t(r) * Sb + t0;
+        if (o < out_len) tile_store<true>(out + o, tile, uint32_t(out_len - o < nbytes ? out_len - o : nbytes));
+    };
+    if constexpr (ND > 0) {
+        if (t0 + kTileBytes <= Sb && in_bytes) {
+            const uint32_t b15 = uint32_t(reinterpret_cast<uintptr_t>(sh)) & 15;
+            const __amdgpu_buffer_rsrc_t rs = chunk_rsrc(sh - b15, (b15 + in_bytes + 15) & ~15u);
+            const uint32_t lane = threadIdx.x & 63;
+            // batch row i: data row i, or i + 1 from row t on (then P last)
+            auto row_of = [&](int i) { return i + (t >= 0 && i >= t ? 1 : 0); };
+            auto row_a = [&](int i) { return b15 + uint32_t(row_of(i)) * uint32_t(Sb) + uint32_t(t0); };
+            u32x4 lo[ND], e1[ND];
+#pragma unroll
+            for (int i = 0; i < ND; ++i) {
+                const uint32_t A = row_a(i), m = A & 15, my = A - m + 16 * threadIdx.x;
+                lo[i] = chunk_load(rs, my);
+                e1[i] = chunk_load(rs, lane == 63 && m ? my + 16 : kNoLoad);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            u32x4 acc = {0, 0, 0, 0};
+#pragma unroll
+            for (int i = 0; i < ND; ++i) {
+                const uint32_t m = row_a(i) & 15;
+                const u32x4 w = m ? funnel16(lo[i], from_next_lane_or(lo[i], e1[i]), m) : lo[i];
+                acc ^= w;
+                const int j = row_of(i);
+                if (j < ND) *reinterpret_cast<u32x4*>(tiles[j] + 16 * threadIdx.x) = w;
+            }
+            if (t >= 0) *reinterpret_cast<u32x4*>(tiles[t] + 16 * threadIdx.x) = acc;
+            __syncthreads();
+#pragma unroll
+            for (int r = 0; r < ND; ++r) store_row(r, tiles[r]);
+            if (t >= 0) tile_store(sh + uint64_t(t) * Sb + t0, tiles[t], nbytes);
+            return;
+        }
+    }
+    uint8_t* tl = tiles[0];
+    u32x4 acc = {0, 0, 0, 0};
+    for (int r = 0; r <= nd; ++r) {   // the data rows, then P
+        if (r == t || (r == nd && t < 0)) continue;
+        const uint8_t* row = sh + uint64_t(r) * Sb;
+        u32x4 w = {0, 0, 0, 0};
+        if (c0 + 16 <= Sb) {
+            w = load_window16(row + c0);
+        } else if (c0 < Sb) {
+            for (uint32_t i = 0; i < uint32_t(Sb - c0); ++i) w = set_byte(w, i, row[c0 + i]);
+        }
+        acc ^= w;
+        if (r < nd) {
+            *reinterpret_cast<u32x4*>(tl + 16 * threadIdx.x) = w;
+            __syncthreads();
+            store_row(r, tl);
+            __syncthreads();
+        }
+    }
+    if (t >= 0) {
+        *reinterpret_cast<u32x4*>(tl + 16 * threadIdx.x) = acc;
+        __syncthreads();
+        store_row(t, tl);
+        tile_store(sh + uint64_t(t) * Sb + t0, tl, nbytes);
+    }
+}
+
 // ----------------------------------------------------------------- host side
 // The batched tile paths take 1..8 rows (ND = the row count; 0: general path
 // only) in tensors below 2 GiB, whose out-of-range buffer loads then start
@@ -576,6 +663,18 @@ XorRecFn xor_rec_fn(int rows) {
 }
 
 inline uint32_t small_bytes(uint64_t n) { return n < (uint64_t(1) << 31) ? uint32_t(n) : 0; }
+
+typedef void (*GsRecoverFn)(uint8_t*, uint64_t, uint32_t, int, int, uint8_t*, uint64_t);
+
+template <int ND = 1>
+GsRecoverFn gs_recover_fn(int nd) {
+    if constexpr (ND > 8) {
+        return &gs_recover_kernel<0>;
+    } else {
+        if (nd == ND) return &gs_recover_kernel<ND>;
+        return gs_recover_fn<ND + 1>(nd);
+    }
+}
 
 static int xor_rows(const uint8_t* in, uint64_t Sb, RowSet rs, uint8_t* out0, uint8_t* out1,
                     hipStream_t st, const char* what, FlatCopy fc = FlatCopy{nullptr, nullptr, 0}) {
@@ -756,6 +855,30 @@ extern "C" int kvec_gs_rdp_recover(void* shards, void* out_TN, int nd, int S, in
         t = a;
     else if (b >= 0 && a < 0)
         t = b;
+    const bool copy_out = T > 0 && n > 0 && nd > 0 && S > 0;
+    if (copy_out && !out_TN) return set_error(KVEC_EINVAL, "kvec_gs_rdp_recover: null output");
+    const uint64_t total = 2 * uint64_t(T > 0 ? T : 0) * uint64_t(n > 0 ? n : 0);
+    const uint64_t cap = uint64_t(nd > 0 ? nd : 0) * uint64_t(S > 0 ? S : 0);
+    const uint64_t nc = total < cap ? total : cap;
+    if (copy_out) {
+        // One pass (rebuild and copy-out) when out overlaps no shard row.
+        const uint64_t Sb = uint64_t(S) * 2;
+        const uintptr_t R0 = uintptr_t(shards), R1 = R0 + uint64_t(nd + 2) * Sb;
+        const uintptr_t O0 = uintptr_t(out_TN), O1 = O0 + total * 2;
+        if (O1 <= R0 || O0 >= R1) {
+            hipLaunchKernelGGL(gs_recover_fn(nd), dim3(blocks_for(int64_t(Sb), kTileBytes)), dim3(kTB), 0, st,
+                               (uint8_t*)shards, Sb, small_bytes(uint64_t(nd + 1) * Sb), nd, t,
+                               (uint8_t*)out_TN, nc * 2);
+            int rc = check_launch("kvec_gs_rdp_recover");
+            if (rc) return rc;
+            if (total > nc) {
+                hipError_t e = hipMemsetAsync((uint16_t*)out_TN + nc, 0, (total - nc) * 2, st);
+                if (e != hipSuccess)
+                    return set_error(KVEC_EHIP, "kvec_gs_rdp_recover: %s", hipGetErrorString(e));
+            }
+            return KVEC_OK;
+        }
+    }
     if (t >= 0 && S > 0) {
         const uint64_t Sb = uint64_t(S) * 2;
         uint8_t* base = (uint8_t*)shards;
@@ -763,10 +886,7 @@ extern "C" int kvec_gs_rdp_recover(void* shards, void* out_TN, int nd, int S, in
                           "kvec_gs_rdp_recover");
         if (rc) return rc;
     }
-    if (T > 0 && n > 0 && nd > 0 && S > 0) {
-        if (!out_TN) return set_error(KVEC_EINVAL, "kvec_gs_rdp_recover: null output");
-        const uint64_t total = 2 * uint64_t(T) * uint64_t(n), cap = uint64_t(nd) * uint64_t(S);
-        const uint64_t nc = total < cap ? total : cap;
+    if (copy_out) {
         int rc = copy_d2d(out_TN, shards, nc * 2, st, "kvec_gs_rdp_recover");
         if (rc) return rc;
         if (total > nc) {

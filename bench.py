@@ -536,7 +536,30 @@ def bench_gs(pkg, torch, oracle, dev, seed, steps, warmup):
     out["rdp_backup"] = {"us": round(kms * 1e3, 2), "alg_bytes": alg,
                          "gbs": round(alg / kms / 1e6, 2),
                          "frac_hbm_peak": round(alg / kms / 1e6 / HBM_PEAK_GBS, 4)}
-    del bsets, K, V, shb, flat
+
+    # fused_recovery_full_kv (benchmark/rdp/kernel.cu:397-521) with rows 0 and 1
+    # reported lost: row 0 rebuilt from P in place, then the data rows copied
+    # out as K_TN || V_TN.  Row 0 is zeroed first, so the output and the
+    # rebuilt row must equal the original K || V.
+    backup(*bsets[1])
+    rsets = [(shb, torch.empty(words, dtype=torch.int16, device=dev)) for _, _, shb in bsets]
+
+    def recover(shb, o):
+        pkg.rdp.rdp_kernel.fused_recovery_full_kv(shb, o, nd, S, T_tok, n_w, sb, 0, 1)
+
+    shb.view(torch.int16)[0].zero_()
+    recover(*rsets[0])
+    torch.cuda.synchronize()
+    kv_flat = torch.cat([K.view(torch.int16).reshape(-1), V.view(torch.int16).reshape(-1)])
+    if not (torch.equal(rsets[0][1], kv_flat) and torch.equal(flat[:words], kv_flat)):
+        raise RuntimeError("gs recovery output differs from K || V")
+    del kv_flat
+    wall, kms = time_kernel(torch, recover, rsets, steps, warmup)
+    alg = nd * S * 2 + S * 2 + words * 2      # survivors + P read; the row and K || V written
+    out["rdp_recover_2lost"] = {"us": round(kms * 1e3, 2), "alg_bytes": alg,
+                                "gbs": round(alg / kms / 1e6, 2),
+                                "frac_hbm_peak": round(alg / kms / 1e6 / HBM_PEAK_GBS, 4)}
+    del bsets, rsets, K, V, shb, flat
 
     # XOR (benchmark/xor/kernel.cu:17-41): the data rows copied into the shard
     # tensor and P, in one pass
@@ -749,7 +772,8 @@ def main():
         log("[bench] gs family (reference codes, packed layouts) on the 512 MiB stream")
         gs = bench_gs(pkg, torch, oracle, dev, args.seed, args.steps, args.warmup)
         log(f"[bench] gs: P/Q {gs['star_diagonal_pq']['us']:.1f} us, backup (pack + P/Q) "
-            f"{gs['rdp_backup']['us']:.1f} us, XOR {gs['xor_encode']['us']:.1f} us, "
+            f"{gs['rdp_backup']['us']:.1f} us, recovery (row + copy-out) "
+            f"{gs['rdp_recover_2lost']['us']:.1f} us, XOR {gs['xor_encode']['us']:.1f} us, "
             f"RS16 {gs['rs16_encode']['us']:.1f} us")
 
     if args.copy_calibration:

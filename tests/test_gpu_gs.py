@@ -212,6 +212,38 @@ def test_gs_backup_and_recovery(pkg, ora, gpu, B, H, T, D, nd):
         assert "recover_ms" in st
 
 
+# The recovery's rebuild and copy-out run as one pass: shard tensors 0 or 10
+# bytes past alignment, outputs misaligned differently, rows of odd length
+# (partial last tiles), padding words in the last data row, nd up to 10 (the
+# row-at-a-time path past 8), every kind of missing pair, and guard words on
+# both sides of both buffers.
+@pytest.mark.parametrize("nd", [1, 2, 3, 6, 8, 9, 10])
+@pytest.mark.parametrize("soff,ooff", [(0, 0), (5, 3)])
+@pytest.mark.parametrize("T,n", [(41, 200), (96, 211)])
+def test_gs_recover_layouts(pkg, ora, gpu, nd, soff, ooff, T, n):
+    total = 2 * T * n
+    S = -(-total // nd) + 3
+    rng = np.random.default_rng(nd * 13 + soff + T)
+    base = rng.integers(0, 65536, (nd + 2, S), dtype=np.uint16)
+    for a, b in [(-1, -1), (0, 1), (nd - 1, -1), (-1, 0), (1, 0), (nd, -1)]:
+        sh = base.copy()
+        for x in (a, b):
+            if 0 <= x < nd:
+                sh[x] = 0
+        exp = sh.copy()
+        ora.gs_recover(exp, nd, S, 0, a, b)
+        exp_out = ora.gs_load_full(exp, nd, S, T, n)
+        sbuf = torch.full(((nd + 2) * S + 16,), 0x3C3C, dtype=torch.int16, device=gpu)
+        sbuf[soff:soff + (nd + 2) * S] = dev(sh.reshape(-1).view(np.int16), gpu)
+        obuf = torch.full((total + 16,), 0x5A5A, dtype=torch.int16, device=gpu)
+        shards = sbuf[soff:soff + (nd + 2) * S].view(nd + 2, S)
+        pkg.rdp.rdp_kernel.fused_recovery_full_kv(shards, obuf[ooff:ooff + total], nd, S, T, n, 0, a, b)
+        assert np.array_equal(host(shards).view(np.uint16), exp), (a, b)
+        assert np.array_equal(host(obuf[ooff:ooff + total]).view(np.uint16), exp_out), (a, b)
+        assert bool((torch.cat([sbuf[:soff], sbuf[soff + (nd + 2) * S:]]) == 0x3C3C).all())
+        assert bool((torch.cat([obuf[:ooff], obuf[ooff + total:]]) == 0x5A5A).all())
+
+
 def test_gs_single_row_recovery_restores_kv(pkg, gpu):
     B, H, T, D, nd = 1, 4, 64, 128, 8
     K = torch.randn(B, H, T, D, device=gpu).half()
