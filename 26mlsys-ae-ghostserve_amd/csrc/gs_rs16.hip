@@ -184,22 +184,33 @@ __device__ __forceinline__ void rs_mix_full(const RsJob& j, const uint32_t (*pta
     }
 }
 
-// The last, partial tile: word loads guarded by the row length.
+// The last, partial tile.  Whole windows are read, and copied, as in a full
+// tile (aligned chunks, each lane storing the chunk that starts inside its
+// window); the one window that reaches past the row's end is read word by
+// word and copies its own words.
 template <int G, int NW>
 __device__ __forceinline__ void rs_mix_tail(const RsJob& j, const uint32_t (*ptab)[kRs16Tab],
-                                            int og, const int64_t* w0, bool copy,
+                                            int og, uint64_t t0b, const int64_t* w0, bool copy,
                                             uint32_t (*acc)[kRsGroup][4]) {
     rs_zero<G, NW>(acc);
     for (int i = 0; i < j.nin; ++i) {
+        const RowWin rw = row_win(reinterpret_cast<const uint8_t*>(j.in_rows[i]) + t0b);
         u32x4 x[NW];
 #pragma unroll
         for (int n = 0; n < NW; ++n) {
-            x[n] = rs_window(j.in_rows[i], w0[n], j.S);
-            if (copy && w0[n] < j.S) {
-                const uint64_t o = uint64_t(reinterpret_cast<const uint8_t*>(j.in_rows[i] + w0[n]) -
-                                            j.copy.src);
-                const int64_t nw = j.S - w0[n] < 8 ? j.S - w0[n] : 8;
-                copy_bytes(j.copy, o, o + 2 * uint64_t(nw));
+            const uint32_t off = 16 * (threadIdx.x + n * kTB);
+            if (w0[n] + 8 <= j.S) {
+                u32x4 lo, hi;
+                win_chunks(rw, off, lo, hi);
+                x[n] = win_join(rw, lo, hi);
+                if (copy) copy_owned<false>(j.copy, rw, off, lo, hi);
+            } else {
+                x[n] = rs_window(j.in_rows[i], w0[n], j.S);
+                if (copy && w0[n] < j.S) {
+                    const uint64_t o = uint64_t(reinterpret_cast<const uint8_t*>(j.in_rows[i] + w0[n]) -
+                                                j.copy.src);
+                    copy_bytes(j.copy, o, o + 2 * uint64_t(j.S - w0[n]));
+                }
             }
         }
         rs_mix_input<G, NW>(ptab, og, j.nin, i, x, acc);
@@ -237,8 +248,8 @@ __device__ __forceinline__ void rs_run_tiles(const RsJob& j, const uint32_t (*pt
                 if (G == 1) rs_mix_full<1, kRsNW>(j, ptab, og, t0b, copy, acc);
                 else rs_mix_full<2, kRsNW>(j, ptab, og, t0b, copy, acc);
             } else if (w0[0] < j.S) {
-                if (G == 1) rs_mix_tail<1, kRsNW>(j, ptab, og, w0, copy, acc);
-                else rs_mix_tail<2, kRsNW>(j, ptab, og, w0, copy, acc);
+                if (G == 1) rs_mix_tail<1, kRsNW>(j, ptab, og, t0b, w0, copy, acc);
+                else rs_mix_tail<2, kRsNW>(j, ptab, og, t0b, w0, copy, acc);
             } else {
                 for (int n = 0; n < kRsNW; ++n)
                     for (int g = 0; g < kRsGroup; ++g)

@@ -48,7 +48,7 @@ __device__ __forceinline__ bool xor_rows_batchable(RowSet rs, uint32_t in_bytes)
     return (rs.skip < 0 && rs.extra < 0) || (rs.skip >= 0 && rs.skip < ND && rs.extra == ND);
 }
 
-// XOR of the ND rows of one whole tile with every row's chunk requested at
+// XOR of the ND rows of one tile with every row's chunk requested at
 // once.  Row i of the batch is row i of `in`, or i + 1 from the skipped row
 // on.  Each lane loads its aligned chunk of the row; the next chunk, which a
 // misaligned window reaches into, is the next lane's (DPP), and lane 63 loads
@@ -104,7 +104,12 @@ __device__ __forceinline__ void xor_rows_tile(const uint8_t* in, uint64_t Sb, ui
     const uint32_t nbytes = uint32_t(Sb - t0 < uint64_t(kTileBytes) ? Sb - t0 : kTileBytes);
     const uint64_t c0 = t0 + 16 * threadIdx.x;
     u32x4 acc = {0, 0, 0, 0};
-    if (t0 + kTileBytes <= Sb && xor_rows_batchable<ND>(rs, in_bytes)) {
+    // Rows of at least one full tile take the batched path in every tile: in a
+    // partial last tile the lanes past the row's end XOR bytes that are not
+    // stored, and their copied chunks carry the next row's bytes (the values
+    // its own tile copies) or lie past the copy range.
+    const bool batched = Sb >= uint64_t(kTileBytes) && xor_rows_batchable<ND>(rs, in_bytes);
+    if (batched) {
         if constexpr (ND > 0) acc = xor_rows_batched<ND>(in, uint32_t(Sb), in_bytes, rs, fc);
     } else if (t0 + kTileBytes <= Sb) {
         // whole tile inside the rows: uniform row windows, loads carry the copy
@@ -124,7 +129,7 @@ __device__ __forceinline__ void xor_rows_tile(const uint8_t* in, uint64_t Sb, ui
         acc = xor_rows_partial(in, Sb, rs, c0, uint32_t(Sb - c0));
     }
     if (fc.dst) {
-        if (t0 + kTileBytes > Sb && c0 < Sb)
+        if (!batched && t0 + kTileBytes > Sb && c0 < Sb)
             for (int r = rs.lo; r < rs.hi; ++r)
                 copy_bytes(fc, uint64_t(r) * Sb + c0, uint64_t(r) * Sb + (c0 + 16 < Sb ? c0 + 16 : Sb));
         if (t0 == 0 && threadIdx.x == 0)
@@ -243,6 +248,35 @@ __device__ __forceinline__ u32x4 gs_src_chunk_bytes(const GsSource& g, const uin
     u32x4 v = {0, 0, 0, 0};
     for (int i = 0; i < 16; ++i)
         if (X + i >= 0) v = set_byte(v, i, gs_src_byte(g, base, X + i));
+    return v;
+}
+
+// The same 16 bytes for X with base + X 16-byte aligned: one aligned load, or
+// two merged where a K/V or V/padding boundary falls inside the chunk; bytes
+// before the tensor (X < 0) or past its end read as 0.  K and V are aligned
+// like their place in the rows, so each load is the aligned 16-byte chunk
+// around a byte of its own tensor and stays in that byte's page.
+__device__ __forceinline__ u32x4 gs_src_chunk(const GsSource& g, const uint8_t* base, int64_t X) {
+    const int64_t kb = g.kb, first = X < 0 ? 0 : X;
+    const int64_t last = X + 15 < g.rows_end - 1 ? X + 15 : g.rows_end - 1;
+    if (first > last) return u32x4{0, 0, 0, 0};
+    auto src = [&](int64_t x) { return x < kb ? 0 : (x < 2 * kb ? 1 : 2); };
+    auto load = [&](int w) {
+        return ld16(w == 0 ? g.K + X : (w == 1 ? g.V + (X - kb) : base + X));
+    };
+    const int ws = src(first), we = src(last);
+    u32x4 v;
+    if (ws == we) {
+        v = load(ws);
+    } else if (we == ws + 1) {
+        const int n = int((ws == 0 ? kb : 2 * kb) - X);   // bytes from the first source
+        const u32x4 a = load(ws);
+        v = (a ^ drop_low_bytes(a, n)) | drop_low_bytes(load(we), n);
+    } else {
+        return gs_src_chunk_bytes(g, base, X);   // both boundaries in one chunk (K under 16 bytes)
+    }
+    if (X < 0) v = drop_low_bytes(v, int(-X));
+    if (X + 16 > g.rows_end) v = v ^ drop_low_bytes(v, int(g.rows_end - X));
     return v;
 }
 
@@ -442,7 +476,9 @@ __global__ __launch_bounds__(kTB) void gs_rdp_parity_kernel(uint16_t* sh, int nd
     const uint64_t t0b = uint64_t(blockIdx.x) * kTileBytes;
     const uint32_t nbytes = uint32_t(Sb - t0b < uint64_t(kTileBytes) ? Sb - t0b : kTileBytes);
     const uint32_t lane = threadIdx.x & 63;
-    const bool fast = w0 + 8 <= S && w0 >= nd - 1;
+    // Lanes with a whole or partial window in the row whose diagonal does not
+    // wrap; the partial lane's words past the row end are never stored.
+    const bool fast = w0 < S && w0 >= nd - 1;
     u32x4 p = {0, 0, 0, 0}, q = {0, 0, 0, 0};
     // Stripes of at least one full tile: every row requested at once.  The
     // general loop below handles shorter stripes, nd > 8, rows tensors of
@@ -481,21 +517,23 @@ __global__ __launch_bounds__(kTB) void gs_rdp_parity_kernel(uint16_t* sh, int nd
         // K/V chunks lie inside K/V by the classification above; row chunks
         // past the tensor's end (lanes past the last word) read as zero
         u32x4 c0;
-        if (FUSED && mixed) c0 = gs_src_chunk_bytes(g, base, X);
+        if (FUSED && mixed) c0 = gs_src_chunk(g, base, X);
         else c0 = (from_kv || my < end) ? ld16(my) : u32x4{0, 0, 0, 0};
         // the shifts run with every lane active (a lane reading a disabled lane
         // gets nothing); lanes at a wave edge then load their neighbour chunk
         u32x4 c1 = from_next_lane(c0), cm = from_prev_lane(c0);
         if (lane == 63 && fast && (mr > 0 || s > 0))
-            c1 = (FUSED && mixed) ? gs_src_chunk_bytes(g, base, X + 16) : ld16(my + 16);
+            c1 = (FUSED && mixed) ? gs_src_chunk(g, base, X + 16)
+                                  : ((from_kv || my + 16 < end) ? ld16(my + 16) : u32x4{0, 0, 0, 0});
         if (lane == 0 && fast && s < 0)
-            cm = (FUSED && mixed) ? gs_src_chunk_bytes(g, base, X - 16) : ld16(my - 16);
+            cm = (FUSED && mixed) ? gs_src_chunk(g, base, X - 16) : ld16(my - 16);
         if (fast) {
             if (FUSED && (from_kv || mixed)) {
                 // This lane's chunk into the data rows.  The window's last mr
                 // bytes are in the next chunk: the next lane stores it, unless
-                // that lane is past the block or is a word-by-word lane (the
-                // row's last words), whose copy covers only its own words.
+                // that lane is past the block or past the row's last word (the
+                // row's last lanes store the next chunk themselves; bytes past
+                // the row are the next row's, stored with the same values).
                 gs_store_chunk(reinterpret_cast<uint8_t*>(sh), X, c0, g.copy_end);
                 if (mr > 0 && (threadIdx.x == kTB - 1 || w0 + 16 > S))
                     gs_store_chunk(reinterpret_cast<uint8_t*>(sh), X + 16, c1, g.copy_end);
@@ -513,8 +551,8 @@ __global__ __launch_bounds__(kTB) void gs_rdp_parity_kernel(uint16_t* sh, int nd
                 // back (k = floor(s / 16) <= -2), past the neighbour lane
                 const int k = (s - 15) / 16;
                 const int64_t Xq = X + 16 * k;
-                const u32x4 a = (FUSED && mixed) ? gs_src_chunk_bytes(g, base, Xq) : ld16(my + 16 * k);
-                const u32x4 b = (FUSED && mixed) ? gs_src_chunk_bytes(g, base, Xq + 16)
+                const u32x4 a = (FUSED && mixed) ? gs_src_chunk(g, base, Xq) : ld16(my + 16 * k);
+                const u32x4 b = (FUSED && mixed) ? gs_src_chunk(g, base, Xq + 16)
                                                  : ld16(my + 16 * k + 16);
                 qw = funnel16(a, b, uint32_t(s - 16 * k));
             }
@@ -556,9 +594,10 @@ __global__ __launch_bounds__(kTB) void gs_rdp_parity_kernel(uint16_t* sh, int nd
 // A block owns one column tile of every row.  Each data row's window is staged
 // in an LDS tile and written with tile_store, so every output byte has exactly
 // one writer whatever the alignment of out.  Full tiles of stripes with
-// nd = ND <= 8 in shards below 2 GiB request every surviving row's chunk at
-// once (the loads of xor_rows_batched, one LDS tile per row); otherwise the
-// rows go one at a time through one LDS tile.  Row t itself is never read.
+// nd = ND <= 8 in shards below 2 GiB, and their partial last tile when a row
+// holds at least one full tile, request every surviving row's chunk at once
+// (the loads of xor_rows_batched, one LDS tile per row); otherwise the rows
+// go one at a time through one LDS tile.  Row t itself is never read.
 // Stores, as measured on the 512 MiB stream: the copy-out non-temporal (232
 // -> 209 us), the rebuilt row plain (non-temporal: 226 us).
 template <int ND>
@@ -576,7 +615,9 @@ __global__ __launch_bounds__(kTB) void gs_recover_kernel(uint8_t* sh, uint64_t S
         if (o < out_len) tile_store<true>(out + o, tile, uint32_t(out_len - o < nbytes ? out_len - o : nbytes));
     };
     if constexpr (ND > 0) {
-        if (t0 + kTileBytes <= Sb && in_bytes) {
+        // every tile of rows of at least one full tile: in a partial last tile
+        // the lanes past the row's end stage bytes that are not stored
+        if (Sb >= uint64_t(kTileBytes) && in_bytes) {
             const uint32_t b15 = uint32_t(reinterpret_cast<uintptr_t>(sh)) & 15;
             const __amdgpu_buffer_rsrc_t rs = chunk_rsrc(sh - b15, (b15 + in_bytes + 15) & ~15u);
             const uint32_t lane = threadIdx.x & 63;

@@ -50,7 +50,7 @@ def test_xor_encode_fused_copy_offsets(pkg, ora, gpu, nd, S, doff, soff):
     assert bool((rest == 0xA5).all())
 
 
-@pytest.mark.parametrize("nd,S", [(4, 262144), (8, 999), (3, 17), (5, 3)])
+@pytest.mark.parametrize("nd,S", [(4, 262144), (8, 999), (3, 17), (5, 3), (6, 4096 * 3 + 37), (2, 5000)])
 def test_xor_reconstruct_matches_oracle(pkg, ora, gpu, nd, S):
     rng = np.random.default_rng(S)
     data = rng.integers(0, 256, nd * S, dtype=np.uint8)
@@ -153,6 +153,8 @@ def test_gs_rdp_parity_row_stride_is_S(pkg, ora, gpu):
     (2048, 9, 1, 0, 0, 0, 0, 0),          # one data row: fused
     (40, 50, 3, 5, 7, 7, 7, -5),          # fused
     (40, 50, 3, 5, 7, 3, 7, -5),          # V misaligned with its rows: copies
+    (1, 5, 2, 3, 0, 5, 0, 0),             # K of 10 bytes: both boundaries in one chunk
+    (2, 3, 3, 1, 0, 6, 0, 1),             # K of 12 bytes
 ])
 def test_gs_fused_backup_layouts(pkg, ora, gpu, T, n, nd, S_extra, koff, voff, soff, sb):
     tn = T * n
