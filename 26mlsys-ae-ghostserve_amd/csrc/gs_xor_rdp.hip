@@ -170,6 +170,62 @@ __global__ __launch_bounds__(kTB) void xor_reconstruct_kernel(const uint8_t* enc
                       FlatCopy{nullptr, nullptr, 0}, tile);
 }
 
+// ------------------------------------------------------- XOR encode from K, V
+// forward_encode_kv's pack (benchmark/xor/main.py:69-90: K bytes then V bytes,
+// zero padding) and encode_xor (benchmark/xor/kernel.cu:17-41) in one pass:
+// data row j of the shard tensor is bytes [j Sb, (j+1) Sb) of the stream
+// K || V || zeros, and row ND their XOR.  The host runs it when the shards, K
+// and V are 16-byte aligned and K's size kb is a multiple of 16, so every
+// aligned 16-byte chunk of the stream lies in K, in V or in the padding: it is
+// read through K's and V's buffer resources at once, the other load (and both,
+// in the padding) out of range and reading nothing.  Each lane stores, to the
+// data rows, the aligned chunk that starts inside its window (as the fused
+// copy of xor_rows_batched does) up to the end of the data rows, and the XOR
+// goes through LDS to row ND.  Rows hold at least one full tile; in a partial
+// last tile the lanes past a row's end store the next row's chunks, the
+// values that row's own tile stores.  kb < 2^30 and (ND + 1) Sb < 2^31.
+template <int ND>
+__global__ __launch_bounds__(kTB) void xor_encode_kv_kernel(const uint8_t* K, const uint8_t* V,
+                                                            uint32_t kb, uint8_t* sh, uint32_t Sb) {
+    __shared__ __attribute__((aligned(16))) uint8_t tile[kTileBytes + 16];
+    const uint32_t t0 = blockIdx.x * uint32_t(kTileBytes);
+    const uint32_t nbytes = Sb - t0 < uint32_t(kTileBytes) ? Sb - t0 : uint32_t(kTileBytes);
+    const uint32_t lane = threadIdx.x & 63;
+    const __amdgpu_buffer_rsrc_t rk = chunk_rsrc(K, kb), rv = chunk_rsrc(V, kb);
+    const uint32_t data_end = uint32_t(ND) * Sb;
+    // the stream's aligned chunk at x (x = kNoLoad: none): x < kb reads K,
+    // kb <= x < 2 kb reads V, anything else is out of range in both
+    auto stream_chunk = [&](uint32_t x) {
+        return chunk_load(rk, x) | chunk_load(rv, x - kb);
+    };
+    u32x4 lo[ND], e1[ND];
+#pragma unroll
+    for (int j = 0; j < ND; ++j) {
+        const uint32_t A = uint32_t(j) * Sb + t0, m = A & 15, my = A - m + 16 * threadIdx.x;
+        lo[j] = stream_chunk(my);
+        e1[j] = stream_chunk(lane == 63 && m ? my + 16 : kNoLoad);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    u32x4 acc = {0, 0, 0, 0};
+#pragma unroll
+    for (int j = 0; j < ND; ++j) {
+        const uint32_t A = uint32_t(j) * Sb + t0, m = A & 15, my = A - m + 16 * threadIdx.x;
+        const u32x4 hi = from_next_lane_or(lo[j], e1[j]);
+        acc ^= m ? funnel16(lo[j], hi, m) : lo[j];
+        const uint32_t c = m ? my + 16 : my;   // the chunk that starts in the window
+        const u32x4 v = m ? hi : lo[j];
+        if (c + 16 <= data_end) {
+            st_stream(sh, c, v);
+        } else if (c < data_end) {
+            const gptr<uint8_t> d = as_global(sh);
+            for (uint32_t i = 0; i < data_end - c; ++i) d[c + i] = byte_of(v, int(i));
+        }
+    }
+    *reinterpret_cast<u32x4*>(tile + 16 * threadIdx.x) = acc;
+    __syncthreads();
+    tile_store(sh + data_end + t0, tile, nbytes);
+}
+
 // ----------------------------------------------------------------- gs RDP P/Q
 // Words (u16).  P[c] = XOR_r D_r[c]; Qfull[d] = XOR_r D_r[(d - r) mod S].
 // Row r starts at byte r*S*2, so its tile is misaligned by mr bytes, and the
@@ -705,6 +761,18 @@ XorRecFn xor_rec_fn(int rows) {
 
 inline uint32_t small_bytes(uint64_t n) { return n < (uint64_t(1) << 31) ? uint32_t(n) : 0; }
 
+typedef void (*XorEncKvFn)(const uint8_t*, const uint8_t*, uint32_t, uint8_t*, uint32_t);
+
+template <int ND = 1>
+XorEncKvFn xor_encode_kv_fn(int nd) {
+    if constexpr (ND > 8) {
+        return nullptr;
+    } else {
+        if (nd == ND) return &xor_encode_kv_kernel<ND>;
+        return xor_encode_kv_fn<ND + 1>(nd);
+    }
+}
+
 typedef void (*GsRecoverFn)(uint8_t*, uint64_t, uint32_t, int, int, uint8_t*, uint64_t);
 
 template <int ND = 1>
@@ -796,6 +864,48 @@ extern "C" int kvec_xor_encode(const void* data_padded, void* shards, int data_s
     if (rc) return rc;
     return xor_rows((const uint8_t*)data_padded, Sb, RowSet{0, data_shards, -1, -1},
                     (uint8_t*)shards + Sb * data_shards, nullptr, st, "kvec_xor_encode");
+}
+
+// forward_encode_kv, benchmark/xor/main.py:69-90 (pack_kv of K then V into the
+// stream, zero padding) followed by encode_xor, benchmark/xor/kernel.cu:158-171.
+extern "C" int kvec_xor_encode_kv(const void* key_input, const void* value_input,
+                                  int64_t kv_half_bytes, void* shards, int data_shards,
+                                  int64_t shard_size, void* stream) {
+    if (data_shards < 1 || shard_size < 0 || kv_half_bytes < 0)
+        return set_error(KVEC_EINVAL, "kvec_xor_encode_kv: data_shards=%d shard_size=%lld kv_bytes=%lld",
+                         data_shards, (long long)shard_size, (long long)kv_half_bytes);
+    const uint64_t Sb = uint64_t(shard_size), kb = uint64_t(kv_half_bytes);
+    const uint64_t data_bytes = Sb * uint64_t(data_shards);
+    if (2 * kb > data_bytes)
+        return set_error(KVEC_EINVAL, "kvec_xor_encode_kv: K and V (%llu bytes) exceed %d rows of %lld",
+                         (unsigned long long)(2 * kb), data_shards, (long long)shard_size);
+    if (!shards || (kb && (!key_input || !value_input)))
+        return set_error(KVEC_EINVAL, "kvec_xor_encode_kv: null pointer");
+    if (Sb == 0) return KVEC_OK;
+    hipStream_t st = as_stream(stream);
+    uint8_t* sh = (uint8_t*)shards;
+    const uintptr_t R0 = uintptr_t(sh), R1 = R0 + data_bytes + Sb;
+    const uintptr_t Kp = uintptr_t(key_input), Vp = uintptr_t(value_input);
+    const bool apart = (Kp + kb <= R0 || Kp >= R1) && (Vp + kb <= R0 || Vp >= R1);
+    const bool aligned = ((R0 | Kp | Vp | kb) & 15) == 0;
+    XorEncKvFn fn = xor_encode_kv_fn(data_shards);
+    if (fn && apart && aligned && Sb >= uint64_t(kTileBytes) && kb < (uint64_t(1) << 30) &&
+        data_bytes + Sb < (uint64_t(1) << 31)) {
+        hipLaunchKernelGGL(fn, dim3(blocks_for(int64_t(Sb), kTileBytes)), dim3(kTB), 0, st,
+                           (const uint8_t*)key_input, (const uint8_t*)value_input, uint32_t(kb), sh,
+                           uint32_t(Sb));
+        return check_launch("kvec_xor_encode_kv");
+    }
+    // otherwise the pack, the zero padding, then encode_xor on the rows in place
+    int rc = copy_d2d(sh, key_input, kb, st, "kvec_xor_encode_kv");
+    if (!rc) rc = copy_d2d(sh + kb, value_input, kb, st, "kvec_xor_encode_kv");
+    if (rc) return rc;
+    if (data_bytes > 2 * kb) {
+        hipError_t e = hipMemsetAsync(sh + 2 * kb, 0, data_bytes - 2 * kb, st);
+        if (e != hipSuccess) return set_error(KVEC_EHIP, "kvec_xor_encode_kv: %s", hipGetErrorString(e));
+    }
+    return xor_rows(sh, Sb, RowSet{0, data_shards, -1, -1}, sh + data_bytes, nullptr, st,
+                    "kvec_xor_encode_kv");
 }
 
 // reconstruct_xor_launcher, benchmark/xor/kernel.cu:173-191

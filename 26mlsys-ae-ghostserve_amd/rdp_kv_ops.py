@@ -28,6 +28,10 @@ def pack_row_from_block(k_blk: torch.Tensor, v_blk: torch.Tensor, shards: torch.
         raise RuntimeError("KV must be contiguous.")
     if shards.dim() != 2:
         raise RuntimeError("shards must be [rows, S].")
+    # the reference leaves this unchecked (an out-of-range row writes past
+    # the tensor); here it is an error like the other argument checks
+    if not 0 <= int(row) < shards.size(0):
+        raise RuntimeError("row must be in [0, shards.size(0)).")
     words = k_blk.numel()
     S = shards.size(1)
     if S < 2 * words:

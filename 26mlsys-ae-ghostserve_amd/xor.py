@@ -7,8 +7,9 @@ order and in-place semantics, backed by libkvec's HIP kernels.
 Differences from the reference, none of which changes an output byte:
   * K/V may be any 2-byte dtype (fp16, bf16, ...) or a 1-byte one (fp8); the
     bytes are coded as raw bits and come back in the input dtype.
-  * forward_encode_kv packs K||V straight into the shard tensor instead of
-    going through two staging copies (the shards are identical).
+  * forward_encode_kv writes K||V into the shard tensor's data rows and P in
+    one pass over K and V (kvec_xor_encode_kv), instead of the reference's
+    pack, staging copy and encode (the shards are identical).
   * Every call is stream-ordered on torch's current stream; unpack does not
     block the host.
 """
@@ -76,20 +77,6 @@ def _check_kv(keys, values):
         raise AssertionError("keys and values must have the same shape")
 
 
-def _pack_into(keys, values, dst_bytes: torch.Tensor):
-    """K bytes then V bytes into dst_bytes[0 : 2*numel*es] (raw bits)."""
-    nbytes = keys.numel() * keys.element_size()
-    if keys.element_size() == 2:
-        B, H, T, D = keys.shape
-        xor_kernel.pack_kv(keys, values, dst_bytes, B * H * D, T)
-    else:
-        if nbytes % 2:
-            raise ValueError("1-byte KV needs an even number of elements")
-        _lib.call("kvec_pack_kv", keys.data_ptr(), values.data_ptr(), dst_bytes.data_ptr(),
-                  nbytes // 2, 1, _stream(dst_bytes))
-    return 2 * nbytes
-
-
 def forward_encode_kv(keys, values, num_data_shards, num_parity_shards):
     """benchmark/xor/main.py:47-133: K||V bytes -> (num_data_shards + 1) shards."""
     if num_parity_shards != 1:
@@ -107,12 +94,10 @@ def forward_encode_kv(keys, values, num_data_shards, num_parity_shards):
     data_bytes = num_data_shards * shard_size
     shards_KV = torch.empty((num_data_shards + num_parity_shards, shard_size), dtype=torch.uint8,
                             device=device)
-    flat = shards_KV.view(-1)
-    _pack_into(keys, values, flat)
-    if pad:
-        flat[total_bytes:data_bytes].zero_()
-    # data rows are already in place: the copy of encode_xor is skipped (same pointer)
-    xor_kernel.encode_xor(flat[:data_bytes], shards_KV, int(num_data_shards), int(shard_size))
+    # the pack (K bytes then V bytes, zero padding) and the encode in one call:
+    # one pass over K and V when the layouts allow it
+    _lib.call("kvec_xor_encode_kv", keys.data_ptr(), values.data_ptr(), total_bytes // 2,
+              shards_KV.data_ptr(), int(num_data_shards), int(shard_size), _stream(shards_KV))
 
     pack_io = 2 * total_bytes
     encode_io = data_bytes + data_bytes + shard_size

@@ -586,6 +586,36 @@ def bench_gs(pkg, torch, oracle, dev, seed, steps, warmup):
                          "frac_hbm_peak": round(alg / kms / 1e6 / HBM_PEAK_GBS, 4)}
     del sets
 
+    # forward_encode_kv (benchmark/xor/main.py:69-90 then encode_xor): K and V
+    # (the stream's two halves) packed into the data rows and P, one pass.
+    # Checked against the plain encode of the same stream.
+    half = STREAM_BYTES // 2
+    kvsets = []
+    for _ in range(2):
+        kv = torch.randint(0, 256, (2, half), generator=g, device=dev, dtype=torch.uint8)
+        kvsets.append((kv[0], kv[1], torch.empty((nd + 1, Sb), dtype=torch.uint8, device=dev)))
+
+    def xenc_kv(k, v, sh):
+        pkg._lib.call("kvec_xor_encode_kv", k.data_ptr(), v.data_ptr(), half, sh.data_ptr(), nd, Sb,
+                      pkg._lib.stream_handle(sh.device))
+
+    k0, v0, sh0 = kvsets[0]
+    xenc_kv(k0, v0, sh0)
+    ref = torch.zeros(nd * Sb, dtype=torch.uint8, device=dev)
+    ref[:half], ref[half:2 * half] = k0, v0
+    shr = torch.empty((nd + 1, Sb), dtype=torch.uint8, device=dev)
+    pkg.xor.xor_kernel.encode_xor(ref, shr, nd, Sb)
+    torch.cuda.synchronize()
+    if not torch.equal(sh0, shr):
+        raise RuntimeError("gs XOR encode from K, V differs from the encode of K || V")
+    del ref, shr
+    wall, kms = time_kernel(torch, xenc_kv, kvsets, steps, warmup)
+    alg = 2 * half + nd * Sb + Sb       # K, V read once; data rows + P written
+    out["xor_encode_from_kv"] = {"us": round(kms * 1e3, 2), "alg_bytes": alg,
+                                 "gbs": round(alg / kms / 1e6, 2),
+                                 "frac_hbm_peak": round(alg / kms / 1e6 / HBM_PEAK_GBS, 4)}
+    del kvsets, k0, v0, sh0
+
     # RS over GF(2^16) (benchmark/rs/kernel.cu:67-102): the data rows copied into
     # the shard tensor and 2 parities, in one pass
     m = 2
@@ -773,7 +803,8 @@ def main():
         gs = bench_gs(pkg, torch, oracle, dev, args.seed, args.steps, args.warmup)
         log(f"[bench] gs: P/Q {gs['star_diagonal_pq']['us']:.1f} us, backup (pack + P/Q) "
             f"{gs['rdp_backup']['us']:.1f} us, recovery (row + copy-out) "
-            f"{gs['rdp_recover_2lost']['us']:.1f} us, XOR {gs['xor_encode']['us']:.1f} us, "
+            f"{gs['rdp_recover_2lost']['us']:.1f} us, XOR {gs['xor_encode']['us']:.1f} us "
+            f"(from K, V {gs['xor_encode_from_kv']['us']:.1f} us), "
             f"RS16 {gs['rs16_encode']['us']:.1f} us")
 
     if args.copy_calibration:

@@ -177,6 +177,14 @@ int kvec_chunk_decode_paged(const kvec_paged_kv* kv, void* pool, const kvec_chun
  * data_padded [data_shards*shard_size] into shards, then P = XOR of them. */
 int kvec_xor_encode(const void* data_padded, void* shards, int data_shards,
                     int64_t shard_size, void* stream);
+/* forward_encode_kv, benchmark/xor/main.py:69-90 (pack_kv of K then V, each
+ * kv_half_bytes raw bytes, into the data stream, zero padding to
+ * data_shards*shard_size) followed by encode_xor (:158-171): one pass over K and
+ * V when shards, K and V are 16-byte aligned, kv_half_bytes is a multiple of
+ * 16, data_shards <= 8 and shard_size >= 4096 (else the copies, then the
+ * encode).  Needs 2*kv_half_bytes <= data_shards*shard_size. */
+int kvec_xor_encode_kv(const void* key_input, const void* value_input, int64_t kv_half_bytes,
+                       void* shards, int data_shards, int64_t shard_size, void* stream);
 /* reconstruct_xor_launcher, :173-191.  missing_indices: device int32 array of
  * missing_count entries; only missing_count == 1 does anything: a data row
  * m < data_shards is rebuilt from P, m == data_shards recomputes P.  The row is

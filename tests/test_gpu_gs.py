@@ -50,6 +50,42 @@ def test_xor_encode_fused_copy_offsets(pkg, ora, gpu, nd, S, doff, soff):
     assert bool((rest == 0xA5).all())
 
 
+# forward_encode_kv's pack and the encode in one call (kvec_xor_encode_kv): the
+# one-pass kernel for 16-byte-aligned K, V and shards with K a multiple of 16
+# bytes (rows aligned or not, padding, partial last tiles, nd 1..8), and the
+# copies-then-encode path otherwise (nd > 8, K not a multiple of 16, rows under
+# one tile, K or V misaligned); the shard tensor's surroundings stay untouched.
+@pytest.mark.parametrize("nd,kb,extra,koff,voff", [
+    (6, 196608, 0, 0, 0), (3, 100000, 6, 0, 0), (8, 40000, 13, 0, 16), (1, 8192, 3000, 16, 0),
+    (2, 4096, 0, 0, 0), (7, 65536, 4099, 0, 0),
+    (9, 40000, 7, 0, 0), (4, 1000, 1, 0, 0), (2, 1024, 77, 0, 0), (5, 65536, 0, 3, 0), (5, 65536, 0, 0, 7)])
+def test_xor_encode_kv_matches_oracle(pkg, ora, gpu, nd, kb, extra, koff, voff):
+    S = -(-2 * kb // nd) + extra
+    rng = np.random.default_rng(nd * 101 + kb + extra)
+    K = rng.integers(0, 256, kb, dtype=np.uint8)
+    V = rng.integers(0, 256, kb, dtype=np.uint8)
+    padded = np.zeros(nd * S, np.uint8)
+    padded[:kb], padded[kb:2 * kb] = K, V
+    want = ora.xor_encode(padded, nd, S)
+    kbuf = torch.zeros(kb + 32, dtype=torch.uint8, device=gpu)
+    vbuf = torch.zeros(kb + 32, dtype=torch.uint8, device=gpu)
+    kbuf[koff:koff + kb] = dev(K, gpu)
+    vbuf[voff:voff + kb] = dev(V, gpu)
+    sbuf = torch.full(((nd + 1) * S + 64,), 0xA5, dtype=torch.uint8, device=gpu)
+    shards = sbuf[16:16 + (nd + 1) * S]
+    pkg._lib.call("kvec_xor_encode_kv", kbuf[koff:].data_ptr(), vbuf[voff:].data_ptr(), kb,
+                  shards.data_ptr(), nd, S, pkg._lib.stream_handle(gpu))
+    assert np.array_equal(host(shards).reshape(nd + 1, S), want)
+    assert bool((torch.cat([sbuf[:16], sbuf[16 + (nd + 1) * S:]]) == 0xA5).all())
+
+
+def test_xor_encode_kv_rejects_short_shards(pkg, gpu):
+    t = torch.zeros(64, dtype=torch.uint8, device=gpu)
+    with pytest.raises(pkg._lib.KvecError, match="exceed"):
+        pkg._lib.call("kvec_xor_encode_kv", t.data_ptr(), t.data_ptr(), 32, t.data_ptr(), 2, 16,
+                      pkg._lib.stream_handle(gpu))
+
+
 @pytest.mark.parametrize("nd,S", [(4, 262144), (8, 999), (3, 17), (5, 3), (6, 4096 * 3 + 37), (2, 5000)])
 def test_xor_reconstruct_matches_oracle(pkg, ora, gpu, nd, S):
     rng = np.random.default_rng(S)
@@ -276,6 +312,12 @@ def test_gs_pack_row(pkg, ora, gpu):
     with pytest.raises(RuntimeError):
         pkg.rdp_kv_ops.pack_row_from_block(dev(np.zeros(S, np.uint16), gpu).view(torch.float16),
                                            dev(np.zeros(S, np.uint16), gpu).view(torch.float16), d, 0)
+    # a row outside the tensor is rejected before anything is written
+    kz = dev(np.ones(w, np.uint16), gpu).view(torch.float16)
+    for bad in (world + 2, -1):
+        with pytest.raises(RuntimeError, match="row must be in"):
+            pkg.rdp_kv_ops.pack_row_from_block(kz, kz, d, bad)
+    assert np.array_equal(host(d), rows)
 
 
 # ------------------------------------------------------------------ gs RS16
