@@ -130,14 +130,18 @@ def forward_encode_kv(keys: torch.Tensor, values: torch.Tensor, num_data_shards:
     shard_sz, pad = shard_size_and_pad(total, num_data_shards)
     total_shards = num_data_shards + num_parity_shards
     assert shard_sz > 0
-    data_padded = torch.empty(num_data_shards * shard_sz, dtype=torch.uint16, device=device)
-    if pad:
-        data_padded.view(torch.int16)[total:].zero_()
-    rs_kernel.pack_fp16_pair_to_u16(keys.contiguous().view(-1), values.contiguous().view(-1),
-                                    data_padded)
+    # K || V and the zero padding go straight into the shard tensor's data rows
+    # (the reference packs into a separate data_padded and the encode copies
+    # it over); the encode then reads the rows in place and writes the parity
+    # rows.  The shard bytes are the same.
     shards = torch.empty((total_shards, shard_sz), dtype=torch.uint16, device=device)
+    data_rows = shards.view(-1)[: num_data_shards * shard_sz]
+    if pad:
+        data_rows.view(torch.int16)[total:].zero_()
+    rs_kernel.pack_fp16_pair_to_u16(keys.contiguous().view(-1), values.contiguous().view(-1),
+                                    data_rows)
     gf_exp, gf_log = device_gf_tables(device)
-    rs_kernel.encode_rs_u16(data_padded, shards, num_data_shards, num_parity_shards, shard_sz,
+    rs_kernel.encode_rs_u16(data_rows, shards, num_data_shards, num_parity_shards, shard_sz,
                             gf_exp, gf_log)
     meta = {
         "B": B, "H": H, "T": T, "D": D,
