@@ -81,6 +81,7 @@ SIGNATURES = {
     "kvec_chunk_decode_paged": (_i, [_kvp, _vp, _csp, _vp, _i, _vp]),
     "kvec_xor_encode": (_i, [_vp, _vp, _i, _i64, _vp]),
     "kvec_xor_encode_kv": (_i, [_vp, _vp, _i64, _vp, _i, _i64, _vp]),
+    "kvec_xor_recover_kv": (_i, [_vp, _vp, _i, _i64, _i64, _i, _vp]),
     "kvec_xor_reconstruct": (_i, [_vp, _vp, _vp, _i64, _i, _vp, _i, _vp]),
     "kvec_pack_kv": (_i, [_vp, _vp, _vp, _i, _i, _vp]),
     "kvec_unpack_kv": (_i, [_vp, _vp, _i, _i, _vp]),

@@ -928,6 +928,50 @@ extern "C" int kvec_xor_reconstruct(const void* encoded_data, void* recovered_da
     return check_launch("kvec_xor_reconstruct");
 }
 
+// backwards_decode_kv, benchmark/xor/main.py:159-194: the missing shard rebuilt
+// in place (reconstruct_xor) and the first out_bytes of the data rows copied
+// out (unpack_kv).  A lost data row: one pass of gs_recover_kernel over the
+// byte rows (P is row data_shards).  A lost P: P recomputed, then the copy-out
+// pass.  missing < 0: the copy-out pass alone.  With out overlapping the
+// shards, the reconstruct and then a copy.
+extern "C" int kvec_xor_recover_kv(void* shards, void* out, int data_shards, int64_t shard_size,
+                                   int64_t out_bytes, int missing, void* stream) {
+    if (!shards || (out_bytes > 0 && !out))
+        return set_error(KVEC_EINVAL, "kvec_xor_recover_kv: null pointer");
+    if (data_shards < 1 || shard_size < 0 || out_bytes < 0 || missing > data_shards)
+        return set_error(KVEC_EINVAL, "kvec_xor_recover_kv: data_shards=%d shard_size=%lld missing=%d",
+                         data_shards, (long long)shard_size, missing);
+    const uint64_t Sb = uint64_t(shard_size), nbytes = uint64_t(out_bytes);
+    if (nbytes > Sb * uint64_t(data_shards))
+        return set_error(KVEC_EINVAL, "kvec_xor_recover_kv: %llu output bytes exceed the data rows",
+                         (unsigned long long)nbytes);
+    if (Sb == 0) return KVEC_OK;
+    hipStream_t st = as_stream(stream);
+    uint8_t* sh = (uint8_t*)shards;
+    const int nd = data_shards;
+    if (missing == nd) {   // P recomputed from the data rows
+        int rc = xor_rows(sh, Sb, RowSet{0, nd, -1, -1}, sh + uint64_t(nd) * Sb, nullptr, st,
+                          "kvec_xor_recover_kv");
+        if (rc) return rc;
+    }
+    if (nbytes == 0 && missing < 0) return KVEC_OK;
+    const int t = missing >= 0 && missing < nd ? missing : -1;
+    const uintptr_t R0 = uintptr_t(sh), R1 = R0 + uint64_t(nd + 1) * Sb;
+    const uintptr_t O0 = uintptr_t(out), O1 = O0 + nbytes;
+    if (nbytes == 0 || O1 <= R0 || O0 >= R1) {
+        if (t < 0 && nbytes == 0) return KVEC_OK;
+        hipLaunchKernelGGL(gs_recover_fn(nd), dim3(blocks_for(int64_t(Sb), kTileBytes)), dim3(kTB), 0, st,
+                           sh, Sb, small_bytes(uint64_t(nd + 1) * Sb), nd, t, (uint8_t*)out, nbytes);
+        return check_launch("kvec_xor_recover_kv");
+    }
+    if (t >= 0) {
+        int rc = xor_rows(sh, Sb, RowSet{0, nd, t, nd}, sh + uint64_t(t) * Sb, nullptr, st,
+                          "kvec_xor_recover_kv");
+        if (rc) return rc;
+    }
+    return copy_d2d(out, sh, nbytes, st, "kvec_xor_recover_kv");
+}
+
 // pack_kv_launcher, benchmark/xor/kernel.cu:193-207: K bytes then V bytes
 // (the little-endian byte split of a 16-bit word is the identity in memory).
 extern "C" int kvec_pack_kv(const void* key_input, const void* value_input, void* kv_bytes, int n,

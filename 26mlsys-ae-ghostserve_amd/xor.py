@@ -120,7 +120,7 @@ def forward_encode_kv(keys, values, num_data_shards, num_parity_shards):
 
 
 def backwards_decode_kv(pkg, missing_shards):
-    """benchmark/xor/main.py:137-212: zero the missing shard, rebuild it (one
+    """benchmark/xor/main.py:137-212: rebuild the missing shard in place (one
     missing shard at most), unpack K, V.  Returns (keys, values, stats)."""
     shards_KV = pkg["shards_KV"]
     T = pkg["seq_len"]
@@ -141,28 +141,19 @@ def backwards_decode_kv(pkg, missing_shards):
         if idx < 0 or idx >= total_shards:
             raise ValueError(f"Missing shard {idx} out of range 0..{total_shards-1}")
 
-    for idx in missing_shards:
-        shards_KV[idx].zero_()
-
-    r_ms = 0.0
-    if len(missing_shards) == 1:
-        missing_idx_tensor = torch.tensor(missing_shards, dtype=torch.int32, device=device)
-        recovered_missing = torch.empty((1, shard_size), dtype=torch.uint8, device=device)
-        xor_kernel.reconstruct_xor(shards_KV, shards_KV, recovered_missing, int(shard_size),
-                                   int(num_data_shards), missing_idx_tensor)
-
-    byte_region = shards_KV[:num_data_shards].contiguous().view(-1)
+    # The missing shard is rebuilt in place and the data rows copied out in one
+    # call (one pass over the rows when a data row is lost).  The reference
+    # zeroes the missing shard first; that row is rewritten in full and never
+    # read, so the zeroing is left out.
     es = torch.empty((), dtype=dtype).element_size()
     de_bytes_needed = 2 * es * T * n
-    if byte_region.numel() < de_bytes_needed:
+    if num_data_shards * shard_size < de_bytes_needed:
         raise RuntimeError("Not enough bytes in reconstructed data region.")
-
     dequant_KV = torch.empty(2 * T * n, dtype=dtype, device=device)
-    if es == 2:
-        xor_kernel.unpack_kv(byte_region, dequant_KV, int(n), int(T))
-    else:
-        _lib.call("kvec_unpack_kv", byte_region.data_ptr(), dequant_KV.data_ptr(),
-                  de_bytes_needed // 4, 1, _stream(byte_region))
+    missing = int(missing_shards[0]) if len(missing_shards) == 1 else -1
+    _lib.call("kvec_xor_recover_kv", shards_KV.data_ptr(), dequant_KV.data_ptr(),
+              int(num_data_shards), int(shard_size), de_bytes_needed, missing, _stream(shards_KV))
+    r_ms = 0.0
 
     keys_out = dequant_KV[:T * n].view(B, H, T, D)
     values_out = dequant_KV[T * n: 2 * T * n].view(B, H, T, D)

@@ -614,7 +614,30 @@ def bench_gs(pkg, torch, oracle, dev, seed, steps, warmup):
     out["xor_encode_from_kv"] = {"us": round(kms * 1e3, 2), "alg_bytes": alg,
                                  "gbs": round(alg / kms / 1e6, 2),
                                  "frac_hbm_peak": round(alg / kms / 1e6 / HBM_PEAK_GBS, 4)}
-    del kvsets, k0, v0, sh0
+
+    # backwards_decode_kv (benchmark/xor/main.py:159-194) with data shard 0 lost:
+    # the row rebuilt from P in place and K || V copied out, one pass
+    xenc_kv(*kvsets[1])
+    rsets = [(sh, torch.empty(2 * half, dtype=torch.uint8, device=dev)) for _, _, sh in kvsets]
+
+    def xdec(sh, o):
+        pkg._lib.call("kvec_xor_recover_kv", sh.data_ptr(), o.data_ptr(), nd, Sb, 2 * half, 0,
+                      pkg._lib.stream_handle(sh.device))
+
+    keep = sh0[0].clone()
+    sh0[0].fill_(0x5A)
+    xdec(*rsets[0])
+    torch.cuda.synchronize()
+    if not (torch.equal(sh0[0], keep) and torch.equal(rsets[0][1][:half], k0) and
+            torch.equal(rsets[0][1][half:], v0)):
+        raise RuntimeError("gs XOR decode differs from the encoded K || V")
+    del keep
+    wall, kms = time_kernel(torch, xdec, rsets, steps, warmup)
+    alg = nd * Sb + Sb + 2 * half       # 5 data rows + P read; the row + K || V written
+    out["xor_decode_1lost"] = {"us": round(kms * 1e3, 2), "alg_bytes": alg,
+                               "gbs": round(alg / kms / 1e6, 2),
+                               "frac_hbm_peak": round(alg / kms / 1e6 / HBM_PEAK_GBS, 4)}
+    del kvsets, rsets, k0, v0, sh0
 
     # RS over GF(2^16) (benchmark/rs/kernel.cu:67-102): the data rows copied into
     # the shard tensor and 2 parities, in one pass
@@ -804,7 +827,8 @@ def main():
         log(f"[bench] gs: P/Q {gs['star_diagonal_pq']['us']:.1f} us, backup (pack + P/Q) "
             f"{gs['rdp_backup']['us']:.1f} us, recovery (row + copy-out) "
             f"{gs['rdp_recover_2lost']['us']:.1f} us, XOR {gs['xor_encode']['us']:.1f} us "
-            f"(from K, V {gs['xor_encode_from_kv']['us']:.1f} us), "
+            f"(from K, V {gs['xor_encode_from_kv']['us']:.1f} us, decode "
+            f"{gs['xor_decode_1lost']['us']:.1f} us), "
             f"RS16 {gs['rs16_encode']['us']:.1f} us")
 
     if args.copy_calibration:

@@ -192,6 +192,12 @@ int kvec_xor_encode_kv(const void* key_input, const void* value_input, int64_t k
 int kvec_xor_reconstruct(const void* encoded_data, void* recovered_data,
                          void* recovered_missing, int64_t shard_size, int data_shards,
                          const int32_t* missing_indices, int missing_count, void* stream);
+/* backwards_decode_kv, benchmark/xor/main.py:159-194: missing shard rebuilt
+ * in place (a data row from P and the others in one pass with the copy-out; P
+ * recomputed when missing == data_shards; missing < 0: nothing rebuilt), then
+ * the first out_bytes of the data rows copied to out (unpack_kv). */
+int kvec_xor_recover_kv(void* shards, void* out, int data_shards, int64_t shard_size,
+                        int64_t out_bytes, int missing, void* stream);
 /* pack_kv_launcher / unpack_kv_launcher, :193-223: K bytes then V bytes of
  * n*seq_len 16-bit words each (little-endian split == memory order). */
 int kvec_pack_kv(const void* key_input, const void* value_input, void* kv_bytes, int n,

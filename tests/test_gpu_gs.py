@@ -79,6 +79,40 @@ def test_xor_encode_kv_matches_oracle(pkg, ora, gpu, nd, kb, extra, koff, voff):
     assert bool((torch.cat([sbuf[:16], sbuf[16 + (nd + 1) * S:]]) == 0xA5).all())
 
 
+# kvec_xor_recover_kv: a lost data row (one pass), a lost P, nothing lost, no
+# output bytes, and an output overlapping the shard tensor (the two-step path).
+@pytest.mark.parametrize("nd,S,out_bytes", [(6, 4096 * 3 + 37, 6 * (4096 * 3 + 37) - 5), (3, 1001, 2000),
+                                            (9, 5000, 9 * 5000)])
+def test_xor_recover_kv_matches_oracle(pkg, ora, gpu, nd, S, out_bytes):
+    rng = np.random.default_rng(nd + S)
+    enc = ora.xor_encode(rng.integers(0, 256, nd * S, dtype=np.uint8), nd, S)
+    st = pkg._lib.stream_handle(gpu)
+    for missing in [0, nd - 1, nd, -1]:
+        sh = enc.copy()
+        if missing >= 0:
+            sh[missing] = 0x77
+        d = dev(sh, gpu)
+        out = torch.full((out_bytes + 32,), 0xEE, dtype=torch.uint8, device=gpu)
+        pkg._lib.call("kvec_xor_recover_kv", d.data_ptr(), out[16:].data_ptr(), nd, S, out_bytes,
+                      missing, st)
+        want = enc if missing >= 0 else sh
+        assert np.array_equal(host(d), want), missing
+        assert np.array_equal(host(out[16:16 + out_bytes]), want[:nd].reshape(-1)[:out_bytes]), missing
+        assert bool((torch.cat([out[:16], out[16 + out_bytes:]]) == 0xEE).all())
+    # no output bytes: the row is still rebuilt
+    d = dev(np.where(np.arange(nd + 1)[:, None] == 1, 0, enc).astype(np.uint8), gpu)
+    pkg._lib.call("kvec_xor_recover_kv", d.data_ptr(), 0, nd, S, 0, 1, st)
+    assert np.array_equal(host(d), enc)
+    # an output inside the shard tensor's own P row (its first out bytes): rebuild, then copy
+    n = min(out_bytes, S)
+    sh = enc.copy()
+    sh[0] = 0
+    d = dev(sh, gpu)
+    pkg._lib.call("kvec_xor_recover_kv", d.data_ptr(), d[nd].data_ptr(), nd, S, n, 0, st)
+    assert np.array_equal(host(d)[:nd], enc[:nd])
+    assert np.array_equal(host(d)[nd, :n], enc[:nd].reshape(-1)[:n])
+
+
 def test_xor_encode_kv_rejects_short_shards(pkg, gpu):
     t = torch.zeros(64, dtype=torch.uint8, device=gpu)
     with pytest.raises(pkg._lib.KvecError, match="exceed"):
@@ -129,7 +163,9 @@ def test_xor_forward_backward_round_trip(pkg, ora, gpu, dtype, nd):
     for miss in range(nd + 1):
         pk2 = dict(pk)
         pk2["shards_KV"] = pk["shards_KV"].clone()
+        pk2["shards_KV"][miss].fill_(0x5A)          # the lost shard's bytes are garbage
         kr, vr, st = pkg.xor.backwards_decode_kv(pk2, [miss])
+        assert torch.equal(pk2["shards_KV"], pk["shards_KV"]), miss   # rebuilt in place
         assert kr.dtype == dtype and kr.shape == k.shape
         assert torch.equal(kr.cpu().view(torch.uint8), k.view(torch.uint8))
         assert torch.equal(vr.cpu().view(torch.uint8), v.view(torch.uint8))
