@@ -67,11 +67,31 @@ def test_rdp_rejects_bad_arguments(pkg):
     assert L.kvec_rdp_encode(arr, 7, 16, 16, 7, 16, None) == -1   # k > p-1
     assert L.kvec_rdp_encode(arr, 6, 16, 16, 7, 24, None) == -1   # row_bytes % 16
     assert L.kvec_rdp_encode(arr, 6, 16, 16, 17, 16, None) == -2  # p too large
-    assert b"p=4" in L.kvec_last_error() or b"not" in L.kvec_last_error() or True
+    assert b"p=17" in L.kvec_last_error()
     bad = (C.c_void_p * 6)(*([16] * 5 + [8]))
     assert L.kvec_rdp_encode(bad, 6, 16, 16, 7, 16, None) == -1   # misaligned shard
     assert b"aligned" in L.kvec_last_error()
     assert L.kvec_rdp_decode(arr, 4, 5, 16, 7, -1, None) == -1    # erased index > k+1
+
+
+def test_xor_one_call_entries_reject_bad_arguments(pkg):
+    """kvec_xor_encode_kv / kvec_xor_recover_kv validate sizes and pointers
+    before any device call (the pointers below are never dereferenced)."""
+    L = pkg._lib.lib()
+    p = 4096
+    # K and V larger than the data rows
+    assert L.kvec_xor_encode_kv(p, p, 100, p, 2, 99, None) == -1
+    assert b"exceed" in L.kvec_last_error()
+    assert L.kvec_xor_encode_kv(p, p, 16, p, 0, 64, None) == -1        # no data shards
+    assert L.kvec_xor_encode_kv(None, p, 16, p, 2, 64, None) == -1     # null K
+    assert b"null" in L.kvec_last_error()
+    assert L.kvec_xor_encode_kv(p, p, 0, p, 2, 0, None) == 0           # empty: nothing to do
+    # recovery: missing index past P, output longer than the data rows, null output
+    assert L.kvec_xor_recover_kv(p, p, 3, 64, 16, 4, None) == -1
+    assert L.kvec_xor_recover_kv(p, p, 3, 64, 3 * 64 + 1, 0, None) == -1
+    assert b"exceed" in L.kvec_last_error()
+    assert L.kvec_xor_recover_kv(p, None, 3, 64, 16, 0, None) == -1
+    assert L.kvec_xor_recover_kv(p, p, 3, 0, 0, 1, None) == 0          # empty rows
 
 
 def test_product_fails_loudly_without_library(pkg, monkeypatch, tmp_path):
@@ -115,10 +135,11 @@ def test_chunk_rejects_bad_arguments(pkg):
     assert rc(col_off=8) == -1                 # misaligned column
     assert rc(col_off=(1 << 20) - 256) == -1   # past the row plane
     assert rc(width=256) == -1                 # cells too small for the chunk
+    assert b"k*(p-1)*width" in L.kvec_last_error()
     assert rc(P=4100) == -1                    # misaligned parity
     assert rc(m=5) == -1
     assert rc(row_bytes=1 << 30) == -2         # (p-1)*R >= 4 GiB
-    assert b"k*(p-1)*width" in L.kvec_last_error() or True
+    assert b"4 GiB" in L.kvec_last_error()
     er = (C.c_int32 * 1)(10)
     assert L.kvec_chunk_decode_paged(C.byref(kv), 4096, C.byref(stripe()), er, 1, None) == -1
     assert L.kvec_chunk_decode_paged(C.byref(kv), 8192, C.byref(stripe()), er, 0, None) == -1
