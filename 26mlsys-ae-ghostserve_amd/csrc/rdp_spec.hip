@@ -127,25 +127,71 @@ __global__ __launch_bounds__(kBS) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
     }
 }
 
-// Same map, read from the kernel argument: one output cell at a time, so the
-// accumulator stays a single register (re-read inputs hit L2).
-__global__ __launch_bounds__(kBS) void rdp_decode_generic_kernel(RdpPtrs sh, RdpPlan plan, int rows,
+// The decode map by input cell, for the generic kernel: each cell the outputs
+// need, with the set of outputs (bit o) that XOR it in.  Built on the host
+// from the plan's per-output masks.
+constexpr int kRdpMaxCells = kRdpMaxShards * kRdpMaxRows;
+static_assert(kRdpMaxOut <= 32, "output sets are 32-bit masks");
+struct RdpCellMap {
+    int ncell, nout;
+    int out_cell[kRdpMaxOut];
+    uint8_t cell[kRdpMaxCells];
+    uint32_t outs[kRdpMaxCells];
+};
+
+inline RdpCellMap rdp_cell_map(const RdpPlan& plan) {
+    RdpCellMap cm{};
+    cm.nout = plan.nout;
+    for (int o = 0; o < plan.nout; ++o) cm.out_cell[o] = plan.out_cell[o];
+    for (int c = 0; c < kRdpMaxCells; ++c) {
+        uint32_t outs = 0;
+        for (int o = 0; o < plan.nout; ++o)
+            if ((plan.mask[o][c >> 6] >> (c & 63)) & 1) outs |= 1u << o;
+        if (outs) {
+            cm.cell[cm.ncell] = uint8_t(c);
+            cm.outs[cm.ncell++] = outs;
+        }
+    }
+    return cm;
+}
+
+// Same map for any (p, k) and any shard size.  Each needed cell is loaded
+// once, eight at a time so that eight are in flight, and folded into every
+// output that uses it (wave-uniform tests of its output set); the outputs
+// accumulate in registers.
+__global__ __launch_bounds__(kBS) void rdp_decode_generic_kernel(RdpPtrs sh, RdpCellMap cm, int rows,
                                                                  uint64_t R, uint32_t nvec) {
+    constexpr int kBatch = 8;
     const uint32_t u = blockIdx.x * kBS + threadIdx.x;
     if (u >= nvec) return;
     const uint32_t off = u << 4;
-    for (int o = 0; o < plan.nout; ++o) {
-        u32x4 acc = {0, 0, 0, 0};
-        for (int w = 0; w < kRdpNW; ++w) {
-            uint64_t m = plan.mask[o][w];
-            while (m) {
-                const int c = w * 64 + __builtin_ctzll(m);
-                m &= m - 1;
-                acc ^= ld16(sh.p[c / rows] + (c % rows) * R + off);
+    u32x4 acc[kRdpMaxOut];
+#pragma unroll
+    for (int o = 0; o < kRdpMaxOut; ++o) acc[o] = u32x4{0, 0, 0, 0};
+    for (int i0 = 0; i0 < cm.ncell; i0 += kBatch) {
+        u32x4 x[kBatch];
+#pragma unroll
+        for (int t = 0; t < kBatch; ++t) {
+            x[t] = u32x4{0, 0, 0, 0};
+            if (i0 + t < cm.ncell) {
+                const int c = cm.cell[i0 + t];
+                x[t] = ld16(sh.p[c / rows] + uint64_t(c % rows) * R + off);
             }
         }
-        const int c = plan.out_cell[o];
-        st_stream(sh.p[c / rows] + (c % rows) * R, off, acc);
+#pragma unroll
+        for (int t = 0; t < kBatch; ++t) {
+            const uint32_t outs = i0 + t < cm.ncell ? cm.outs[i0 + t] : 0u;
+#pragma unroll
+            for (int o = 0; o < kRdpMaxOut; ++o)
+                if ((outs >> o) & 1) acc[o] ^= x[t];
+        }
+    }
+#pragma unroll
+    for (int o = 0; o < kRdpMaxOut; ++o) {
+        if (o < cm.nout) {
+            const int c = cm.out_cell[o];
+            st_stream(sh.p[c / rows] + uint64_t(c % rows) * R, off, acc[o]);
+        }
     }
 }
 
@@ -198,13 +244,19 @@ DecFn pick_decode(int e0, int e1) {
     }
 }
 
-// Compile-time XOR networks are built for the full-width codes p = 3, 5, 7
-// (shards below 4 GiB); everything else takes the generic kernel.
-static DecFn decode_fn(int p, int k, int e0, int e1) {
-    if (p == 7 && k == 6) return pick_decode<7, 6, true>(e0, e1);
-    if (p == 5 && k == 4) return pick_decode<5, 4, true>(e0, e1);
-    if (p == 3 && k == 2) return pick_decode<3, 2, true>(e0, e1);
+// Compile-time XOR networks are built for the full-width codes p = 3, 5, 7,
+// through buffer resources (shards below 4 GiB) or flat addresses (larger);
+// everything else takes the generic kernel.
+template <bool BUF>
+static DecFn decode_fn_t(int p, int k, int e0, int e1) {
+    if (p == 7 && k == 6) return pick_decode<7, 6, BUF>(e0, e1);
+    if (p == 5 && k == 4) return pick_decode<5, 4, BUF>(e0, e1);
+    if (p == 3 && k == 2) return pick_decode<3, 2, BUF>(e0, e1);
     return nullptr;
+}
+
+static DecFn decode_fn(int p, int k, int e0, int e1, bool buf) {
+    return buf ? decode_fn_t<true>(p, k, e0, e1) : decode_fn_t<false>(p, k, e0, e1);
 }
 
 static unsigned rdp_grid(uint32_t nvec) { return blocks_for(nvec, kBS); }
@@ -269,7 +321,7 @@ extern "C" int kvec_rdp_decode(void* const* shards, int k, int p, int64_t row_by
     if (a < 0 || row_bytes == 0) return KVEC_OK;
     const uint32_t nvec = uint32_t(row_bytes / 16);
     const bool buf = fits_buffer(uint64_t(p - 1) * uint64_t(row_bytes));
-    DecFn fn = buf ? decode_fn(p, k, a, b) : nullptr;
+    DecFn fn = decode_fn(p, k, a, b, buf);
     if (fn) {
         hipLaunchKernelGGL(fn, dim3(rdp_grid(nvec)), dim3(kBS), 0, as_stream(stream), s,
                            uint64_t(row_bytes), nvec);
@@ -278,8 +330,8 @@ extern "C" int kvec_rdp_decode(void* const* shards, int k, int p, int64_t row_by
         RdpPlan plan = make_rdp_plan(p, k, a, b);
         if (!plan.ok)
             return set_error(KVEC_EDECODE, "kvec_rdp_decode: pattern (%d, %d) not decodable", a, b);
-        hipLaunchKernelGGL(rdp_decode_generic_kernel, grid, block, 0, as_stream(stream), s, plan, p - 1,
-                           uint64_t(row_bytes), nvec);
+        hipLaunchKernelGGL(rdp_decode_generic_kernel, grid, block, 0, as_stream(stream), s,
+                           rdp_cell_map(plan), p - 1, uint64_t(row_bytes), nvec);
     }
     return check_launch("kvec_rdp_decode");
 }

@@ -52,12 +52,14 @@ def test_rdp_decode_all_patterns(pkg, ora, gpu, p, k):
             assert np.array_equal(_host(dev[s], (p - 1, R)), full[s]), (p, k, e0, e1, s)
 
 
-def test_rdp_decode_inconsistent_input_matches_oracle(pkg, ora, gpu):
+@pytest.mark.parametrize("p,k", [(7, 6), (11, 7), (5, 3)])   # compiled networks, then the generic kernel
+def test_rdp_decode_inconsistent_input_matches_oracle(pkg, ora, gpu, p, k):
     """On input that is not a codeword the decoder is still a fixed function of
     the surviving bytes; the GPU and the oracle pick the same equations."""
-    p, k, R = 7, 6, 256
-    rng = np.random.default_rng(99)
-    for e0, e1 in [(2, -1), (6, -1), (7, -1), (0, 7), (6, 7), (1, 4), (3, 6)]:
+    R = 256
+    rng = np.random.default_rng(99 + p * k)
+    pats = [(2, -1), (k, -1), (k + 1, -1), (0, k + 1), (k, k + 1), (1, k - 1), (0, k)]
+    for e0, e1 in pats:
         cols = [rng.integers(0, 256, (p - 1, R), dtype=np.uint8) for _ in range(k + 2)]
         want = [c.copy() for c in cols]
         ora.rdp_decode(want, p, e0, e1)
@@ -105,3 +107,41 @@ def test_rs8_decode_all_patterns(pkg, ora, gpu, k, m):
         for s in range(k + m):
             got = dev_sh[s].cpu().numpy()
             assert np.array_equal(got, want[s]) and np.array_equal(got, full[s]), (er, s)
+
+
+def test_rdp_flat_addressing_large_shards(pkg, ora, gpu):
+    """Shards of 4 GiB or more are addressed with flat 64-bit pointers (the
+    buffer-resource kernels reach below 4 GiB): the encode and the compiled
+    decode networks at p = 7, k = 6 with row planes of 715,827,904 B, so each
+    shard holds 4,294,967,424 B.  P and Q are checked against the oracle on
+    sampled stripe columns; decodes are byte-compared at full size."""
+    p, k, R = 7, 6, 715_827_904
+    nb = (p - 1) * R
+    free, _ = torch.cuda.mem_get_info(gpu)
+    if free < (k + 4) * nb + (8 << 30):
+        pytest.skip(f"needs {((k + 4) * nb) >> 30} GiB of free device memory")
+    shards = [torch.empty(nb, dtype=torch.uint8, device=gpu) for _ in range(k + 2)]
+    try:
+        for t in shards[:k]:
+            t.random_(0, 256)
+        pkg.spec.rdp_encode(shards[:k], shards[k], shards[k + 1], p=p)
+        rng = np.random.default_rng(7)
+        offs = np.sort(rng.choice(R // 16, 512, replace=False)) * 16
+        lane = (offs[:, None] + np.arange(16)[None, :]).reshape(-1)
+        idx = torch.from_numpy((np.arange(p - 1)[:, None] * R + lane[None, :]).reshape(-1)).to(gpu)
+        cols = [t[idx].cpu().numpy().reshape(p - 1, -1) for t in shards]
+        Pw, Qw = ora.rdp_encode(cols[:k], p)
+        assert np.array_equal(cols[k], Pw) and np.array_equal(cols[k + 1], Qw)
+        for a, b in [(0, 1), (2, 6), (6, 7), (3, -1)]:
+            keep = [shards[e].clone() for e in (a, b) if e >= 0]
+            for e in (a, b):
+                if e >= 0:
+                    shards[e].zero_()
+            pkg.spec.rdp_decode(shards, p, [a, b])
+            torch.cuda.synchronize()
+            for e, want in zip([e for e in (a, b) if e >= 0], keep):
+                assert torch.equal(shards[e], want), (a, b, e)
+            del keep
+    finally:
+        del shards
+        torch.cuda.empty_cache()
