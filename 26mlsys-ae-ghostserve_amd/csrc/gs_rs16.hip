@@ -12,6 +12,10 @@
 // register carries the low bytes of four words and one the high bytes, so a
 // coefficient costs 12 v_perm_b32 per four words and no memory lookup.
 //
+// The encode's coefficients are powers of alpha^(p+1); when the caller's tables
+// have alpha = 2 (checked per block), the encode instead folds the inputs by
+// Horner's rule with packed-word doublings (below), about half the VALU work.
+//
 // Reconstruction folds the reference's two steps (right-hand side b, then
 // x = V^-1 b) into one coefficient per (output, input) pair: exact in the
 // field, so the bytes are those of the two-step computation.  The inverse is
@@ -217,6 +221,126 @@ __device__ __forceinline__ void rs_mix_tail(const RsJob& j, const uint32_t (*pta
     }
 }
 
+// ------------------------------------------------------------ Horner encode
+// The encode's coefficients are powers, c(p, i) = g_p^i with g_p = alpha^(p+1),
+// so parity p is also D_0 ^ g_p (D_1 ^ g_p (D_2 ^ ...)): inputs taken from the
+// last to the first, the accumulator multiplied by g_p before each one.  With
+// alpha = 2 that product is p + 1 doublings, each a shift of the two packed
+// words and, for a word whose top bit was set, an XOR of the field
+// polynomial's low 16 bits: three or four VALU ops per dword instead of the
+// byte maps' twelve v_perm_b32 and six XORs per coefficient.  The kernel takes
+// this path only after checking, from the caller's tables, that every
+// coefficient's map equals its chain of doublings on all sixteen basis
+// symbols (both are GF(2)-linear, so they then agree on every symbol).
+typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+typedef short i16x2 __attribute__((ext_vector_type(2)));
+
+// Scalar doubling, for the check: x * 2 with reduction word `red`.
+__host__ __device__ __forceinline__ uint16_t gf16_dbl(uint16_t x, uint16_t red) {
+    return uint16_t((x << 1) ^ ((x & 0x8000u) ? red : 0u));
+}
+
+// Two packed words times 2; red2 holds the reduction word in both halves.
+__device__ __forceinline__ uint32_t gf16_dbl2(uint32_t x, uint32_t red2) {
+    const uint32_t sh = __builtin_bit_cast(uint32_t, u16x2(__builtin_bit_cast(u16x2, x) << 1));
+    const uint32_t top = __builtin_bit_cast(uint32_t, i16x2(__builtin_bit_cast(i16x2, x) >> 15));
+    return __builtin_amdgcn_bitop3_b32(sh, top, red2, 0x78);   // sh ^ (top & red2)
+}
+
+// (x * 2) ^ y
+__device__ __forceinline__ uint32_t gf16_dbl2_xor(uint32_t x, uint32_t red2, uint32_t y) {
+    const uint32_t sh = __builtin_bit_cast(uint32_t, u16x2(__builtin_bit_cast(u16x2, x) << 1));
+    const uint32_t top = __builtin_bit_cast(uint32_t, i16x2(__builtin_bit_cast(i16x2, x) >> 15));
+    return xor3(sh, top & red2, y);
+}
+
+// acc[n][g] = acc[n][g] * alpha^(g+1) ^ x[n]; acc in natural word order.
+template <int G, int NW>
+__device__ __forceinline__ void rs_horner_step(uint32_t red2, const u32x4* x, uint32_t (*acc)[kRsGroup][4]) {
+#pragma unroll
+    for (int n = 0; n < NW; ++n) {
+        const uint32_t xv[4] = {x[n].x, x[n].y, x[n].z, x[n].w};
+#pragma unroll
+        for (int g = 0; g < G; ++g)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                uint32_t a = acc[n][g][q];
+#pragma unroll
+                for (int d = 0; d < g; ++d) a = gf16_dbl2(a, red2);
+                acc[n][g][q] = gf16_dbl2_xor(a, red2, xv[q]);
+            }
+    }
+}
+
+template <int G, int NW>
+__device__ __forceinline__ void rs_horner_first(const u32x4* x, uint32_t (*acc)[kRsGroup][4]) {
+#pragma unroll
+    for (int n = 0; n < NW; ++n)
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            acc[n][g][0] = x[n].x;
+            acc[n][g][1] = x[n].y;
+            acc[n][g][2] = x[n].z;
+            acc[n][g][3] = x[n].w;
+        }
+}
+
+// rs_mix_full with Horner's order: the last input first, the input before in
+// flight while one is folded in.  (Two inputs in flight measured the same.)
+template <int G, int NW>
+__device__ __forceinline__ void rs_horner_full(const RsJob& j, uint32_t red2, uint64_t t0b, bool copy,
+                                               uint32_t (*acc)[kRsGroup][4]) {
+    const int nin = j.nin;
+    u32x4 lo[NW], hi[NW];
+    RowWin rw = row_win(reinterpret_cast<const uint8_t*>(j.in_rows[nin - 1]) + t0b);
+#pragma unroll
+    for (int n = 0; n < NW; ++n) win_chunks(rw, 16 * (threadIdx.x + n * kTB), lo[n], hi[n]);
+    for (int i = nin - 1; i >= 0; --i) {
+        u32x4 x[NW];
+#pragma unroll
+        for (int n = 0; n < NW; ++n) {
+            x[n] = win_join(rw, lo[n], hi[n]);
+            if (copy) copy_owned<false>(j.copy, rw, 16 * (threadIdx.x + n * kTB), lo[n], hi[n]);
+        }
+        if (i > 0) {
+            rw = row_win(reinterpret_cast<const uint8_t*>(j.in_rows[i - 1]) + t0b);
+#pragma unroll
+            for (int n = 0; n < NW; ++n) win_chunks(rw, 16 * (threadIdx.x + n * kTB), lo[n], hi[n]);
+        }
+        if (i == nin - 1) rs_horner_first<G, NW>(x, acc);
+        else rs_horner_step<G, NW>(red2, x, acc);
+    }
+}
+
+// rs_mix_tail with Horner's order.
+template <int G, int NW>
+__device__ __forceinline__ void rs_horner_tail(const RsJob& j, uint32_t red2, uint64_t t0b, const int64_t* w0,
+                                               bool copy, uint32_t (*acc)[kRsGroup][4]) {
+    for (int i = j.nin - 1; i >= 0; --i) {
+        const RowWin rw = row_win(reinterpret_cast<const uint8_t*>(j.in_rows[i]) + t0b);
+        u32x4 x[NW];
+#pragma unroll
+        for (int n = 0; n < NW; ++n) {
+            const uint32_t off = 16 * (threadIdx.x + n * kTB);
+            if (w0[n] + 8 <= j.S) {
+                u32x4 lo, hi;
+                win_chunks(rw, off, lo, hi);
+                x[n] = win_join(rw, lo, hi);
+                if (copy) copy_owned<false>(j.copy, rw, off, lo, hi);
+            } else {
+                x[n] = rs_window(j.in_rows[i], w0[n], j.S);
+                if (copy && w0[n] < j.S) {
+                    const uint64_t o = uint64_t(reinterpret_cast<const uint8_t*>(j.in_rows[i] + w0[n]) -
+                                                j.copy.src);
+                    copy_bytes(j.copy, o, o + 2 * uint64_t(j.S - w0[n]));
+                }
+            }
+        }
+        if (i == j.nin - 1) rs_horner_first<G, NW>(x, acc);
+        else rs_horner_step<G, NW>(red2, x, acc);
+    }
+}
+
 constexpr int kRsNW = 2;                              // windows per thread
 constexpr uint32_t kRsTile = kTileBytes * kRsNW;      // logical bytes per row per tile
 constexpr uint32_t kRsStage = kRsTile + 16;           // LDS staging row
@@ -224,9 +348,13 @@ constexpr uint32_t kRsStage = kRsTile + 16;           // LDS staging row
 // Stream every tile of the job through the tables already in LDS; `tile`
 // holds kRsGroup staging rows of kRsStage bytes.  Window n of thread t covers
 // logical bytes 16 (t + n kTB) .. +15 of the tile, so each window's loads are
-// contiguous across the block.
+// contiguous across the block.  HORNER selects the Horner encode (all
+// outputs in one group, accumulators in natural word order; red2 holds the
+// reduction word in both halves).  The two are separate loops: sharing one
+// loop made the encode kernel spill registers.
+template <bool HORNER>
 __device__ __forceinline__ void rs_run_tiles(const RsJob& j, const uint32_t (*ptab)[kRs16Tab],
-                                             uint8_t* tile) {
+                                             uint8_t* tile, uint32_t red2) {
     const uint64_t Sb = uint64_t(j.S) * 2;
     const uint64_t ntiles = (Sb + kRsTile - 1) / kRsTile;
     for (uint64_t tt = blockIdx.x; tt < ntiles; tt += gridDim.x) {
@@ -244,7 +372,17 @@ __device__ __forceinline__ void rs_run_tiles(const RsJob& j, const uint32_t (*pt
             const int G = j.nout - og < kRsGroup ? j.nout - og : kRsGroup;
             uint32_t acc[kRsNW][kRsGroup][4];
             static_assert(kRsGroup == 2, "one instantiation per group size");
-            if (nbytes == kRsTile) {
+            if (HORNER && nbytes == kRsTile) {
+                if (G == 1) rs_horner_full<1, kRsNW>(j, red2, t0b, copy, acc);
+                else rs_horner_full<2, kRsNW>(j, red2, t0b, copy, acc);
+            } else if (HORNER && w0[0] < j.S) {
+                if (G == 1) rs_horner_tail<1, kRsNW>(j, red2, t0b, w0, copy, acc);
+                else rs_horner_tail<2, kRsNW>(j, red2, t0b, w0, copy, acc);
+            } else if (HORNER) {
+                for (int n = 0; n < kRsNW; ++n)
+                    for (int g = 0; g < kRsGroup; ++g)
+                        acc[n][g][0] = acc[n][g][1] = acc[n][g][2] = acc[n][g][3] = 0;
+            } else if (nbytes == kRsTile) {
                 if (G == 1) rs_mix_full<1, kRsNW>(j, ptab, og, t0b, copy, acc);
                 else rs_mix_full<2, kRsNW>(j, ptab, og, t0b, copy, acc);
             } else if (w0[0] < j.S) {
@@ -258,7 +396,8 @@ __device__ __forceinline__ void rs_run_tiles(const RsJob& j, const uint32_t (*pt
             for (int g = 0; g < G; ++g)
                 for (int n = 0; n < kRsNW; ++n)
                     *reinterpret_cast<u32x4*>(tile + g * kRsStage + 16 * (threadIdx.x + n * kTB)) =
-                        join_bytes(acc[n][g]);
+                        HORNER ? u32x4{acc[n][g][0], acc[n][g][1], acc[n][g][2], acc[n][g][3]}
+                               : join_bytes(acc[n][g]);
             __syncthreads();
             for (int g = 0; g < G; ++g)
                 tile_store(reinterpret_cast<uint8_t*>(j.out_rows[og + g]) + t0b, tile + g * kRsStage,
@@ -284,8 +423,26 @@ __global__ __launch_bounds__(kTB) __attribute__((amdgpu_waves_per_eu(4))) void r
     }
     __syncthreads();
     rs_build_perm_tables(ptab, basis, coef, j.nout * j.nin, ex, lg);
+    // Horner's order when every basis product c(p, i) * 2^b the tables give
+    // equals 2^b doubled (p + 1) i times, the reduction word being 0x8000 * 2
+    // from the tables.
+    __shared__ int s_horner;
+    __shared__ uint16_t s_red;
+    if (threadIdx.x == 0) {
+        s_red = gf16_mul_tab(0x8000, 2, ex, lg);
+        s_horner = j.nout <= kRsGroup;
+    }
     __syncthreads();
-    rs_run_tiles(j, ptab, tile);
+    for (int e = threadIdx.x; e < j.nout * j.nin * 16; e += kTB) {
+        const int t = e >> 4, b = e & 15;
+        const int p = t / j.nin, i = t % j.nin;
+        uint16_t v = uint16_t(1u << b);
+        for (int d = 0; d < (p + 1) * i; ++d) v = gf16_dbl(v, s_red);
+        if (v != basis[t][b]) s_horner = 0;
+    }
+    __syncthreads();
+    if (s_horner) rs_run_tiles<true>(j, ptab, tile, uint32_t(s_red) * 0x10001u);
+    else rs_run_tiles<false>(j, ptab, tile, 0u);
 }
 
 // benchmark/rs/kernel.cu:105-222 with the right-hand side folded into the
@@ -399,7 +556,7 @@ __global__ __launch_bounds__(kTB) __attribute__((amdgpu_waves_per_eu(4))) void r
     __syncthreads();
     rs_build_perm_tables(ptab, basis, coef, m * nin, ex, lg);
     __syncthreads();
-    rs_run_tiles(j, ptab, tile);
+    rs_run_tiles<false>(j, ptab, tile, 0u);
 }
 
 static int rs_grid(int64_t S) {

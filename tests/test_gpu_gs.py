@@ -372,6 +372,27 @@ def test_rs16_encode_matches_oracle(pkg, ora, gpu, k, m, S):
     assert np.array_equal(host(shards), want)
 
 
+@pytest.mark.parametrize("k,m,S", [(6, 2, 16384 + 5), (4, 1, 3000), (7, 2, 9)])
+def test_rs16_encode_other_generator(pkg, ora, gpu, k, m, S):
+    """Tables of the same field with generator alpha^2 = 4 (log base 4): the
+    coefficients alpha'^((p+1) i) are no longer chains of doublings, so the
+    encode must leave its Horner path and still give the reference's bytes for
+    these tables."""
+    ex0, lg0 = ora.gf16_tables()
+    n = np.arange(2 * 65535, dtype=np.int64)
+    ex = ex0[(2 * n) % 65535].astype(np.uint16)
+    lg = ((lg0.astype(np.int64) * 32768) % 65535).astype(np.uint16)   # 2 * 32768 = 1 mod 65535
+    lg[0] = 0
+    assert ex[1] == 4 and all(ex[lg[x]] == x for x in (1, 2, 3, 0x8000, 0xFFFF))
+    rng = np.random.default_rng(k * 7 + S)
+    data = rng.integers(0, 65536, k * S, dtype=np.uint16)
+    want = ora.rs16_encode(data, k, m, S, ex, lg)
+    assert not np.array_equal(want, ora.rs16_encode(data, k, m, S, ex0, lg0))
+    shards = torch.zeros((k + m, S), dtype=torch.uint16, device=gpu)
+    pkg.rs.rs_kernel.encode_rs_u16(dev(data, gpu), shards, k, m, S, dev(ex, gpu), dev(lg, gpu))
+    assert np.array_equal(host(shards), want)
+
+
 @pytest.mark.parametrize("k,m,S", [(6, 2, 4096), (3, 3, 4096 * 2 + 5), (4, 1, 1000), (2, 2, 9)])
 @pytest.mark.parametrize("doff,soff", [(0, 0), (3, 3), (1, 5), (0, 8), (7, 15)])
 def test_rs16_encode_fused_copy_offsets(pkg, ora, gpu, k, m, S, doff, soff):
