@@ -156,42 +156,58 @@ inline RdpCellMap rdp_cell_map(const RdpPlan& plan) {
 }
 
 // Same map for any (p, k) and any shard size.  Each needed cell is loaded
-// once, eight at a time so that eight are in flight, and folded into every
-// output that uses it (wave-uniform tests of its output set); the outputs
-// accumulate in registers.
-__global__ __launch_bounds__(kBS) void rdp_decode_generic_kernel(RdpPtrs sh, RdpCellMap cm, int rows,
-                                                                 uint64_t R, uint32_t nvec) {
-    constexpr int kBatch = 8;
+// once, BATCH at a time so that BATCH are in flight, and folded into every
+// output that uses it (wave-uniform tests of its output set); the 2 ROWS
+// outputs accumulate in registers.  Sized per p, so that small codes keep
+// more loads in flight.
+template <int ROWS, int BATCH>
+__global__ __launch_bounds__(kBS) void rdp_decode_generic_kernel(RdpPtrs sh, RdpCellMap cm, uint64_t R,
+                                                                 uint32_t nvec) {
+    constexpr int NOUT = 2 * ROWS;
+    static_assert(NOUT <= kRdpMaxOut, "outputs of one stripe");
     const uint32_t u = blockIdx.x * kBS + threadIdx.x;
     if (u >= nvec) return;
     const uint32_t off = u << 4;
-    u32x4 acc[kRdpMaxOut];
+    u32x4 acc[NOUT];
 #pragma unroll
-    for (int o = 0; o < kRdpMaxOut; ++o) acc[o] = u32x4{0, 0, 0, 0};
-    for (int i0 = 0; i0 < cm.ncell; i0 += kBatch) {
-        u32x4 x[kBatch];
+    for (int o = 0; o < NOUT; ++o) acc[o] = u32x4{0, 0, 0, 0};
+    for (int i0 = 0; i0 < cm.ncell; i0 += BATCH) {
+        u32x4 x[BATCH];
 #pragma unroll
-        for (int t = 0; t < kBatch; ++t) {
+        for (int t = 0; t < BATCH; ++t) {
             x[t] = u32x4{0, 0, 0, 0};
             if (i0 + t < cm.ncell) {
                 const int c = cm.cell[i0 + t];
-                x[t] = ld16(sh.p[c / rows] + uint64_t(c % rows) * R + off);
+                x[t] = ld16(sh.p[c / ROWS] + uint64_t(c % ROWS) * R + off);
             }
         }
 #pragma unroll
-        for (int t = 0; t < kBatch; ++t) {
+        for (int t = 0; t < BATCH; ++t) {
             const uint32_t outs = i0 + t < cm.ncell ? cm.outs[i0 + t] : 0u;
 #pragma unroll
-            for (int o = 0; o < kRdpMaxOut; ++o)
+            for (int o = 0; o < NOUT; ++o)
                 if ((outs >> o) & 1) acc[o] ^= x[t];
         }
     }
 #pragma unroll
-    for (int o = 0; o < kRdpMaxOut; ++o) {
+    for (int o = 0; o < NOUT; ++o) {
         if (o < cm.nout) {
             const int c = cm.out_cell[o];
-            st_stream(sh.p[c / rows] + uint64_t(c % rows) * R, off, acc[o]);
+            st_stream(sh.p[c / ROWS] + uint64_t(c % ROWS) * R, off, acc[o]);
         }
+    }
+}
+
+typedef void (*GenericDecFn)(RdpPtrs, RdpCellMap, uint64_t, uint32_t);
+
+static GenericDecFn generic_decode_fn(int p) {
+    switch (p) {
+        case 3: return &rdp_decode_generic_kernel<2, 16>;
+        case 5: return &rdp_decode_generic_kernel<4, 16>;
+        case 7: return &rdp_decode_generic_kernel<6, 16>;
+        case 11: return &rdp_decode_generic_kernel<10, 8>;
+        case 13: return &rdp_decode_generic_kernel<12, 12>;
+        default: return nullptr;
     }
 }
 
@@ -330,8 +346,10 @@ extern "C" int kvec_rdp_decode(void* const* shards, int k, int p, int64_t row_by
         RdpPlan plan = make_rdp_plan(p, k, a, b);
         if (!plan.ok)
             return set_error(KVEC_EDECODE, "kvec_rdp_decode: pattern (%d, %d) not decodable", a, b);
-        hipLaunchKernelGGL(rdp_decode_generic_kernel, grid, block, 0, as_stream(stream), s,
-                           rdp_cell_map(plan), p - 1, uint64_t(row_bytes), nvec);
+        GenericDecFn gfn = generic_decode_fn(p);
+        if (!gfn) return set_error(KVEC_EUNSUPPORTED, "kvec_rdp_decode: p=%d", p);
+        hipLaunchKernelGGL(gfn, grid, block, 0, as_stream(stream), s, rdp_cell_map(plan),
+                           uint64_t(row_bytes), nvec);
     }
     return check_launch("kvec_rdp_decode");
 }
