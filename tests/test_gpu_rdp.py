@@ -32,7 +32,8 @@ def test_rdp_encode_matches_oracle(pkg, ora, gpu, p, k, R):
     assert np.array_equal(_host(Q, (p - 1, R)), Qw)
 
 
-@pytest.mark.parametrize("p,k", [(7, 6), (5, 4), (3, 2), (7, 4), (11, 10), (13, 12)])
+# (7, 6), (5, 4), (3, 2): compiled networks; the others: the generic kernel of each p
+@pytest.mark.parametrize("p,k", [(7, 6), (5, 4), (3, 2), (7, 4), (11, 10), (13, 12), (3, 1), (5, 2)])
 def test_rdp_decode_all_patterns(pkg, ora, gpu, p, k):
     R = 1024 + 16
     rng = np.random.default_rng(p + 17 * k)
