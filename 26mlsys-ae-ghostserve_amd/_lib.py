@@ -65,8 +65,8 @@ SIGNATURES = {
     "kvec_version": (_i, []),
     "kvec_strerror": (C.c_char_p, [_i]),
     "kvec_last_error": (C.c_char_p, []),
-    "kvec_rdp_encode": (_i, [_pp, _i, _vp, _vp, _i, _i64, _vp]),
-    "kvec_rdp_decode": (_i, [_pp, _i, _i, _i64, _i, _i, _vp]),
+    "kvec_rdp_encode": (_i, [_pp, _i, _vp, _vp, _i, _i64, _i64, _vp]),
+    "kvec_rdp_decode": (_i, [_pp, _i, _i, _i64, _i64, _i, _i, _vp]),
     "kvec_rdp_row_bytes": (_i64, [_i64, _i, _i, _i64]),
     "kvec_rs8_cauchy": (_i, [_i, _i, _vp]),
     "kvec_rs8_encode": (_i, [_pp, _i, _pp, _i, _i64, _vp]),
@@ -75,7 +75,7 @@ SIGNATURES = {
     "kvec_kv_gather": (_i, [_kvp, _vp, _vp]),
     "kvec_kv_gather_split": (_i, [_kvp, _vp, _vp, _vp]),
     "kvec_kv_scatter": (_i, [_kvp, _vp, _vp, _vp]),
-    "kvec_rdp_encode_paged": (_i, [_kvp, _pp, _i, _vp, _vp, _i, _i64, _vp]),
+    "kvec_rdp_encode_paged": (_i, [_kvp, _pp, _i, _vp, _vp, _i, _i64, _i64, _vp]),
     "kvec_chunk_width": (_i64, [_i64, _i, _i, _i64]),
     "kvec_chunk_encode_paged": (_i, [_kvp, _csp, _vp]),
     "kvec_chunk_decode_paged": (_i, [_kvp, _vp, _csp, _vp, _i, _vp]),

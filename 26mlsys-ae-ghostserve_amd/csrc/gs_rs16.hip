@@ -575,12 +575,9 @@ extern "C" int kvec_rs16_pack(const void* k, const void* v, void* out, int64_t N
     if ((N_k && (!k || !out)) || (N_v && (!v || !out)))
         return set_error(KVEC_EINVAL, "kvec_rs16_pack: null pointer");
     hipStream_t st = as_stream(stream);
-    hipError_t e = hipSuccess;
-    if (N_k) e = hipMemcpyAsync(out, k, uint64_t(N_k) * 2, hipMemcpyDeviceToDevice, st);
-    if (e == hipSuccess && N_v)
-        e = hipMemcpyAsync((uint16_t*)out + N_k, v, uint64_t(N_v) * 2, hipMemcpyDeviceToDevice, st);
-    if (e != hipSuccess) return set_error(KVEC_EHIP, "kvec_rs16_pack: %s", hipGetErrorString(e));
-    return KVEC_OK;
+    int rc = copy_d2d(out, k, uint64_t(N_k) * 2, st, "kvec_rs16_pack");
+    if (rc) return rc;
+    return copy_d2d((uint16_t*)out + N_k, v, uint64_t(N_v) * 2, st, "kvec_rs16_pack");
 }
 
 // u16_to_fp16_split, benchmark/rs/kernel.cu:245-263: inverse of the pack.
@@ -590,12 +587,9 @@ extern "C" int kvec_rs16_split(const void* in, void* k_out, void* v_out, int64_t
     if ((N_k && (!in || !k_out)) || (N_v && (!in || !v_out)))
         return set_error(KVEC_EINVAL, "kvec_rs16_split: null pointer");
     hipStream_t st = as_stream(stream);
-    hipError_t e = hipSuccess;
-    if (N_k) e = hipMemcpyAsync(k_out, in, uint64_t(N_k) * 2, hipMemcpyDeviceToDevice, st);
-    if (e == hipSuccess && N_v)
-        e = hipMemcpyAsync(v_out, (const uint16_t*)in + N_k, uint64_t(N_v) * 2, hipMemcpyDeviceToDevice, st);
-    if (e != hipSuccess) return set_error(KVEC_EHIP, "kvec_rs16_split: %s", hipGetErrorString(e));
-    return KVEC_OK;
+    int rc = copy_d2d(k_out, in, uint64_t(N_k) * 2, st, "kvec_rs16_split");
+    if (rc) return rc;
+    return copy_d2d(v_out, (const uint16_t*)in + N_k, uint64_t(N_v) * 2, st, "kvec_rs16_split");
 }
 
 // encode_rs_u16, benchmark/rs/kernel.cu:265-285: copy the data rows, then the
@@ -617,11 +611,16 @@ extern "C" int kvec_rs16_encode(const void* data_padded, void* shards, int data_
     const uint64_t data_bytes = uint64_t(data_shards) * S * 2;
     // The data rows are copied by the coding kernel itself when the two
     // buffers are disjoint and equally aligned modulo 16 bytes; otherwise (or
-    // with no parity to code) by a separate stream-ordered copy.
+    // with no parity to code) by a separate stream-ordered copy.  The data
+    // must not overlap the parity rows the kernel writes, nor the data rows
+    // unless it is them (a partial overlap has no stream-ordered meaning).
+    if (ranges_overlap(data_padded, data_bytes, (uint16_t*)shards + uint64_t(data_shards) * S,
+                       uint64_t(parity_shards) * S * 2))
+        return set_error(KVEC_EINVAL, "kvec_rs16_encode: data overlaps the parity rows");
     const bool fuse = parity_shards > 0 && fused_copy_ok(data_padded, shards, data_bytes);
-    if (!fuse && shards != data_padded) {
-        hipError_t e = hipMemcpyAsync(shards, data_padded, data_bytes, hipMemcpyDeviceToDevice, st);
-        if (e != hipSuccess) return set_error(KVEC_EHIP, "kvec_rs16_encode: %s", hipGetErrorString(e));
+    if (!fuse) {
+        int rc = copy_d2d(shards, data_padded, data_bytes, st, "kvec_rs16_encode");
+        if (rc) return rc;
     }
     if (parity_shards == 0) return KVEC_OK;
     RsJob j{};

@@ -795,13 +795,6 @@ static int xor_rows(const uint8_t* in, uint64_t Sb, RowSet rs, uint8_t* out0, ui
     return check_launch(what);
 }
 
-static int copy_d2d(void* dst, const void* src, uint64_t n, hipStream_t st, const char* what) {
-    if (n == 0 || dst == src) return KVEC_OK;
-    hipError_t e = hipMemcpyAsync(dst, src, n, hipMemcpyDeviceToDevice, st);
-    if (e != hipSuccess) return set_error(KVEC_EHIP, "%s: %s", what, hipGetErrorString(e));
-    return KVEC_OK;
-}
-
 typedef void (*GsParityFn)(uint16_t*, int, int64_t, int, GsSource, uint64_t, GsStar);
 
 template <bool FUSED, int ND = 1>
@@ -854,8 +847,11 @@ extern "C" int kvec_xor_encode(const void* data_padded, void* shards, int data_s
                          (long long)shard_size);
     hipStream_t st = as_stream(stream);
     const uint64_t Sb = uint64_t(shard_size);
+    if (ranges_overlap(data_padded, Sb * data_shards, (uint8_t*)shards + Sb * data_shards, Sb))
+        return set_error(KVEC_EINVAL, "kvec_xor_encode: data overlaps the parity row");
     // The data rows are copied by the parity kernel's own loads when the two
-    // buffers are disjoint and equally aligned modulo 16 bytes.
+    // buffers are disjoint and equally aligned modulo 16 bytes; else (same
+    // buffer: no copy; partial overlap: refused) by a copy first.
     if (Sb && fused_copy_ok(data_padded, shards, Sb * data_shards))
         return xor_rows((const uint8_t*)data_padded, Sb, RowSet{0, data_shards, -1, -1},
                         (uint8_t*)shards + Sb * data_shards, nullptr, st, "kvec_xor_encode",
@@ -901,8 +897,8 @@ extern "C" int kvec_xor_encode_kv(const void* key_input, const void* value_input
     if (!rc) rc = copy_d2d(sh + kb, value_input, kb, st, "kvec_xor_encode_kv");
     if (rc) return rc;
     if (data_bytes > 2 * kb) {
-        hipError_t e = hipMemsetAsync(sh + 2 * kb, 0, data_bytes - 2 * kb, st);
-        if (e != hipSuccess) return set_error(KVEC_EHIP, "kvec_xor_encode_kv: %s", hipGetErrorString(e));
+        rc = zero_d(sh + 2 * kb, data_bytes - 2 * kb, st, "kvec_xor_encode_kv");
+        if (rc) return rc;
     }
     return xor_rows(sh, Sb, RowSet{0, data_shards, -1, -1}, sh + data_bytes, nullptr, st,
                     "kvec_xor_encode_kv");
@@ -932,8 +928,9 @@ extern "C" int kvec_xor_reconstruct(const void* encoded_data, void* recovered_da
 // in place (reconstruct_xor) and the first out_bytes of the data rows copied
 // out (unpack_kv).  A lost data row: one pass of gs_recover_kernel over the
 // byte rows (P is row data_shards).  A lost P: P recomputed, then the copy-out
-// pass.  missing < 0: the copy-out pass alone.  With out overlapping the
-// shards, the reconstruct and then a copy.
+// pass.  missing < 0: the copy-out pass alone.  With out inside the shard
+// tensor, the reconstruct and then a copy (out == shards: no copy; an output
+// that overlaps the bytes it copies is refused).
 extern "C" int kvec_xor_recover_kv(void* shards, void* out, int data_shards, int64_t shard_size,
                                    int64_t out_bytes, int missing, void* stream) {
     if (!shards || (out_bytes > 0 && !out))
@@ -949,6 +946,13 @@ extern "C" int kvec_xor_recover_kv(void* shards, void* out, int data_shards, int
     hipStream_t st = as_stream(stream);
     uint8_t* sh = (uint8_t*)shards;
     const int nd = data_shards;
+    const uintptr_t R0 = uintptr_t(sh), R1 = R0 + uint64_t(nd + 1) * Sb;
+    const uintptr_t O0 = uintptr_t(out), O1 = O0 + nbytes;
+    // An output inside the shard tensor gets the rebuild and then the copy-out;
+    // the copy's own source and destination must then be the same bytes or
+    // disjoint.
+    if (out != shards && ranges_overlap(out, nbytes, sh, nbytes))
+        return set_error(KVEC_EINVAL, "kvec_xor_recover_kv: output overlaps the data rows it copies");
     if (missing == nd) {   // P recomputed from the data rows
         int rc = xor_rows(sh, Sb, RowSet{0, nd, -1, -1}, sh + uint64_t(nd) * Sb, nullptr, st,
                           "kvec_xor_recover_kv");
@@ -956,8 +960,6 @@ extern "C" int kvec_xor_recover_kv(void* shards, void* out, int data_shards, int
     }
     if (nbytes == 0 && missing < 0) return KVEC_OK;
     const int t = missing >= 0 && missing < nd ? missing : -1;
-    const uintptr_t R0 = uintptr_t(sh), R1 = R0 + uint64_t(nd + 1) * Sb;
-    const uintptr_t O0 = uintptr_t(out), O1 = O0 + nbytes;
     if (nbytes == 0 || O1 <= R0 || O0 >= R1) {
         if (t < 0 && nbytes == 0) return KVEC_OK;
         hipLaunchKernelGGL(gs_recover_fn(nd), dim3(blocks_for(int64_t(Sb), kTileBytes)), dim3(kTB), 0, st,
@@ -1055,6 +1057,11 @@ extern "C" int kvec_gs_rdp_recover(void* shards, void* out_TN, int nd, int S, in
     const uint64_t total = 2 * uint64_t(T > 0 ? T : 0) * uint64_t(n > 0 ? n : 0);
     const uint64_t cap = uint64_t(nd > 0 ? nd : 0) * uint64_t(S > 0 ? S : 0);
     const uint64_t nc = total < cap ? total : cap;
+    // An output inside the shard tensor gets the rebuild and then the copy-out;
+    // the copy's own source and destination must then be the same bytes or
+    // disjoint.
+    if (copy_out && out_TN != shards && ranges_overlap(out_TN, nc * 2, shards, nc * 2))
+        return set_error(KVEC_EINVAL, "kvec_gs_rdp_recover: output overlaps the data rows it copies");
     if (copy_out) {
         // One pass (rebuild and copy-out) when out overlaps no shard row.
         const uint64_t Sb = uint64_t(S) * 2;
@@ -1066,12 +1073,7 @@ extern "C" int kvec_gs_rdp_recover(void* shards, void* out_TN, int nd, int S, in
                                (uint8_t*)out_TN, nc * 2);
             int rc = check_launch("kvec_gs_rdp_recover");
             if (rc) return rc;
-            if (total > nc) {
-                hipError_t e = hipMemsetAsync((uint16_t*)out_TN + nc, 0, (total - nc) * 2, st);
-                if (e != hipSuccess)
-                    return set_error(KVEC_EHIP, "kvec_gs_rdp_recover: %s", hipGetErrorString(e));
-            }
-            return KVEC_OK;
+            return zero_d((uint16_t*)out_TN + nc, (total - nc) * 2, st, "kvec_gs_rdp_recover");
         }
     }
     if (t >= 0 && S > 0) {
@@ -1084,11 +1086,7 @@ extern "C" int kvec_gs_rdp_recover(void* shards, void* out_TN, int nd, int S, in
     if (copy_out) {
         int rc = copy_d2d(out_TN, shards, nc * 2, st, "kvec_gs_rdp_recover");
         if (rc) return rc;
-        if (total > nc) {
-            hipError_t e = hipMemsetAsync((uint16_t*)out_TN + nc, 0, (total - nc) * 2, st);
-            if (e != hipSuccess)
-                return set_error(KVEC_EHIP, "kvec_gs_rdp_recover: %s", hipGetErrorString(e));
-        }
+        return zero_d((uint16_t*)out_TN + nc, (total - nc) * 2, st, "kvec_gs_rdp_recover");
     }
     return KVEC_OK;
 }

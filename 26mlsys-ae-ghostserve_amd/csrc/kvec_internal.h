@@ -172,12 +172,71 @@ __host__ __device__ __forceinline__ uint32_t fdiv(uint32_t n, const FastDiv& f) 
     return (((n - q) >> f.s1) + q) >> f.s2;
 }
 
+// ------------------------------------------------------------- RDP stripes
+// Stripe geometry of a spec RDP shard set.  Every shard is (p-1)*R bytes, cut
+// into stripes of (p-1)*U bytes (the last one shorter when U does not divide
+// R).  Stripe s has rows of g_s = min(U, R - s*U) bytes, row r at byte
+// s*(p-1)*U + r*g_s of the shard, and byte offset o < g_s of its rows is one
+// RDP instance.  U = 0 (or U >= R) is a single stripe: p-1 row planes of R
+// bytes.  Kernels run one wave per 1 KiB of a stripe's row (16 bytes per
+// lane), so every wave-uniform quantity below is a scalar.
+constexpr uint32_t kRdpWaveBytes = 1024;
+
+struct RdpGeom {
+    uint64_t U;        // row bytes of a full stripe
+    uint64_t g_last;   // row bytes of the last stripe
+    uint32_t ns;       // stripes
+    FastDiv bps;       // waves (1 KiB row pieces) per stripe
+};
+
+// rows-per-stripe (p-1) is a kernel template parameter; R, U in bytes.
+inline RdpGeom make_rdp_geom(uint64_t R, uint64_t U) {
+    RdpGeom g{};
+    if (U == 0 || U >= R) U = R;
+    g.U = U;
+    g.ns = U ? uint32_t((R + U - 1) / U) : 0;
+    g.g_last = U ? R - uint64_t(g.ns - 1) * U : 0;
+    g.bps = make_fastdiv(uint32_t((U + kRdpWaveBytes - 1) / kRdpWaveBytes));
+    return g;
+}
+inline uint64_t rdp_waves(const RdpGeom& g) { return uint64_t(g.ns) * g.bps.d; }
+
+// The calling wave's stripe: its shard-relative base, its row length, and the
+// lane's byte offset within the rows (>= g when the lane is past the row end).
+struct RdpWave {
+    uint64_t base;
+    uint64_t g;
+    uint32_t within;
+};
+__device__ __forceinline__ RdpWave rdp_wave(const RdpGeom& G, int rows, uint32_t wave, uint32_t lane) {
+    const uint32_t s = fdiv(wave, G.bps);
+    const uint32_t cb = wave - s * G.bps.d;
+    RdpWave w;
+    w.base = uint64_t(s) * uint64_t(rows) * G.U;
+    w.g = s + 1 == G.ns ? G.g_last : G.U;
+    w.within = cb * kRdpWaveBytes + lane * 16;
+    return w;
+}
+
 // ------------------------------------------------------------- host status
 int set_error(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
 int check_launch(const char* what);
 inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// Whether [a, a+na) and [b, b+nb) share a byte.
+inline bool ranges_overlap(const void* a, uint64_t na, const void* b, uint64_t nb) {
+    const uintptr_t x = reinterpret_cast<uintptr_t>(a), y = reinterpret_cast<uintptr_t>(b);
+    return na && nb && x < y + nb && y < x + na;
+}
+
+// Stream-ordered device copies and zero fills done by kernels (copy.hip), so
+// that no entry point records a memcpy or memset node under graph capture.
+// copy_d2d: n bytes, any alignments; dst == src is a no-op; other overlaps
+// are refused (KVEC_EINVAL).
+int copy_d2d(void* dst, const void* src, uint64_t n, hipStream_t st, const char* what);
+int zero_d(void* dst, uint64_t n, hipStream_t st, const char* what);
 
 inline bool is_prime(int p) {
     if (p < 2) return false;

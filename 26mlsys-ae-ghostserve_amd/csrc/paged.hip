@@ -52,8 +52,10 @@ __global__ __launch_bounds__(kGBS) void kv_scatter_kernel(PagedGeom g, const uin
 }
 
 // ------------------------------------------------- fused gather + RDP encode
-// Stream cell (shard j, row r, lane offset o) is stream byte (j*(p-1) + r)*R + o;
-// with R a multiple of the record size its record is (j*(p-1) + r)*(R/rec) + o/rec.
+// Cell (shard j, row r, byte o of stripe s's rows) is stream byte
+// j*(p-1)*R + s*(p-1)*U + r*g_s + o (stripe geometry: kvec_internal.h); with
+// R, U and so g_s multiples of the record size, its record is
+// j*(recs per shard) + (s*(p-1)*U + r*g_s)/rec + o/rec.
 // Each cell is loaded from the pool once, stored to its data shard and folded
 // into P and Q in registers.  A thread owns one lane offset and a block is one
 // wave.  Shards go in groups of paged_group(p, k) (18 cells for p = 7): the
@@ -64,6 +66,7 @@ __global__ __launch_bounds__(kGBS) void kv_scatter_kernel(PagedGeom g, const uin
 // (whole-stripe groups, 2-shard groups and groups whose page-table loads ride
 // with the previous group's cells were 1-3 % slower).
 constexpr int kFBS = 64;
+static_assert(kFBS * 16 == kRdpWaveBytes, "one wave per 1 KiB of a stripe row");
 
 constexpr int paged_group(int P, int K) {
     const int g = 18 / (P - 1);
@@ -72,16 +75,19 @@ constexpr int paged_group(int P, int K) {
 
 template <int P, int K>
 __global__ __launch_bounds__(kFBS) __attribute__((amdgpu_waves_per_eu(1, 2))) void rdp_encode_paged_kernel(
-        PagedGeom g, Ptrs<16> d, uint8_t* __restrict__ Pp, uint8_t* __restrict__ Qp, uint64_t R,
-        uint32_t recs_per_row, uint32_t nvec) {
+        PagedGeom g, Ptrs<16> d, uint8_t* __restrict__ Pp, uint8_t* __restrict__ Qp, RdpGeom geo,
+        uint32_t nb, uint32_t recs_per_shard) {
     constexpr int ROWS = P - 1, G = paged_group(P, K);
-    const uint32_t u = blockIdx.x * kFBS + threadIdx.x;
-    if (u >= nvec) return;
-    const uint32_t off = u << 4;
+    const RdpWave w = rdp_wave(geo, ROWS, blockIdx.x, threadIdx.x);
+    if (w.within >= w.g) return;
+    const uint32_t off = w.within;
     const uint32_t w0 = fdiv(off, g.div_rec);
     const uint32_t inner = off - w0 * g.div_rec.d;
-    const uint64_t nb = ROWS * R;
-    auto rec = [&](int j, int r) { return uint32_t(j * ROWS + r) * recs_per_row + w0; };
+    // per lane: the record of (shard 0, row 0); row r adds r * g_rec records
+    const uint32_t lane_rec = fdiv(uint32_t(w.base), g.div_rec) + w0;
+    const uint32_t g_rec = fdiv(uint32_t(w.g), g.div_rec);
+    auto rec = [&](int j, int r) { return uint32_t(j) * recs_per_shard + uint32_t(r) * g_rec + lane_rec; };
+    const uint32_t rb = uint32_t(w.base), rg = uint32_t(w.g);
     RdpAcc<P> pr[ROWS], q[ROWS];
 #pragma unroll
     for (int j0 = 0; j0 < K; j0 += G) {
@@ -106,7 +112,7 @@ __global__ __launch_bounds__(kFBS) __attribute__((amdgpu_waves_per_eu(1, 2))) vo
             const ShardView<true> sv(d.p[j], nb);
 #pragma unroll
             for (int r = 0; r < ROWS; ++r) {
-                sv.store(r * R, off, x[gg][r]);
+                sv.store(rb + r * rg, off, x[gg][r]);
                 pr[r].add(x[gg][r]);
                 const int dg = (r + j) % P;
                 if (dg != P - 1) q[dg].add(x[gg][r]);
@@ -126,14 +132,14 @@ __global__ __launch_bounds__(kFBS) __attribute__((amdgpu_waves_per_eu(1, 2))) vo
 #pragma unroll
     for (int r = 0; r < ROWS; ++r) {
         const u32x4 pv = pr[r].get();
-        sp.store(r * R, off, pv);
+        sp.store(rb + r * rg, off, pv);
         if (r >= 1) q[r - 1].add(pv);
     }
 #pragma unroll
-    for (int r = 0; r < ROWS; ++r) sq.store(r * R, off, q[r].get());
+    for (int r = 0; r < ROWS; ++r) sq.store(rb + r * rg, off, q[r].get());
 }
 
-typedef void (*PagedEncFn)(PagedGeom, Ptrs<16>, uint8_t*, uint8_t*, uint64_t, uint32_t, uint32_t);
+typedef void (*PagedEncFn)(PagedGeom, Ptrs<16>, uint8_t*, uint8_t*, RdpGeom, uint32_t, uint32_t);
 
 template <int P, int K = 1>
 PagedEncFn pick_paged(int k) {
@@ -208,7 +214,7 @@ extern "C" int kvec_kv_scatter(const kvec_paged_kv* kv, void* pool, const void* 
 }
 
 extern "C" int kvec_rdp_encode_paged(const kvec_paged_kv* kv, void* const* data, int k, void* P,
-                                     void* Q, int p, int64_t row_bytes, void* stream) {
+                                     void* Q, int p, int64_t row_bytes, int64_t unit_bytes, void* stream) {
     PagedGeom g;
     int rc = make_geom(kv, &g, "kvec_rdp_encode_paged");
     if (rc) return rc;
@@ -218,6 +224,10 @@ extern "C" int kvec_rdp_encode_paged(const kvec_paged_kv* kv, void* const* data,
         return set_error(KVEC_EINVAL,
                          "kvec_rdp_encode_paged: row_bytes=%lld must be a multiple of 2*token_bytes",
                          (long long)row_bytes);
+    if (unit_bytes < 0 || unit_bytes % kRdpWaveBytes || unit_bytes % (2 * kv->token_bytes))
+        return set_error(KVEC_EINVAL,
+                         "kvec_rdp_encode_paged: unit_bytes=%lld must be 0 or a multiple of 1024 and "
+                         "of 2*token_bytes", (long long)unit_bytes);
     if (!fits_buffer(uint64_t(p - 1) * uint64_t(row_bytes)))
         return set_error(KVEC_EUNSUPPORTED, "kvec_rdp_encode_paged: shards must be < 4 GiB");
     const uint64_t stream_bytes = g.recs_total * g.rec;
@@ -235,9 +245,9 @@ extern "C" int kvec_rdp_encode_paged(const kvec_paged_kv* kv, void* const* data,
     }
     PagedEncFn fn = paged_fn(p, k);
     if (!fn) return set_error(KVEC_EUNSUPPORTED, "kvec_rdp_encode_paged: p=%d k=%d not built", p, k);
-    const uint32_t nvec = uint32_t(row_bytes / 16);
-    const uint32_t spr = uint32_t(row_bytes / g.rec);
-    hipLaunchKernelGGL(fn, dim3(blocks_for(nvec, kFBS)), dim3(kFBS), 0, as_stream(stream), g, d,
-                       (uint8_t*)P, (uint8_t*)Q, uint64_t(row_bytes), spr, nvec);
+    const uint64_t nb = uint64_t(p - 1) * uint64_t(row_bytes);
+    const RdpGeom geo = make_rdp_geom(uint64_t(row_bytes), uint64_t(unit_bytes));
+    hipLaunchKernelGGL(fn, dim3(unsigned(rdp_waves(geo))), dim3(kFBS), 0, as_stream(stream), g, d,
+                       (uint8_t*)P, (uint8_t*)Q, geo, uint32_t(nb), uint32_t(nb / g.rec));
     return check_launch("kvec_rdp_encode_paged");
 }

@@ -37,12 +37,11 @@ constexpr int rdp_group(int P, int K) {
 
 template <int P, int K, bool BUF>
 __global__ __launch_bounds__(kBS) __attribute__((amdgpu_waves_per_eu(1, 2))) void rdp_encode_kernel(
-        RdpPtrs d, uint8_t* __restrict__ Pp, uint8_t* __restrict__ Qp, uint64_t R, uint32_t nvec) {
+        RdpPtrs d, uint8_t* __restrict__ Pp, uint8_t* __restrict__ Qp, RdpGeom geo, uint64_t nb) {
     constexpr int ROWS = P - 1, G = rdp_group(P, K);
-    const uint64_t nb = ROWS * R;
-    const uint32_t u = blockIdx.x * kBS + threadIdx.x;
-    if (u >= nvec) return;
-    const uint32_t off = u << 4;
+    const RdpWave w = rdp_wave(geo, ROWS, blockIdx.x, threadIdx.x);
+    if (w.within >= w.g) return;
+    const uint32_t off = w.within;
     RdpAcc<P> pr[ROWS], q[ROWS];
 #pragma unroll
     for (int j0 = 0; j0 < K; j0 += G) {
@@ -52,7 +51,7 @@ __global__ __launch_bounds__(kBS) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
             if (j0 + g >= K) break;
             const ShardView<BUF> sv(d.p[j0 + g], nb);
 #pragma unroll
-            for (int r = 0; r < ROWS; ++r) x[g][r] = sv.load(r * R, off);
+            for (int r = 0; r < ROWS; ++r) x[g][r] = sv.load(w.base + r * w.g, off);
         }
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
@@ -78,12 +77,12 @@ __global__ __launch_bounds__(kBS) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
 #pragma unroll
     for (int r = 0; r < ROWS; ++r) {
         const u32x4 pv = pr[r].get();
-        sp.store(r * R, off, pv);
+        sp.store(w.base + r * w.g, off, pv);
         // The P cell of row r lies on diagonal (r + p - 1) % p = r - 1.
         if (r >= 1) q[r - 1].add(pv);
     }
 #pragma unroll
-    for (int r = 0; r < ROWS; ++r) sq.store(r * R, off, q[r].get());
+    for (int r = 0; r < ROWS; ++r) sq.store(w.base + r * w.g, off, q[r].get());
 }
 
 // ---------------------------------------------------------------- decode
@@ -93,20 +92,19 @@ __global__ __launch_bounds__(kBS) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
 // the cells where their maps differ.
 template <int P, int K, int E0, int E1, bool BUF>
 __global__ __launch_bounds__(kBS) __attribute__((amdgpu_waves_per_eu(1, 2))) void rdp_decode_kernel(
-        RdpPtrs sh, uint64_t R, uint32_t nvec) {
+        RdpPtrs sh, RdpGeom geo, uint64_t nb) {
     constexpr int ROWS = P - 1;
     constexpr int NC = (K + 2) * ROWS;
     constexpr RdpPlan plan = make_rdp_plan(P, K, E0, E1);
     static_assert(plan.ok, "RDP erasure pattern not decodable");
-    const uint64_t nb = ROWS * R;
-    const uint32_t u = blockIdx.x * kBS + threadIdx.x;
-    if (u >= nvec) return;
-    const uint32_t off = u << 4;
+    const RdpWave w = rdp_wave(geo, ROWS, blockIdx.x, threadIdx.x);
+    if (w.within >= w.g) return;
+    const uint32_t off = w.within;
     u32x4 x[NC];
 #pragma unroll
     for (int c = 0; c < NC; ++c) {
         if (!((plan.need[c >> 6] >> (c & 63)) & 1)) continue;
-        x[c] = ShardView<BUF>(sh.p[c / ROWS], nb).load((c % ROWS) * R, off);
+        x[c] = ShardView<BUF>(sh.p[c / ROWS], nb).load(w.base + (c % ROWS) * w.g, off);
     }
     __builtin_amdgcn_sched_barrier(0);
     constexpr RdpSched sch = make_rdp_sched(plan);
@@ -123,7 +121,7 @@ __global__ __launch_bounds__(kBS) __attribute__((amdgpu_waves_per_eu(1, 2))) voi
 #pragma unroll
     for (int o = 0; o < plan.nout; ++o) {
         const int c = plan.out_cell[o];
-        ShardView<BUF>(sh.p[c / ROWS], nb).store((c % ROWS) * R, off, acc[o]);
+        ShardView<BUF>(sh.p[c / ROWS], nb).store(w.base + (c % ROWS) * w.g, off, acc[o]);
     }
 }
 
@@ -161,13 +159,12 @@ inline RdpCellMap rdp_cell_map(const RdpPlan& plan) {
 // outputs accumulate in registers.  Sized per p, so that small codes keep
 // more loads in flight.
 template <int ROWS, int BATCH>
-__global__ __launch_bounds__(kBS) void rdp_decode_generic_kernel(RdpPtrs sh, RdpCellMap cm, uint64_t R,
-                                                                 uint32_t nvec) {
+__global__ __launch_bounds__(kBS) void rdp_decode_generic_kernel(RdpPtrs sh, RdpCellMap cm, RdpGeom geo) {
     constexpr int NOUT = 2 * ROWS;
     static_assert(NOUT <= kRdpMaxOut, "outputs of one stripe");
-    const uint32_t u = blockIdx.x * kBS + threadIdx.x;
-    if (u >= nvec) return;
-    const uint32_t off = u << 4;
+    const RdpWave w = rdp_wave(geo, ROWS, blockIdx.x, threadIdx.x);
+    if (w.within >= w.g) return;
+    const uint64_t off = w.base + w.within;
     u32x4 acc[NOUT];
 #pragma unroll
     for (int o = 0; o < NOUT; ++o) acc[o] = u32x4{0, 0, 0, 0};
@@ -178,7 +175,7 @@ __global__ __launch_bounds__(kBS) void rdp_decode_generic_kernel(RdpPtrs sh, Rdp
             x[t] = u32x4{0, 0, 0, 0};
             if (i0 + t < cm.ncell) {
                 const int c = cm.cell[i0 + t];
-                x[t] = ld16(sh.p[c / ROWS] + uint64_t(c % ROWS) * R + off);
+                x[t] = ld16(sh.p[c / ROWS] + uint64_t(c % ROWS) * w.g + off);
             }
         }
 #pragma unroll
@@ -193,12 +190,12 @@ __global__ __launch_bounds__(kBS) void rdp_decode_generic_kernel(RdpPtrs sh, Rdp
     for (int o = 0; o < NOUT; ++o) {
         if (o < cm.nout) {
             const int c = cm.out_cell[o];
-            st_stream(sh.p[c / ROWS] + uint64_t(c % ROWS) * R, off, acc[o]);
+            st_stream(sh.p[c / ROWS] + uint64_t(c % ROWS) * w.g, off, acc[o]);
         }
     }
 }
 
-typedef void (*GenericDecFn)(RdpPtrs, RdpCellMap, uint64_t, uint32_t);
+typedef void (*GenericDecFn)(RdpPtrs, RdpCellMap, RdpGeom);
 
 static GenericDecFn generic_decode_fn(int p) {
     switch (p) {
@@ -212,8 +209,8 @@ static GenericDecFn generic_decode_fn(int p) {
 }
 
 // ---------------------------------------------------------------- dispatch
-typedef void (*EncFn)(RdpPtrs, uint8_t*, uint8_t*, uint64_t, uint32_t);
-typedef void (*DecFn)(RdpPtrs, uint64_t, uint32_t);
+typedef void (*EncFn)(RdpPtrs, uint8_t*, uint8_t*, RdpGeom, uint64_t);
+typedef void (*DecFn)(RdpPtrs, RdpGeom, uint64_t);
 
 template <int P, bool BUF, int K = 1>
 EncFn pick_encode(int k) {
@@ -275,9 +272,7 @@ static DecFn decode_fn(int p, int k, int e0, int e1, bool buf) {
     return buf ? decode_fn_t<true>(p, k, e0, e1) : decode_fn_t<false>(p, k, e0, e1);
 }
 
-static unsigned rdp_grid(uint32_t nvec) { return blocks_for(nvec, kBS); }
-
-static int check_geom(int k, int p, int64_t row_bytes, const char* fn) {
+static int check_geom(int k, int p, int64_t row_bytes, int64_t unit_bytes, const char* fn) {
     if (!is_prime(p) || p < 3) return set_error(KVEC_EINVAL, "%s: p=%d is not an odd prime", fn, p);
     if (p > kRdpMaxP) return set_error(KVEC_EUNSUPPORTED, "%s: p=%d > %d", fn, p, kRdpMaxP);
     if (k < 1 || k > p - 1) return set_error(KVEC_EINVAL, "%s: k=%d not in [1, p-1=%d]", fn, k, p - 1);
@@ -286,6 +281,9 @@ static int check_geom(int k, int p, int64_t row_bytes, const char* fn) {
                          (long long)row_bytes);
     if (row_bytes >= (int64_t(1) << 32))
         return set_error(KVEC_EUNSUPPORTED, "%s: row_bytes=%lld must be < 4 GiB", fn, (long long)row_bytes);
+    if (unit_bytes < 0 || unit_bytes % kRdpWaveBytes != 0)
+        return set_error(KVEC_EINVAL, "%s: unit_bytes=%lld must be 0 or a positive multiple of %u", fn,
+                         (long long)unit_bytes, kRdpWaveBytes);
     return KVEC_OK;
 }
 
@@ -294,8 +292,8 @@ static int check_geom(int k, int p, int64_t row_bytes, const char* fn) {
 using namespace kvec;
 
 extern "C" int kvec_rdp_encode(const void* const* data, int k, void* P, void* Q, int p,
-                               int64_t row_bytes, void* stream) {
-    int rc = check_geom(k, p, row_bytes, "kvec_rdp_encode");
+                               int64_t row_bytes, int64_t unit_bytes, void* stream) {
+    int rc = check_geom(k, p, row_bytes, unit_bytes, "kvec_rdp_encode");
     if (rc) return rc;
     if (!data || !P || !Q) return set_error(KVEC_EINVAL, "kvec_rdp_encode: null pointer");
     RdpPtrs d{};
@@ -307,18 +305,19 @@ extern "C" int kvec_rdp_encode(const void* const* data, int k, void* P, void* Q,
     if (!aligned16(P) || !aligned16(Q))
         return set_error(KVEC_EINVAL, "kvec_rdp_encode: P/Q not 16-byte aligned");
     if (row_bytes == 0) return KVEC_OK;
-    const bool buf = fits_buffer(uint64_t(p - 1) * uint64_t(row_bytes));
+    const uint64_t nb = uint64_t(p - 1) * uint64_t(row_bytes);
+    const bool buf = fits_buffer(nb);
     EncFn fn = buf ? encode_fn<true>(p, k) : encode_fn<false>(p, k);
     if (!fn) return set_error(KVEC_EUNSUPPORTED, "kvec_rdp_encode: p=%d k=%d not built", p, k);
-    const uint32_t nvec = uint32_t(row_bytes / 16);
-    hipLaunchKernelGGL(fn, dim3(rdp_grid(nvec)), dim3(kBS), 0, as_stream(stream), d,
-                       (uint8_t*)P, (uint8_t*)Q, uint64_t(row_bytes), nvec);
+    const RdpGeom geo = make_rdp_geom(uint64_t(row_bytes), uint64_t(unit_bytes));
+    hipLaunchKernelGGL(fn, dim3(unsigned(rdp_waves(geo))), dim3(kBS), 0, as_stream(stream), d,
+                       (uint8_t*)P, (uint8_t*)Q, geo, nb);
     return check_launch("kvec_rdp_encode");
 }
 
-extern "C" int kvec_rdp_decode(void* const* shards, int k, int p, int64_t row_bytes, int e0, int e1,
-                               void* stream) {
-    int rc = check_geom(k, p, row_bytes, "kvec_rdp_decode");
+extern "C" int kvec_rdp_decode(void* const* shards, int k, int p, int64_t row_bytes, int64_t unit_bytes,
+                               int e0, int e1, void* stream) {
+    int rc = check_geom(k, p, row_bytes, unit_bytes, "kvec_rdp_decode");
     if (rc) return rc;
     if (!shards) return set_error(KVEC_EINVAL, "kvec_rdp_decode: null shard array");
     if (e0 < -1 || e0 > k + 1 || e1 < -1 || e1 > k + 1)
@@ -335,21 +334,19 @@ extern "C" int kvec_rdp_decode(void* const* shards, int k, int p, int64_t row_by
     if (a < 0) { a = b; b = -1; }
     if (b >= 0 && b < a) { int t = a; a = b; b = t; }
     if (a < 0 || row_bytes == 0) return KVEC_OK;
-    const uint32_t nvec = uint32_t(row_bytes / 16);
-    const bool buf = fits_buffer(uint64_t(p - 1) * uint64_t(row_bytes));
-    DecFn fn = decode_fn(p, k, a, b, buf);
+    const uint64_t nb = uint64_t(p - 1) * uint64_t(row_bytes);
+    const RdpGeom geo = make_rdp_geom(uint64_t(row_bytes), uint64_t(unit_bytes));
+    const dim3 grid(unsigned(rdp_waves(geo))), block(kBS);
+    DecFn fn = decode_fn(p, k, a, b, fits_buffer(nb));
     if (fn) {
-        hipLaunchKernelGGL(fn, dim3(rdp_grid(nvec)), dim3(kBS), 0, as_stream(stream), s,
-                           uint64_t(row_bytes), nvec);
+        hipLaunchKernelGGL(fn, grid, block, 0, as_stream(stream), s, geo, nb);
     } else {
-        const dim3 grid(blocks_for(nvec, kBS)), block(kBS);
         RdpPlan plan = make_rdp_plan(p, k, a, b);
         if (!plan.ok)
             return set_error(KVEC_EDECODE, "kvec_rdp_decode: pattern (%d, %d) not decodable", a, b);
         GenericDecFn gfn = generic_decode_fn(p);
         if (!gfn) return set_error(KVEC_EUNSUPPORTED, "kvec_rdp_decode: p=%d", p);
-        hipLaunchKernelGGL(gfn, grid, block, 0, as_stream(stream), s, rdp_cell_map(plan),
-                           uint64_t(row_bytes), nvec);
+        hipLaunchKernelGGL(gfn, grid, block, 0, as_stream(stream), s, rdp_cell_map(plan), geo);
     }
     return check_launch("kvec_rdp_decode");
 }

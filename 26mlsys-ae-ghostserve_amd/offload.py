@@ -66,7 +66,13 @@ class ParityOffload:
 
     def to_device(self, col_off: int, width: int) -> torch.cuda.Event:
         """Restore those columns from the host mirrors (e.g. after the device
-        copy of the parity was lost); the current stream is made to wait."""
-        done = self._copy(col_off, width, False, None)
-        torch.cuda.current_stream(self.device).wait_event(done)
+        copy of the parity was lost).  The copies start after the work already
+        queued on the current stream (an encode or decode that still reads or
+        writes those columns), and the current stream is made to wait for
+        them."""
+        cur = torch.cuda.current_stream(self.device)
+        ready = torch.cuda.Event()
+        ready.record(cur)
+        done = self._copy(col_off, width, False, ready)
+        cur.wait_event(done)
         return done

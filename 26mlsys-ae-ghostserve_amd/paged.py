@@ -89,9 +89,10 @@ def rdp_row_bytes_for(kv: PagedKV, k: int, p: int) -> int:
 
 
 def rdp_encode_paged(kv: PagedKV, data: Sequence[torch.Tensor], P: torch.Tensor, Q: torch.Tensor,
-                     p: int = 7, row_bytes: int | None = None) -> int:
+                     p: int = 7, row_bytes: int | None = None, unit_bytes: int = 0) -> int:
     """Gather kv's chunk into the k data shards and write their RDP parity, in
-    one pass over the pool.  Returns the row-plane size used."""
+    one pass over the pool (stripe geometry of ``spec``; unit_bytes a multiple
+    of 1024 and of the token record).  Returns the row size used."""
     if row_bytes is None:
         row_bytes = rdp_row_bytes_for(kv, len(data), p)
     _lib.require_cuda(*data, P, Q, what="RDP shard")
@@ -99,5 +100,5 @@ def rdp_encode_paged(kv: PagedKV, data: Sequence[torch.Tensor], P: torch.Tensor,
         if t.numel() * t.element_size() < (p - 1) * row_bytes:
             raise ValueError("shard smaller than (p-1)*row_bytes")
     _lib.call("kvec_rdp_encode_paged", kv.c, _lib.ptr_array(data), len(data), P.data_ptr(),
-              Q.data_ptr(), int(p), int(row_bytes), _lib.stream_handle(P.device))
+              Q.data_ptr(), int(p), int(row_bytes), int(unit_bytes), _lib.stream_handle(P.device))
     return int(row_bytes)

@@ -5,10 +5,18 @@ star-diagonal code in :mod:`.rdp`); they are the codes the KV-cache stripe
 configurations are defined with.  Shards are separate HBM buffers: a stripe
 set is k data tensors plus its parity tensors, each a contiguous byte tensor.
 
-RDP stripe geometry: every shard holds p-1 row planes of ``row_bytes`` bytes
-(row r at byte r*row_bytes); column p-1 of the code is the row parity P and Q
-holds the diagonals 0..p-2 (Corbett et al., FAST 2004).  A byte stream is cut
-into k consecutive shards of (p-1)*row_bytes bytes, zero-padded at the end.
+RDP stripe geometry: every shard holds (p-1)*row_bytes bytes, cut into
+stripes of (p-1)*unit_bytes bytes (the last one shorter when unit_bytes does
+not divide row_bytes).  Stripe s has p-1 rows of g_s = min(unit_bytes,
+row_bytes - s*unit_bytes) bytes, row r at s*(p-1)*unit_bytes + r*g_s, and every
+byte offset of its rows is one RDP instance; unit_bytes = 0 is a single stripe
+of p-1 row planes.  Column p-1 of the code is the row parity P and Q holds the
+diagonals 0..p-2 (Corbett et al., FAST 2004).  A byte stream is cut into k
+consecutive shards of (p-1)*row_bytes bytes, zero-padded at the end.
+
+``RDP_UNIT`` (64 KiB) is the stripe unit the KV chunk stripes use: with it each
+wave's loads of a shard stay inside one 384 KiB stripe (p = 7), which MI355X's
+HBM serves markedly faster than p-1 row planes far apart.
 """
 from __future__ import annotations
 
@@ -19,6 +27,9 @@ import numpy as np
 import torch
 
 from . import _lib
+
+
+RDP_UNIT = 65536
 
 
 def _nbytes(t: torch.Tensor) -> int:
@@ -48,26 +59,28 @@ def _row_bytes_of(shards: Sequence[torch.Tensor], p: int, row_bytes: int | None)
 
 
 def rdp_encode(data: Sequence[torch.Tensor], P: torch.Tensor, Q: torch.Tensor, p: int = 7,
-               row_bytes: int | None = None) -> None:
+               row_bytes: int | None = None, unit_bytes: int = 0) -> None:
     """Write the row parity P and diagonal parity Q of ``data`` (k <= p-1 shards)."""
     _lib.require_cuda(*data, P, Q, what="RDP shard")
     R = _row_bytes_of(list(data) + [P, Q], p, row_bytes)
     _lib.call("kvec_rdp_encode", _lib.ptr_array(data), len(data), P.data_ptr(), Q.data_ptr(),
-              int(p), R, _lib.stream_handle(P.device))
+              int(p), R, int(unit_bytes), _lib.stream_handle(P.device))
 
 
 def rdp_decode(shards: Sequence[torch.Tensor], p: int, erased: Sequence[int],
-               row_bytes: int | None = None) -> None:
+               row_bytes: int | None = None, unit_bytes: int = 0) -> None:
     """Rebuild up to two erased shards in place; ``shards`` = data..., P, Q."""
-    er = [int(e) for e in erased if e is not None and int(e) >= 0]
-    if len(set(er)) > 2:
+    # distinct indices, in order, before the count check and the padding: a
+    # repeated index must not push a third erasure out of the list
+    er = list(dict.fromkeys(int(e) for e in erased if e is not None and int(e) >= 0))
+    if len(er) > 2:
         raise ValueError("RDP recovers at most two erased shards")
     er = (er + [-1, -1])[:2]
     _lib.require_cuda(*shards, what="RDP shard")
     R = _row_bytes_of(shards, p, row_bytes)
     k = len(shards) - 2
-    _lib.call("kvec_rdp_decode", _lib.ptr_array(shards), k, int(p), R, er[0], er[1],
-              _lib.stream_handle(shards[0].device))
+    _lib.call("kvec_rdp_decode", _lib.ptr_array(shards), k, int(p), R, int(unit_bytes), er[0],
+              er[1], _lib.stream_handle(shards[0].device))
 
 
 def alloc_rdp_stripe(k: int, p: int, row_bytes: int, device, parity: bool = True):

@@ -45,19 +45,26 @@ const char* kvec_last_error(void);
 /* No reference counterpart (the reference "RDP" is the gs star-diagonal code
  * below); this is Row-Diagonal Parity as Corbett et al. define it (FAST 2004),
  * the double-parity code of the p = 7, k = 6 KV chunk stripes.
- * Stripe: p prime (3..13), k data shards (1 <= k <= p-1; data columns k..p-2
- * are implicit zeros), each shard buffer holds p-1 row planes of `row_bytes`
- * bytes (row r at offset r*row_bytes); row_bytes % 16 == 0.  Column p-1 is
- * the row parity P, Q holds diagonals 0..p-2 over columns 0..p-1. */
+ * Code: p prime (3..13), k data shards (1 <= k <= p-1; data columns k..p-2
+ * are implicit zeros), column p-1 is the row parity P, Q holds diagonals
+ * 0..p-2 over columns 0..p-1.
+ * Geometry: every shard buffer holds (p-1)*row_bytes bytes, row_bytes % 16 ==
+ * 0, cut into stripes of (p-1)*unit_bytes bytes (the last one shorter when
+ * unit_bytes does not divide row_bytes).  Stripe s has p-1 rows of
+ * g_s = min(unit_bytes, row_bytes - s*unit_bytes) bytes, row r at shard byte
+ * s*(p-1)*unit_bytes + r*g_s, and every byte offset of its rows is one RDP
+ * instance.  unit_bytes is 0 (one stripe: p-1 row planes of row_bytes bytes)
+ * or a multiple of 1024; 65536 is the fastest on MI355X (each wave's loads of
+ * a shard then stay inside one 384 KiB stripe). */
 
 /* P, Q from data[0..k-1] (host array of k device pointers). */
 int kvec_rdp_encode(const void* const* data, int k, void* P, void* Q, int p,
-                    int64_t row_bytes, void* stream);
+                    int64_t row_bytes, int64_t unit_bytes, void* stream);
 
 /* Rebuild up to two erased shards in place.  shards = host array of k+2
  * device pointers (data..., P, Q); e0/e1 are shard indices in [0, k+1] or -1. */
-int kvec_rdp_decode(void* const* shards, int k, int p, int64_t row_bytes, int e0,
-                    int e1, void* stream);
+int kvec_rdp_decode(void* const* shards, int k, int p, int64_t row_bytes, int64_t unit_bytes,
+                    int e0, int e1, void* stream);
 
 /* Smallest row plane size (multiple of `granule`, itself a multiple of 16) whose
  * k*(p-1) row planes hold `stream_bytes` bytes.  Host-only arithmetic. */
@@ -119,10 +126,11 @@ int kvec_kv_gather_split(const kvec_paged_kv* kv, void* out_k, void* out_v, void
 int kvec_kv_scatter(const kvec_paged_kv* kv, void* pool, const void* in, void* stream);
 /* Fused gather + spec RDP encode: the chunk's stream, cut into k data shards
  * of (p-1)*row_bytes bytes (zero padded), is written to data[0..k-1] and its
- * P, Q to P, Q, reading every pool byte once.  row_bytes must be a multiple of
- * 2*token_bytes (one token record) and k*(p-1)*row_bytes >= the stream bytes. */
+ * P, Q to P, Q (stripe geometry as kvec_rdp_encode), reading every pool byte
+ * once.  row_bytes and unit_bytes must be multiples of 2*token_bytes (one
+ * token record) and k*(p-1)*row_bytes >= the stream bytes. */
 int kvec_rdp_encode_paged(const kvec_paged_kv* kv, void* const* data, int k, void* P, void* Q,
-                          int p, int64_t row_bytes, void* stream);
+                          int p, int64_t row_bytes, int64_t unit_bytes, void* stream);
 
 /* ================= chunked coding of a paged pool (spec family) ================= */
 /* No reference function: the reference codes each prefill step's KV after an

@@ -498,6 +498,41 @@ int kvo_rdp_decode(uint8_t* const* cols, int k, int p, int64_t R, int e0, int e1
     return 0;
 }
 
+/* Striped geometry: each shard of (p-1)*R bytes is cut into stripes of
+ * (p-1)*U bytes (the last one shorter when U does not divide R); stripe s has
+ * rows of g_s = min(U, R - s*U) bytes, row r at s*(p-1)*U + r*g_s, and is coded
+ * on its own.  U = 0 or U >= R is the single-stripe layout above. */
+#define KVO_MAX_STRIPE_SHARDS 64
+int kvo_rdp_encode_striped(const uint8_t* const* data, int k, uint8_t* P, uint8_t* Q, int p,
+                           int64_t R, int64_t U) {
+    if (U <= 0 || U >= R) return kvo_rdp_encode(data, k, P, Q, p, R);
+    if (k < 1 || k > KVO_MAX_STRIPE_SHARDS) return -1;
+    const int rows = p - 1;
+    for (int64_t s = 0; s * U < R; ++s) {
+        const int64_t base = s * rows * U, g = (R - s * U < U) ? R - s * U : U;
+        const uint8_t* d[KVO_MAX_STRIPE_SHARDS];
+        for (int j = 0; j < k; ++j) d[j] = data[j] + base;
+        int rc = kvo_rdp_encode(d, k, P + base, Q + base, p, g);
+        if (rc) return rc;
+    }
+    return 0;
+}
+
+int kvo_rdp_decode_striped(uint8_t* const* cols, int k, int p, int64_t R, int64_t U, int e0,
+                           int e1) {
+    if (U <= 0 || U >= R) return kvo_rdp_decode(cols, k, p, R, e0, e1);
+    if (k < 1 || k + 2 > KVO_MAX_STRIPE_SHARDS) return -1;
+    const int rows = p - 1;
+    for (int64_t s = 0; s * U < R; ++s) {
+        const int64_t base = s * rows * U, g = (R - s * U < U) ? R - s * U : U;
+        uint8_t* c[KVO_MAX_STRIPE_SHARDS];
+        for (int j = 0; j < k + 2; ++j) c[j] = cols[j] + base;
+        int rc = kvo_rdp_decode(c, k, p, g, e0, e1);
+        if (rc) return rc;
+    }
+    return 0;
+}
+
 /* ======================================================================== */
 /* spec family: RS over GF(2^8), systematic Cauchy                          */
 /* ======================================================================== */

@@ -71,6 +71,11 @@ int kvo_rdp_encode(const uint8_t* const* data, int k, uint8_t* P, uint8_t* Q, in
                    int64_t R);
 /* cols[0..k+1] = data..., P, Q.  e0/e1 are erased shard indices or -1. */
 int kvo_rdp_decode(uint8_t* const* cols, int k, int p, int64_t R, int e0, int e1);
+/* striped geometry: stripes of (p-1)*U bytes, rows of min(U, R - s*U) bytes */
+int kvo_rdp_encode_striped(const uint8_t* const* data, int k, uint8_t* P, uint8_t* Q, int p,
+                           int64_t R, int64_t U);
+int kvo_rdp_decode_striped(uint8_t* const* cols, int k, int p, int64_t R, int64_t U, int e0,
+                           int e1);
 
 /* ---------------- spec family: RS over GF(2^8) (Cauchy) ---------------- */
 int kvo_rs8_encode(const uint8_t* const* data, int k, uint8_t* const* parity, int m,

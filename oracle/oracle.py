@@ -64,6 +64,8 @@ def _declare(L):
         "kvo_rs16_reconstruct": (I, [P, I64, I, I, P, I, P, P, P]),
         "kvo_rdp_encode": (I, [P, I, P, P, I, I64]),
         "kvo_rdp_decode": (I, [P, I, I, I64, I, I]),
+        "kvo_rdp_encode_striped": (I, [P, I, P, P, I, I64, I64]),
+        "kvo_rdp_decode_striped": (I, [P, I, I, I64, I64, I, I]),
         "kvo_rs8_encode": (I, [P, I, P, I, I64]),
         "kvo_rs8_decode": (I, [P, I, I, I64, P, I]),
         "kvo_kv_gather": (I, [P, I64, I, I64, I, P, I, I, I, I, P]),
@@ -209,21 +211,26 @@ def rs16_reconstruct(shards, S, k, m, missing_data, parity_used, ex, lg):
 
 
 # ----------------------------- spec: RDP -----------------------------
-def rdp_encode(data, p: int):
-    """data: list of k arrays shaped [(p-1), R] uint8.  Returns (P, Q)."""
+def rdp_encode(data, p: int, unit: int = 0):
+    """data: list of k shard arrays of (p-1)*R bytes (shaped [(p-1), R] or
+    flat).  unit = 0: p-1 row planes of R bytes; else stripes of (p-1)*unit
+    bytes (rows of min(unit, R - s*unit) bytes).  Returns (P, Q) shaped like
+    data[0]."""
     k = len(data)
-    R = data[0].shape[1]
-    P_ = np.zeros((p - 1, R), np.uint8)
-    Q_ = np.zeros((p - 1, R), np.uint8)
-    _check(lib().kvo_rdp_encode(_ptrs(data), k, _p(P_), _p(Q_), p, R), "rdp_encode")
+    R = data[0].size // (p - 1)
+    P_ = np.zeros(data[0].shape, np.uint8)
+    Q_ = np.zeros(data[0].shape, np.uint8)
+    _check(lib().kvo_rdp_encode_striped(_ptrs(data), k, _p(P_), _p(Q_), p, R, int(unit)),
+           "rdp_encode")
     return P_, Q_
 
 
-def rdp_decode(cols, p: int, e0: int, e1: int = -1):
-    """cols: k data + P + Q arrays [(p-1), R]; erased ones are rewritten in place."""
+def rdp_decode(cols, p: int, e0: int, e1: int = -1, unit: int = 0):
+    """cols: k data + P + Q shard arrays (as rdp_encode); erased ones are
+    rewritten in place."""
     k = len(cols) - 2
-    R = cols[0].shape[1]
-    _check(lib().kvo_rdp_decode(_ptrs(cols), k, p, R, e0, e1), "rdp_decode")
+    R = cols[0].size // (p - 1)
+    _check(lib().kvo_rdp_decode_striped(_ptrs(cols), k, p, R, int(unit), e0, e1), "rdp_decode")
 
 
 # ----------------------------- spec: RS8 -----------------------------

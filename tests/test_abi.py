@@ -63,15 +63,20 @@ def test_rdp_row_bytes(pkg):
 def test_rdp_rejects_bad_arguments(pkg):
     L = pkg._lib.lib()
     arr = (C.c_void_p * 6)(*([16] * 6))
-    assert L.kvec_rdp_encode(arr, 6, 16, 16, 4, 16, None) == -1   # p not prime
-    assert L.kvec_rdp_encode(arr, 7, 16, 16, 7, 16, None) == -1   # k > p-1
-    assert L.kvec_rdp_encode(arr, 6, 16, 16, 7, 24, None) == -1   # row_bytes % 16
-    assert L.kvec_rdp_encode(arr, 6, 16, 16, 17, 16, None) == -2  # p too large
+    assert L.kvec_rdp_encode(arr, 6, 16, 16, 4, 16, 0, None) == -1   # p not prime
+    assert L.kvec_rdp_encode(arr, 7, 16, 16, 7, 16, 0, None) == -1   # k > p-1
+    assert L.kvec_rdp_encode(arr, 6, 16, 16, 7, 24, 0, None) == -1   # row_bytes % 16
+    assert L.kvec_rdp_encode(arr, 6, 16, 16, 17, 16, 0, None) == -2  # p too large
     assert b"p=17" in L.kvec_last_error()
     bad = (C.c_void_p * 6)(*([16] * 5 + [8]))
-    assert L.kvec_rdp_encode(bad, 6, 16, 16, 7, 16, None) == -1   # misaligned shard
+    assert L.kvec_rdp_encode(bad, 6, 16, 16, 7, 16, 0, None) == -1   # misaligned shard
     assert b"aligned" in L.kvec_last_error()
-    assert L.kvec_rdp_decode(arr, 4, 5, 16, 7, -1, None) == -1    # erased index > k+1
+    assert L.kvec_rdp_decode(arr, 4, 5, 16, 0, 7, -1, None) == -1    # erased index > k+1
+    # the stripe unit is 0 or a positive multiple of 1024
+    assert L.kvec_rdp_encode(arr, 6, 16, 16, 7, 4096, 512, None) == -1
+    assert b"unit_bytes" in L.kvec_last_error()
+    assert L.kvec_rdp_encode(arr, 6, 16, 16, 7, 4096, -1024, None) == -1
+    assert L.kvec_rdp_decode(arr, 4, 5, 4096, 1000, 0, -1, None) == -1
 
 
 def test_xor_one_call_entries_reject_bad_arguments(pkg):
@@ -92,6 +97,39 @@ def test_xor_one_call_entries_reject_bad_arguments(pkg):
     assert b"exceed" in L.kvec_last_error()
     assert L.kvec_xor_recover_kv(p, None, 3, 64, 16, 0, None) == -1
     assert L.kvec_xor_recover_kv(p, p, 3, 0, 0, 1, None) == 0          # empty rows
+
+
+def test_pack_unpack_reject_bad_arguments(pkg):
+    """xor_kernel.pack_kv / unpack_kv (benchmark/xor/kernel.cu:193-223): negative
+    sizes and null pointers are refused on the host; zero words is a no-op."""
+    L = pkg._lib.lib()
+    p = 4096
+    assert L.kvec_pack_kv(p, p, p, -1, 4, None) == -1
+    assert L.kvec_pack_kv(p, p, p, 4, -2, None) == -1
+    assert b"seq_len=-2" in L.kvec_last_error()
+    assert L.kvec_pack_kv(None, p, p, 4, 4, None) == -1
+    assert L.kvec_pack_kv(p, p, None, 4, 4, None) == -1
+    assert b"null" in L.kvec_last_error()
+    assert L.kvec_pack_kv(None, None, None, 0, 4, None) == 0
+    assert L.kvec_unpack_kv(p, p, -1, 4, None) == -1
+    assert L.kvec_unpack_kv(None, p, 4, 4, None) == -1
+    assert L.kvec_unpack_kv(p, None, 4, 4, None) == -1
+    assert L.kvec_unpack_kv(None, None, 4, 0, None) == 0
+
+
+def test_copy_entries_reject_partial_overlap(pkg):
+    """Entry points that copy the caller's data rows into the shard tensor
+    accept the same buffer (no copy) or disjoint ones; a partial overlap has no
+    stream-ordered meaning and is refused before any launch."""
+    L = pkg._lib.lib()
+    base, S = 1 << 20, 4096
+    ex = lg = 4096
+    # RS16: data_padded is k*S words; shards + one row overlaps it
+    assert L.kvec_rs16_encode(base + 2 * S, base, 4, 2, S, ex, lg, None) == -1
+    assert b"overlap" in L.kvec_last_error()
+    # XOR: data rows [base + S, +4S) against the shard tensor at base
+    assert L.kvec_xor_encode(base + S, base, 4, S, None) == -1
+    assert b"overlap" in L.kvec_last_error()
 
 
 def test_product_fails_loudly_without_library(pkg, monkeypatch, tmp_path):

@@ -172,6 +172,89 @@ def test_rdp_equations_hold(ora, p, k):
         assert not acc.any(), d
 
 
+def _stripe_rows(buf, p, R, U, s):
+    """Rows of stripe s of a striped shard, located by the geometry's
+    definition (row r at s*(p-1)*U + r*g_s, g_s = min(U, R - s*U))."""
+    g = min(U, R - s * U)
+    base = s * (p - 1) * U
+    return [buf[base + r * g: base + (r + 1) * g] for r in range(p - 1)]
+
+
+@pytest.mark.parametrize("p,k,R,U", [(7, 6, 3 * 64 + 48, 64), (5, 4, 96, 32), (7, 3, 80, 16),
+                                     (3, 2, 50, 16), (11, 10, 40, 16)])
+def test_rdp_striped_equations_hold(ora, p, k, R, U):
+    """Every stripe of the striped layout satisfies the row and diagonal
+    equations on its own rows (the last stripe's rows are shorter), and every
+    byte of the shards belongs to exactly one stripe row."""
+    rng = np.random.default_rng(R + U)
+    data = [rng.integers(0, 256, (p - 1) * R, dtype=np.uint8) for _ in range(k)]
+    P, Q = ora.rdp_encode(data, p, unit=U)
+    ns = -(-R // U)
+    seen = np.zeros((p - 1) * R, np.int32)
+    for s in range(ns):
+        g = min(U, R - s * U)
+        base = s * (p - 1) * U
+        seen[base: base + (p - 1) * g] += 1
+        cols = [_stripe_rows(data[j], p, R, U, s) if j < k else [np.zeros(g, np.uint8)] * (p - 1)
+                for j in range(p - 1)] + [_stripe_rows(P, p, R, U, s)]
+        Qs = _stripe_rows(Q, p, R, U, s)
+        for r in range(p - 1):
+            acc = np.zeros(g, np.uint8)
+            for c in range(p):
+                acc ^= cols[c][r]
+            assert not acc.any(), (s, r)
+        for d in range(p - 1):
+            acc = Qs[d].copy()
+            for c in range(p):
+                r = (d - c) % p
+                if r < p - 1:
+                    acc ^= cols[c][r]
+            assert not acc.any(), (s, d)
+    assert (seen == 1).all()
+
+
+def test_rdp_striped_planted_byte(ora):
+    """A single data byte at row 1, offset 5 of stripe 2 (p = 5, U = 16,
+    R = 40: stripes of rows 16, 16, 8) lands in P at the same place and in Q on
+    diagonal (1 + column) mod 5, nowhere else."""
+    p, k, R, U = 5, 4, 40, 16
+    data = [np.zeros((p - 1) * R, np.uint8) for _ in range(k)]
+    s, r, o, j = 2, 1, 5, 2
+    g = min(U, R - s * U)                     # 8
+    pos = s * (p - 1) * U + r * g + o         # 128 + 8 + 5
+    data[j][pos] = 0x5A
+    P, Q = ora.rdp_encode(data, p, unit=U)
+    assert P.nonzero()[0].tolist() == [pos] and P[pos] == 0x5A
+    d_data = (r + j) % p                      # 3
+    d_p = (r + p - 1) % p                     # the P cell's diagonal: 0
+    want = sorted(s * (p - 1) * U + d * g + o for d in (d_data, d_p) if d < p - 1)
+    assert Q.nonzero()[0].tolist() == want
+    assert all(Q[x] == 0x5A for x in want)
+    # unit 0 and unit >= R are the single-stripe layout
+    Pa, Qa = ora.rdp_encode(data, p, unit=0)
+    Pb, Qb = ora.rdp_encode(data, p, unit=4 * R)
+    assert np.array_equal(Pa, Pb) and np.array_equal(Qa, Qb)
+    assert not np.array_equal(Qa, Q)
+
+
+@pytest.mark.parametrize("p,k,U", [(7, 6, 16), (5, 2, 32), (11, 10, 16)])
+def test_rdp_striped_decode_all_pairs(ora, p, k, U):
+    R = 3 * U + 16
+    rng = np.random.default_rng(p * k)
+    data = [rng.integers(0, 256, (p - 1) * R, dtype=np.uint8) for _ in range(k)]
+    P, Q = ora.rdp_encode(data, p, unit=U)
+    full = data + [P, Q]
+    pats = [(e, -1) for e in range(k + 2)] + list(itertools.combinations(range(k + 2), 2))
+    for e0, e1 in pats:
+        cols = [x.copy() for x in full]
+        for e in (e0, e1):
+            if e >= 0:
+                cols[e][:] = rng.integers(0, 256, cols[e].shape, dtype=np.uint8)
+        ora.rdp_decode(cols, p, e0, e1, unit=U)
+        for s in range(k + 2):
+            assert np.array_equal(cols[s], full[s]), (e0, e1, s)
+
+
 def test_rdp_linearity(ora):
     p, k, R = 7, 6, 64
     a = _rdp_rand(p, k, R, 1)
