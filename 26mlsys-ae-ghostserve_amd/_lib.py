@@ -76,6 +76,7 @@ SIGNATURES = {
     "kvec_kv_gather_split": (_i, [_kvp, _vp, _vp, _vp]),
     "kvec_kv_scatter": (_i, [_kvp, _vp, _vp, _vp]),
     "kvec_rdp_encode_paged": (_i, [_kvp, _pp, _i, _vp, _vp, _i, _i64, _i64, _vp]),
+    "kvec_rdp_decode_paged": (_i, [_kvp, _vp, _pp, _i, _vp, _vp, _i, _i64, _i64, _i, _i, _vp]),
     "kvec_chunk_width": (_i64, [_i64, _i, _i, _i64]),
     "kvec_chunk_encode_paged": (_i, [_kvp, _csp, _vp]),
     "kvec_chunk_decode_paged": (_i, [_kvp, _vp, _csp, _vp, _i, _vp]),

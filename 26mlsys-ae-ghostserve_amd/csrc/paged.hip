@@ -10,6 +10,7 @@
 // whole contiguous runs of records and a wave's 1 KiB of stream is one
 // contiguous 1 KiB of a pool page.  Addressing: paged_geom.h.
 #include "paged_geom.h"
+#include "rdp_plan.h"
 
 namespace kvec {
 
@@ -139,6 +140,138 @@ __global__ __launch_bounds__(kFBS) __attribute__((amdgpu_waves_per_eu(1, 2))) vo
     for (int r = 0; r < ROWS; ++r) sq.store(rb + r * rg, off, q[r].get());
 }
 
+// ------------------------------------------------- fused RDP decode into the pool
+// The inverse of the fused encode: up to two lost shards of the stripe set
+// are rebuilt, lost data cells straight into their pool pages (and into the
+// data shard buffers when the caller keeps them), lost P / Q cells into the
+// parity buffers.  Surviving data cells are read from the pool (the pool is
+// the primary copy of the data) or, when the caller passes the data shard
+// buffers, from those; padding cells past the stream read as zero and are
+// never stored.
+//
+// p = 7, k = 6 without data buffers (the KV chunk stripes) runs the
+// erasure pattern's XOR map solved at compile time, in the shape of the
+// fused encode: every needed cell's page-table entry is requested, then every
+// cell, then the straight-line network; anything else runs the map from the
+// kernel argument, one output at a time (re-read inputs hit the cache).
+template <int P, int K, int E0, int E1>
+__global__ __launch_bounds__(kFBS) __attribute__((amdgpu_waves_per_eu(1, 2))) void rdp_decode_paged_kernel(
+        PagedGeom g, uint8_t* __restrict__ Pp, uint8_t* __restrict__ Qp, RdpGeom geo, uint32_t nb,
+        uint32_t recs_per_shard) {
+    constexpr int ROWS = P - 1, NC = (K + 2) * ROWS;
+    constexpr RdpPlan plan = make_rdp_plan(P, K, E0, E1);
+    static_assert(plan.ok, "RDP erasure pattern not decodable");
+    constexpr RdpSched sch = make_rdp_sched(plan);
+    const RdpWave w = rdp_wave(geo, ROWS, blockIdx.x, threadIdx.x);
+    if (w.within >= w.g) return;
+    const uint32_t off = w.within;
+    const uint32_t w0 = fdiv(off, g.div_rec);
+    const uint32_t inner = off - w0 * g.div_rec.d;
+    const uint32_t lane_rec = fdiv(uint32_t(w.base), g.div_rec) + w0;
+    const uint32_t g_rec = fdiv(uint32_t(w.g), g.div_rec);
+    auto rec = [&](int c) {
+        return uint32_t(c / ROWS) * recs_per_shard + uint32_t(c % ROWS) * g_rec + lane_rec;
+    };
+    auto needed = [&](int c) { return (plan.need[c >> 6] >> (c & 63)) & 1; };
+    const uint32_t rb = uint32_t(w.base), rg = uint32_t(w.g);
+    CellRef ref[NC], refo[plan.nout];
+#pragma unroll
+    for (int c = 0; c < K * ROWS; ++c)
+        if (needed(c)) ref[c] = cell_ref(g, rec(c));
+#pragma unroll
+    for (int o = 0; o < plan.nout; ++o)
+        if (plan.out_cell[o] < K * ROWS) refo[o] = cell_ref(g, rec(plan.out_cell[o]));
+    __builtin_amdgcn_sched_barrier(0);
+    const ShardView<true> sp(Pp, nb), sq(Qp, nb);
+    u32x4 x[NC];
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+        if (!needed(c)) continue;
+        const int s = c / ROWS, r = c % ROWS;
+        x[c] = s < K ? cell_load_ref(g, ref[c], inner) : (s == K ? sp : sq).load(rb + r * rg, off);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    u32x4 acc[plan.nout];
+#pragma unroll
+    for (int i = 0; i < plan.nout; ++i) {
+        const int o = sch.order[i];
+        Xor3Acc a(sch.base[o] < 0 ? u32x4{0, 0, 0, 0} : acc[sch.base[o]]);
+#pragma unroll
+        for (int c = 0; c < NC; ++c)
+            if ((sch.dmask[o][c >> 6] >> (c & 63)) & 1) a.add(x[c]);
+        acc[o] = a.get();
+    }
+#pragma unroll
+    for (int o = 0; o < plan.nout; ++o) {
+        const int c = plan.out_cell[o], s = c / ROWS, r = c % ROWS;
+        if (s < K) cell_store_ref(g, refo[o], inner, acc[o]);
+        else (s == K ? sp : sq).store(rb + r * rg, off, acc[o]);
+    }
+}
+
+__global__ __launch_bounds__(kFBS) void rdp_decode_paged_generic(PagedGeom g, Ptrs<16> d, uint8_t* Pp,
+                                                                 uint8_t* Qp, RdpGeom geo, int rows, int k,
+                                                                 RdpPlan plan, uint32_t recs_per_shard) {
+    const RdpWave w = rdp_wave(geo, rows, blockIdx.x, threadIdx.x);
+    if (w.within >= w.g) return;
+    const uint32_t off = w.within;
+    const uint32_t w0 = fdiv(off, g.div_rec);
+    const uint32_t inner = off - w0 * g.div_rec.d;
+    const uint32_t lane_rec = fdiv(uint32_t(w.base), g.div_rec) + w0;
+    const uint32_t g_rec = fdiv(uint32_t(w.g), g.div_rec);
+    const bool bufs = d.p[0] != nullptr;
+    auto place = [&](int s, int r) { return w.base + uint64_t(r) * w.g + off; };
+    for (int o = 0; o < plan.nout; ++o) {
+        u32x4 acc = {0, 0, 0, 0};
+        for (int wd = 0; wd < kRdpNW; ++wd) {
+            uint64_t msk = plan.mask[o][wd];
+            while (msk) {
+                const int c = wd * 64 + __builtin_ctzll(msk);
+                msk &= msk - 1;
+                const int s = c / rows, r = c - s * rows;
+                if (s < k)
+                    acc ^= bufs ? ld16(d.p[s] + place(s, r))
+                                : cell_load(g, uint32_t(s) * recs_per_shard + uint32_t(r) * g_rec + lane_rec,
+                                            inner);
+                else
+                    acc ^= ld16((s == k ? Pp : Qp) + place(s, r));
+            }
+        }
+        const int c = plan.out_cell[o], s = c / rows, r = c - s * rows;
+        if (s < k) {
+            cell_store(g, uint32_t(s) * recs_per_shard + uint32_t(r) * g_rec + lane_rec, inner, acc);
+            if (bufs) st_stream(d.p[s], place(s, r), acc);
+        } else {
+            st_stream(s == k ? Pp : Qp, place(s, r), acc);
+        }
+    }
+}
+
+typedef void (*PagedDecFn)(PagedGeom, uint8_t*, uint8_t*, RdpGeom, uint32_t, uint32_t);
+
+template <int E0, int E1>
+PagedDecFn pick_paged_dec76(int e1) {
+    if constexpr (E1 > 7) {
+        return nullptr;
+    } else {
+        if (e1 == E1) return &rdp_decode_paged_kernel<7, 6, E0, E1>;
+        return pick_paged_dec76<E0, E1 + 1>(e1);
+    }
+}
+
+template <int E0 = 0>
+PagedDecFn paged_dec76(int e0, int e1) {
+    if constexpr (E0 > 7) {
+        return nullptr;
+    } else {
+        if (e0 == E0) {
+            if (e1 < 0) return &rdp_decode_paged_kernel<7, 6, E0, -1>;
+            return pick_paged_dec76<E0, E0 + 1>(e1);
+        }
+        return paged_dec76<E0 + 1>(e0, e1);
+    }
+}
+
 typedef void (*PagedEncFn)(PagedGeom, Ptrs<16>, uint8_t*, uint8_t*, RdpGeom, uint32_t, uint32_t);
 
 template <int P, int K = 1>
@@ -250,4 +383,64 @@ extern "C" int kvec_rdp_encode_paged(const kvec_paged_kv* kv, void* const* data,
     hipLaunchKernelGGL(fn, dim3(unsigned(rdp_waves(geo))), dim3(kFBS), 0, as_stream(stream), g, d,
                        (uint8_t*)P, (uint8_t*)Q, geo, uint32_t(nb), uint32_t(nb / g.rec));
     return check_launch("kvec_rdp_encode_paged");
+}
+
+extern "C" int kvec_rdp_decode_paged(const kvec_paged_kv* kv, void* pool, void* const* data, int k,
+                                     void* P, void* Q, int p, int64_t row_bytes, int64_t unit_bytes,
+                                     int e0, int e1, void* stream) {
+    PagedGeom g;
+    int rc = make_geom(kv, &g, "kvec_rdp_decode_paged");
+    if (rc) return rc;
+    if (!pool || pool != kv->pool)
+        return set_error(KVEC_EINVAL, "kvec_rdp_decode_paged: pool must be kv->pool");
+    if (!is_prime(p) || p < 3 || p > 13 || k < 1 || k > p - 1)
+        return set_error(KVEC_EINVAL, "kvec_rdp_decode_paged: p=%d k=%d", p, k);
+    if (row_bytes <= 0 || row_bytes % (2 * kv->token_bytes))
+        return set_error(KVEC_EINVAL,
+                         "kvec_rdp_decode_paged: row_bytes=%lld must be a multiple of 2*token_bytes",
+                         (long long)row_bytes);
+    if (unit_bytes < 0 || unit_bytes % kRdpWaveBytes || unit_bytes % (2 * kv->token_bytes))
+        return set_error(KVEC_EINVAL,
+                         "kvec_rdp_decode_paged: unit_bytes=%lld must be 0 or a multiple of 1024 and "
+                         "of 2*token_bytes", (long long)unit_bytes);
+    if (!fits_buffer(uint64_t(p - 1) * uint64_t(row_bytes)))
+        return set_error(KVEC_EUNSUPPORTED, "kvec_rdp_decode_paged: shards must be < 4 GiB");
+    const uint64_t stream_bytes = g.recs_total * g.rec;
+    if (uint64_t(k) * (p - 1) * uint64_t(row_bytes) < stream_bytes)
+        return set_error(KVEC_EINVAL, "kvec_rdp_decode_paged: k*(p-1)*row_bytes < stream bytes");
+    if (uint64_t(k) * (p - 1) * uint64_t(row_bytes) / g.rec >= (uint64_t(1) << 32))
+        return set_error(KVEC_EUNSUPPORTED, "kvec_rdp_decode_paged: stripe too large for 32-bit records");
+    if (!P || !Q || !aligned16(P) || !aligned16(Q))
+        return set_error(KVEC_EINVAL, "kvec_rdp_decode_paged: null or misaligned parity");
+    if (e0 < -1 || e0 > k + 1 || e1 < -1 || e1 > k + 1)
+        return set_error(KVEC_EINVAL, "kvec_rdp_decode_paged: erased index out of [-1, %d]", k + 1);
+    Ptrs<16> d{};
+    if (data) {
+        for (int j = 0; j < k; ++j) {
+            if (!data[j] || !aligned16(data[j]))
+                return set_error(KVEC_EINVAL, "kvec_rdp_decode_paged: data[%d] null or misaligned", j);
+            d.p[j] = (uint8_t*)data[j];
+        }
+    }
+    int a = e0, b = e1;
+    if (a == b) b = -1;
+    if (a < 0) { a = b; b = -1; }
+    if (b >= 0 && b < a) { int t = a; a = b; b = t; }
+    if (a < 0) return KVEC_OK;
+    const uint64_t nb = uint64_t(p - 1) * uint64_t(row_bytes);
+    const RdpGeom geo = make_rdp_geom(uint64_t(row_bytes), uint64_t(unit_bytes));
+    const dim3 grid(unsigned(rdp_waves(geo))), block(kFBS);
+    const uint32_t rps = uint32_t(nb / g.rec);
+    PagedDecFn fn = (p == 7 && k == 6 && !data) ? paged_dec76(a, b) : nullptr;
+    if (fn) {
+        hipLaunchKernelGGL(fn, grid, block, 0, as_stream(stream), g, (uint8_t*)P, (uint8_t*)Q, geo,
+                           uint32_t(nb), rps);
+    } else {
+        RdpPlan plan = make_rdp_plan(p, k, a, b);
+        if (!plan.ok)
+            return set_error(KVEC_EDECODE, "kvec_rdp_decode_paged: pattern (%d, %d) not decodable", a, b);
+        hipLaunchKernelGGL(rdp_decode_paged_generic, grid, block, 0, as_stream(stream), g, d, (uint8_t*)P,
+                           (uint8_t*)Q, geo, p - 1, k, plan, rps);
+    }
+    return check_launch("kvec_rdp_decode_paged");
 }

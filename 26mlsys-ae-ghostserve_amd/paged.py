@@ -102,3 +102,29 @@ def rdp_encode_paged(kv: PagedKV, data: Sequence[torch.Tensor], P: torch.Tensor,
     _lib.call("kvec_rdp_encode_paged", kv.c, _lib.ptr_array(data), len(data), P.data_ptr(),
               Q.data_ptr(), int(p), int(row_bytes), int(unit_bytes), _lib.stream_handle(P.device))
     return int(row_bytes)
+
+
+def rdp_decode_paged(kv: PagedKV, P: torch.Tensor, Q: torch.Tensor, erased: Sequence[int], k: int,
+                     p: int = 7, row_bytes: int | None = None, unit_bytes: int = 0,
+                     data: Sequence[torch.Tensor] | None = None) -> None:
+    """Rebuild up to two lost shards of kv's stripe set (data 0..k-1, P = k,
+    Q = k+1): lost data straight into the pool pages (and into ``data`` when
+    the data shard buffers are given), lost parity into P / Q.  Surviving data
+    is read from ``data`` when given, else from the pool."""
+    er = list(dict.fromkeys(int(e) for e in erased if e is not None and int(e) >= 0))
+    if len(er) > 2:
+        raise ValueError("RDP recovers at most two erased shards")
+    er = (er + [-1, -1])[:2]
+    if row_bytes is None:
+        row_bytes = rdp_row_bytes_for(kv, k, p)
+    shards = [P, Q] + (list(data) if data is not None else [])
+    _lib.require_cuda(*shards, what="RDP shard")
+    for t in shards:
+        if t.numel() * t.element_size() < (p - 1) * row_bytes:
+            raise ValueError("shard smaller than (p-1)*row_bytes")
+    if data is not None and len(data) != k:
+        raise ValueError(f"expected {k} data shards")
+    _lib.call("kvec_rdp_decode_paged", kv.c, kv.pool.data_ptr(),
+              _lib.ptr_array(data) if data is not None else None, int(k), P.data_ptr(),
+              Q.data_ptr(), int(p), int(row_bytes), int(unit_bytes), er[0], er[1],
+              _lib.stream_handle(P.device))

@@ -4,27 +4,39 @@
 Workload (the configuration the metric is quoted on): RDP p=7, k=6 data + 2
 parity shards, encoding one 16 x 2048-token Llama-3.1-8B KV chunk for one TP
 shard: 32 layers x [2 (K,V), 16*2048 tokens, 1 KV head, 128] bf16 = 512 MiB,
-N(0,1) values from a seed.  One step = one encode of the whole chunk from its
-six data shard buffers (inputs resident in HBM) into the P and Q buffers.  Two
+N(0,1) values from a seed.  The shards are cut into RDP stripes of 6 rows of
+64 KiB (spec.RDP_UNIT).  One step = one encode of the whole chunk from its six
+data shard buffers (inputs resident in HBM) into the P and Q buffers.  Two
 buffer sets alternate so the 256 MB MALL cannot serve repeats.
-
-The 2-erasure decode of the same stripe set (all 28 shard pairs, each
-byte-compared against the originals at full size) is reported alongside.
 
 Algorithmic bytes per step = 536,870,912 read + 178,956,971 written
 = 715,827,883 B; `value` is that over the wall time of the timed steps, and
 `roofline.achieved` is that over the average launch duration: one HIP event
 pair on the launch stream around the K back-to-back launches, divided by K.
-Before any number is printed, the outputs are checked byte-exact against the
-CPU oracle on a sample of stripe columns (each column offset is an
-independent RDP instance).
+Before any number is printed, every timed output is checked byte-exact
+against the CPU oracle at full size.
+
+Reported alongside, each checked the same way before it is timed:
+  * the 2-erasure decode of the same stripe set, all 28 shard pairs;
+  * the fused paged gather + encode of the chunk from a 16-token-page pool,
+    and the fused decode of two lost shards straight back into the pool;
+  * RS(6,2) over GF(2^8) on a 1 x 32,768-token stripe (encode, decode);
+  * chunked fp8 coding (RDP p=7 + RS(5,3) per 2048-token prefill chunk),
+    its decode into the pool and the parity offload over PCIe;
+  * the reference's own codes (XOR, star-diagonal P/Q, RS over GF(2^16)) in
+    the reference's packed layouts, encodes and recoveries;
+  * the XOR k=4 single-parity stripe of 256 KiB bf16 shards on the CPU path;
+  * CPU baselines (the oracle, C + OpenMP) for every configuration, on all
+    host cores and on one, with the CPU model.
 
     python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-cpu-baseline]
 """
 import argparse
 import importlib
+import itertools
 import json
 import os
+import random
 import sys
 import time
 
@@ -37,7 +49,7 @@ STREAM_BYTES = L * 2 * B * T * H * D * ES          # 536,870,912
 P_RDP, K_RDP = 7, 6
 PARITY_BYTES = -(-2 * STREAM_BYTES // K_RDP)        # 178,956,971 (2 of k=6 shards)
 ALG_BYTES = STREAM_BYTES + PARITY_BYTES             # 715,827,883
-
+UNIT = 65536                                        # RDP stripe rows (spec.RDP_UNIT)
 
 TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "rdp_encode_p7k6_hbm_bytes.md")
 
@@ -58,6 +70,36 @@ def log(msg):
     print(msg, file=sys.stderr, flush=True)
 
 
+def cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def host_cores():
+    try:
+        return len(os.sched_getaffinity(0))
+    except AttributeError:
+        return os.cpu_count() or 1
+
+
+def gbs(nbytes, us):
+    return round(nbytes / us / 1e3, 2)
+
+
+def frac(nbytes, us):
+    return round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4)
+
+
+def host(t):
+    """Full host copy of a device tensor's bytes (numpy uint8)."""
+    return t.contiguous().view(-1).view(__import__("torch").uint8).cpu().numpy()
+
+
 def make_sets(pkg, torch, dev, nsets, seed):
     spec = pkg.spec
     R = spec.rdp_row_bytes(STREAM_BYTES, K_RDP, P_RDP, 256)
@@ -76,22 +118,11 @@ def make_sets(pkg, torch, dev, nsets, seed):
     return R, sets
 
 
-def sample_check(pkg, torch, oracle, R, data, P, Q, nsample=2048, seed=1):
-    """Byte-exact check of P and Q on `nsample` random 16-byte stripe columns."""
+def check_rdp_full(oracle, data, P, Q):
+    """P and Q of the whole stripe set against the oracle's encode."""
     import numpy as np
-    rng = np.random.default_rng(seed)
-    offs = np.sort(rng.choice(R // 16, size=nsample, replace=False)) * 16
-    lane = (offs[:, None] + np.arange(16)[None, :]).reshape(-1)
-    rows = np.arange(P_RDP - 1)[:, None] * R + lane[None, :]
-    idx = torch.from_numpy(rows.reshape(-1)).to(P.device)
-
-    def cols(t):
-        return t[idx].cpu().numpy().reshape(P_RDP - 1, -1)
-
-    sub = [np.ascontiguousarray(cols(d)) for d in data]
-    Pw, Qw = oracle.rdp_encode(sub, P_RDP)
-    ok = np.array_equal(cols(P), Pw) and np.array_equal(cols(Q), Qw)
-    return ok
+    Pw, Qw = oracle.rdp_encode([host(d) for d in data], P_RDP, unit=UNIT)
+    return np.array_equal(host(P), Pw) and np.array_equal(host(Q), Qw)
 
 
 def time_kernel(torch, fn, sets, steps, warmup):
@@ -116,15 +147,28 @@ def time_kernel(torch, fn, sets, steps, warmup):
     return wall, e0.elapsed_time(e1) / steps
 
 
+def time_us(torch, fn, n=8, pre=2):
+    """Average microseconds of `n` launches of fn(i) after `pre` untimed ones."""
+    stream = torch.cuda.current_stream()
+    for i in range(pre):
+        fn(i)
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for i in range(n):
+        fn(i)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) * 1e3 / n
+
+
 def decode_all_pairs(pkg, torch, sets, R, seed):
     """2-erasure decode of every shard pair, in a seeded order: zero the two
     shards, decode, byte-compare against the originals at full size, then time
     the decode on both buffer sets.  Returns per-pair kernel microseconds."""
-    import itertools
-    import random
     pairs = list(itertools.combinations(range(K_RDP + 2), 2))
     random.Random(seed).shuffle(pairs)
-    stream = torch.cuda.current_stream()
     times = {}
     for a, b in pairs:
         for data, P, Q in sets:
@@ -132,36 +176,27 @@ def decode_all_pairs(pkg, torch, sets, R, seed):
             keep = [shards[a].clone(), shards[b].clone()]
             shards[a].zero_()
             shards[b].zero_()
-            pkg.spec.rdp_decode(shards, P_RDP, [a, b], R)
+            pkg.spec.rdp_decode(shards, P_RDP, [a, b], R, unit_bytes=UNIT)
             if not (torch.equal(shards[a], keep[0]) and torch.equal(shards[b], keep[1])):
                 raise RuntimeError(f"RDP decode of pair ({a}, {b}) is not byte-exact")
             del keep
+
         # decoding a consistent stripe set rewrites the same bytes, so the
-        # launches can repeat; two untimed ones first let the write-back of
-        # the clones and fills above drain before the timed ones
-        for i in range(2):
+        # launches can repeat; the untimed ones first let the write-back of
+        # the clones and fills above drain
+        def dec(i):
             data, P, Q = sets[i % 2]
-            pkg.spec.rdp_decode(list(data) + [P, Q], P_RDP, [a, b], R)
-        torch.cuda.synchronize()
-        e0 = torch.cuda.Event(enable_timing=True)
-        e1 = torch.cuda.Event(enable_timing=True)
-        e0.record(stream)
-        for i in range(8):
-            data, P, Q = sets[i % 2]
-            pkg.spec.rdp_decode(list(data) + [P, Q], P_RDP, [a, b], R)
-        e1.record(stream)
-        torch.cuda.synchronize()
-        times[(a, b)] = e0.elapsed_time(e1) * 1e3 / 8
+            pkg.spec.rdp_decode(list(data) + [P, Q], P_RDP, [a, b], R, unit_bytes=UNIT)
+
+        times[(a, b)] = time_us(torch, dec)
     return times
 
 
 def bench_rs8(pkg, torch, oracle, dev, seed, steps, warmup):
     """RS(6,2) over GF(2^8)/0x11D (Cauchy) on a long-context stripe:
-    1 x 32,768 tokens x 32 layers x [2, 1, 128] bf16 = 512 MiB.  Encode is
-    sample-checked against the oracle; 2-erasure decodes (seeded patterns) are
-    byte-compared at full size.  Algorithmic bytes as for RDP: 715,827,883."""
-    import itertools
-    import random
+    1 x 32,768 tokens x 32 layers x [2, 1, 128] bf16 = 512 MiB.  The encode is
+    checked against the oracle at full size; 2-erasure decodes (seeded
+    patterns) are byte-compared at full size.  Algorithmic bytes as for RDP."""
     import numpy as np
     k, m = 6, 2
     S = -(-STREAM_BYTES // (k * 16)) * 16
@@ -178,15 +213,11 @@ def bench_rs8(pkg, torch, oracle, dev, seed, steps, warmup):
     for data, par in sets:
         pkg.spec.rs8_encode(data, par)
     torch.cuda.synchronize()
-    rng = np.random.default_rng(seed + 7)
-    for si, (data, par) in enumerate(sets):
-        offs = np.sort(rng.choice(S // 16, 4096, replace=False)) * 16
-        idx = torch.from_numpy((offs[:, None] + np.arange(16)).reshape(-1)).to(dev)
-        sub = [np.ascontiguousarray(d[idx].cpu().numpy()) for d in data]
-        want = oracle.rs8_encode(sub, m)
-        for i in range(m):
-            if not np.array_equal(par[i][idx].cpu().numpy(), want[i]):
-                raise RuntimeError("RS8 encode mismatch vs oracle")
+    for data, par in sets:
+        want = oracle.rs8_encode([host(d) for d in data], m)
+        if not all(np.array_equal(host(par[i]), want[i]) for i in range(m)):
+            raise RuntimeError("RS8 encode mismatch vs oracle")
+        del want
 
     def enc(data, par):
         pkg.spec.rs8_encode(data, par)
@@ -196,7 +227,6 @@ def bench_rs8(pkg, torch, oracle, dev, seed, steps, warmup):
     pats = list(itertools.combinations(range(k + m), 2))
     random.Random(seed).shuffle(pats)
     pats = pats[:6]
-    stream = torch.cuda.current_stream()
     dec_us = []
     for er in pats:
         for data, par in sets:
@@ -208,97 +238,147 @@ def bench_rs8(pkg, torch, oracle, dev, seed, steps, warmup):
             if not all(torch.equal(sh[e], kp) for e, kp in zip(er, keep)):
                 raise RuntimeError(f"RS8 decode of {er} is not byte-exact")
             del keep
-        for i in range(2):      # untimed: drain the write-back of the fills above
+
+        def dec(i):
             data, par = sets[i % 2]
             pkg.spec.rs8_decode(list(data) + list(par), k, er)
-        torch.cuda.synchronize()
-        e0 = torch.cuda.Event(enable_timing=True)
-        e1 = torch.cuda.Event(enable_timing=True)
-        e0.record(stream)
-        for i in range(8):
-            data, par = sets[i % 2]
-            pkg.spec.rs8_decode(list(data) + list(par), k, er)
-        e1.record(stream)
-        torch.cuda.synchronize()
-        dec_us.append(e0.elapsed_time(e1) * 1e3 / 8)
+
+        dec_us.append(time_us(torch, dec))
+    cpu_set = [host(d) for d in sets[0][0]]
     del sets
     dmean = sum(dec_us) / len(dec_us)
     return {
         "workload": "rs8_cauchy_k6m2_1x32768tok_llama3.1-8b",
         "shard_bytes": S,
+        "encode_byte_exact_full": True,
         "encode_us": round(enc_us, 2),
-        "encode_gbs": round(ALG_BYTES / enc_us / 1e3, 2),
-        "encode_frac_hbm_peak": round(ALG_BYTES / enc_us / 1e3 / HBM_PEAK_GBS, 4),
+        "encode_gbs": gbs(ALG_BYTES, enc_us),
+        "encode_frac_hbm_peak": frac(ALG_BYTES, enc_us),
         "encode_us_per_2048tok": round(enc_us / 16, 2),
         "decode_patterns": [list(p) for p in pats],
         "decode_byte_exact": True,
         "decode_mean_us": round(dmean, 2),
-        "decode_gbs": round(ALG_BYTES / dmean / 1e3, 2),
-        "decode_frac_hbm_peak": round(ALG_BYTES / dmean / 1e3 / HBM_PEAK_GBS, 4),
-    }
+        "decode_gbs": gbs(ALG_BYTES, dmean),
+        "decode_frac_hbm_peak": frac(ALG_BYTES, dmean),
+    }, cpu_set
 
 
 FUSED_ALG_BYTES = 2 * STREAM_BYTES + PARITY_BYTES   # 1,252,698,795: pool read, shards + P,Q written
 
 
-def bench_paged(pkg, torch, oracle, dev, seed, steps, warmup):
-    """Fused paged gather + RDP p=7 encode: the same 16 x 2048-token chunk, held
-    in a pool of 16-token pages ([32, 2048, 16, 2, 1, 128] bf16) behind a seeded
-    random page table, is gathered into the six data shards and coded in one
-    pass.  Checked byte-exact against the oracle's gather and encode."""
+def paged_sets(pkg, torch, dev, seed, n):
+    """The 16 x 2048-token chunk in a pool of 16-token pages
+    ([32, 2048, 16, 2, 1, 128] bf16) behind a seeded random page table."""
     import numpy as np
     page_tokens = 16
     pps = T // page_tokens
     npages = B * pps
-    sets = []
     rng = np.random.default_rng(seed + 5)
-    for s in range(2):
+    out = []
+    for s in range(n):
         g = torch.Generator(device=dev)
         g.manual_seed(seed + 200 + s)
         pool = torch.randn(L, npages, page_tokens, 2, H, D, generator=g, device=dev,
                            dtype=torch.float32).to(torch.bfloat16)
         table = torch.from_numpy(rng.permutation(npages).astype(np.int32).reshape(B, pps)).to(dev)
-        kv = pkg.paged.PagedKV(pool, table, 0, T)
-        R = pkg.paged.rdp_row_bytes_for(kv, K_RDP, P_RDP)
-        n = (P_RDP - 1) * R
+        out.append(pkg.paged.PagedKV(pool, table, 0, T))
+    return out, page_tokens, npages
+
+
+def bench_paged(pkg, torch, oracle, dev, seed, steps, warmup):
+    """Fused paged gather + RDP p=7 encode of the chunk from its pool pages into
+    the six data shards and P, Q, in one pass; then the fused decode of two lost
+    shards straight back into the pool (survivors read from the pool).  Data
+    shards, P and Q are checked against the oracle's gather and encode at full
+    size; every decode pattern is byte-compared with the pool at full size."""
+    import numpy as np
+    kvs, page_tokens, npages = paged_sets(pkg, torch, dev, seed, 2)
+    R = pkg.paged.rdp_row_bytes_for(kvs[0], K_RDP, P_RDP)
+    n = (P_RDP - 1) * R
+    sets = []
+    for kv in kvs:
         data = [torch.empty(n, dtype=torch.uint8, device=dev) for _ in range(K_RDP)]
-        Pt = torch.empty(n, dtype=torch.uint8, device=dev)
-        Qt = torch.empty(n, dtype=torch.uint8, device=dev)
-        sets.append((kv, data, Pt, Qt))
+        sets.append((kv, data, torch.empty(n, dtype=torch.uint8, device=dev),
+                     torch.empty(n, dtype=torch.uint8, device=dev)))
 
     def step(kv, data, Pt, Qt):
-        pkg.paged.rdp_encode_paged(kv, data, Pt, Qt, P_RDP, R)
+        pkg.paged.rdp_encode_paged(kv, data, Pt, Qt, P_RDP, R, unit_bytes=UNIT)
 
     for st in sets:
         step(*st)
     torch.cuda.synchronize()
-    # correctness: stream vs the oracle's gather (full size), parity on sampled columns
-    kv, data, Pt, Qt = sets[0]
-    pool_h = kv.pool.cpu().view(torch.uint8).numpy().reshape(L, npages, page_tokens, 2, -1)
-    stream = oracle.kv_gather(pool_h, kv.page_table.cpu().numpy(), page_tokens, 0, T).reshape(-1)
-    del pool_h
-    n = (P_RDP - 1) * R
-    for j in range(K_RDP):
-        want = np.zeros(n, np.uint8)
-        seg = stream[j * n:(j + 1) * n]
-        want[:seg.size] = seg
-        if not np.array_equal(data[j].cpu().numpy(), want):
-            raise RuntimeError(f"fused gather: data shard {j} differs from the oracle gather")
-    del stream
-    if not sample_check(pkg, torch, oracle, R, data, Pt, Qt, seed=seed + 9):
-        raise RuntimeError("fused gather + RDP encode parity mismatch vs oracle")
+    for kv, data, Pt, Qt in sets:
+        pool_h = host(kv.pool).reshape(L, npages, page_tokens, 2, -1)
+        stream = oracle.kv_gather(pool_h, kv.page_table.cpu().numpy(), page_tokens, 0, T).reshape(-1)
+        del pool_h
+        padded = np.zeros(K_RDP * n, np.uint8)
+        padded[: stream.size] = stream
+        del stream
+        want = [padded[j * n:(j + 1) * n] for j in range(K_RDP)]
+        for j in range(K_RDP):
+            if not np.array_equal(host(data[j]), want[j]):
+                raise RuntimeError(f"fused gather: data shard {j} differs from the oracle gather")
+        Pw, Qw = oracle.rdp_encode(want, P_RDP, unit=UNIT)
+        if not (np.array_equal(host(Pt), Pw) and np.array_equal(host(Qt), Qw)):
+            raise RuntimeError("fused gather + RDP encode parity mismatch vs oracle")
+        del padded, want, Pw, Qw
     wall, kms = time_kernel(torch, step, sets, steps, warmup)
-    us = kms * 1e3
-    del sets
+    enc_us = kms * 1e3
+
+    # decode into the pool: every erasure pair of the 8 shards
+    pairs = list(itertools.combinations(range(K_RDP + 2), 2))
+    random.Random(seed + 3).shuffle(pairs)
+    per = {}
+    for a, b in pairs:
+        for kv, data, Pt, Qt in sets:
+            pool0 = kv.pool.clone()
+            par0 = [Pt.clone(), Qt.clone()]
+            s = kv.gather()
+            for e in (a, b):
+                if e < K_RDP:
+                    lo, hi = e * n, min((e + 1) * n, s.numel())
+                    s[lo:hi] = 0x5A
+                else:
+                    (Pt if e == K_RDP else Qt).fill_(0xC3)
+            kv.scatter(s)
+            del s
+            pkg.paged.rdp_decode_paged(kv, Pt, Qt, [a, b], K_RDP, P_RDP, R, unit_bytes=UNIT)
+            if not (torch.equal(kv.pool, pool0) and torch.equal(Pt, par0[0]) and
+                    torch.equal(Qt, par0[1])):
+                raise RuntimeError(f"paged decode of ({a}, {b}) did not restore the pool")
+            del pool0, par0
+
+        def dec(i):
+            kv, data, Pt, Qt = sets[i % 2]
+            pkg.paged.rdp_decode_paged(kv, Pt, Qt, [a, b], K_RDP, P_RDP, R, unit_bytes=UNIT)
+
+        per[(a, b)] = time_us(torch, dec)
+    del sets, kvs
+    dmean = sum(per.values()) / len(per)
+    worst = max(per, key=per.get)
+    data_pairs = [v for (a, b), v in per.items() if b < K_RDP]
     return {
         "workload": "paged_gather_rdp_p7_k6_encode_llama3.1-8b_16x2048tok",
         "page_tokens": page_tokens,
         "pool_pages_per_layer": npages,
-        "byte_exact": True,
+        "unit_bytes": UNIT,
+        "byte_exact_full": True,
         "alg_bytes": FUSED_ALG_BYTES,
-        "us": round(us, 2),
-        "gbs": round(FUSED_ALG_BYTES / us / 1e3, 2),
-        "frac_hbm_peak": round(FUSED_ALG_BYTES / us / 1e3 / HBM_PEAK_GBS, 4),
+        "us": round(enc_us, 2),
+        "gbs": gbs(FUSED_ALG_BYTES, enc_us),
+        "frac_hbm_peak": frac(FUSED_ALG_BYTES, enc_us),
+        "decode_into_pool": {
+            "pairs": len(per),
+            "byte_exact_full": True,
+            "alg_bytes": ALG_BYTES,
+            "mean_us": round(dmean, 2),
+            "gbs": gbs(ALG_BYTES, dmean),
+            "frac_hbm_peak": frac(ALG_BYTES, dmean),
+            "two_data_shards_mean_us": round(sum(data_pairs) / len(data_pairs), 2),
+            "slowest_pair": list(worst),
+            "slowest_us": round(per[worst], 2),
+            "per_pair_us": {f"{a},{b}": round(t, 2) for (a, b), t in sorted(per.items())},
+        },
     }
 
 
@@ -309,8 +389,9 @@ def bench_chunked(pkg, torch, oracle, dev, seed, warmup):
     pages behind a seeded shuffled page table, arriving as 16 chunks of 2048
     tokens.  Each chunk is coded once, straight from the pool, with RDP p=7 and
     RS(5,3) sharing 5 data shards, into its columns of the whole-sequence
-    stripes.  Checked against the oracle on sampled columns; decode of lost data
-    shards back into the pool is byte-compared at full size."""
+    stripes.  Every chunk's parity is checked against the oracle's
+    whole-sequence encode at full size; decode of lost data shards back into
+    the pool is byte-compared at full size."""
     import numpy as np
     CL, CB, CT, NCH, page_tokens = 32, 16, 32768, 16, 16
     ct = CT // NCH
@@ -338,26 +419,17 @@ def bench_chunked(pkg, torch, oracle, dev, seed, warmup):
     for c in range(NCH):
         st.encode(kvs[c], c)
     torch.cuda.synchronize()
-    # sampled-column check of chunk 5 against the oracle codes of its gathered cells
-    c = 5
-    s = kvs[c].gather()
-    cells = torch.zeros(k * (p - 1) * W, dtype=torch.uint8, device=dev)
-    cells[: s.numel()] = s
-    del s
-    offs = np.sort(rng.choice(W // 16, 2048, replace=False)) * 16
-    lane = torch.from_numpy((offs[:, None] + np.arange(16)).reshape(-1)).to(dev)
-    cv = cells.view(k, p - 1, W)
-    sub = [np.ascontiguousarray(cv[j][:, lane].cpu().numpy()) for j in range(k)]
-    del cells, cv
-    Pw, Qw = oracle.rdp_encode(sub, p)
-    rsw = oracle.rs8_encode([x.reshape(-1) for x in sub], m)
-    cols = c * W + lane
-
-    def at(t):
-        return t.view(p - 1, R)[:, cols].cpu().numpy()
-
-    if not (np.array_equal(at(st.P), Pw) and np.array_equal(at(st.Q), Qw) and
-            all(np.array_equal(at(st.rs[i]).reshape(-1), rsw[i]) for i in range(m))):
+    # every chunk's parity against the oracle's whole-sequence encode
+    pool_h = host(pool).reshape(CL, npages, page_tokens, 2, -1)
+    wW, _, Pw, Qw, rsw = oracle.chunked_encode(pool_h, table.cpu().numpy(), page_tokens, ct, NCH,
+                                               k, p, m)
+    del pool_h
+    if wW != W:
+        raise RuntimeError("chunk width differs from the oracle's")
+    ok = np.array_equal(host(st.P), Pw.reshape(-1)) and np.array_equal(host(st.Q), Qw.reshape(-1))
+    ok = ok and all(np.array_equal(host(st.rs[i]), rsw[i].reshape(-1)) for i in range(m))
+    del Pw, Qw, rsw
+    if not ok:
         raise RuntimeError("chunked RDP + RS encode mismatch vs oracle")
 
     # timed: the 16 chunks in arrival order, `warmup` untimed passes first
@@ -437,38 +509,46 @@ def bench_chunked(pkg, torch, oracle, dev, seed, warmup):
             raise RuntimeError(f"chunked decode {name}: parity not restored")
         dec[name] = round(e0.elapsed_time(e1) * 1e3, 2)
         del ref, ref_sh
+    cpu_case = (host(pool).reshape(CL, npages, page_tokens, 2, -1), table.cpu().numpy(), page_tokens,
+                ct, k, p, m, W)
     del st, pool, kvs
     return {
         "workload": "chunked_fp8_rdp_p7_k5_rs_k5m3_16x32768tok_16chunks",
         "chunk_tokens": ct, "chunks": NCH, "chunk_stream_bytes": chunk_bytes,
-        "width": W, "row_bytes": R, "byte_exact_sampled": True,
+        "width": W, "row_bytes": R, "byte_exact_full": True,
         "alg_bytes_per_chunk": alg,
         "encode_us_per_chunk": round(enc_us, 2),
-        "encode_gbs": round(alg / enc_us / 1e3, 2),
-        "encode_frac_hbm_peak": round(alg / enc_us / 1e3 / HBM_PEAK_GBS, 4),
+        "encode_gbs": gbs(alg, enc_us),
+        "encode_frac_hbm_peak": frac(alg, enc_us),
         "wall_us_per_chunk": round(wall * 1e6 / NCH, 2),
         "decode_us": dec,
         "decode_byte_exact": True,
         "parity_offload": offload,
-    }
+    }, cpu_case
+
+
+def _entry(us, alg):
+    return {"us": round(us, 2), "alg_bytes": alg, "gbs": gbs(alg, us), "frac_hbm_peak": frac(alg, us)}
 
 
 def bench_gs(pkg, torch, oracle, dev, seed, steps, warmup):
     """The reference's own codes (bit-exact family) on the same 512 MiB
-    Llama-3.1-8B stream, in the reference's packed layouts:
-      star-diagonal P/Q  compute_rdp_parity on rows [(6+2), S] u16 (nd = 6),
-      XOR                encode_xor of data_padded into [(6+1), S] u8,
-      RS GF(2^16)        encode_rs_u16 of data_padded into [(6+2), S] u16.
-    Each output is checked on sampled columns (P, XOR and RS against the
-    oracle on the gathered columns, Q against its definition) before timing."""
+    Llama-3.1-8B stream, in the reference's packed layouts: star-diagonal P/Q
+    (compute_rdp_parity), fused_backup_full_kv, fused_recovery_full_kv, XOR
+    (encode_xor, reconstruct_xor, forward_encode_kv, backwards_decode_kv) and
+    RS over GF(2^16) (encode_rs_u16, reconstruct_rs_u16_inplace).  Each output
+    is checked against the oracle (or the original bytes) at full size before
+    it is timed."""
     import numpy as np
-    rng = np.random.default_rng(seed + 400)
     nd, sb = 6, 0
     words = STREAM_BYTES // 2
     S = -(-words // nd)
     g = torch.Generator(device=dev)
     g.manual_seed(seed + 401)
     out = {}
+
+    def u16(t):
+        return host(t).view(np.uint16)
 
     # star-diagonal P/Q (bench_ghostserve_rdp.py:121-150, benchmark/rdp/kernel.cu:76-107)
     rows = [torch.zeros((nd + 2, S), dtype=torch.uint16, device=dev) for _ in range(2)]
@@ -481,22 +561,14 @@ def bench_gs(pkg, torch, oracle, dev, seed, steps, warmup):
 
     par(rows[0])
     torch.cuda.synchronize()
-    cols = np.sort(rng.choice(S, 4096, replace=False))
-    h = rows[0].cpu().numpy()
-    if not np.array_equal(h[nd, cols], np.bitwise_xor.reduce(h[:nd, cols], axis=0)):
-        raise RuntimeError("gs P mismatch")
-    q = np.zeros(cols.size, np.uint16)
-    for r in range(nd):
-        c = (cols - r) % S
-        q ^= np.where(c != (sb + r) % S, h[r, c], 0).astype(np.uint16)
-    if not np.array_equal(h[nd + 1, cols], q):
-        raise RuntimeError("gs Q mismatch")
-    del h
+    want = u16(rows[0]).reshape(nd + 2, S).copy()
+    want[nd:] = 0
+    oracle.gs_parity(want, nd, S, sb)
+    if not np.array_equal(u16(rows[0]), want.reshape(-1)):
+        raise RuntimeError("gs P/Q mismatch vs oracle")
+    del want
     wall, kms = time_kernel(torch, par, [(r,) for r in rows], steps, warmup)
-    alg = nd * S * 2 + 2 * S * 2
-    out["star_diagonal_pq"] = {"us": round(kms * 1e3, 2), "alg_bytes": alg,
-                               "gbs": round(alg / kms / 1e6, 2),
-                               "frac_hbm_peak": round(alg / kms / 1e6 / HBM_PEAK_GBS, 4)}
+    out["star_diagonal_pq"] = _entry(kms * 1e3, nd * S * 2 + 2 * S * 2)
     del rows
 
     # fused_backup_full_kv (benchmark/rdp/kernel.cu:366-395): K_TN || V_TN packed
@@ -517,48 +589,33 @@ def bench_gs(pkg, torch, oracle, dev, seed, steps, warmup):
     backup(*bsets[0])
     torch.cuda.synchronize()
     K, V, shb = bsets[0]
-    flat = shb.view(torch.int16).view(-1)
-    if not (torch.equal(flat[:words // 2], K.view(torch.int16).reshape(-1)) and
-            torch.equal(flat[words // 2:words], V.view(torch.int16).reshape(-1))):
-        raise RuntimeError("gs backup data rows differ from K || V")
-    hc = shb.view(torch.int16).cpu().numpy().view(np.uint16)
-    if not np.array_equal(hc[nd, cols], np.bitwise_xor.reduce(hc[:nd, cols], axis=0)):
-        raise RuntimeError("gs backup P mismatch")
-    q = np.zeros(cols.size, np.uint16)
-    for r in range(nd):
-        c = (cols - r) % S
-        q ^= np.where(c != (sb + r) % S, hc[r, c], 0).astype(np.uint16)
-    if not np.array_equal(hc[nd + 1, cols], q):
-        raise RuntimeError("gs backup Q mismatch")
-    del hc
+    want = oracle.gs_backup(u16(K).reshape(T_tok, n_w), u16(V).reshape(T_tok, n_w), nd, sb)
+    if not np.array_equal(u16(shb), want.reshape(-1)):
+        raise RuntimeError("gs backup mismatch vs oracle")
+    del want
     wall, kms = time_kernel(torch, backup, bsets, steps, warmup)
-    alg = words * 2 + nd * S * 2 + 2 * S * 2   # K/V read once; data rows + P/Q written
-    out["rdp_backup"] = {"us": round(kms * 1e3, 2), "alg_bytes": alg,
-                         "gbs": round(alg / kms / 1e6, 2),
-                         "frac_hbm_peak": round(alg / kms / 1e6 / HBM_PEAK_GBS, 4)}
+    out["rdp_backup"] = _entry(kms * 1e3, words * 2 + nd * S * 2 + 2 * S * 2)
 
     # fused_recovery_full_kv (benchmark/rdp/kernel.cu:397-521) with rows 0 and 1
     # reported lost: row 0 rebuilt from P in place, then the data rows copied
     # out as K_TN || V_TN.  Row 0 is zeroed first, so the output and the
     # rebuilt row must equal the original K || V.
     backup(*bsets[1])
-    rsets = [(shb, torch.empty(words, dtype=torch.int16, device=dev)) for _, _, shb in bsets]
+    rsets = [(shb_, torch.empty(words, dtype=torch.int16, device=dev)) for _, _, shb_ in bsets]
 
-    def recover(shb, o):
-        pkg.rdp.rdp_kernel.fused_recovery_full_kv(shb, o, nd, S, T_tok, n_w, sb, 0, 1)
+    def recover(shb_, o):
+        pkg.rdp.rdp_kernel.fused_recovery_full_kv(shb_, o, nd, S, T_tok, n_w, sb, 0, 1)
 
     shb.view(torch.int16)[0].zero_()
     recover(*rsets[0])
     torch.cuda.synchronize()
     kv_flat = torch.cat([K.view(torch.int16).reshape(-1), V.view(torch.int16).reshape(-1)])
+    flat = shb.view(torch.int16).view(-1)
     if not (torch.equal(rsets[0][1], kv_flat) and torch.equal(flat[:words], kv_flat)):
         raise RuntimeError("gs recovery output differs from K || V")
     del kv_flat
     wall, kms = time_kernel(torch, recover, rsets, steps, warmup)
-    alg = nd * S * 2 + S * 2 + words * 2      # survivors + P read; the row and K || V written
-    out["rdp_recover_2lost"] = {"us": round(kms * 1e3, 2), "alg_bytes": alg,
-                                "gbs": round(alg / kms / 1e6, 2),
-                                "frac_hbm_peak": round(alg / kms / 1e6 / HBM_PEAK_GBS, 4)}
+    out["rdp_recover_2lost"] = _entry(kms * 1e3, nd * S * 2 + S * 2 + words * 2)
     del bsets, rsets, K, V, shb, flat
 
     # XOR (benchmark/xor/kernel.cu:17-41): the data rows copied into the shard
@@ -574,21 +631,36 @@ def bench_gs(pkg, torch, oracle, dev, seed, steps, warmup):
 
     xenc(*sets[0])
     torch.cuda.synchronize()
-    cb = np.sort(rng.choice(Sb, 4096, replace=False))
-    dsub = np.ascontiguousarray(sets[0][0].view(nd, Sb)[:, torch.from_numpy(cb).to(dev)].cpu().numpy())
-    want = oracle.xor_encode(dsub.reshape(-1), nd, cb.size)
-    if not np.array_equal(sets[0][1][:, torch.from_numpy(cb).to(dev)].cpu().numpy(), want):
-        raise RuntimeError("gs XOR mismatch")
+    want = oracle.xor_encode(host(sets[0][0]), nd, Sb)
+    if not np.array_equal(host(sets[0][1]), want.reshape(-1)):
+        raise RuntimeError("gs XOR mismatch vs oracle")
+    del want
     wall, kms = time_kernel(torch, xenc, sets, steps, warmup)
-    alg = nd * Sb + nd * Sb + Sb       # data read once; data rows + P written
-    out["xor_encode"] = {"us": round(kms * 1e3, 2), "alg_bytes": alg,
-                         "gbs": round(alg / kms / 1e6, 2),
-                         "frac_hbm_peak": round(alg / kms / 1e6 / HBM_PEAK_GBS, 4)}
-    del sets
+    out["xor_encode"] = _entry(kms * 1e3, nd * Sb + nd * Sb + Sb)
+
+    # reconstruct_xor (benchmark/xor/kernel.cu:47-88) in place with shard 2
+    # missing: the row rebuilt from P, into the tensor and recovered_missing
+    xenc(*sets[1])
+    miss = torch.tensor([2], dtype=torch.int32, device=dev)
+    rm = [torch.empty((1, Sb), dtype=torch.uint8, device=dev) for _ in range(2)]
+    keep = sets[0][1][2].clone()
+    sets[0][1][2].fill_(0x33)
+
+    def xrec(i):
+        sh = sets[i % 2][1]
+        pkg.xor.xor_kernel.reconstruct_xor(sh, sh, rm[i % 2], Sb, nd, miss)
+
+    xrec(0)
+    torch.cuda.synchronize()
+    if not (torch.equal(sets[0][1][2], keep) and torch.equal(rm[0][0], keep)):
+        raise RuntimeError("gs reconstruct_xor did not restore the shard")
+    del keep
+    out["xor_reconstruct_1lost"] = _entry(time_us(torch, xrec), nd * Sb + 2 * Sb)
+    del sets, rm
 
     # forward_encode_kv (benchmark/xor/main.py:69-90 then encode_xor): K and V
     # (the stream's two halves) packed into the data rows and P, one pass.
-    # Checked against the plain encode of the same stream.
+    # Checked against the oracle encode of K || V.
     half = STREAM_BYTES // 2
     kvsets = []
     for _ in range(2):
@@ -601,19 +673,16 @@ def bench_gs(pkg, torch, oracle, dev, seed, steps, warmup):
 
     k0, v0, sh0 = kvsets[0]
     xenc_kv(k0, v0, sh0)
-    ref = torch.zeros(nd * Sb, dtype=torch.uint8, device=dev)
-    ref[:half], ref[half:2 * half] = k0, v0
-    shr = torch.empty((nd + 1, Sb), dtype=torch.uint8, device=dev)
-    pkg.xor.xor_kernel.encode_xor(ref, shr, nd, Sb)
     torch.cuda.synchronize()
-    if not torch.equal(sh0, shr):
-        raise RuntimeError("gs XOR encode from K, V differs from the encode of K || V")
-    del ref, shr
+    dp = np.zeros(nd * Sb, np.uint8)
+    dp[:half], dp[half:2 * half] = host(k0), host(v0)
+    want = oracle.xor_encode(dp, nd, Sb)
+    del dp
+    if not np.array_equal(host(sh0), want.reshape(-1)):
+        raise RuntimeError("gs XOR encode from K, V mismatch vs oracle")
+    del want
     wall, kms = time_kernel(torch, xenc_kv, kvsets, steps, warmup)
-    alg = 2 * half + nd * Sb + Sb       # K, V read once; data rows + P written
-    out["xor_encode_from_kv"] = {"us": round(kms * 1e3, 2), "alg_bytes": alg,
-                                 "gbs": round(alg / kms / 1e6, 2),
-                                 "frac_hbm_peak": round(alg / kms / 1e6 / HBM_PEAK_GBS, 4)}
+    out["xor_encode_from_kv"] = _entry(kms * 1e3, 2 * half + nd * Sb + Sb)
 
     # backwards_decode_kv (benchmark/xor/main.py:159-194) with data shard 0 lost:
     # the row rebuilt from P in place and K || V copied out, one pass
@@ -633,10 +702,7 @@ def bench_gs(pkg, torch, oracle, dev, seed, steps, warmup):
         raise RuntimeError("gs XOR decode differs from the encoded K || V")
     del keep
     wall, kms = time_kernel(torch, xdec, rsets, steps, warmup)
-    alg = nd * Sb + Sb + 2 * half       # 5 data rows + P read; the row + K || V written
-    out["xor_decode_1lost"] = {"us": round(kms * 1e3, 2), "alg_bytes": alg,
-                               "gbs": round(alg / kms / 1e6, 2),
-                               "frac_hbm_peak": round(alg / kms / 1e6 / HBM_PEAK_GBS, 4)}
+    out["xor_decode_1lost"] = _entry(kms * 1e3, nd * Sb + Sb + 2 * half)
     del kvsets, rsets, k0, v0, sh0
 
     # RS over GF(2^16) (benchmark/rs/kernel.cu:67-102): the data rows copied into
@@ -654,19 +720,35 @@ def bench_gs(pkg, torch, oracle, dev, seed, steps, warmup):
 
     renc(*sets[0])
     torch.cuda.synchronize()
-    cw = torch.from_numpy(np.sort(rng.choice(S, 2048, replace=False))).to(dev)
-    dsub = np.ascontiguousarray(sets[0][0].view(torch.int16).view(nd, S)[:, cw].cpu().numpy()
-                                .view(np.uint16))
     exh, lgh = oracle.gf16_tables()
-    want = oracle.rs16_encode(dsub.reshape(-1), nd, m, cw.numel(), exh, lgh)
-    if not np.array_equal(sets[0][1].view(torch.int16)[:, cw].cpu().numpy().view(np.uint16), want):
-        raise RuntimeError("gs RS16 mismatch")
+    want = oracle.rs16_encode(u16(sets[0][0]), nd, m, S, exh, lgh)
+    if not np.array_equal(u16(sets[0][1]), want.reshape(-1)):
+        raise RuntimeError("gs RS16 mismatch vs oracle")
+    del want
     wall, kms = time_kernel(torch, renc, sets, steps, warmup)
-    alg = nd * S * 2 + (nd + m) * S * 2   # data read once; data rows + parity written
-    out["rs16_encode"] = {"us": round(kms * 1e3, 2), "alg_bytes": alg,
-                          "gbs": round(alg / kms / 1e6, 2),
-                          "frac_hbm_peak": round(alg / kms / 1e6 / HBM_PEAK_GBS, 4)}
-    del sets
+    out["rs16_encode"] = _entry(kms * 1e3, nd * S * 2 + (nd + m) * S * 2)
+
+    # reconstruct_rs_u16_inplace (benchmark/rs/kernel.cu:105-222) with data rows
+    # 1 and 4 lost, from parities 0 and 1 (benchmark/rs/main.py:150-165's choice)
+    renc(*sets[1])
+    md = torch.tensor([1, 4], dtype=torch.int32, device=dev)
+    pu = torch.tensor([0, 1], dtype=torch.int32, device=dev)
+    sh = sets[0][1].view(torch.int16)
+    keep = sh[[1, 4]].clone()
+    sh[1].fill_(0x1111)
+    sh[4].fill_(0x4444)
+
+    def rrec(i):
+        pkg.rs.rs_kernel.reconstruct_rs_u16_inplace(sets[i % 2][1], S, nd, m, md, pu, ex, lg)
+
+    rrec(0)
+    torch.cuda.synchronize()
+    if not torch.equal(sh[[1, 4]], keep):
+        raise RuntimeError("gs RS16 reconstruct did not restore the rows")
+    del keep
+    out["rs16_reconstruct_2lost"] = _entry(time_us(torch, rrec), nd * S * 2 + 2 * S * 2)
+    del sets, sh
+
     # The serving plugin's per-step parity (bench_ghostserve_rdp.py:334-360):
     # Llama-3.1-8B at TP8, a 2048-token prefill step, one [K | V] row per rank
     # of w = 2048 x 1 KV head x 128 words each, so rows [(8+2), 2w] u16.  A small
@@ -684,17 +766,11 @@ def bench_gs(pkg, torch, oracle, dev, seed, steps, warmup):
 
     par8(rows8[0])
     torch.cuda.synchronize()
-    h = rows8[0].cpu().numpy()
-    cs = np.sort(rng.choice(S8, 2048, replace=False))
-    if not np.array_equal(h[nd8, cs], np.bitwise_xor.reduce(h[:nd8, cs], axis=0)):
-        raise RuntimeError("gs P mismatch (plugin step)")
-    q = np.zeros(cs.size, np.uint16)
-    for r in range(nd8):
-        c = (cs - r) % S8
-        q ^= np.where(c != r % S8, h[r, c], 0).astype(np.uint16)
-    if not np.array_equal(h[nd8 + 1, cs], q):
-        raise RuntimeError("gs Q mismatch (plugin step)")
-    del h
+    want = u16(rows8[0]).reshape(nd8 + 2, S8).copy()
+    want[nd8:] = 0
+    oracle.gs_parity(want, nd8, S8, 0)
+    if not np.array_equal(u16(rows8[0]), want.reshape(-1)):
+        raise RuntimeError("gs P/Q mismatch vs oracle (plugin step)")
     _, kms = time_kernel(torch, par8, [(r,) for r in rows8], 50, 5)
     one = []
     for i in range(20):
@@ -705,31 +781,142 @@ def bench_gs(pkg, torch, oracle, dev, seed, steps, warmup):
     alg8 = nd8 * S8 * 2 + 2 * S8 * 2
     out["plugin_step_pq_tp8"] = {"rows": [nd8 + 2, S8], "alg_bytes": alg8,
                                  "us_back_to_back": round(kms * 1e3, 2),
+                                 "gbs_back_to_back": gbs(alg8, kms * 1e3),
                                  "us_launch_and_sync_median": round(sorted(one)[len(one) // 2], 2)}
     del rows8
     out["workload"] = "gs_family_nd6_llama3.1-8b_16x2048tok_512MiB"
-    out["byte_exact_sampled"] = True
+    out["byte_exact_full"] = True
     return out
 
 
-def cpu_baseline(oracle, torch, data, R, budget_s=10.0):
+C0_K, C0_SHARD = 4, 2 * 512 * 1 * 128 * 2          # 262,144 B: [2, 512 tok, 1, 128] bf16
+C0_ALG = C0_K * C0_SHARD + C0_SHARD                  # 1,310,720 B
+
+
+def bench_c0(pkg, torch, oracle, dev, seed, budget_s):
+    """XOR single parity, k=4 data shards + 1: each shard a bf16 KV chunk
+    [2 (K,V), 512 tokens, 1 KV head, 128] = 256 KiB, N(0,1) from a seed.  Encode,
+    erase one seeded data shard, reconstruct, compare byte-exact; on the CPU
+    path (the oracle's encode_xor / reconstruct_xor, benchmark/xor/kernel.cu:
+    17-88) on one core and on all cores, and on the GPU (xor_kernel)."""
     import numpy as np
-    host = [np.ascontiguousarray(d.cpu().numpy().reshape(P_RDP - 1, R)) for d in data]
-    n, t = 0, 0.0
-    t0 = time.perf_counter()
-    while t < budget_s:
-        oracle.rdp_encode(host, P_RDP)
+    g = torch.Generator(device="cpu").manual_seed(seed + 500)
+    chunks = torch.randn(C0_K, 2, 512, 1, 128, generator=g).to(torch.bfloat16)
+    dp = chunks.view(torch.uint8).numpy().reshape(-1).copy()
+    lost = random.Random(seed).randrange(C0_K)
+    # CPU path: encode, erase, reconstruct, compare
+    sh = oracle.xor_encode(dp, C0_K, C0_SHARD)
+    orig = sh.copy()
+    sh[lost] = 0
+    rec = oracle.xor_reconstruct(sh, C0_SHARD, C0_K, [lost])
+    if not (np.array_equal(sh, orig) and np.array_equal(rec[0], orig[lost])):
+        raise RuntimeError("C0 CPU reconstruct is not byte-exact")
+
+    def rate(fn):
+        n, t0 = 0, time.perf_counter()
+        while True:
+            fn()
+            n += 1
+            t = time.perf_counter() - t0
+            if t >= budget_s:
+                return C0_ALG * n / t / 1e9, n
+
+    cpu = {}
+    all_cores = oracle.num_threads()
+    for label, th in (("1core", 1), ("allcores", all_cores)):
+        oracle.set_num_threads(th)
+        e, ne = rate(lambda: oracle.xor_encode(dp, C0_K, C0_SHARD))
+        r, nr = rate(lambda: oracle.xor_reconstruct(sh, C0_SHARD, C0_K, [lost]))
+        cpu[label] = {"threads": th, "encode_gbs": round(e, 3), "reconstruct_gbs": round(r, 3),
+                      "encode_us": round(C0_ALG / e / 1e3, 2),
+                      "reconstruct_us": round(C0_ALG / r / 1e3, 2)}
+    oracle.set_num_threads(all_cores)
+    # GPU: the same bytes through xor_kernel
+    d_dp = torch.from_numpy(dp).to(dev)
+    d_sh = torch.empty((C0_K + 1, C0_SHARD), dtype=torch.uint8, device=dev)
+    d_rm = torch.empty((1, C0_SHARD), dtype=torch.uint8, device=dev)
+    miss = torch.tensor([lost], dtype=torch.int32, device=dev)
+    pkg.xor.xor_kernel.encode_xor(d_dp, d_sh, C0_K, C0_SHARD)
+    d_sh[lost].zero_()
+    pkg.xor.xor_kernel.reconstruct_xor(d_sh, d_sh, d_rm, C0_SHARD, C0_K, miss)
+    torch.cuda.synchronize()
+    if not (np.array_equal(host(d_sh), orig.reshape(-1)) and np.array_equal(host(d_rm), orig[lost])):
+        raise RuntimeError("C0 GPU encode / reconstruct is not byte-exact")
+    enc_us = time_us(torch, lambda i: pkg.xor.xor_kernel.encode_xor(d_dp, d_sh, C0_K, C0_SHARD), 50, 5)
+    rec_us = time_us(torch, lambda i: pkg.xor.xor_kernel.reconstruct_xor(d_sh, d_sh, d_rm, C0_SHARD,
+                                                                         C0_K, miss), 50, 5)
+    return {
+        "workload": "xor_k4_bf16_kv_chunks_256KiB_shards",
+        "shard_bytes": C0_SHARD, "k": C0_K, "erased": lost, "alg_bytes": C0_ALG,
+        "byte_exact": True,
+        "cpu_path": {"kind": "port", "cpu_model": cpu_model(), **cpu},
+        "gpu": {"encode_us": round(enc_us, 2), "encode_gbs": gbs(C0_ALG, enc_us),
+                "reconstruct_us": round(rec_us, 2), "reconstruct_gbs": gbs(C0_ALG, rec_us),
+                "note": "launch-bound: 1.3 MB per launch"},
+    }
+
+
+def _rate(fn, nbytes, budget_s):
+    n, t0 = 0, time.perf_counter()
+    while True:
+        fn()
         n += 1
         t = time.perf_counter() - t0
-    gbs = ALG_BYTES * n / t / 1e9
-    return {
-        "value": round(gbs, 3),
-        "unit": "GB/s",
-        "cores": oracle.num_threads(),
-        "kind": "port",
-        "sample": f"oracle RDP p=7 k=6 encode of the full 512 MiB chunk stripe set, "
-                  f"{n} runs in {t:.1f} s (C, OpenMP over stripe columns)",
-    }
+        if t >= budget_s:
+            return nbytes * n / t / 1e9, n, t
+
+
+def cpu_baselines(oracle, c1_host, R, rs8_host, chunk_case, budget_s):
+    """The oracle (C, OpenMP over stripe columns) on the same full workloads:
+    C1 encode and C2 decode (all 28 pairs cycled) on the 512 MiB stripe set,
+    RS(6,2) encode, and one chunk of the fp8 chunked coder; all host cores, and
+    the C1 encode on one core too."""
+    import numpy as np
+    all_cores = oracle.num_threads()
+    out = {"cpu_model": cpu_model(), "cores": all_cores, "kind": "port"}
+    v, n, t = _rate(lambda: oracle.rdp_encode(c1_host, P_RDP, unit=UNIT), ALG_BYTES, budget_s)
+    out["c1_rdp_encode"] = {"gbs": round(v, 3), "threads": all_cores, "runs": n}
+    main = {"value": round(v, 3), "unit": "GB/s", "cores": all_cores, "kind": "port",
+            "sample": f"oracle RDP p=7 k=6 encode (64 KiB stripe rows) of the full 512 MiB chunk "
+                      f"stripe set, {n} runs in {t:.1f} s (C, OpenMP over stripe columns)"}
+    oracle.set_num_threads(1)
+    v1, n1, _ = _rate(lambda: oracle.rdp_encode(c1_host, P_RDP, unit=UNIT), ALG_BYTES, budget_s / 2)
+    out["c1_rdp_encode_1core"] = {"gbs": round(v1, 3), "threads": 1, "runs": n1}
+    oracle.set_num_threads(all_cores)
+    Pw, Qw = oracle.rdp_encode(c1_host, P_RDP, unit=UNIT)
+    full = list(c1_host) + [Pw, Qw]
+    pairs = list(itertools.combinations(range(K_RDP + 2), 2))
+    it = iter(itertools.cycle(pairs))
+
+    def dec():
+        a, b = next(it)
+        oracle.rdp_decode(full, P_RDP, a, b, unit=UNIT)
+
+    v, n, _ = _rate(dec, ALG_BYTES, budget_s / 2)
+    out["c2_rdp_decode_pairs"] = {"gbs": round(v, 3), "threads": all_cores, "runs": n}
+    del full
+    if rs8_host is not None:
+        v, n, _ = _rate(lambda: oracle.rs8_encode(rs8_host, 2), ALG_BYTES, budget_s / 2)
+        out["c3_rs8_encode"] = {"gbs": round(v, 3), "threads": all_cores, "runs": n}
+    if chunk_case is not None:
+        pool_h, table, page_tokens, ct, k, p, m, W = chunk_case
+        alg = 0
+
+        def one_chunk():
+            s = oracle.kv_gather(pool_h, table, page_tokens, 5 * ct, ct)
+            cells = oracle.chunk_cells(s, k, p, W)
+            data = [np.ascontiguousarray(cells[j]) for j in range(k)]
+            oracle.rdp_encode(data, p)
+            oracle.rs8_encode([d.reshape(-1) for d in data], m)
+            return s.size
+
+        sb = one_chunk()
+        alg = 2 * sb + (2 + m) * (p - 1) * W    # pool read + cells written, parity written
+        v, n, _ = _rate(one_chunk, alg, budget_s / 2)
+        out["c4_chunk_encode"] = {"gbs": round(v, 3), "threads": all_cores, "runs": n,
+                                  "us_per_chunk": round(alg / v / 1e3, 1),
+                                  "note": "gather into cells, then RDP + RS(5,3)"}
+    return main, out
 
 
 def main():
@@ -744,6 +931,9 @@ def main():
     ap.add_argument("--no-paged", action="store_true")
     ap.add_argument("--no-chunked", action="store_true")
     ap.add_argument("--no-gs", action="store_true")
+    ap.add_argument("--no-c0", action="store_true")
+    ap.add_argument("--cpu-budget", type=float, default=10.0,
+                    help="seconds of CPU work for the main CPU baseline (others take less)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run three 256 MiB device copies (reference kernel of known "
                          "size for HBM byte counters)")
@@ -762,16 +952,16 @@ def main():
     R, sets = make_sets(pkg, torch, dev, 2, args.seed)
 
     def enc(data, P, Q):
-        pkg.spec.rdp_encode(data, P, Q, P_RDP, R)
+        pkg.spec.rdp_encode(data, P, Q, P_RDP, R, unit_bytes=UNIT)
 
     enc(*sets[0])
     enc(*sets[1])
     torch.cuda.synchronize()
-    for s, (data, P, Q) in enumerate(sets):
-        if not sample_check(pkg, torch, oracle, R, data, P, Q, seed=s + 1):
+    for data, P, Q in sets:
+        if not check_rdp_full(oracle, data, P, Q):
             print(json.dumps({"error": "RDP encode mismatch vs oracle"}))
             sys.exit(1)
-    log("[bench] parity check vs oracle passed")
+    log("[bench] encode checked byte-exact against the oracle at full size")
 
     wall, kavg = time_kernel(torch, enc, sets, args.steps, args.warmup)
     ms_step = wall * 1e3 / args.steps
@@ -792,44 +982,60 @@ def main():
             "pairs": len(dec),
             "byte_exact": True,
             "mean_us": round(dec_us, 2),
-            "gbs": round(ALG_BYTES / dec_us / 1e3, 2),
-            "frac_hbm_peak": round(ALG_BYTES / dec_us / 1e3 / HBM_PEAK_GBS, 4),
+            "gbs": gbs(ALG_BYTES, dec_us),
+            "frac_hbm_peak": frac(ALG_BYTES, dec_us),
             "slowest_pair": list(worst),
             "slowest_us": round(dec[worst], 2),
+            "slowest_frac_hbm_peak": frac(ALG_BYTES, dec[worst]),
             "per_pair_us": {f"{a},{b}": round(t, 2) for (a, b), t in sorted(dec.items())},
         }
+    c1_host = [host(d) for d in sets[0][0]] if not args.no_cpu_baseline else None
+    del sets
+    torch.cuda.empty_cache()
 
     fused = None
     if not args.no_paged:
-        log("[bench] fused paged gather + RDP encode")
+        log("[bench] fused paged gather + RDP encode, and the decode into the pool")
         fused = bench_paged(pkg, torch, oracle, dev, args.seed, args.steps, args.warmup)
         log(f"[bench] fused: {fused['us']:.1f} us ({fused['gbs']:.0f} GB/s of "
-            f"{FUSED_ALG_BYTES} B)")
+            f"{FUSED_ALG_BYTES} B); decode into the pool mean "
+            f"{fused['decode_into_pool']['mean_us']:.1f} us")
+        torch.cuda.empty_cache()
 
-    chunked = None
+    chunked, chunk_case = None, None
     if not args.no_chunked:
         log("[bench] chunked fp8 coding: RDP p=7 + RS(5,3) per 2048-token chunk")
-        chunked = bench_chunked(pkg, torch, oracle, dev, args.seed, max(1, args.warmup // 2))
+        chunked, chunk_case = bench_chunked(pkg, torch, oracle, dev, args.seed,
+                                            max(1, args.warmup // 2))
         log(f"[bench] chunked: {chunked['encode_us_per_chunk']:.1f} us/chunk "
             f"({chunked['encode_gbs']:.0f} GB/s), decode {chunked['decode_us']}")
+        torch.cuda.empty_cache()
 
-    rs8 = None
+    rs8, rs8_host = None, None
     if not args.no_rs8:
         log("[bench] RS(6,2) GF(2^8) on the 1 x 32768-token stripe")
-        rs8 = bench_rs8(pkg, torch, oracle, dev, args.seed, args.steps, args.warmup)
+        rs8, rs8_host = bench_rs8(pkg, torch, oracle, dev, args.seed, args.steps, args.warmup)
         log(f"[bench] rs8: encode {rs8['encode_us']:.1f} us ({rs8['encode_gbs']:.0f} GB/s), "
             f"decode {rs8['decode_mean_us']:.1f} us ({rs8['decode_gbs']:.0f} GB/s)")
+        torch.cuda.empty_cache()
 
     gs = None
     if not args.no_gs:
         log("[bench] gs family (reference codes, packed layouts) on the 512 MiB stream")
         gs = bench_gs(pkg, torch, oracle, dev, args.seed, args.steps, args.warmup)
-        log(f"[bench] gs: P/Q {gs['star_diagonal_pq']['us']:.1f} us, backup (pack + P/Q) "
-            f"{gs['rdp_backup']['us']:.1f} us, recovery (row + copy-out) "
-            f"{gs['rdp_recover_2lost']['us']:.1f} us, XOR {gs['xor_encode']['us']:.1f} us "
-            f"(from K, V {gs['xor_encode_from_kv']['us']:.1f} us, decode "
-            f"{gs['xor_decode_1lost']['us']:.1f} us), "
-            f"RS16 {gs['rs16_encode']['us']:.1f} us")
+        log(f"[bench] gs: P/Q {gs['star_diagonal_pq']['us']:.1f} us, backup "
+            f"{gs['rdp_backup']['us']:.1f} us, recovery {gs['rdp_recover_2lost']['us']:.1f} us, "
+            f"XOR {gs['xor_encode']['us']:.1f} us (reconstruct "
+            f"{gs['xor_reconstruct_1lost']['us']:.1f} us, from K, V "
+            f"{gs['xor_encode_from_kv']['us']:.1f} us, decode {gs['xor_decode_1lost']['us']:.1f} us), "
+            f"RS16 {gs['rs16_encode']['us']:.1f} us (reconstruct "
+            f"{gs['rs16_reconstruct_2lost']['us']:.1f} us)")
+        torch.cuda.empty_cache()
+
+    c0 = None
+    if not args.no_c0:
+        log("[bench] XOR k=4 single parity, 256 KiB bf16 shards (CPU path, and the GPU)")
+        c0 = bench_c0(pkg, torch, oracle, dev, args.seed, min(2.0, args.cpu_budget / 4))
 
     if args.copy_calibration:
         src = torch.empty(1 << 28, dtype=torch.uint8, device=dev)
@@ -839,10 +1045,10 @@ def main():
         torch.cuda.synchronize()
         del src, dst
 
-    cpu = None
+    cpu, cpus = None, None
     if not args.no_cpu_baseline:
-        log("[bench] timing CPU oracle baseline")
-        cpu = cpu_baseline(oracle, torch, sets[0][0], R)
+        log("[bench] timing CPU oracle baselines")
+        cpu, cpus = cpu_baselines(oracle, c1_host, R, rs8_host, chunk_case, args.cpu_budget)
 
     out = {
         "metric": "KV parity encode/decode GB/s (% of HBM peak); us per 2048-tok chunk, 1 GPU",
@@ -861,9 +1067,10 @@ def main():
             "workload": "rdp_p7_k6_encode_llama3.1-8b_kv_16x2048tok",
             "layers": L, "batch": B, "tokens": T, "kv_heads": H, "head_dim": D,
             "kv_dtype": "bf16", "stream_bytes": STREAM_BYTES, "p": P_RDP, "k": K_RDP,
-            "row_bytes": R, "alg_bytes_per_step": ALG_BYTES,
+            "row_bytes": R, "unit_bytes": UNIT, "alg_bytes_per_step": ALG_BYTES,
             "us_per_2048tok_chunk": round(ms_step * 1e3, 2),
             "pct_hbm_peak": round(100 * value / HBM_PEAK_GBS, 2),
+            "byte_exact_full": True,
         },
         "roofline": {
             "bound": "hbm",
@@ -874,11 +1081,13 @@ def main():
             "traffic": measured_traffic(),
         },
         "cpu_baseline": cpu,
+        "cpu_baselines": cpus,
         "decode_2erasure": dec_out,
         "rs8_gf256": rs8,
-        "paged_gather_rdp_encode": fused,
+        "paged_gather_rdp": fused,
         "chunked_fp8_rdp_rs": chunked,
         "gs_family": gs,
+        "c0_xor_cpu_path": c0,
     }
     print(json.dumps(out), flush=True)
 

@@ -131,6 +131,18 @@ int kvec_kv_scatter(const kvec_paged_kv* kv, void* pool, const void* in, void* s
  * token record) and k*(p-1)*row_bytes >= the stream bytes. */
 int kvec_rdp_encode_paged(const kvec_paged_kv* kv, void* const* data, int k, void* P, void* Q,
                           int p, int64_t row_bytes, int64_t unit_bytes, void* stream);
+/* Inverse of kvec_rdp_encode_paged (the reference's recovery + load_full back
+ * into K/V, benchmark/rdp/kernel.cu:305-345 and benchmark/rdp/main.py:95-126,
+ * with textbook RDP and the pool as the destination): up to two erased shards
+ * e0, e1 (data 0..k-1, P = k, Q = k+1, or -1) are rebuilt; lost data cells
+ * are written straight into their pool pages (pool == kv->pool) and, when
+ * `data` (host array of k device pointers, or NULL) is given, into the data
+ * shards too; lost P / Q into P / Q.  Surviving data is read from `data` when
+ * given, else from the pool.  Same geometry arguments as the encode.
+ * Page-table entries of one chunk must be distinct. */
+int kvec_rdp_decode_paged(const kvec_paged_kv* kv, void* pool, void* const* data, int k, void* P,
+                          void* Q, int p, int64_t row_bytes, int64_t unit_bytes, int e0, int e1,
+                          void* stream);
 
 /* ================= chunked coding of a paged pool (spec family) ================= */
 /* No reference function: the reference codes each prefill step's KV after an

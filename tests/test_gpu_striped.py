@@ -150,3 +150,79 @@ def test_striped_encode_in_hip_graph(pkg, ora, gpu):
         torch.cuda.synchronize()
         Pw, Qw = ora.rdp_encode(host, p, unit=U)
         assert np.array_equal(P.cpu().numpy(), Pw) and np.array_equal(Q.cpu().numpy(), Qw), it
+
+
+def _garble_shard_in_pool(kv, e, n, seed):
+    """Overwrite the pool bytes that data shard e holds (stream bytes
+    [e*n, (e+1)*n)) with seeded noise."""
+    s = kv.gather()
+    lo, hi = e * n, min((e + 1) * n, s.numel())
+    if lo < hi:
+        g = torch.Generator(device="cpu").manual_seed(seed)
+        s[lo:hi] = torch.randint(0, 256, (hi - lo,), generator=g, dtype=torch.uint8).to(s.device)
+        kv.scatter(s)
+
+
+# (p, k, unit, keep_data): the compiled p = 7, k = 6 networks reading the
+# survivors from the pool, and the generic map (data buffers kept, other codes)
+@pytest.mark.parametrize("p,k,U,keep", [(7, 6, 4096, False), (7, 6, 0, False), (7, 6, 1024, True),
+                                        (5, 4, 2048, False), (7, 3, 4096, True)])
+def test_paged_decode_restores_pool_every_pattern(pkg, ora, gpu, p, k, U, keep):
+    L, B, pps, pt, H, D = 2, 3, 4, 16, 1, 128
+    pool, table = make_pool(gpu, L, B, pps, pt, H, D, torch.bfloat16, seed=p + k + U)
+    kv = pkg.paged.PagedKV(pool.to(gpu), table.to(gpu), 0, pps * pt)
+    R = pkg.paged.rdp_row_bytes_for(kv, k, p)
+    n = (p - 1) * R
+    data = [torch.empty(n, dtype=torch.uint8, device=gpu) for _ in range(k)]
+    P = torch.empty(n, dtype=torch.uint8, device=gpu)
+    Q = torch.empty(n, dtype=torch.uint8, device=gpu)
+    pkg.paged.rdp_encode_paged(kv, data, P, Q, p, R, unit_bytes=U)
+    torch.cuda.synchronize()
+    pool0 = kv.pool.clone()
+    data0 = [d.clone() for d in data]
+    P0, Q0 = P.clone(), Q.clone()
+    pats = [(e, -1) for e in range(k + 2)] + list(itertools.combinations(range(k + 2), 2))
+    for i, (e0, e1) in enumerate(pats):
+        for e in (e0, e1):
+            if e < 0:
+                continue
+            if e < k:
+                _garble_shard_in_pool(kv, e, n, seed=i * 10 + e)
+                if keep:
+                    data[e].fill_(0xA5)
+            else:
+                (P if e == k else Q).fill_(0x3C)
+        pkg.paged.rdp_decode_paged(kv, P, Q, [e0, e1], k, p, R, unit_bytes=U,
+                                   data=data if keep else None)
+        torch.cuda.synchronize()
+        assert torch.equal(kv.pool, pool0), (e0, e1)
+        assert torch.equal(P, P0) and torch.equal(Q, Q0), (e0, e1)
+        if keep:
+            assert all(torch.equal(a, b) for a, b in zip(data, data0)), (e0, e1)
+
+
+def test_paged_decode_matches_oracle_on_noncodeword(pkg, ora, gpu):
+    """On parity that does not match the pool, the rebuilt pool bytes are the
+    oracle decode of the gathered stripe (the same fixed map)."""
+    p, k, U = 7, 6, 4096
+    L, B, pps, pt, H, D = 2, 2, 4, 16, 1, 128
+    pool, table = make_pool(gpu, L, B, pps, pt, H, D, torch.bfloat16, seed=77)
+    kv = pkg.paged.PagedKV(pool.to(gpu), table.to(gpu), 0, pps * pt)
+    R = pkg.paged.rdp_row_bytes_for(kv, k, p)
+    n = (p - 1) * R
+    rng = np.random.default_rng(8)
+    Ph = rng.integers(0, 256, n, dtype=np.uint8)
+    Qh = rng.integers(0, 256, n, dtype=np.uint8)
+    P, Q = torch.from_numpy(Ph).to(gpu), torch.from_numpy(Qh).to(gpu)
+    for e0, e1 in [(1, 4), (0, 6), (2, 7), (5, -1)]:
+        stream = kv.gather().cpu().numpy()
+        padded = np.zeros(k * n, np.uint8)
+        padded[: stream.size] = stream
+        cols = [padded[j * n:(j + 1) * n].copy() for j in range(k)] + [P.cpu().numpy(), Q.cpu().numpy()]
+        ora.rdp_decode(cols, p, e0, e1, unit=U)
+        pkg.paged.rdp_decode_paged(kv, P, Q, [e0, e1], k, p, R, unit_bytes=U)
+        torch.cuda.synchronize()
+        got = kv.gather().cpu().numpy()
+        want = np.concatenate(cols[:k])[: got.size]
+        assert np.array_equal(got, want), (e0, e1)
+        assert np.array_equal(P.cpu().numpy(), cols[k]) and np.array_equal(Q.cpu().numpy(), cols[k + 1])
