@@ -53,8 +53,9 @@ class ChunkStripe(C.Structure):
         ("rs", C.POINTER(C.c_void_p)),
         ("m", C.c_int),
         ("row_bytes", C.c_int64),
-        ("col_off", C.c_int64),
+        ("region_off", C.c_int64),
         ("width", C.c_int64),
+        ("unit_bytes", C.c_int64),
     ]
 
 

@@ -1,20 +1,24 @@
 // chunk.hip -- chunked coding of a paged KV pool, as prefill chunks arrive.
 //
-// One pass over a chunk's token records in the pool writes, at the chunk's own
-// columns of whole-sequence stripes:
+// One pass over a chunk's token records in the pool writes, in the chunk's own
+// region of whole-sequence stripes:
 //   * (optionally) the k data shards,
 //   * textbook RDP(p) row parity P and diagonal parity Q over those k shards
 //     (k <= p-1; columns k..p-2 of the code are implicit zeros),
 //   * systematic RS(k, m) parity over GF(2^8)/0x11D (Cauchy) over the same k
 //     shards.
 //
-// Layout: chunk c's stream (its token records in order, paged_geom.h) is cut
-// into k*(p-1) cells of W bytes; cell (shard j, row r) is stream bytes
-// [(j*(p-1) + r)*W, +W) and lands at columns [col_off, col_off + W) of row
-// plane r of shard j, where a shard holds p-1 row planes of R bytes.  Both codes
-// work column by column, so a chunk touches only its own columns: no parity is
-// read back, and the union of the per-chunk encodes is the encode of the whole
-// sequence's stripes.
+// Layout: every shard of the whole-sequence stripe set holds one region of
+// (p-1)*W bytes per chunk; chunk c's region starts at region_off (c*(p-1)*W
+// for chunks in order).  A region is a spec RDP stripe set in the striped
+// geometry of kvec_internal.h with rows of W bytes and unit U: stripe s has
+// p-1 rows of g_s = min(U, W - s*U) bytes, row r at region_off + s*(p-1)*U +
+// r*g_s.  Chunk c's stream (its token records in order, paged_geom.h), zero
+// padded to k*(p-1)*W bytes, is cut into k shard pieces of (p-1)*W bytes, so
+// data byte (shard j, stripe s, row r, offset o) is stream byte
+// j*(p-1)*W + s*(p-1)*U + r*g_s + o.  Both codes work on their own stripe
+// instances, so a chunk touches only its own region: no parity is read back,
+// and each chunk's region is final once it is coded.
 //
 // The inverse rebuilds lost data cells straight into the pool pages: surviving
 // data cells are read from the pool (the pool is the primary copy of the data),
@@ -33,11 +37,41 @@ constexpr int kCBS = 128;
 constexpr uint32_t kWData = 1u, kWP = 2u, kWQ = 4u, kWRs = 3;
 
 struct ChunkGeom {
-    uint64_t R;              // row-plane bytes of the whole-sequence stripe
-    uint32_t col_off;        // chunk's first column (bytes)
-    uint32_t recs_per_cell;  // W / record bytes
-    uint32_t nvec;           // W / 16
+    uint64_t nb;              // bytes of every shard buffer
+    uint32_t region;          // byte offset of the chunk's region in every shard
+    uint32_t recs_per_shard;  // (p-1)*W / record bytes: one data shard's piece
+    RdpGeom geo;              // the region's stripes (rows of W bytes, unit U)
+    uint32_t nwaves;          // waves over the stripes' rows (1 KiB each)
 };
+
+// A thread's place in the chunk's region: wave blockIdx*2 + (tid >> 6) of the
+// stripes' rows, 16 bytes per lane.  Row r of the thread's stripe starts at
+// shard byte rowbase + r*g (wave-uniform); the thread's bytes are at o within
+// the row.  Its data cell (j, r) is record j*recs_per_shard + r*g_rec + lane_rec.
+struct ChunkPos {
+    uint32_t rowbase, g, o;
+    uint32_t lane_rec, g_rec, inner;
+    bool ok;
+};
+
+__device__ __forceinline__ ChunkPos chunk_pos(const PagedGeom& g, const ChunkGeom& cg, int rows) {
+    const uint32_t wave = blockIdx.x * (kCBS / 64) + (threadIdx.x >> 6);
+    const RdpWave w = rdp_wave(cg.geo, rows, wave, threadIdx.x & 63);
+    ChunkPos c;
+    c.ok = wave < cg.nwaves && w.within < w.g;
+    c.rowbase = cg.region + uint32_t(w.base);
+    c.g = uint32_t(w.g);
+    c.o = w.within;
+    const uint32_t w0 = fdiv(c.o, g.div_rec);
+    c.inner = c.o - w0 * g.rec;
+    c.lane_rec = fdiv(uint32_t(w.base), g.div_rec) + w0;
+    c.g_rec = fdiv(c.g, g.div_rec);
+    return c;
+}
+
+__device__ __forceinline__ uint32_t cell_rec(const ChunkGeom& cg, const ChunkPos& c, int j, int r) {
+    return uint32_t(j) * cg.recs_per_shard + uint32_t(r) * c.g_rec + c.lane_rec;
+}
 
 template <int N>
 struct Gf8Tab {
@@ -54,10 +88,10 @@ __device__ __forceinline__ void stage_tables(uint32_t (*lds)[6], const Gf8Tab<N>
     __syncthreads();
 }
 
-// Pool cell (shard j, row r) of the thread's column; zero for padding records.
-__device__ __forceinline__ u32x4 load_cell(const PagedGeom& g, const ChunkGeom& cg, int j, int r,
-                                           int rows, uint32_t w0, uint32_t inner) {
-    return cell_load(g, uint32_t(j * rows + r) * cg.recs_per_cell + w0, inner);
+// Pool cell (shard j, row r) of the thread's instance; zero for padding records.
+__device__ __forceinline__ u32x4 load_cell(const PagedGeom& g, const ChunkGeom& cg, const ChunkPos& c,
+                                           int j, int r) {
+    return cell_load(g, cell_rec(cg, c, j, r), c.inner);
 }
 
 // ------------------------------------------------------------------ encode
@@ -83,14 +117,12 @@ __global__ __launch_bounds__(kCBS) void chunk_encode_kernel(PagedGeom g, ChunkGe
     constexpr int NT = K * M > 0 ? K * M : 1;
     __shared__ uint32_t tab[NT][6];
     stage_tables<NT>(tab, rs);
-    const uint32_t u = blockIdx.x * kCBS + threadIdx.x;
-    if (u >= cg.nvec) return;
-    const uint32_t o = u << 4;
-    const uint32_t w0 = fdiv(o, g.div_rec);
-    const uint32_t inner = o - w0 * g.rec;
-    const uint64_t nb = ROWS * cg.R;
-    const uint32_t lane = cg.col_off + o;
-    auto rec = [&](int j, int r) { return uint32_t(j * ROWS + r) * cg.recs_per_cell + w0; };
+    const ChunkPos cp = chunk_pos(g, cg, ROWS);
+    if (!cp.ok) return;
+    const uint32_t inner = cp.inner, lane = cp.o;
+    const uint64_t nb = cg.nb;
+    auto rec = [&](int j, int r) { return cell_rec(cg, cp, j, r); };
+    auto row = [&](int r) { return cp.rowbase + uint32_t(r) * cp.g; };
     CellRef ref[2][K];
     u32x4 x[2][K];
 #pragma unroll
@@ -118,10 +150,10 @@ __global__ __launch_bounds__(kCBS) void chunk_encode_kernel(PagedGeom g, ChunkGe
         }
         if constexpr (DATA) {
 #pragma unroll
-            for (int j = 0; j < K; ++j) ShardView<true>(d.p[j], nb).store(r * cg.R, lane, x[c][j]);
+            for (int j = 0; j < K; ++j) ShardView<true>(d.p[j], nb).store(row(r), lane, x[c][j]);
         }
         const u32x4 pr = xor_all<K>(x[c]);
-        sp.store(r * cg.R, lane, pr);
+        sp.store(row(r), lane, pr);
         // cell (r, j) lies on diagonal (r + j) % p; the P cell of row r on r - 1
 #pragma unroll
         for (int j = 0; j < K; ++j) {
@@ -143,13 +175,13 @@ __global__ __launch_bounds__(kCBS) void chunk_encode_kernel(PagedGeom g, ChunkGe
 #pragma unroll
             for (int i = 0; i < M; ++i)
                 ShardView<true>(par.p[2 + i], (wmask & (1u << (kWRs + i))) ? nb : 0)
-                    .store(r * cg.R, lane, acc[i]);
+                    .store(row(r), lane, acc[i]);
         }
         asm volatile("" ::: "memory");
     }
     const ShardView<true> sq(par.p[1], (wmask & kWQ) ? nb : 0);
 #pragma unroll
-    for (int r = 0; r < ROWS; ++r) sq.store(r * cg.R, lane, q[r]);
+    for (int r = 0; r < ROWS; ++r) sq.store(row(r), lane, q[r]);
 }
 
 // ------------------------------------------------------------------ RS decode
@@ -171,14 +203,12 @@ __global__ __launch_bounds__(kCBS) void chunk_rs_decode_kernel(PagedGeom g, Chun
                                                                RsDecodeIo io, Gf8Tab<K * NOUT> mix) {
     __shared__ uint32_t tab[K * NOUT][6];
     stage_tables<K * NOUT>(tab, mix);
-    const uint32_t u = blockIdx.x * kCBS + threadIdx.x;
-    if (u >= cg.nvec) return;
-    const uint32_t o = u << 4;
-    const uint32_t w0 = fdiv(o, g.div_rec);
-    const uint32_t inner = o - w0 * g.rec;
-    const uint64_t nb = uint64_t(ROWS) * cg.R;
-    const uint32_t lane = cg.col_off + o;
-    auto rec = [&](int shard, int r) { return uint32_t(shard * ROWS + r) * cg.recs_per_cell + w0; };
+    const ChunkPos cp = chunk_pos(g, cg, ROWS);
+    if (!cp.ok) return;
+    const uint32_t inner = cp.inner, lane = cp.o;
+    const uint64_t nb = cg.nb;
+    auto rec = [&](int shard, int r) { return cell_rec(cg, cp, shard, r); };
+    auto row = [&](int r) { return cp.rowbase + uint32_t(r) * cp.g; };
     CellRef rin[3][K], rout[3][NOUT];
     auto refs = [&](int r) {
 #pragma unroll
@@ -189,7 +219,7 @@ __global__ __launch_bounds__(kCBS) void chunk_rs_decode_kernel(PagedGeom g, Chun
             if (io.dst_shard[i] >= 0) rout[r % 3][i] = cell_ref(g, rec(io.dst_shard[i], r));
     };
     auto load_in = [&](int q, int r) {
-        return io.in_buf[q] ? ShardView<true>(io.in_buf[q], nb).load(r * cg.R, lane)
+        return io.in_buf[q] ? ShardView<true>(io.in_buf[q], nb).load(row(r), lane)
                             : cell_load_ref(g, rin[r % 3][q], inner);
     };
     u32x4 x[2][K];
@@ -218,7 +248,7 @@ __global__ __launch_bounds__(kCBS) void chunk_rs_decode_kernel(PagedGeom g, Chun
 #pragma unroll
         for (int i = 0; i < NOUT; ++i) {
             if (io.dst_shard[i] >= 0) cell_store_ref(g, rout[r % 3][i], inner, acc[i]);
-            if (io.out_buf[i]) ShardView<true>(io.out_buf[i], nb).store(r * cg.R, lane, acc[i]);
+            if (io.out_buf[i]) ShardView<true>(io.out_buf[i], nb).store(row(r), lane, acc[i]);
         }
         asm volatile("" ::: "memory");
     }
@@ -230,21 +260,17 @@ __global__ __launch_bounds__(kCBS) void chunk_rs_decode_kernel(PagedGeom g, Chun
 // One output cell at a time, so re-read inputs come from cache.
 __device__ __forceinline__ u32x4 rdp_cell_load(const PagedGeom& g, const ChunkGeom& cg, int k,
                                                int rows, const uint8_t* P, const uint8_t* Q, int c,
-                                               uint32_t w0, uint32_t inner, uint32_t lane) {
+                                               const ChunkPos& cp) {
     const int s = c / rows, r = c - s * rows;
-    if (s < k) return load_cell(g, cg, s, r, rows, w0, inner);
-    return ld16((s == k ? P : Q) + uint64_t(r) * cg.R + lane);
+    if (s < k) return load_cell(g, cg, cp, s, r);
+    return ld16((s == k ? P : Q) + uint64_t(cp.rowbase + uint32_t(r) * cp.g) + cp.o);
 }
 
 __global__ __launch_bounds__(kCBS) void chunk_rdp_decode_kernel(PagedGeom g, ChunkGeom cg, int k,
                                                                 int rows, Ptrs<kChunkMaxK> d,
                                                                 uint8_t* P, uint8_t* Q, RdpPlan plan) {
-    const uint32_t u = blockIdx.x * kCBS + threadIdx.x;
-    if (u >= cg.nvec) return;
-    const uint32_t o = u << 4;
-    const uint32_t w0 = fdiv(o, g.div_rec);
-    const uint32_t inner = o - w0 * g.rec;
-    const uint32_t lane = cg.col_off + o;
+    const ChunkPos cp = chunk_pos(g, cg, rows);
+    if (!cp.ok) return;
     for (int oc = 0; oc < plan.nout; ++oc) {
         u32x4 acc = {0, 0, 0, 0};
         for (int wd = 0; wd < kRdpNW; ++wd) {
@@ -252,16 +278,17 @@ __global__ __launch_bounds__(kCBS) void chunk_rdp_decode_kernel(PagedGeom g, Chu
             while (msk) {
                 const int c = wd * 64 + __builtin_ctzll(msk);
                 msk &= msk - 1;
-                acc ^= rdp_cell_load(g, cg, k, rows, P, Q, c, w0, inner, lane);
+                acc ^= rdp_cell_load(g, cg, k, rows, P, Q, c, cp);
             }
         }
         const int c = plan.out_cell[oc];
         const int s = c / rows, r = c - s * rows;
+        const uint64_t rowoff = cp.rowbase + uint32_t(r) * cp.g;
         if (s < k) {
-            cell_store(g, uint32_t(s * rows + r) * cg.recs_per_cell + w0, inner, acc);
-            if (d.p[s]) st_stream(d.p[s] + uint64_t(r) * cg.R, lane, acc);
+            cell_store(g, cell_rec(cg, cp, s, r), cp.inner, acc);
+            if (d.p[s]) st_stream(d.p[s] + rowoff, cp.o, acc);
         } else {
-            st_stream((s == k ? P : Q) + uint64_t(r) * cg.R, lane, acc);
+            st_stream((s == k ? P : Q) + rowoff, cp.o, acc);
         }
     }
 }
@@ -276,22 +303,20 @@ __global__ __launch_bounds__(kCBS) void chunk_rdp_decode_fixed(PagedGeom g, Chun
     constexpr int ROWS = P - 1, NC = (K + 2) * ROWS;
     constexpr RdpPlan plan = make_rdp_plan(P, K, E0, E1);
     static_assert(plan.ok, "RDP erasure pattern not decodable");
-    const uint32_t u = blockIdx.x * kCBS + threadIdx.x;
-    if (u >= cg.nvec) return;
-    const uint32_t o = u << 4;
-    const uint32_t w0 = fdiv(o, g.div_rec);
-    const uint32_t inner = o - w0 * g.rec;
-    const uint64_t nb = uint64_t(ROWS) * cg.R;
-    const uint32_t lane = cg.col_off + o;
+    const ChunkPos cp = chunk_pos(g, cg, ROWS);
+    if (!cp.ok) return;
+    const uint32_t inner = cp.inner, lane = cp.o;
+    const uint64_t nb = cg.nb;
+    auto row = [&](int r) { return cp.rowbase + uint32_t(r) * cp.g; };
     auto needed = [&](int c) { return (plan.need[c >> 6] >> (c & 63)) & 1; };
     CellRef ref[NC], refo[plan.nout];   // c = shard * ROWS + row
 #pragma unroll
     for (int c = 0; c < NC; ++c)
-        if (c < K * ROWS && needed(c)) ref[c] = cell_ref(g, uint32_t(c) * cg.recs_per_cell + w0);
+        if (c < K * ROWS && needed(c)) ref[c] = cell_ref(g, cell_rec(cg, cp, c / ROWS, c % ROWS));
 #pragma unroll
     for (int i = 0; i < plan.nout; ++i)
         if (plan.out_cell[i] < K * ROWS)
-            refo[i] = cell_ref(g, uint32_t(plan.out_cell[i]) * cg.recs_per_cell + w0);
+            refo[i] = cell_ref(g, cell_rec(cg, cp, plan.out_cell[i] / ROWS, plan.out_cell[i] % ROWS));
     __builtin_amdgcn_sched_barrier(0);
     const ShardView<true> sp(Pp, nb), sq(Qp, nb);
     u32x4 x[NC];
@@ -299,7 +324,7 @@ __global__ __launch_bounds__(kCBS) void chunk_rdp_decode_fixed(PagedGeom g, Chun
     for (int c = 0; c < NC; ++c) {
         if (!needed(c)) continue;
         const int s = c / ROWS, r = c % ROWS;
-        x[c] = s < K ? cell_load_ref(g, ref[c], inner) : (s == K ? sp : sq).load(r * cg.R, lane);
+        x[c] = s < K ? cell_load_ref(g, ref[c], inner) : (s == K ? sp : sq).load(row(r), lane);
     }
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
@@ -311,9 +336,9 @@ __global__ __launch_bounds__(kCBS) void chunk_rdp_decode_fixed(PagedGeom g, Chun
         const int c = plan.out_cell[i], s = c / ROWS, r = c % ROWS;
         if (s < K) {
             cell_store_ref(g, refo[i], inner, acc);
-            if (d.p[s]) st_stream(d.p[s] + uint64_t(r) * cg.R, lane, acc);
+            if (d.p[s]) st_stream(d.p[s] + uint64_t(row(r)), lane, acc);
         } else {
-            (s == K ? sp : sq).store(r * cg.R, lane, acc);
+            (s == K ? sp : sq).store(row(r), lane, acc);
         }
     }
 }
@@ -457,13 +482,19 @@ static int check_chunk(const kvec_paged_kv* kv, const kvec_chunk_stripe* st, Chu
     if (k < 1 || k > p - 1 || k > kChunkMaxK)
         return set_error(KVEC_EINVAL, "%s: k=%d not in [1, p-1]", fn, k);
     if (m < 0 || m > kChunkMaxM) return set_error(KVEC_EINVAL, "%s: m=%d not in [0, %d]", fn, m, kChunkMaxM);
-    const uint64_t R = uint64_t(st->row_bytes), W = uint64_t(st->width), off = uint64_t(st->col_off);
-    if (st->row_bytes <= 0 || st->width <= 0 || st->col_off < 0 || R % 16 || off % 16)
-        return set_error(KVEC_EINVAL, "%s: row_bytes/col_off must be multiples of 16, width > 0", fn);
+    const uint64_t R = uint64_t(st->row_bytes), W = uint64_t(st->width), off = uint64_t(st->region_off);
+    const uint64_t U = uint64_t(st->unit_bytes);
+    if (st->row_bytes <= 0 || st->width <= 0 || st->region_off < 0 || st->unit_bytes < 0 || R % 16 ||
+        off % 16)
+        return set_error(KVEC_EINVAL, "%s: row_bytes/region_off must be multiples of 16, width > 0", fn);
     if (W % a->g.rec)
         return set_error(KVEC_EINVAL, "%s: width=%llu must be a multiple of the record size %u", fn,
                          (unsigned long long)W, a->g.rec);
-    if (off + W > R) return set_error(KVEC_EINVAL, "%s: col_off + width > row_bytes", fn);
+    if (U % kRdpWaveBytes || U % a->g.rec)
+        return set_error(KVEC_EINVAL, "%s: unit_bytes=%llu must be 0 or a multiple of 1024 and of the "
+                         "record size %u", fn, (unsigned long long)U, a->g.rec);
+    if (off + uint64_t(p - 1) * W > uint64_t(p - 1) * R)
+        return set_error(KVEC_EINVAL, "%s: region_off + (p-1)*width > (p-1)*row_bytes", fn);
     if (!fits_buffer(uint64_t(p - 1) * R))
         return set_error(KVEC_EUNSUPPORTED, "%s: (p-1)*row_bytes must be < 4 GiB", fn);
     const uint64_t cells = uint64_t(k) * uint64_t(p - 1);
@@ -471,7 +502,7 @@ static int check_chunk(const kvec_paged_kv* kv, const kvec_chunk_stripe* st, Chu
         return set_error(KVEC_EINVAL, "%s: k*(p-1)*width=%llu < chunk stream bytes %llu", fn,
                          (unsigned long long)(cells * W),
                          (unsigned long long)(a->g.recs_total * a->g.rec));
-    if (cells * (W / a->g.rec) >= (uint64_t(1) << 32))
+    if (cells * (W / a->g.rec) >= (uint64_t(1) << 32) || a->g.recs_total * a->g.rec >= (uint64_t(1) << 32))
         return set_error(KVEC_EUNSUPPORTED, "%s: chunk too large for 32-bit record indices", fn);
     if (!st->P || !st->Q || !aligned16(st->P) || !aligned16(st->Q))
         return set_error(KVEC_EINVAL, "%s: P/Q null or not 16-byte aligned", fn);
@@ -492,15 +523,18 @@ static int check_chunk(const kvec_paged_kv* kv, const kvec_chunk_stripe* st, Chu
                 return set_error(KVEC_EINVAL, "%s: data[%d] null or not 16-byte aligned", fn, j);
             a->d.p[j] = (uint8_t*)st->data[j];
         }
-    a->cg.R = R;
-    a->cg.col_off = uint32_t(off);
-    a->cg.recs_per_cell = uint32_t(W / a->g.rec);
-    a->cg.nvec = uint32_t(W / 16);
+    a->cg.nb = uint64_t(p - 1) * R;
+    a->cg.region = uint32_t(off);
+    a->cg.recs_per_shard = uint32_t(uint64_t(p - 1) * W / a->g.rec);
+    a->cg.geo = make_rdp_geom(W, U);
+    a->cg.nwaves = uint32_t(rdp_waves(a->cg.geo));
     a->k = k;
     a->p = p;
     a->m = m;
     return KVEC_OK;
 }
+
+static dim3 chunk_grid(const ChunkGeom& cg) { return dim3(blocks_for(cg.nwaves, kCBS / 64)); }
 
 static int run_encode(const ChunkArgs& a, uint32_t wmask, hipStream_t st, const char* fn) {
     EncLauncher L = encode_launcher(a.p, a.k, a.m);
@@ -509,7 +543,7 @@ static int run_encode(const ChunkArgs& a, uint32_t wmask, hipStream_t st, const 
     cauchy(a.k, a.m, C);
     uint32_t tab[kChunkMaxK * kChunkMaxM][6];
     for (int i = 0; i < a.k * a.m; ++i) perm_tables(C[i], tab[i]);
-    L(dim3(blocks_for(a.cg.nvec, kCBS)), st, a.g, a.cg, a.d, a.par, tab, wmask);
+    L(chunk_grid(a.cg), st, a.g, a.cg, a.d, a.par, tab, wmask);
     return check_launch(fn);
 }
 
@@ -555,7 +589,7 @@ extern "C" int kvec_chunk_decode_paged(const kvec_paged_kv* kv, void* pool,
     for (int i = 0; i < m; ++i) nrs += er[k + 2 + i];
     const bool eP = er[k], eQ = er[k + 1];
     hipStream_t hs = as_stream(stream);
-    const dim3 grid(blocks_for(a.cg.nvec, kCBS));
+    const dim3 grid = chunk_grid(a.cg);
     uint32_t reenc = (eP ? kWP : 0u) | (eQ ? kWQ : 0u);
     if (nd > 0 && nd <= m - nrs) {
         // RS: data shards and RS parity, data first (index order k..k+m-1 for parity)

@@ -9,10 +9,10 @@ serving loop.
 Here the copies run on a side stream (default priority) into pinned host
 buffers, ordered after the encode through an event, so the next chunk's
 encode runs while the previous chunk's parity crosses PCIe.  A chunk's parity
-lives in its own columns of the whole-sequence stripes (``chunked``), so
-offloading chunk c never races with encoding chunk c+1; the host copy of each
-shard keeps the same [p-1, row_bytes] layout, so a restore is the same copies
-in the other direction.
+is one contiguous region of every parity shard (``chunked``), so offloading
+chunk c is one copy per shard and never races with encoding chunk c+1; the
+host copy of each shard has the shard's own layout, so a restore is the same
+copies in the other direction.
 """
 from __future__ import annotations
 
@@ -24,55 +24,51 @@ import torch
 class ParityOffload:
     """Pinned host mirrors of parity shards plus a copy stream.
 
-    ``shards`` are the device parity tensors (each ``rows * row_bytes`` bytes,
-    row-major [rows, row_bytes]); the host mirrors have the same shape.
+    ``shards`` are the device parity tensors (contiguous, equally sized); the
+    host mirrors are byte tensors of the same size.
     """
 
-    def __init__(self, shards: Sequence[torch.Tensor], rows: int, row_bytes: int):
+    def __init__(self, shards: Sequence[torch.Tensor]):
         if not shards:
             raise ValueError("no parity shards")
-        for t in shards:
-            if t.numel() * t.element_size() != rows * row_bytes or not t.is_contiguous():
-                raise ValueError("each parity shard must be a contiguous rows*row_bytes buffer")
+        sizes = {t.numel() * t.element_size() for t in shards}
+        if len(sizes) != 1 or not all(t.is_contiguous() for t in shards):
+            raise ValueError("parity shards must be contiguous and of one size")
         self.device = shards[0].device
-        self.rows, self.row_bytes = int(rows), int(row_bytes)
-        self.dev = [t.view(torch.uint8).view(rows, row_bytes) for t in shards]
-        self.host = [torch.empty((rows, row_bytes), dtype=torch.uint8, pin_memory=True)
-                     for _ in shards]
+        self.nbytes = sizes.pop()
+        self.dev = [t.view(torch.uint8).view(-1) for t in shards]
+        self.host = [torch.empty(self.nbytes, dtype=torch.uint8, pin_memory=True) for _ in shards]
         self.stream = torch.cuda.Stream(device=self.device)
 
-    def _copy(self, col_off: int, width: int, to_host: bool, after: torch.cuda.Event | None):
-        if col_off < 0 or width <= 0 or col_off + width > self.row_bytes:
-            raise ValueError("column range outside the row planes")
+    def _copy(self, off: int, nbytes: int, to_host: bool, after: torch.cuda.Event):
+        if off < 0 or nbytes <= 0 or off + nbytes > self.nbytes:
+            raise ValueError("byte range outside the parity shards")
         done = torch.cuda.Event()
         with torch.cuda.stream(self.stream):
-            if after is not None:
-                self.stream.wait_event(after)
+            self.stream.wait_event(after)
             for d, h in zip(self.dev, self.host):
-                for r in range(self.rows):
-                    src, dst = (d, h) if to_host else (h, d)
-                    dst[r, col_off:col_off + width].copy_(src[r, col_off:col_off + width],
-                                                          non_blocking=True)
+                src, dst = (d, h) if to_host else (h, d)
+                dst[off:off + nbytes].copy_(src[off:off + nbytes], non_blocking=True)
             done.record(self.stream)
         return done
 
-    def to_host(self, col_off: int, width: int) -> torch.cuda.Event:
-        """Copy columns [col_off, col_off+width) of every parity row plane to
-        the host mirrors, after the work already queued on the current stream.
-        Returns the event that marks the copies done."""
+    def to_host(self, off: int, nbytes: int) -> torch.cuda.Event:
+        """Copy bytes [off, off+nbytes) of every parity shard (a chunk's
+        region) to the host mirrors, after the work already queued on the
+        current stream.  Returns the event that marks the copies done."""
         ready = torch.cuda.Event()
         ready.record(torch.cuda.current_stream(self.device))
-        return self._copy(col_off, width, True, ready)
+        return self._copy(off, nbytes, True, ready)
 
-    def to_device(self, col_off: int, width: int) -> torch.cuda.Event:
-        """Restore those columns from the host mirrors (e.g. after the device
+    def to_device(self, off: int, nbytes: int) -> torch.cuda.Event:
+        """Restore those bytes from the host mirrors (e.g. after the device
         copy of the parity was lost).  The copies start after the work already
         queued on the current stream (an encode or decode that still reads or
-        writes those columns), and the current stream is made to wait for
+        writes those bytes), and the current stream is made to wait for
         them."""
         cur = torch.cuda.current_stream(self.device)
         ready = torch.cuda.Event()
         ready.record(cur)
-        done = self._copy(col_off, width, False, ready)
+        done = self._copy(off, nbytes, False, ready)
         cur.wait_event(done)
         return done

@@ -32,6 +32,15 @@ from . import _lib
 RDP_UNIT = 65536
 
 
+def rdp_unit_for(record_bytes: int = 16) -> int:
+    """The stripe unit for streams of ``record_bytes`` records: the largest
+    common multiple of 1024 and the record size up to RDP_UNIT (or that
+    common multiple itself when it is larger)."""
+    import math
+    lcm = 1024 * int(record_bytes) // math.gcd(1024, int(record_bytes))
+    return max(lcm, RDP_UNIT // lcm * lcm)
+
+
 def _nbytes(t: torch.Tensor) -> int:
     return t.numel() * t.element_size()
 

@@ -388,10 +388,10 @@ def bench_chunked(pkg, torch, oracle, dev, seed, warmup):
     encodings, per-layer fp32 scale carried alongside) in a pool of 16-token
     pages behind a seeded shuffled page table, arriving as 16 chunks of 2048
     tokens.  Each chunk is coded once, straight from the pool, with RDP p=7 and
-    RS(5,3) sharing 5 data shards, into its columns of the whole-sequence
-    stripes.  Every chunk's parity is checked against the oracle's
-    whole-sequence encode at full size; decode of lost data shards back into
-    the pool is byte-compared at full size."""
+    RS(5,3) sharing 5 data shards, into its own region of the whole-sequence
+    stripes (RDP stripes of 64 KiB rows).  Every chunk's parity is checked
+    against the oracle's whole-sequence encode at full size; decode of lost
+    data shards back into the pool is byte-compared at full size."""
     import numpy as np
     CL, CB, CT, NCH, page_tokens = 32, 16, 32768, 16, 16
     ct = CT // NCH
@@ -411,8 +411,8 @@ def bench_chunked(pkg, torch, oracle, dev, seed, warmup):
     chunk_bytes = kvs[0].stream_bytes()
     st = pkg.chunked.ChunkedStripes(chunk_bytes, 2 * kvs[0].token_bytes, NCH, dev, k=k, p=p, m=m,
                                     keep_data=False, scales=scales)
-    W, R = st.width, st.row_bytes
-    parity_w = (2 + m) * (p - 1) * W
+    W, R, nr, U = st.width, st.row_bytes, st.region_bytes, st.unit_bytes
+    parity_w = (2 + m) * nr
     alg = chunk_bytes + parity_w
     stream = torch.cuda.current_stream()
 
@@ -422,7 +422,7 @@ def bench_chunked(pkg, torch, oracle, dev, seed, warmup):
     # every chunk's parity against the oracle's whole-sequence encode
     pool_h = host(pool).reshape(CL, npages, page_tokens, 2, -1)
     wW, _, Pw, Qw, rsw = oracle.chunked_encode(pool_h, table.cpu().numpy(), page_tokens, ct, NCH,
-                                               k, p, m)
+                                               k, p, m, U)
     del pool_h
     if wW != W:
         raise RuntimeError("chunk width differs from the oracle's")
@@ -452,13 +452,13 @@ def bench_chunked(pkg, torch, oracle, dev, seed, warmup):
     # chunk's encode: the 16 chunks pipelined (which also touches every host
     # page once), then one chunk's copies alone
     par = [st.P, st.Q] + list(st.rs)
-    off = pkg.offload.ParityOffload(par, p - 1, R)
+    off = pkg.offload.ParityOffload(par)
     torch.cuda.synchronize()
     tp = time.perf_counter()
     evs_off = []
     for c in range(NCH):
         st.encode(kvs[c], c)
-        evs_off.append(off.to_host(c * W, W))
+        evs_off.append(off.to_host(st.region(c), nr))
     for e in evs_off:
         e.synchronize()
     torch.cuda.synchronize()
@@ -466,7 +466,7 @@ def bench_chunked(pkg, torch, oracle, dev, seed, warmup):
     t1 = torch.cuda.Event(enable_timing=True)
     t2 = torch.cuda.Event(enable_timing=True)
     t1.record(off.stream)
-    off.to_host(W, W)
+    off.to_host(st.region(1), nr)
     t2.record(off.stream)
     t2.synchronize()
     d2h_ms = t1.elapsed_time(t2)
@@ -489,13 +489,11 @@ def bench_chunked(pkg, torch, oracle, dev, seed, warmup):
         sbytes = kvc.gather()
         for e in er:
             if e < k:
-                for r in range(p - 1):
-                    lo = (e * (p - 1) + r) * W
-                    hi = min(lo + W, sbytes.numel())
-                    if lo < hi:
-                        sbytes[lo:hi] = 0
+                lo, hi = e * nr, min((e + 1) * nr, sbytes.numel())
+                if lo < hi:
+                    sbytes[lo:hi] = 0
             else:
-                st.shards()[e - k].view(p - 1, R)[:, c * W:(c + 1) * W] = 0
+                st.shards()[e - k][st.region(c):st.region(c) + nr] = 0
         kvc.scatter(sbytes)
         del sbytes
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -510,12 +508,12 @@ def bench_chunked(pkg, torch, oracle, dev, seed, warmup):
         dec[name] = round(e0.elapsed_time(e1) * 1e3, 2)
         del ref, ref_sh
     cpu_case = (host(pool).reshape(CL, npages, page_tokens, 2, -1), table.cpu().numpy(), page_tokens,
-                ct, k, p, m, W)
+                ct, k, p, m, W, U)
     del st, pool, kvs
     return {
         "workload": "chunked_fp8_rdp_p7_k5_rs_k5m3_16x32768tok_16chunks",
         "chunk_tokens": ct, "chunks": NCH, "chunk_stream_bytes": chunk_bytes,
-        "width": W, "row_bytes": R, "byte_exact_full": True,
+        "width": W, "row_bytes": R, "unit_bytes": U, "region_bytes": nr, "byte_exact_full": True,
         "alg_bytes_per_chunk": alg,
         "encode_us_per_chunk": round(enc_us, 2),
         "encode_gbs": gbs(alg, enc_us),
@@ -874,17 +872,18 @@ def cpu_baselines(oracle, c1_host, R, rs8_host, chunk_case, budget_s):
     import numpy as np
     all_cores = oracle.num_threads()
     out = {"cpu_model": cpu_model(), "cores": all_cores, "kind": "port"}
-    v, n, t = _rate(lambda: oracle.rdp_encode(c1_host, P_RDP, unit=UNIT), ALG_BYTES, budget_s)
+    par = (np.zeros_like(c1_host[0]), np.zeros_like(c1_host[0]))    # written in place
+    v, n, t = _rate(lambda: oracle.rdp_encode(c1_host, P_RDP, unit=UNIT, out=par), ALG_BYTES, budget_s)
     out["c1_rdp_encode"] = {"gbs": round(v, 3), "threads": all_cores, "runs": n}
     main = {"value": round(v, 3), "unit": "GB/s", "cores": all_cores, "kind": "port",
             "sample": f"oracle RDP p=7 k=6 encode (64 KiB stripe rows) of the full 512 MiB chunk "
                       f"stripe set, {n} runs in {t:.1f} s (C, OpenMP over stripe columns)"}
     oracle.set_num_threads(1)
-    v1, n1, _ = _rate(lambda: oracle.rdp_encode(c1_host, P_RDP, unit=UNIT), ALG_BYTES, budget_s / 2)
+    v1, n1, _ = _rate(lambda: oracle.rdp_encode(c1_host, P_RDP, unit=UNIT, out=par), ALG_BYTES,
+                      budget_s / 2)
     out["c1_rdp_encode_1core"] = {"gbs": round(v1, 3), "threads": 1, "runs": n1}
     oracle.set_num_threads(all_cores)
-    Pw, Qw = oracle.rdp_encode(c1_host, P_RDP, unit=UNIT)
-    full = list(c1_host) + [Pw, Qw]
+    full = list(c1_host) + list(par)
     pairs = list(itertools.combinations(range(K_RDP + 2), 2))
     it = iter(itertools.cycle(pairs))
 
@@ -896,18 +895,19 @@ def cpu_baselines(oracle, c1_host, R, rs8_host, chunk_case, budget_s):
     out["c2_rdp_decode_pairs"] = {"gbs": round(v, 3), "threads": all_cores, "runs": n}
     del full
     if rs8_host is not None:
-        v, n, _ = _rate(lambda: oracle.rs8_encode(rs8_host, 2), ALG_BYTES, budget_s / 2)
+        rpar = [np.zeros_like(rs8_host[0]) for _ in range(2)]
+        v, n, _ = _rate(lambda: oracle.rs8_encode(rs8_host, 2, out=rpar), ALG_BYTES, budget_s / 2)
         out["c3_rs8_encode"] = {"gbs": round(v, 3), "threads": all_cores, "runs": n}
     if chunk_case is not None:
-        pool_h, table, page_tokens, ct, k, p, m, W = chunk_case
-        alg = 0
+        pool_h, table, page_tokens, ct, k, p, m, W, U = chunk_case
+        cpar = [np.zeros((p - 1) * W, np.uint8) for _ in range(2 + m)]
 
         def one_chunk():
             s = oracle.kv_gather(pool_h, table, page_tokens, 5 * ct, ct)
             cells = oracle.chunk_cells(s, k, p, W)
-            data = [np.ascontiguousarray(cells[j]) for j in range(k)]
-            oracle.rdp_encode(data, p)
-            oracle.rs8_encode([d.reshape(-1) for d in data], m)
+            data = [cells[j] for j in range(k)]
+            oracle.rdp_encode(data, p, U, out=(cpar[0], cpar[1]))
+            oracle.rs8_encode(data, m, out=cpar[2:])
             return s.size
 
         sb = one_chunk()

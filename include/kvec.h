@@ -152,12 +152,14 @@ int kvec_rdp_decode_paged(const kvec_paged_kv* kv, void* pool, void* const* data
  *
  * A whole-sequence stripe set is k data shards (optional: NULL data means the
  * pool is the only copy of the data), P, Q and m RS parity shards, each
- * (p-1)*row_bytes bytes: p-1 row planes of row_bytes.  Chunk c's stream (the
- * kvec_paged_kv chunk) is cut into k*(p-1) cells of `width` bytes; cell (shard
- * j, row r) = stream bytes [(j*(p-1) + r)*width, +width), zero padded, placed at
- * columns [col_off, col_off + width) of row plane r of shard j.  Every code is
- * column-wise, so encoding chunk c writes only its own columns, reads no parity,
- * and the per-chunk encodes together equal the encode of the whole stripe set.
+ * (p-1)*row_bytes bytes.  Chunk c owns the region of (p-1)*width bytes at
+ * region_off of every shard (c*(p-1)*width for chunks in order), which is an
+ * RDP stripe set in the striped geometry of kvec_rdp_encode with rows of
+ * `width` bytes and unit `unit_bytes`.  The chunk's stream (the kvec_paged_kv
+ * chunk), zero padded to k*(p-1)*width bytes, is cut into k pieces of
+ * (p-1)*width bytes, piece j being data shard j's region.  Every code works on
+ * its own stripe instances, so encoding chunk c writes only its own region,
+ * reads no parity, and the per-chunk encodes together code the whole set.
  * Built: p in {3, 5, 7}, 2 <= k <= p-1, 0 <= m <= 3 (decode: k <= 6). */
 typedef struct kvec_chunk_stripe {
     void* const* data;  /* host array of k device pointers, or NULL */
@@ -167,19 +169,21 @@ typedef struct kvec_chunk_stripe {
     int p;
     void* const* rs;    /* host array of m device pointers (RS parity 0..m-1) */
     int m;
-    int64_t row_bytes;  /* R, multiple of 16; (p-1)*R < 4 GiB */
-    int64_t col_off;    /* this chunk's first column, multiple of 16 */
-    int64_t width;      /* this chunk's columns, a multiple of 2*token_bytes */
+    int64_t row_bytes;  /* R: every shard is (p-1)*R bytes, < 4 GiB; R % 16 == 0 */
+    int64_t region_off; /* this chunk's region in every shard, multiple of 16 */
+    int64_t width;      /* the region's row bytes, a multiple of 2*token_bytes */
+    int64_t unit_bytes; /* stripe unit of the region: 0 or a multiple of 1024 and of
+                           2*token_bytes (65536 is the fastest) */
 } kvec_chunk_stripe;
 
 /* Smallest cell width (multiple of record_bytes) whose k*(p-1) cells hold
  * chunk_stream_bytes bytes.  Host-only arithmetic; -1 on bad arguments. */
 int64_t kvec_chunk_width(int64_t chunk_stream_bytes, int k, int p, int64_t record_bytes);
 /* One pass over the chunk's pool pages: data shards (if given), P, Q and the
- * RS parity at the chunk's columns. */
+ * RS parity in the chunk's region. */
 int kvec_chunk_encode_paged(const kvec_paged_kv* kv, const kvec_chunk_stripe* stripe,
                             void* stream);
-/* Rebuild the chunk's columns of the erased shards.  erased: host int32 array of
+/* Rebuild the chunk's region of the erased shards.  erased: host int32 array of
  * shard indices, data 0..k-1, P = k, Q = k+1, RS parity i = k+2+i.  Lost data
  * cells are written into the pool pages (pool == kv->pool; surviving data is
  * read from the pool) and into the data shards when given; lost parity shards

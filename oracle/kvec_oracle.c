@@ -401,30 +401,34 @@ static inline void xor_into(uint8_t* restrict dst, const uint8_t* restrict src, 
  * the row parity P and Q[d] is the XOR of diagonal d = (row + col) mod p over
  * columns 0..p-1, for d = 0..p-2 (diagonal p-1 is not stored).  Each byte
  * offset of a row plane is an independent RDP instance. */
+/* Columns [o0, o0 + n) of one stripe whose p-1 rows are R bytes apart. */
+static void rdp_encode_cols(const uint8_t* const* data, int k, uint8_t* P, uint8_t* Q, int p,
+                            int64_t R, int64_t o0, int64_t n) {
+    const int rows = p - 1;
+    for (int r = 0; r < rows; ++r) {
+        memset(P + r * R + o0, 0, (size_t)n);
+        memset(Q + r * R + o0, 0, (size_t)n);
+    }
+    for (int j = 0; j < k; ++j)
+        for (int r = 0; r < rows; ++r) {
+            const uint8_t* src = data[j] + r * R + o0;
+            xor_into(P + r * R + o0, src, n);
+            const int d = (r + j) % p;
+            if (d != p - 1) xor_into(Q + d * R + o0, src, n);
+        }
+    for (int r = 0; r < rows; ++r) {
+        const int d = (r + p - 1) % p;
+        if (d != p - 1) xor_into(Q + d * R + o0, P + r * R + o0, n);
+    }
+}
+
 int kvo_rdp_encode(const uint8_t* const* data, int k, uint8_t* P, uint8_t* Q, int p,
                    int64_t R) {
     if (!is_prime(p) || p < 3 || k < 1 || k > p - 1 || R < 0) return -1;
-    const int rows = p - 1;
     const int64_t BLK = 1 << 14;
 #pragma omp parallel for schedule(static)
-    for (int64_t o0 = 0; o0 < R; o0 += BLK) {
-        const int64_t n = (R - o0 < BLK) ? R - o0 : BLK;
-        for (int r = 0; r < rows; ++r) {
-            memset(P + r * R + o0, 0, (size_t)n);
-            memset(Q + r * R + o0, 0, (size_t)n);
-        }
-        for (int j = 0; j < k; ++j)
-            for (int r = 0; r < rows; ++r) {
-                const uint8_t* src = data[j] + r * R + o0;
-                xor_into(P + r * R + o0, src, n);
-                const int d = (r + j) % p;
-                if (d != p - 1) xor_into(Q + d * R + o0, src, n);
-            }
-        for (int r = 0; r < rows; ++r) {
-            const int d = (r + p - 1) % p;
-            if (d != p - 1) xor_into(Q + d * R + o0, P + r * R + o0, n);
-        }
-    }
+    for (int64_t o0 = 0; o0 < R; o0 += BLK)
+        rdp_encode_cols(data, k, P, Q, p, R, o0, (R - o0 < BLK) ? R - o0 : BLK);
     return 0;
 }
 
@@ -506,14 +510,16 @@ int kvo_rdp_decode(uint8_t* const* cols, int k, int p, int64_t R, int e0, int e1
 int kvo_rdp_encode_striped(const uint8_t* const* data, int k, uint8_t* P, uint8_t* Q, int p,
                            int64_t R, int64_t U) {
     if (U <= 0 || U >= R) return kvo_rdp_encode(data, k, P, Q, p, R);
-    if (k < 1 || k > KVO_MAX_STRIPE_SHARDS) return -1;
+    if (!is_prime(p) || p < 3 || k < 1 || k > p - 1 || k > KVO_MAX_STRIPE_SHARDS) return -1;
     const int rows = p - 1;
-    for (int64_t s = 0; s * U < R; ++s) {
+    const int64_t ns = (R + U - 1) / U;
+    /* stripes are independent codes: one per thread at a time */
+#pragma omp parallel for schedule(static)
+    for (int64_t s = 0; s < ns; ++s) {
         const int64_t base = s * rows * U, g = (R - s * U < U) ? R - s * U : U;
         const uint8_t* d[KVO_MAX_STRIPE_SHARDS];
         for (int j = 0; j < k; ++j) d[j] = data[j] + base;
-        int rc = kvo_rdp_encode(d, k, P + base, Q + base, p, g);
-        if (rc) return rc;
+        rdp_encode_cols(d, k, P + base, Q + base, p, g, 0, g);
     }
     return 0;
 }
@@ -523,14 +529,16 @@ int kvo_rdp_decode_striped(uint8_t* const* cols, int k, int p, int64_t R, int64_
     if (U <= 0 || U >= R) return kvo_rdp_decode(cols, k, p, R, e0, e1);
     if (k < 1 || k + 2 > KVO_MAX_STRIPE_SHARDS) return -1;
     const int rows = p - 1;
-    for (int64_t s = 0; s * U < R; ++s) {
+    const int64_t ns = (R + U - 1) / U;
+    int rc = 0;
+#pragma omp parallel for schedule(static) reduction(|: rc)
+    for (int64_t s = 0; s < ns; ++s) {
         const int64_t base = s * rows * U, g = (R - s * U < U) ? R - s * U : U;
         uint8_t* c[KVO_MAX_STRIPE_SHARDS];
         for (int j = 0; j < k + 2; ++j) c[j] = cols[j] + base;
-        int rc = kvo_rdp_decode(c, k, p, g, e0, e1);
-        if (rc) return rc;
+        rc |= kvo_rdp_decode(c, k, p, g, e0, e1) != 0;
     }
-    return 0;
+    return rc ? -3 : 0;
 }
 
 /* ======================================================================== */

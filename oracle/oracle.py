@@ -211,15 +211,18 @@ def rs16_reconstruct(shards, S, k, m, missing_data, parity_used, ex, lg):
 
 
 # ----------------------------- spec: RDP -----------------------------
-def rdp_encode(data, p: int, unit: int = 0):
+def rdp_encode(data, p: int, unit: int = 0, out=None):
     """data: list of k shard arrays of (p-1)*R bytes (shaped [(p-1), R] or
     flat).  unit = 0: p-1 row planes of R bytes; else stripes of (p-1)*unit
     bytes (rows of min(unit, R - s*unit) bytes).  Returns (P, Q) shaped like
-    data[0]."""
+    data[0], written into ``out`` = (P, Q) when given."""
     k = len(data)
     R = data[0].size // (p - 1)
-    P_ = np.zeros(data[0].shape, np.uint8)
-    Q_ = np.zeros(data[0].shape, np.uint8)
+    if out is None:
+        P_ = np.zeros(data[0].shape, np.uint8)
+        Q_ = np.zeros(data[0].shape, np.uint8)
+    else:
+        P_, Q_ = out
     _check(lib().kvo_rdp_encode_striped(_ptrs(data), k, _p(P_), _p(Q_), p, R, int(unit)),
            "rdp_encode")
     return P_, Q_
@@ -234,10 +237,10 @@ def rdp_decode(cols, p: int, e0: int, e1: int = -1, unit: int = 0):
 
 
 # ----------------------------- spec: RS8 -----------------------------
-def rs8_encode(data, m: int):
+def rs8_encode(data, m: int, out=None):
     k = len(data)
     S = data[0].size
-    par = [np.zeros(S, np.uint8) for _ in range(m)]
+    par = [np.zeros(S, np.uint8) for _ in range(m)] if out is None else out
     _check(lib().kvo_rs8_encode(_ptrs(data), k, _ptrs(par), m, S), "rs8_encode")
     return par
 
@@ -276,32 +279,38 @@ def chunk_width(chunk_stream_bytes: int, k: int, p: int, record_bytes: int) -> i
 
 
 def chunk_cells(stream: np.ndarray, k: int, p: int, width: int) -> np.ndarray:
-    """One chunk's stream cut into cells [k, p-1, width], zero padded."""
+    """One chunk's stream, zero padded to k*(p-1)*width bytes, as its k data
+    shard pieces [k, (p-1)*width]."""
     flat = np.zeros(k * (p - 1) * width, np.uint8)
     flat[: stream.size] = stream.reshape(-1)
-    return flat.reshape(k, p - 1, width)
+    return flat.reshape(k, (p - 1) * width)
 
 
 def chunked_encode(pool: np.ndarray, page_table: np.ndarray, page_tokens: int,
-                   chunk_tokens: int, n_chunks: int, k: int, p: int, m: int):
+                   chunk_tokens: int, n_chunks: int, k: int, p: int, m: int, unit: int = 0):
     """Whole-sequence stripes of a paged pool coded chunk by chunk.
 
-    Chunk c (positions c*chunk_tokens.. of every sequence) is gathered, cut
-    into cells and placed at columns [c*width, (c+1)*width) of every row plane;
-    P, Q (RDP p) and the m RS parities are then the codes of the assembled data
-    shards.  Returns (width, data [k x (p-1, R)], P, Q, rs [m x (p-1, R)])."""
+    Chunk c (positions c*chunk_tokens.. of every sequence) is gathered, zero
+    padded and cut into k pieces of (p-1)*width bytes; piece j is data shard
+    j's region c, at byte c*(p-1)*width.  Each region is its own RDP stripe set
+    (rows of width bytes, stripe unit ``unit``), coded with RDP(p) and the m RS
+    parities.  Returns (width, data [k flat shards], P, Q, rs [m flat shards])."""
     tb = pool.shape[-1]
     rec = 2 * tb
     L = pool.shape[0]
     B = page_table.shape[0]
     width = chunk_width(L * B * chunk_tokens * rec, k, p, rec)
-    R = n_chunks * width
-    data = [np.zeros((p - 1, R), np.uint8) for _ in range(k)]
+    n = (p - 1) * width
+    data = [np.zeros(n_chunks * n, np.uint8) for _ in range(k)]
+    P_ = np.zeros(n_chunks * n, np.uint8)
+    Q_ = np.zeros(n_chunks * n, np.uint8)
+    rs = [np.zeros(n_chunks * n, np.uint8) for _ in range(m)]
     for c in range(n_chunks):
         s = kv_gather(pool, page_table, page_tokens, c * chunk_tokens, chunk_tokens)
         cells = chunk_cells(s, k, p, width)
+        reg = slice(c * n, (c + 1) * n)
         for j in range(k):
-            data[j][:, c * width:(c + 1) * width] = cells[j]
-    P_, Q_ = rdp_encode(data, p)
-    rs = [x.reshape(p - 1, R) for x in rs8_encode([d.reshape(-1) for d in data], m)]
+            data[j][reg] = cells[j]
+        rdp_encode([d[reg] for d in data], p, unit, out=(P_[reg], Q_[reg]))
+        rs8_encode([d[reg] for d in data], m, out=[x[reg] for x in rs])
     return width, data, P_, Q_, rs

@@ -81,11 +81,17 @@ def main():
     pool = u8(rng, L, npages, pt, 2, tb)
     table = rng.permutation(npages)[: B * pps].astype(np.int32).reshape(B, pps)
     stream = ora.kv_gather(pool, table, pt, 3, 9)
-    W, cdata, cP, cQ, crs = ora.chunked_encode(pool, table, pt, 8, 2, 5, 7, 3)
     out["paged"] = dict(pool=pool, table=table, page_tokens=pt, tok_off=3, tokens=9,
                         stream=stream)
-    out["chunked"] = dict(pool=pool, table=table, page_tokens=pt, chunk_tokens=8, n_chunks=2,
-                          width=W, data=np.stack(cdata), P=cP, Q=cQ, rs=np.stack(crs))
+    # chunked: 256-byte records, 32-token chunks -> rows of 1280 bytes, so each
+    # chunk region holds two stripes of the 1024-byte unit (rows 1024 and 256)
+    L, B, pps, pt, tb, unit = 2, 2, 4, 16, 128, 1024
+    npages = B * pps + 1
+    cpool = u8(rng, L, npages, pt, 2, tb)
+    ctable = rng.permutation(npages)[: B * pps].astype(np.int32).reshape(B, pps)
+    W, cdata, cP, cQ, crs = ora.chunked_encode(cpool, ctable, pt, 32, 2, 5, 7, 3, unit)
+    out["chunked"] = dict(pool=cpool, table=ctable, page_tokens=pt, chunk_tokens=32, n_chunks=2,
+                          unit=unit, width=W, data=np.stack(cdata), P=cP, Q=cQ, rs=np.stack(crs))
 
     for name, arrs in out.items():
         np.savez_compressed(os.path.join(HERE, f"{name}.npz"),

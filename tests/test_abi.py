@@ -159,10 +159,10 @@ def test_chunk_rejects_bad_arguments(pkg):
 
     def stripe(**kw):
         a = dict(data=None, k=5, P=4096, Q=8192, p=7, rs=C.cast(rs, C.POINTER(C.c_void_p)),
-                 m=3, row_bytes=1 << 20, col_off=0, width=256 * 64)
+                 m=3, row_bytes=1 << 20, region_off=0, width=256 * 64, unit_bytes=65536)
         a.update(kw)
         return lib.ChunkStripe(a["data"], a["k"], a["P"], a["Q"], a["p"], a["rs"], a["m"],
-                               a["row_bytes"], a["col_off"], a["width"])
+                               a["row_bytes"], a["region_off"], a["width"], a["unit_bytes"])
 
     def rc(**kw):
         return L.kvec_chunk_encode_paged(C.byref(kv), C.byref(stripe(**kw)), None)
@@ -170,8 +170,11 @@ def test_chunk_rejects_bad_arguments(pkg):
     assert rc(p=9) == -1                       # not prime
     assert rc(k=7) == -1                       # k > p-1
     assert rc(width=250) == -1                 # not a record multiple
-    assert rc(col_off=8) == -1                 # misaligned column
-    assert rc(col_off=(1 << 20) - 256) == -1   # past the row plane
+    assert rc(region_off=8) == -1              # misaligned region
+    assert rc(region_off=6 * (1 << 20) - 256) == -1   # region past the shard
+    assert b"region_off" in L.kvec_last_error()
+    assert rc(unit_bytes=1536) == -1           # a record multiple, not a 1 KiB one
+    assert rc(unit_bytes=-1024) == -1
     assert rc(width=256) == -1                 # cells too small for the chunk
     assert b"k*(p-1)*width" in L.kvec_last_error()
     assert rc(P=4100) == -1                    # misaligned parity

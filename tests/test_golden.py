@@ -70,7 +70,8 @@ def test_oracle_reproduces_paged_and_chunked(ora):
     assert np.array_equal(s, g["stream"])
     c = load("chunked")
     W, data, P, Q, rs = ora.chunked_encode(c["pool"], c["table"], int(c["page_tokens"]),
-                                           int(c["chunk_tokens"]), int(c["n_chunks"]), 5, 7, 3)
+                                           int(c["chunk_tokens"]), int(c["n_chunks"]), 5, 7, 3,
+                                           int(c["unit"]))
     assert W == int(c["width"])
     assert np.array_equal(np.stack(data), c["data"])
     assert np.array_equal(P, c["P"]) and np.array_equal(Q, c["Q"])
@@ -164,12 +165,11 @@ def test_gpu_paged_and_chunked_golden(pkg, gpu):
     ct, nc = int(c["chunk_tokens"]), int(c["n_chunks"])
     kv0 = pkg.chunked.chunk_kv(pool, table, 0, ct)
     st = pkg.chunked.ChunkedStripes(kv0.stream_bytes(), 2 * kv0.token_bytes, nc, gpu, k=5, p=7,
-                                    m=3, keep_data=True)
+                                    m=3, keep_data=True, unit_bytes=int(c["unit"]))
     assert st.width == int(c["width"])
     for ci in range(nc):
         st.encode(pkg.chunked.chunk_kv(pool, table, ci, ct), ci)
-    R = st.row_bytes
-    got = lambda t: t.view(6, R).cpu().numpy()  # noqa: E731
+    got = lambda t: t.cpu().numpy()  # noqa: E731
     assert np.array_equal(np.stack([got(t) for t in st.data]), c["data"])
     assert np.array_equal(got(st.P), c["P"]) and np.array_equal(got(st.Q), c["Q"])
     assert np.array_equal(np.stack([got(t) for t in st.rs]), c["rs"])

@@ -51,21 +51,20 @@ def test_chunked_encode_matches_oracle(pkg, ora, gpu, cfg, keep_data):
     L, B, pps, pt, H, D, k, p, m, ct = cfg
     pool, table, pool_d, table_d, nc, st = setup(pkg, gpu, L, B, pps, pt, H, D, k, p, m, ct,
                                                  keep_data, seed=sum(cfg))
-    W, data, P, Q, rs = ora.chunked_encode(pool_u8(pool), table.numpy(), pt, ct, nc, k, p, m)
+    W, data, P, Q, rs = ora.chunked_encode(pool_u8(pool), table.numpy(), pt, ct, nc, k, p, m,
+                                           st.unit_bytes)
     assert st.width == W and st.row_bytes == nc * W
     sentinel = 0xA5
     for t in st.shards():
         t.fill_(sentinel)
-    R = st.row_bytes
     for c in range(nc):
         st.encode(pkg.chunked.chunk_kv(pool_d, table_d, c, ct), c)
         torch.cuda.synchronize()
-        # chunk c wrote exactly its own columns
-        later = slice((c + 1) * W, R)
+        # chunk c wrote exactly its own region
+        later = st.region(c + 1)
         for t in st.shards():
-            v = t.view(p - 1, R)
-            assert bool((v[:, later] == sentinel).all()), f"chunk {c} wrote past its columns"
-    got = [t.view(p - 1, R).cpu().numpy() for t in st.shards()]
+            assert bool((t[later:] == sentinel).all()), f"chunk {c} wrote past its region"
+    got = [t.cpu().numpy() for t in st.shards()]
     want = (data if keep_data else []) + [P, Q] + rs
     names = ([f"data{j}" for j in range(k)] if keep_data else []) + ["P", "Q"] + \
         [f"rs{i}" for i in range(m)]
@@ -75,27 +74,25 @@ def test_chunked_encode_matches_oracle(pkg, ora, gpu, cfg, keep_data):
 
 
 def erase(pkg, st, kv, c, erased, gen):
-    """Overwrite chunk c's cells of the erased shards: data in the pool pages
-    (through the stream and the scatter), parity in its columns.  Returns
-    whether a pool byte was overwritten (cells past the stream are padding)."""
-    k, p, W, R = st.k, st.p, st.width, st.row_bytes
+    """Overwrite chunk c's region of the erased shards: data in the pool pages
+    (through the stream and the scatter), parity in its region.  Returns
+    whether a pool byte was overwritten (bytes past the stream are padding)."""
+    k, nr = st.k, st.region_bytes
+    reg = slice(st.region(c), st.region(c) + nr)
     s = kv.gather()
     n = s.numel()
     touched = False
     for e in erased:
         if e < k:
-            for r in range(p - 1):
-                lo = (e * (p - 1) + r) * W
-                hi = min(lo + W, n)
-                if lo < n:
-                    touched = True
-                    s[lo:hi] = torch.randint(0, 256, (hi - lo,), generator=gen,
-                                             dtype=torch.uint8).to(s.device)
+            lo, hi = e * nr, min((e + 1) * nr, n)
+            if lo < n:
+                touched = True
+                s[lo:hi] = torch.randint(0, 256, (hi - lo,), generator=gen,
+                                         dtype=torch.uint8).to(s.device)
             if st.data is not None:
-                st.data[e].view(p - 1, R)[:, c * W:(c + 1) * W] = 0x3C
+                st.data[e][reg] = 0x3C
         else:
-            st.shards()[(k if st.data is not None else 0) + e - k] \
-                .view(p - 1, R)[:, c * W:(c + 1) * W] = 0x5A
+            st.shards()[(k if st.data is not None else 0) + e - k][reg] = 0x5A
     kv.scatter(s)
     return touched
 
@@ -166,7 +163,7 @@ def test_chunked_decode_other_shapes(pkg, gpu, cfg):
 
 def test_chunked_encode_repeatable_at_scale(pkg, ora, gpu):
     """A 64 MiB fp8 chunk (about 1,100 blocks): encoding it twice gives the same
-    bytes, which match the oracle on sampled stripe columns."""
+    bytes, which match the oracle at full size."""
     L, B, pps, pt, H, D, k, p, m, ct = 8, 16, 128, 16, 1, 128, 5, 7, 3, 2048
     pool, table, pool_d, table_d, nc, st = setup(pkg, gpu, L, B, pps, pt, H, D, k, p, m, ct,
                                                  False, seed=21)
@@ -178,15 +175,12 @@ def test_chunked_encode_repeatable_at_scale(pkg, ora, gpu):
         torch.cuda.synchronize()
         for i, (a, b) in enumerate(zip(st.shards(), first)):
             assert torch.equal(a, b), f"shard {i} differs between two encodes"
-    W, R = st.width, st.row_bytes
-    s = kv.gather().cpu().numpy()
-    cells = ora.chunk_cells(s, k, p, W)
-    rng = np.random.default_rng(5)
-    cols = (np.sort(rng.choice(W // 16, 512, replace=False))[:, None] * 16 + np.arange(16)).reshape(-1)
-    sub = [np.ascontiguousarray(cells[j][:, cols]) for j in range(k)]
-    Pw, Qw = ora.rdp_encode(sub, p)
-    rsw = ora.rs8_encode([x.reshape(-1) for x in sub], m)
-    got = [t.view(p - 1, R)[:, torch.from_numpy(cols).to(gpu)].cpu().numpy() for t in st.shards()]
+    W, nr = st.width, st.region_bytes
+    cells = ora.chunk_cells(kv.gather().cpu().numpy(), k, p, W)
+    data = [np.ascontiguousarray(cells[j]) for j in range(k)]
+    Pw, Qw = ora.rdp_encode(data, p, st.unit_bytes)
+    rsw = ora.rs8_encode(data, m)
+    got = [t[:nr].cpu().numpy() for t in st.shards()]
     assert np.array_equal(got[0], Pw) and np.array_equal(got[1], Qw)
     for i in range(m):
-        assert np.array_equal(got[2 + i].reshape(-1), rsw[i]), i
+        assert np.array_equal(got[2 + i], rsw[i]), i

@@ -509,7 +509,7 @@ def test_kv_gather_matches_indexing(ora, tb, page_tokens, tok_off, T):
 
 # ------------------------------------------------------------------ chunked
 def test_chunk_cells_cut_and_pad(ora):
-    """Cells read in (shard, row) order give back the stream, then zeros."""
+    """The k pieces read in order give back the stream, then zeros."""
     rng = np.random.default_rng(11)
     k, p, rec = 5, 7, 32
     for n in (1, 31, 32 * 30, 32 * 30 + 5, 999):
@@ -517,30 +517,47 @@ def test_chunk_cells_cut_and_pad(ora):
         W = ora.chunk_width(n, k, p, rec)
         assert W % rec == 0 and k * (p - 1) * W >= n and k * (p - 1) * (W - rec) < n
         cells = ora.chunk_cells(s, k, p, W)
-        assert cells.shape == (k, p - 1, W)
+        assert cells.shape == (k, (p - 1) * W)
         flat = cells.reshape(-1)
         assert np.array_equal(flat[:n], s) and not flat[n:].any()
 
 
-def test_chunked_encode_is_per_chunk(ora):
-    """Coding chunk c alone gives the columns of chunk c of the whole-sequence
-    code (each column is its own RDP/RS instance), and the data shards hold the
-    gathered chunks side by side."""
-    rng = np.random.default_rng(12)
+@pytest.mark.parametrize("unit", [0, 64, 128])
+def test_chunked_encode_is_per_chunk(ora, unit):
+    """Chunk c owns region c of every shard ((p-1)*W bytes at c*(p-1)*W): the
+    data regions hold the gathered chunk's pieces side by side, and each
+    region's P, Q and RS parity are the codes of that region alone (striped
+    geometry with rows of W bytes and the given unit)."""
+    rng = np.random.default_rng(12 + unit)
     L, B, pps, pt, tb = 2, 3, 4, 16, 32
     npages = B * pps + 2
     pool = rng.integers(0, 256, (L, npages, pt, 2, tb), dtype=np.uint8)
     table = rng.permutation(npages)[: B * pps].astype(np.int32).reshape(B, pps)
     k, p, m, ct, nc = 5, 7, 3, 16, 4
-    W, data, P, Q, rs = ora.chunked_encode(pool, table, pt, ct, nc, k, p, m)
+    W, data, P, Q, rs = ora.chunked_encode(pool, table, pt, ct, nc, k, p, m, unit)
+    n = (p - 1) * W
+    assert all(x.size == nc * n for x in data + [P, Q] + rs)
     for c in range(nc):
-        cols = slice(c * W, (c + 1) * W)
+        reg = slice(c * n, (c + 1) * n)
         s = ora.kv_gather(pool, table, pt, c * ct, ct)
         cells = ora.chunk_cells(s, k, p, W)
         for j in range(k):
-            assert np.array_equal(data[j][:, cols], cells[j])
-        Pc, Qc = ora.rdp_encode([np.ascontiguousarray(cells[j]) for j in range(k)], p)
-        assert np.array_equal(P[:, cols], Pc) and np.array_equal(Q[:, cols], Qc)
-        rc = ora.rs8_encode([np.ascontiguousarray(cells[j]).reshape(-1) for j in range(k)], m)
+            assert np.array_equal(data[j][reg], cells[j])
+        Pc, Qc = ora.rdp_encode([np.ascontiguousarray(cells[j]) for j in range(k)], p, unit)
+        assert np.array_equal(P[reg], Pc) and np.array_equal(Q[reg], Qc)
+        rc = ora.rs8_encode([np.ascontiguousarray(cells[j]) for j in range(k)], m)
         for i in range(m):
-            assert np.array_equal(rs[i][:, cols], rc[i].reshape(p - 1, W))
+            assert np.array_equal(rs[i][reg], rc[i])
+    # every row of every stripe of a region satisfies RDP's equations (pinned
+    # independently of the oracle's encode in test_rdp_striped_equations_hold)
+    if unit:
+        c, s_ = 1, 0
+        g = min(unit, W - s_ * unit)
+        base = c * n + s_ * (p - 1) * unit
+        rows = lambda x: [x[base + r * g: base + (r + 1) * g] for r in range(p - 1)]  # noqa: E731
+        Pr = rows(P)
+        for r in range(p - 1):
+            acc = Pr[r].copy()
+            for j in range(k):
+                acc ^= rows(data[j])[r]
+            assert not acc.any()
