@@ -17,7 +17,7 @@ import functools
 import numpy as np
 import torch
 
-from . import _lib
+from . import _lib, spec
 
 GF_SIZE = 1 << 16
 GF_ORDER = GF_SIZE - 1
@@ -114,9 +114,17 @@ def shard_size_and_pad(total_symbols: int, num_data_shards: int):
     return shard_size, pad
 
 
+SCHEMES = ("ghostserve", "spec")
+
+
 def forward_encode_kv(keys: torch.Tensor, values: torch.Tensor, num_data_shards: int,
-                      num_parity_shards: int):
-    """benchmark/rs/main.py:63-137: returns (shards [(k+m), S] uint16, meta)."""
+                      num_parity_shards: int, scheme: str = "ghostserve"):
+    """benchmark/rs/main.py:63-137: returns (shards [(k+m), S] uint16, meta).
+    scheme="spec": RS over GF(2^8)/0x11D with the Cauchy parity block (bytes
+    of the same rows) instead of GF(2^16); S is then rounded up to a multiple
+    of 8 words (16-byte rows)."""
+    if scheme not in SCHEMES:
+        raise ValueError(f"scheme must be one of {SCHEMES}, not {scheme!r}")
     assert keys.element_size() == 2 and values.element_size() == 2 and keys.dtype == values.dtype
     device = keys.device
     assert device.type == "cuda"
@@ -128,6 +136,9 @@ def forward_encode_kv(keys: torch.Tensor, values: torch.Tensor, num_data_shards:
     assert num_data_shards > 0 and num_parity_shards >= 0
 
     shard_sz, pad = shard_size_and_pad(total, num_data_shards)
+    if scheme == "spec":
+        shard_sz = -(-shard_sz // 8) * 8
+        pad = num_data_shards * shard_sz - total
     total_shards = num_data_shards + num_parity_shards
     assert shard_sz > 0
     # K || V and the zero padding go straight into the shard tensor's data rows
@@ -140,9 +151,14 @@ def forward_encode_kv(keys: torch.Tensor, values: torch.Tensor, num_data_shards:
         data_rows.view(torch.int16)[total:].zero_()
     rs_kernel.pack_fp16_pair_to_u16(keys.contiguous().view(-1), values.contiguous().view(-1),
                                     data_rows)
-    gf_exp, gf_log = device_gf_tables(device)
-    rs_kernel.encode_rs_u16(data_rows, shards, num_data_shards, num_parity_shards, shard_sz,
-                            gf_exp, gf_log)
+    if scheme == "spec":
+        rows = shards.view(torch.uint8).view(total_shards, -1)
+        spec.rs8_encode([rows[i] for i in range(num_data_shards)],
+                        [rows[num_data_shards + i] for i in range(num_parity_shards)])
+    else:
+        gf_exp, gf_log = device_gf_tables(device)
+        rs_kernel.encode_rs_u16(data_rows, shards, num_data_shards, num_parity_shards, shard_sz,
+                                gf_exp, gf_log)
     meta = {
         "B": B, "H": H, "T": T, "D": D,
         "N_k": N_k, "N_v": N_v,
@@ -152,13 +168,16 @@ def forward_encode_kv(keys: torch.Tensor, values: torch.Tensor, num_data_shards:
         "num_data": num_data_shards,
         "num_parity": num_parity_shards,
         "dtype": keys.dtype,
+        "scheme": scheme,
     }
     return shards, meta
 
 
 def backwards_decode_kv(shards: torch.Tensor, meta: dict, missing_shards):
     """benchmark/rs/main.py:140-206: rebuild missing data shards in place from
-    the first surviving parities, then split K, V.  Returns (K, V)."""
+    the first surviving parities, then split K, V.  Returns (K, V).  For meta
+    of scheme "spec" every missing shard (data or parity, at most m) is
+    rebuilt by the GF(2^8) decode."""
     device = shards.device
     num_data = meta["num_data"]
     num_parity = meta["num_parity"]
@@ -175,6 +194,14 @@ def backwards_decode_kv(shards: torch.Tensor, meta: dict, missing_shards):
     if len(missing_data) > len(avail_par):
         raise RuntimeError("Not enough parity shards to reconstruct the missing data shards.")
 
+    if meta.get("scheme", "ghostserve") == "spec":
+        if len(set(missing_shards)) > num_parity:
+            raise RuntimeError("Not enough parity shards to reconstruct the missing shards.")
+        if missing_shards:
+            rows = shards.view(torch.uint8).view(num_data + num_parity, -1)
+            spec.rs8_decode([rows[i] for i in range(num_data + num_parity)], num_data,
+                            [int(i) for i in missing_shards])
+        missing_data = []
     gf_exp, gf_log = device_gf_tables(device)
     if missing_data:
         if len(missing_data) > 16:
