@@ -123,8 +123,14 @@ struct ShardView<true> {
         return __builtin_bit_cast(
             u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, lane_off, (uint32_t)row_off, kAuxLoadNT));
     }
+    // Stores fold the row offset into the lane offset and pass an immediate
+    // soffset of 0.  The compiler enforces the wait states between a store of
+    // more than 64 bits and a VALU write of its data registers only for
+    // stores without an SGPR soffset; with the row offset in an SGPR it let
+    // such writes follow a store back to back (found by scanning the
+    // generated code), which the code here never allows.
     __device__ __forceinline__ void store(uint64_t row_off, uint32_t lane_off, u32x4 v) const {
-        __builtin_amdgcn_raw_buffer_store_b128(v, rs, lane_off, (uint32_t)row_off, kAuxStoreNT);
+        __builtin_amdgcn_raw_buffer_store_b128(v, rs, lane_off + (uint32_t)row_off, 0, kAuxStoreNT);
     }
 };
 
