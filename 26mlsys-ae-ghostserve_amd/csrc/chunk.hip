@@ -32,6 +32,10 @@ namespace kvec {
 constexpr int kChunkMaxK = 12;
 constexpr int kChunkMaxM = 4;
 constexpr int kCBS = 128;
+// Rows of cells in flight per thread.  Three rows measured the same as two on
+// the 16 x 2048-token fp8 chunk; all k(p-1) cells at once measured 12 % slower
+// (the RS products then run as one long VALU phase with no loads in flight).
+constexpr int kChunkDepth = 2;
 
 // write-mask bits of the encode kernel; RS parity i is bit kWRs + i
 constexpr uint32_t kWData = 1u, kWP = 2u, kWQ = 4u, kWRs = 3;
@@ -95,9 +99,10 @@ __device__ __forceinline__ u32x4 load_cell(const PagedGeom& g, const ChunkGeom& 
 }
 
 // ------------------------------------------------------------------ encode
-// Rows are software pipelined two deep: while row r is coded and stored, row
-// r+1's cells are in flight and row r+2's page-table entries are being
-// fetched, so a thread holds two rows of cells and two rows of references.
+// Rows are software pipelined kChunkDepth deep: while row r is coded and
+// stored, the next rows' cells are in flight and the row after them has its
+// page-table entries fetched, so a thread holds kChunkDepth rows of cells and
+// of references.
 // Program order is what keeps the loads early: stores to the shards could
 // alias the pool as far as the compiler knows, and the compiler barrier after
 // each row also keeps the GF tables from being hoisted out of the row loop
@@ -123,30 +128,32 @@ __global__ __launch_bounds__(kCBS) void chunk_encode_kernel(PagedGeom g, ChunkGe
     const uint64_t nb = cg.nb;
     auto rec = [&](int j, int r) { return cell_rec(cg, cp, j, r); };
     auto row = [&](int r) { return cp.rowbase + uint32_t(r) * cp.g; };
-    CellRef ref[2][K];
-    u32x4 x[2][K];
+    constexpr int DEPTH = kChunkDepth;
+    CellRef ref[DEPTH][K];
+    u32x4 x[DEPTH][K];
 #pragma unroll
-    for (int j = 0; j < K; ++j) ref[0][j] = cell_ref(g, rec(j, 0));
-    if constexpr (ROWS > 1) {
+    for (int d0 = 0; d0 < DEPTH && d0 < ROWS; ++d0)
 #pragma unroll
-        for (int j = 0; j < K; ++j) ref[1][j] = cell_ref(g, rec(j, 1));
-    }
+        for (int j = 0; j < K; ++j) ref[d0][j] = cell_ref(g, rec(j, d0));
 #pragma unroll
-    for (int j = 0; j < K; ++j) x[0][j] = cell_load_ref(g, ref[0][j], inner);
+    for (int d0 = 0; d0 + 1 < DEPTH && d0 < ROWS; ++d0)
+#pragma unroll
+        for (int j = 0; j < K; ++j) x[d0][j] = cell_load_ref(g, ref[d0][j], inner);
     u32x4 q[ROWS];
 #pragma unroll
     for (int r = 0; r < ROWS; ++r) q[r] = u32x4{0, 0, 0, 0};
     const ShardView<true> sp(par.p[0], (wmask & kWP) ? nb : 0);
 #pragma unroll
     for (int r = 0; r < ROWS; ++r) {
-        const int c = r & 1;
-        if (r + 1 < ROWS) {
+        const int c = r % DEPTH;
+        if (r + DEPTH - 1 < ROWS) {
+            const int n = (r + DEPTH - 1) % DEPTH;
 #pragma unroll
-            for (int j = 0; j < K; ++j) x[c ^ 1][j] = cell_load_ref(g, ref[c ^ 1][j], inner);
+            for (int j = 0; j < K; ++j) x[n][j] = cell_load_ref(g, ref[n][j], inner);
         }
-        if (r + 2 < ROWS) {
+        if (r + DEPTH < ROWS) {
 #pragma unroll
-            for (int j = 0; j < K; ++j) ref[c][j] = cell_ref(g, rec(j, r + 2));
+            for (int j = 0; j < K; ++j) ref[c][j] = cell_ref(g, rec(j, r + DEPTH));
         }
         if constexpr (DATA) {
 #pragma unroll
