@@ -479,7 +479,7 @@ struct ChunkArgs {
 };
 
 static int check_chunk(const kvec_paged_kv* kv, const kvec_chunk_stripe* st, ChunkArgs* a,
-                       const char* fn) {
+                       bool writes_pool, const char* fn) {
     int rc = make_geom(kv, &a->g, fn);
     if (rc) return rc;
     if (!st) return set_error(KVEC_EINVAL, "%s: null stripe", fn);
@@ -531,6 +531,24 @@ static int check_chunk(const kvec_paged_kv* kv, const kvec_chunk_stripe* st, Chu
             a->d.p[j] = (uint8_t*)st->data[j];
         }
     a->cg.nb = uint64_t(p - 1) * R;
+    {
+        // every shard of the stripe set may be written (and the pool, by a
+        // decode); nothing written may share a byte with anything else
+        Span w[kChunkMaxK + 3 + kChunkMaxM];
+        Span r[2] = {pool_span(kv), table_span(kv)};
+        int nw = 0, nr = 2;
+        if (writes_pool) {
+            w[nw++] = r[0];
+            r[0] = r[1];
+            nr = 1;
+        }
+        w[nw++] = Span{st->P, a->cg.nb, "P", -1};
+        w[nw++] = Span{st->Q, a->cg.nb, "Q", -1};
+        for (int i = 0; i < m; ++i) w[nw++] = Span{st->rs[i], a->cg.nb, "rs", i};
+        if (a->have_data)
+            for (int j = 0; j < k; ++j) w[nw++] = Span{st->data[j], a->cg.nb, "data", j};
+        if ((rc = check_no_alias(w, nw, r, nr, fn))) return rc;
+    }
     a->cg.region = uint32_t(off);
     a->cg.recs_per_shard = uint32_t(uint64_t(p - 1) * W / a->g.rec);
     a->cg.geo = make_rdp_geom(W, U);
@@ -568,7 +586,7 @@ extern "C" int64_t kvec_chunk_width(int64_t chunk_stream_bytes, int k, int p, in
 extern "C" int kvec_chunk_encode_paged(const kvec_paged_kv* kv, const kvec_chunk_stripe* st,
                                        void* stream) {
     ChunkArgs a;
-    int rc = check_chunk(kv, st, &a, "kvec_chunk_encode_paged");
+    int rc = check_chunk(kv, st, &a, false, "kvec_chunk_encode_paged");
     if (rc) return rc;
     uint32_t wmask = kWP | kWQ | (a.have_data ? kWData : 0u);
     for (int i = 0; i < a.m; ++i) wmask |= 1u << (kWRs + i);
@@ -580,7 +598,7 @@ extern "C" int kvec_chunk_decode_paged(const kvec_paged_kv* kv, void* pool,
                                        int n_erased, void* stream) {
     static const char* fn = "kvec_chunk_decode_paged";
     ChunkArgs a;
-    int rc = check_chunk(kv, st, &a, fn);
+    int rc = check_chunk(kv, st, &a, true, fn);
     if (rc) return rc;
     if (!pool || pool != kv->pool) return set_error(KVEC_EINVAL, "%s: pool must be kv->pool", fn);
     if (n_erased < 0 || (n_erased > 0 && !erased)) return set_error(KVEC_EINVAL, "%s: bad erasure list", fn);

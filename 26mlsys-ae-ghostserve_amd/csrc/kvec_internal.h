@@ -237,6 +237,21 @@ inline bool ranges_overlap(const void* a, uint64_t na, const void* b, uint64_t n
     return na && nb && x < y + nb && y < x + na;
 }
 
+// One buffer of a launch, for check_no_alias (idx < 0: no index in messages).
+struct Span {
+    const void* p;
+    uint64_t n;
+    const char* name;
+    int idx;
+};
+
+// Host check before a launch that no buffer it writes (w) shares a byte with
+// another written buffer or with a buffer it only reads (r; those may alias
+// each other).  The kernels read their inputs while other blocks of the same
+// launch write their outputs, so with such an overlap the bytes a block reads
+// would depend on block timing.  KVEC_EINVAL names the first pair found.
+int check_no_alias(const Span* w, int nw, const Span* r, int nr, const char* fn);
+
 // Stream-ordered device copies and zero fills done by kernels (copy.hip), so
 // that no entry point records a memcpy or memset node under graph capture.
 // copy_d2d: n bytes, any alignments; dst == src is a no-op; other overlaps

@@ -314,6 +314,8 @@ extern "C" int kvec_kv_gather(const kvec_paged_kv* kv, void* out, void* stream) 
     if (!out || !aligned16(out)) return set_error(KVEC_EINVAL, "kvec_kv_gather: output null or misaligned");
     const uint32_t ncells = uint32_t(g.recs_total * g.rec / 16);
     if (ncells == 0) return KVEC_OK;
+    const Span w[1] = {{out, uint64_t(ncells) * 16, "out", -1}}, r[2] = {pool_span(kv), table_span(kv)};
+    if ((rc = check_no_alias(w, 1, r, 2, "kvec_kv_gather"))) return rc;
     hipLaunchKernelGGL(kv_gather_kernel, dim3(blocks_for(ncells, kGBS)), dim3(kGBS), 0,
                        as_stream(stream), g, (uint8_t*)out, ncells);
     return check_launch("kvec_kv_gather");
@@ -327,6 +329,10 @@ extern "C" int kvec_kv_gather_split(const kvec_paged_kv* kv, void* out_k, void* 
         return set_error(KVEC_EINVAL, "kvec_kv_gather_split: output null or misaligned");
     const uint32_t ncells = uint32_t(g.recs_total * g.rec / 16);
     if (ncells == 0) return KVEC_OK;
+    const uint64_t half = uint64_t(ncells) * 8;
+    const Span w[2] = {{out_k, half, "out_k", -1}, {out_v, half, "out_v", -1}},
+               r[2] = {pool_span(kv), table_span(kv)};
+    if ((rc = check_no_alias(w, 2, r, 2, "kvec_kv_gather_split"))) return rc;
     hipLaunchKernelGGL(kv_gather_split_kernel, dim3(blocks_for(ncells, kGBS)), dim3(kGBS), 0,
                        as_stream(stream), g, (uint8_t*)out_k, (uint8_t*)out_v, ncells,
                        uint32_t(kv->token_bytes));
@@ -341,6 +347,8 @@ extern "C" int kvec_kv_scatter(const kvec_paged_kv* kv, void* pool, const void* 
     if (!in || !aligned16(in)) return set_error(KVEC_EINVAL, "kvec_kv_scatter: input null or misaligned");
     const uint32_t ncells = uint32_t(g.recs_total * g.rec / 16);
     if (ncells == 0) return KVEC_OK;
+    const Span w[1] = {pool_span(kv)}, r[2] = {{in, uint64_t(ncells) * 16, "in", -1}, table_span(kv)};
+    if ((rc = check_no_alias(w, 1, r, 2, "kvec_kv_scatter"))) return rc;
     hipLaunchKernelGGL(kv_scatter_kernel, dim3(blocks_for(ncells, kGBS)), dim3(kGBS), 0,
                        as_stream(stream), g, (const uint8_t*)in, ncells);
     return check_launch("kvec_kv_scatter");
@@ -376,9 +384,17 @@ extern "C" int kvec_rdp_encode_paged(const kvec_paged_kv* kv, void* const* data,
             return set_error(KVEC_EINVAL, "kvec_rdp_encode_paged: data[%d] null or misaligned", j);
         d.p[j] = (uint8_t*)data[j];
     }
+    const uint64_t nb = uint64_t(p - 1) * uint64_t(row_bytes);
+    {
+        Span w[kRdpMaxShards];
+        const Span r[2] = {pool_span(kv), table_span(kv)};
+        for (int j = 0; j < k; ++j) w[j] = Span{data[j], nb, "data", j};
+        w[k] = Span{P, nb, "P", -1};
+        w[k + 1] = Span{Q, nb, "Q", -1};
+        if ((rc = check_no_alias(w, k + 2, r, 2, "kvec_rdp_encode_paged"))) return rc;
+    }
     PagedEncFn fn = paged_fn(p, k);
     if (!fn) return set_error(KVEC_EUNSUPPORTED, "kvec_rdp_encode_paged: p=%d k=%d not built", p, k);
-    const uint64_t nb = uint64_t(p - 1) * uint64_t(row_bytes);
     const RdpGeom geo = make_rdp_geom(uint64_t(row_bytes), uint64_t(unit_bytes));
     hipLaunchKernelGGL(fn, dim3(unsigned(rdp_waves(geo))), dim3(kFBS), 0, as_stream(stream), g, d,
                        (uint8_t*)P, (uint8_t*)Q, geo, uint32_t(nb), uint32_t(nb / g.rec));
@@ -428,6 +444,19 @@ extern "C" int kvec_rdp_decode_paged(const kvec_paged_kv* kv, void* pool, void* 
     if (b >= 0 && b < a) { int t = a; a = b; b = t; }
     if (a < 0) return KVEC_OK;
     const uint64_t nb = uint64_t(p - 1) * uint64_t(row_bytes);
+    {
+        // the pool, P, Q and the data shards are each read and may be
+        // rewritten, so none may share a byte with another
+        Span w[kRdpMaxShards + 1];
+        const Span r[1] = {table_span(kv)};
+        int nw = 0;
+        w[nw++] = pool_span(kv);
+        w[nw++] = Span{P, nb, "P", -1};
+        w[nw++] = Span{Q, nb, "Q", -1};
+        if (data)
+            for (int j = 0; j < k; ++j) w[nw++] = Span{data[j], nb, "data", j};
+        if ((rc = check_no_alias(w, nw, r, 1, "kvec_rdp_decode_paged"))) return rc;
+    }
     const RdpGeom geo = make_rdp_geom(uint64_t(row_bytes), uint64_t(unit_bytes));
     const dim3 grid(unsigned(rdp_waves(geo))), block(kFBS);
     const uint32_t rps = uint32_t(nb / g.rec);

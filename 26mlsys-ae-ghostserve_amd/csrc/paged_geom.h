@@ -110,6 +110,16 @@ __device__ __forceinline__ void cell_store(const PagedGeom& g, uint32_t w, uint3
     if (valid) st_stream(g.pool_w, off, v);
 }
 
+// The whole pool and the page table, for the alias checks (after make_geom).
+inline Span pool_span(const kvec_paged_kv* kv) {
+    return Span{kv->pool, uint64_t(kv->layers) * uint64_t(kv->pool_pages) * uint64_t(kv->page_tokens) * 2 *
+                              uint64_t(kv->token_bytes),
+                "pool", -1};
+}
+inline Span table_span(const kvec_paged_kv* kv) {
+    return Span{kv->page_table, uint64_t(kv->batch) * uint64_t(kv->pages_per_seq) * 4, "page_table", -1};
+}
+
 inline int make_geom(const kvec_paged_kv* kv, PagedGeom* g, const char* fn) {
     if (!kv) return set_error(KVEC_EINVAL, "%s: null descriptor", fn);
     if (!kv->pool || !kv->page_table) return set_error(KVEC_EINVAL, "%s: null pool or page table", fn);

@@ -1,10 +1,13 @@
 // rdp_spec.hip -- textbook RDP (Corbett et al., FAST 2004) over a prime p.
 //
-// Geometry: every shard is its own HBM buffer of p-1 row planes; byte offset o
-// of the row planes is an independent RDP instance.  A thread owns one 16-byte
-// lane offset and streams all k*(p-1) cells of its stripe column through
-// registers, so each data byte is read from HBM once and each parity byte is
-// written once.  The diagonal of a cell is a compile-time constant after
+// Geometry: every shard is its own HBM buffer, cut into stripes of p-1 rows
+// (RdpGeom, kvec_internal.h: rows of U bytes, a shorter last stripe; U = 0 is
+// one stripe of p-1 row planes).  Byte offset o of a stripe's rows is an
+// independent RDP instance.  Rows of 16-64 KiB measured fastest: the time
+// follows the distance between the rows one column's cells come from (15 MB
+// apart with row planes: 8 % slower).  A thread owns one 16-byte lane offset
+// and streams all k*(p-1) cells of its stripe column through registers, so
+// each data byte is read from HBM once and each parity byte is written once.  The diagonal of a cell is a compile-time constant after
 // unrolling, so the "shift" of the diagonal parity costs no data movement at
 // all: it is only a choice of accumulator register.
 //
@@ -19,7 +22,7 @@ namespace kvec {
 
 // ---------------------------------------------------------------- encode
 // A thread owns one 16-byte lane offset; a block is one wave, so each load
-// instruction reads 1 KiB contiguous from one row plane.  Memory-level
+// instruction reads 1 KiB contiguous from one stripe row.  Memory-level
 // parallelism comes from each thread requesting many cells before folding any
 // of them in: the cells of rdp_group(p, k) shards (all k*(p-1) cells for p <= 7) are
 // issued back to back, and a scheduling barrier keeps the compiler from
@@ -306,6 +309,12 @@ extern "C" int kvec_rdp_encode(const void* const* data, int k, void* P, void* Q,
         return set_error(KVEC_EINVAL, "kvec_rdp_encode: P/Q not 16-byte aligned");
     if (row_bytes == 0) return KVEC_OK;
     const uint64_t nb = uint64_t(p - 1) * uint64_t(row_bytes);
+    {
+        Span w[2] = {{P, nb, "P", -1}, {Q, nb, "Q", -1}};
+        Span r[kRdpMaxShards];
+        for (int j = 0; j < k; ++j) r[j] = Span{data[j], nb, "data", j};
+        if ((rc = check_no_alias(w, 2, r, k, "kvec_rdp_encode"))) return rc;
+    }
     const bool buf = fits_buffer(nb);
     EncFn fn = buf ? encode_fn<true>(p, k) : encode_fn<false>(p, k);
     if (!fn) return set_error(KVEC_EUNSUPPORTED, "kvec_rdp_encode: p=%d k=%d not built", p, k);
@@ -335,6 +344,14 @@ extern "C" int kvec_rdp_decode(void* const* shards, int k, int p, int64_t row_by
     if (b >= 0 && b < a) { int t = a; a = b; b = t; }
     if (a < 0 || row_bytes == 0) return KVEC_OK;
     const uint64_t nb = uint64_t(p - 1) * uint64_t(row_bytes);
+    {
+        // the rebuilt shards must not share a byte with any other shard
+        Span w[2], r[kRdpMaxShards];
+        int nw = 0, nr = 0;
+        for (int j = 0; j < k + 2; ++j)
+            (j == a || j == b ? w[nw++] : r[nr++]) = Span{shards[j], nb, "shard", j};
+        if ((rc = check_no_alias(w, nw, r, nr, "kvec_rdp_decode"))) return rc;
+    }
     const RdpGeom geo = make_rdp_geom(uint64_t(row_bytes), uint64_t(unit_bytes));
     const dim3 grid(unsigned(rdp_waves(geo))), block(kBS);
     DecFn fn = decode_fn(p, k, a, b, fits_buffer(nb));

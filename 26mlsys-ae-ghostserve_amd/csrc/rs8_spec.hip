@@ -174,6 +174,12 @@ extern "C" int kvec_rs8_encode(const void* const* data, int k, void* const* pari
             return set_error(KVEC_EINVAL, "kvec_rs8_encode: parity[%d] null or not 16-byte aligned", i);
         out[i] = (uint8_t*)parity[i];
     }
+    {
+        Span w[kRs8MaxM], r[kRs8MaxK];
+        for (int i = 0; i < m; ++i) w[i] = Span{out[i], uint64_t(shard_bytes), "parity", i};
+        for (int j = 0; j < k; ++j) r[j] = Span{in[j], uint64_t(shard_bytes), "data", j};
+        if ((rc = check_no_alias(w, m, r, k, "kvec_rs8_encode"))) return rc;
+    }
     uint8_t C[kRs8MaxM * kRs8MaxK];
     cauchy(k, m, C);
     return launch_mix(in, k, out, m, C, shard_bytes, as_stream(stream), "kvec_rs8_encode");
@@ -199,6 +205,14 @@ extern "C" int kvec_rs8_decode(void* const* shards, int k, int m, int64_t shard_
     }
     if (ne == 0) return KVEC_OK;
     if (ne > m) return set_error(KVEC_EDECODE, "kvec_rs8_decode: %d erasures > m=%d", ne, m);
+    {
+        // the rebuilt shards must not share a byte with any other shard
+        Span w[kRs8MaxM], r[kRs8MaxK + kRs8MaxM];
+        int nw = 0, nr = 0;
+        for (int s = 0; s < k + m; ++s)
+            (er[s] ? w[nw++] : r[nr++]) = Span{shards[s], uint64_t(shard_bytes), "shard", s};
+        if ((rc = check_no_alias(w, nw, r, nr, "kvec_rs8_decode"))) return rc;
+    }
     int surv[kRs8MaxK], outs[kRs8MaxM], no = 0;
     uint8_t M[kRs8MaxM * kRs8MaxK];
     if (!rs8_decode_rows(k, m, er, surv, outs, &no, M))

@@ -22,6 +22,28 @@ int check_launch(const char* what) {
     return KVEC_OK;
 }
 
+static void span_label(const Span& s, char* buf, size_t n) {
+    if (s.idx >= 0) snprintf(buf, n, "%s[%d]", s.name, s.idx);
+    else snprintf(buf, n, "%s", s.name);
+}
+
+int check_no_alias(const Span* w, int nw, const Span* r, int nr, const char* fn) {
+    for (int i = 0; i < nw; ++i) {
+        const Span* hit = nullptr;
+        for (int j = i + 1; j < nw && !hit; ++j)
+            if (ranges_overlap(w[i].p, w[i].n, w[j].p, w[j].n)) hit = &w[j];
+        for (int j = 0; j < nr && !hit; ++j)
+            if (ranges_overlap(w[i].p, w[i].n, r[j].p, r[j].n)) hit = &r[j];
+        if (hit) {
+            char a[64], b[64];
+            span_label(w[i], a, sizeof a);
+            span_label(*hit, b, sizeof b);
+            return set_error(KVEC_EINVAL, "%s: %s overlaps %s", fn, a, b);
+        }
+    }
+    return KVEC_OK;
+}
+
 }  // namespace kvec
 
 extern "C" int kvec_version(void) { return 100; }

@@ -18,10 +18,14 @@ After the attention backend's ``forward_extend``, the KV slots that step wrote
 Environment (as the reference reads it): RDP_STAR_BASE, FT_METRICS_FILE,
 FT_PROG_START_MONO.
 
-What differs, with no parity byte changed:
+What differs:
   * the delta is gathered by the paged-gather kernel straight into the row,
     K half and V half (one pass; the reference indexes the pool twice, copies
-    to fp16 and packs) -- KV of any 2-byte dtype is coded as raw bits;
+    to fp16 and packs).  KV of any 2-byte dtype is coded as raw bits.  For an
+    fp16 pool the parity bytes are the reference's; for a bf16 pool they are
+    on purpose not, since the reference's .to(torch.float16) before packing
+    (bench_ghostserve_rdp.py:345-346) is lossy and its parity cannot rebuild
+    the bf16 cache;
   * the host copy of P/Q runs on a side stream into pinned buffers and the
     record is written once that copy has finished (checked at the next step
     or at ``flush()``), instead of a device-wide synchronize per chunk; its

@@ -12,6 +12,16 @@ from conftest import ROOT
 HEADER = os.path.join(ROOT, "include", "kvec.h")
 
 
+@pytest.fixture
+def fake_ptrs():
+    """Tests that pass made-up device addresses expect every call to fail on
+    the host before any launch.  Should one pass its checks by mistake, its
+    launch must not reach a real GPU: they run only where none is visible."""
+    import torch
+    if torch.cuda.is_available():
+        pytest.skip("made-up device addresses: CPU-only test")
+
+
 def declared_symbols():
     text = open(HEADER).read()
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
@@ -60,7 +70,7 @@ def test_rdp_row_bytes(pkg):
     assert spec.rdp_row_bytes(1, 2, 3, 16) == 16
 
 
-def test_rdp_rejects_bad_arguments(pkg):
+def test_rdp_rejects_bad_arguments(pkg, fake_ptrs):
     L = pkg._lib.lib()
     arr = (C.c_void_p * 6)(*([16] * 6))
     assert L.kvec_rdp_encode(arr, 6, 16, 16, 4, 16, 0, None) == -1   # p not prime
@@ -79,7 +89,7 @@ def test_rdp_rejects_bad_arguments(pkg):
     assert L.kvec_rdp_decode(arr, 4, 5, 4096, 1000, 0, -1, None) == -1
 
 
-def test_xor_one_call_entries_reject_bad_arguments(pkg):
+def test_xor_one_call_entries_reject_bad_arguments(pkg, fake_ptrs):
     """kvec_xor_encode_kv / kvec_xor_recover_kv validate sizes and pointers
     before any device call (the pointers below are never dereferenced)."""
     L = pkg._lib.lib()
@@ -99,7 +109,7 @@ def test_xor_one_call_entries_reject_bad_arguments(pkg):
     assert L.kvec_xor_recover_kv(p, p, 3, 0, 0, 1, None) == 0          # empty rows
 
 
-def test_pack_unpack_reject_bad_arguments(pkg):
+def test_pack_unpack_reject_bad_arguments(pkg, fake_ptrs):
     """xor_kernel.pack_kv / unpack_kv (benchmark/xor/kernel.cu:193-223): negative
     sizes and null pointers are refused on the host; zero words is a no-op."""
     L = pkg._lib.lib()
@@ -117,7 +127,7 @@ def test_pack_unpack_reject_bad_arguments(pkg):
     assert L.kvec_unpack_kv(None, None, 4, 0, None) == 0
 
 
-def test_copy_entries_reject_partial_overlap(pkg):
+def test_copy_entries_reject_partial_overlap(pkg, fake_ptrs):
     """Entry points that copy the caller's data rows into the shard tensor
     accept the same buffer (no copy) or disjoint ones; a partial overlap has no
     stream-ordered meaning and is refused before any launch."""
@@ -149,16 +159,16 @@ def test_chunk_width(pkg):
     assert L.kvec_chunk_width(-1, 5, 7, 256) == -1
 
 
-def test_chunk_rejects_bad_arguments(pkg):
+def test_chunk_rejects_bad_arguments(pkg, fake_ptrs):
     """Argument checks run on the host before any launch (fake aligned pointers)."""
     lib = pkg._lib
     L = lib.lib()
-    table = C.c_void_p(4096)
-    kv = lib.PagedKV(4096, 64, 2, 128, 16, 4096, 3, 4, 0, 16)
-    rs = (C.c_void_p * 3)(4096, 8192, 12288)
+    G = 1 << 30  # disjoint fake buffers: pool, table, P, Q, RS parity
+    kv = lib.PagedKV(G, 64, 2, 128, 16, 2 * G, 3, 4, 0, 16)
+    rs = (C.c_void_p * 3)(5 * G, 6 * G, 7 * G)
 
     def stripe(**kw):
-        a = dict(data=None, k=5, P=4096, Q=8192, p=7, rs=C.cast(rs, C.POINTER(C.c_void_p)),
+        a = dict(data=None, k=5, P=3 * G, Q=4 * G, p=7, rs=C.cast(rs, C.POINTER(C.c_void_p)),
                  m=3, row_bytes=1 << 20, region_off=0, width=256 * 64, unit_bytes=65536)
         a.update(kw)
         return lib.ChunkStripe(a["data"], a["k"], a["P"], a["Q"], a["p"], a["rs"], a["m"],
@@ -177,14 +187,84 @@ def test_chunk_rejects_bad_arguments(pkg):
     assert rc(unit_bytes=-1024) == -1
     assert rc(width=256) == -1                 # cells too small for the chunk
     assert b"k*(p-1)*width" in L.kvec_last_error()
-    assert rc(P=4100) == -1                    # misaligned parity
+    assert rc(P=3 * G + 4) == -1               # misaligned parity
     assert rc(m=5) == -1
     assert rc(row_bytes=1 << 30) == -2         # (p-1)*R >= 4 GiB
     assert b"4 GiB" in L.kvec_last_error()
     er = (C.c_int32 * 1)(10)
-    assert L.kvec_chunk_decode_paged(C.byref(kv), 4096, C.byref(stripe()), er, 1, None) == -1
-    assert L.kvec_chunk_decode_paged(C.byref(kv), 8192, C.byref(stripe()), er, 0, None) == -1
-    del table
+    assert L.kvec_chunk_decode_paged(C.byref(kv), G, C.byref(stripe()), er, 1, None) == -1
+    assert b"erased index 10" in L.kvec_last_error()
+    assert L.kvec_chunk_decode_paged(C.byref(kv), 8 * G, C.byref(stripe()), er, 0, None) == -1
+    assert b"kv->pool" in L.kvec_last_error()
+
+
+def test_written_buffers_must_not_alias(pkg, fake_ptrs):
+    """Every spec entry point refuses, before any launch, a buffer it writes
+    that shares a byte with another buffer of the call: its kernels read
+    their inputs while other blocks of the same launch write the outputs.
+    Fake addresses; nothing is dereferenced and every call below fails."""
+    lib = pkg._lib
+    L = lib.lib()
+    G = 1 << 30
+    R = 4096
+    nb = 6 * R
+
+    def err():
+        return L.kvec_last_error().decode()
+
+    data = (C.c_void_p * 6)(*[G * (j + 1) for j in range(6)])
+    assert L.kvec_rdp_encode(data, 6, 3 * G + 1024, 9 * G, 7, R, 0, None) == -1
+    assert "P overlaps data[2]" in err()
+    assert L.kvec_rdp_encode(data, 6, 8 * G, 8 * G + nb - 16, 7, R, 65536, None) == -1
+    assert "P overlaps Q" in err()
+    sh = (C.c_void_p * 8)(*[G * (j + 1) for j in range(6)] + [8 * G, 9 * G])
+    sh[4] = 2 * G + nb - 16                     # lost shard 4 ends inside shard 1
+    assert L.kvec_rdp_decode(sh, 6, 7, R, 0, 4, -1, None) == -1
+    assert "shard[4] overlaps shard[1]" in err()
+    assert L.kvec_rdp_decode(sh, 6, 7, R, 0, 7, 4, None) == -1
+
+    par = (C.c_void_p * 2)(8 * G, G + 16)
+    assert L.kvec_rs8_encode(data, 6, par, 2, R, None) == -1
+    assert "parity[1] overlaps data[0]" in err()
+    rs_sh = (C.c_void_p * 8)(*[G * (j + 1) for j in range(8)])
+    rs_sh[5] = rs_sh[2]
+    er = (C.c_int32 * 1)(2)
+    assert L.kvec_rs8_decode(rs_sh, 6, 2, R, er, 1, None) == -1
+    assert "shard[2] overlaps shard[5]" in err()
+
+    # paged: 2 layers x 3 sequences x 16 tokens of 256-byte records
+    pool, table = 20 * G, 21 * G
+    kv = lib.PagedKV(pool, 64, 2, 128, 16, table, 3, 4, 0, 16)
+    assert L.kvec_kv_gather(C.byref(kv), pool + 256, None) == -1
+    assert "out overlaps pool" in err()
+    assert L.kvec_kv_gather_split(C.byref(kv), 22 * G, table, None) == -1
+    assert "out_v overlaps page_table" in err()
+    assert L.kvec_kv_scatter(C.byref(kv), pool, pool + 512, None) == -1
+    assert "pool overlaps in" in err()
+    Rp = 768
+    assert L.kvec_rdp_encode_paged(C.byref(kv), data, 6, pool + 4096, 9 * G, 7, Rp, 0, None) == -1
+    assert "P overlaps pool" in err()
+    dd = (C.c_void_p * 6)(*[G * (j + 1) for j in range(6)])
+    dd[3] = 8 * G
+    assert L.kvec_rdp_decode_paged(C.byref(kv), pool, dd, 6, 8 * G, 9 * G, 7, Rp, 0, 1, 3,
+                                   None) == -1
+    assert "P overlaps data[3]" in err()
+    assert L.kvec_rdp_decode_paged(C.byref(kv), pool, None, 6, table, 9 * G, 7, Rp, 0, 1, -1,
+                                   None) == -1
+    assert "P overlaps page_table" in err()
+
+    # chunked: an RS parity shard inside Q; a decode's pool inside P
+    rs = (C.c_void_p * 3)(5 * G, 4 * G + 4096, 7 * G)
+    ck = lib.PagedKV(G, 64, 2, 128, 16, 2 * G, 3, 4, 0, 16)
+    st = lib.ChunkStripe(None, 5, 3 * G, 4 * G, 7, C.cast(rs, C.POINTER(C.c_void_p)), 3, 1 << 20,
+                         0, 256 * 64, 65536)
+    assert L.kvec_chunk_encode_paged(C.byref(ck), C.byref(st), None) == -1
+    assert "Q overlaps rs[1]" in err()
+    rs[1] = 6 * G
+    ck2 = lib.PagedKV(3 * G + 4096, 64, 2, 128, 16, 2 * G, 3, 4, 0, 16)
+    er2 = (C.c_int32 * 1)(0)
+    assert L.kvec_chunk_decode_paged(C.byref(ck2), 3 * G + 4096, C.byref(st), er2, 1, None) == -1
+    assert "pool overlaps P" in err()
 
 
 def test_build_rejects_register_spills():
