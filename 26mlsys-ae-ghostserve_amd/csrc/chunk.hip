@@ -31,11 +31,7 @@ namespace kvec {
 
 constexpr int kChunkMaxK = 12;
 constexpr int kChunkMaxM = 4;
-constexpr int kCBS = 128;
-// Rows of cells in flight per thread.  Three rows measured the same as two on
-// the 16 x 2048-token fp8 chunk; all k(p-1) cells at once measured 12 % slower
-// (the RS products then run as one long VALU phase with no loads in flight).
-constexpr int kChunkDepth = 2;
+constexpr int kCBS = 128;  // the decode kernels: two waves per block
 
 // write-mask bits of the encode kernel; RS parity i is bit kWRs + i
 constexpr uint32_t kWData = 1u, kWP = 2u, kWQ = 4u, kWRs = 3;
@@ -99,96 +95,96 @@ __device__ __forceinline__ u32x4 load_cell(const PagedGeom& g, const ChunkGeom& 
 }
 
 // ------------------------------------------------------------------ encode
-// Rows are software pipelined kChunkDepth deep: while row r is coded and
-// stored, the next rows' cells are in flight and the row after them has its
-// page-table entries fetched, so a thread holds kChunkDepth rows of cells and
-// of references.
-// Program order is what keeps the loads early: stores to the shards could
-// alias the pool as far as the compiler knows, and the compiler barrier after
-// each row also keeps the GF tables from being hoisted out of the row loop
-// (they are re-read from LDS per row instead of pinning 6*k*m registers).
-// Parity outputs switched off by `wmask` get a buffer resource of size 0,
-// whose stores the hardware drops, so the kernel has no branches after the
-// bounds check.  Whether the data shards are written is a template parameter
-// instead: dropped stores still occupy the memory pipeline, and the
-// parity-only encode would issue k(p-1) of them per thread.
+// One row per wave.  A block of p-1 waves owns one 1 KiB column piece of a
+// stripe; wave r codes row r.  It loads its k cells (page-table entries, then
+// the cells) and writes the data cells, P[r] and the RS parity of row r, none
+// of which needs another row.  Q mixes rows: cell (r, j) lies on diagonal
+// (r + j) % p and P[r] on r - 1, so every wave XORs its cells into the LDS
+// accumulators of their diagonals, and after one barrier wave d stores Q[d].
+// Compared with one wave walking all rows of its column (two rows in flight,
+// 165 VGPRs, 3 waves per SIMD), the waves are p-1 times more numerous and
+// short, and at 55 VGPRs and 6 KiB of LDS per block five blocks share a CU:
+// the encode of the 16 x 2048-token fp8 chunk went from 103.6 to 98.7 us.
+// The same kernel with the Q diagonals exchanged through per-(diagonal, row)
+// LDS slots (37 KiB per block, four blocks per CU) took 103.0 us, and with
+// two or four columns per wave (fewer, longer waves) 102.7 and 112.7 us.
 template <int P, int K, int M, bool DATA>
-__global__ __launch_bounds__(kCBS) void chunk_encode_kernel(PagedGeom g, ChunkGeom cg,
-                                                            Ptrs<kChunkMaxK> d,
-                                                            Ptrs<2 + kChunkMaxM> par,
-                                                            Gf8Tab<(K * M > 0 ? K * M : 1)> rs,
-                                                            uint32_t wmask) {
+__global__ __launch_bounds__((P - 1) * 64) void chunk_encode_rows_kernel(
+        PagedGeom g, ChunkGeom cg, Ptrs<kChunkMaxK> d, Ptrs<2 + kChunkMaxM> par,
+        Gf8Tab<(K * M > 0 ? K * M : 1)> rs, uint32_t wmask) {
     constexpr int ROWS = P - 1;
     constexpr int NT = K * M > 0 ? K * M : 1;
     __shared__ uint32_t tab[NT][6];
+    __shared__ uint32_t qacc[ROWS][4][64];  // Q[diagonal], dword-major per lane
+    const int r = int(__builtin_amdgcn_readfirstlane(threadIdx.x >> 6));
+    const uint32_t lane = threadIdx.x & 63;
+    const RdpWave w = rdp_wave(cg.geo, ROWS, blockIdx.x, lane);
+    // Lanes past a short last stripe's row end take offset 0 of the row: they
+    // compute lane 0's values and store them to lane 0's addresses (lane 0 is
+    // always inside the row), and they still reach the barrier.
+    const uint32_t o = w.within < w.g ? w.within : 0u;
+    const uint32_t w0 = fdiv(o, g.div_rec);
+    const uint32_t inner = o - w0 * g.rec;
+    // cell (j, r) is record j*recs_per_shard + rbase + w0: rbase is the
+    // wave's, w0 <= dmax the lane's record within the 1 KiB piece
+    const uint32_t rbase = uint32_t(r) * fdiv(uint32_t(w.g), g.div_rec) + fdiv(uint32_t(w.base), g.div_rec);
+    const uint32_t piece = uint32_t(__builtin_amdgcn_readfirstlane(w.within));  // lane 0: the piece's start
+    const uint32_t dmax = fdiv(piece + kRdpWaveBytes - 16, g.div_rec);
+    CellRef ref[K];
+#pragma unroll
+    for (int j = 0; j < K; ++j) ref[j] = cell_ref_run(g, uint32_t(j) * cg.recs_per_shard + rbase, w0, dmax);
+    u32x4 x[K];
+#pragma unroll
+    for (int j = 0; j < K; ++j) x[j] = cell_load_ref(g, ref[j], inner);
+    // while the cells are in flight: clear this row's Q accumulators and stage
+    // the RS tables (the barrier inside orders both before any use)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) qacc[r][e][lane] = 0;
     stage_tables<NT>(tab, rs);
-    const ChunkPos cp = chunk_pos(g, cg, ROWS);
-    if (!cp.ok) return;
-    const uint32_t inner = cp.inner, lane = cp.o;
+    const uint32_t soff = cg.region + uint32_t(w.base) + uint32_t(r) * uint32_t(w.g) + o;
     const uint64_t nb = cg.nb;
-    auto rec = [&](int j, int r) { return cell_rec(cg, cp, j, r); };
-    auto row = [&](int r) { return cp.rowbase + uint32_t(r) * cp.g; };
-    constexpr int DEPTH = kChunkDepth;
-    CellRef ref[DEPTH][K];
-    u32x4 x[DEPTH][K];
+    // Outputs that wmask switches off get a buffer resource of size 0, whose
+    // stores the hardware drops.  With no branches around the stores, the
+    // compiler cannot sink each output's products into a branch of its own
+    // and keep every input's fields live across them.
+    auto out = [&](uint8_t* p, uint32_t bit) { return ShardView<true>(p, (wmask & bit) ? nb : 0); };
+    if constexpr (DATA) {
 #pragma unroll
-    for (int d0 = 0; d0 < DEPTH && d0 < ROWS; ++d0)
+        for (int j = 0; j < K; ++j) ShardView<true>(d.p[j], nb).store(0, soff, x[j]);
+    }
+    const u32x4 pr = xor_all<K>(x);
+    out(par.p[0], kWP).store(0, soff, pr);
+    auto qadd = [&](int dg, const u32x4& v) {
+        atomicXor(&qacc[dg][0][lane], v.x);
+        atomicXor(&qacc[dg][1][lane], v.y);
+        atomicXor(&qacc[dg][2][lane], v.z);
+        atomicXor(&qacc[dg][3][lane], v.w);
+    };
 #pragma unroll
-        for (int j = 0; j < K; ++j) ref[d0][j] = cell_ref(g, rec(j, d0));
+    for (int j = 0; j < K; ++j) {
+        const int dg = (r + j) % P;
+        if (dg != P - 1) qadd(dg, x[j]);  // diagonal p-1 is not stored
+    }
+    if (r >= 1) qadd(r - 1, pr);
+    if constexpr (M > 0) {
+        u32x4 acc[M];
 #pragma unroll
-    for (int d0 = 0; d0 + 1 < DEPTH && d0 < ROWS; ++d0)
-#pragma unroll
-        for (int j = 0; j < K; ++j) x[d0][j] = cell_load_ref(g, ref[d0][j], inner);
-    u32x4 q[ROWS];
-#pragma unroll
-    for (int r = 0; r < ROWS; ++r) q[r] = u32x4{0, 0, 0, 0};
-    const ShardView<true> sp(par.p[0], (wmask & kWP) ? nb : 0);
-#pragma unroll
-    for (int r = 0; r < ROWS; ++r) {
-        const int c = r % DEPTH;
-        if (r + DEPTH - 1 < ROWS) {
-            const int n = (r + DEPTH - 1) % DEPTH;
-#pragma unroll
-            for (int j = 0; j < K; ++j) x[n][j] = cell_load_ref(g, ref[n][j], inner);
-        }
-        if (r + DEPTH < ROWS) {
-#pragma unroll
-            for (int j = 0; j < K; ++j) ref[c][j] = cell_ref(g, rec(j, r + DEPTH));
-        }
-        if constexpr (DATA) {
-#pragma unroll
-            for (int j = 0; j < K; ++j) ShardView<true>(d.p[j], nb).store(row(r), lane, x[c][j]);
-        }
-        const u32x4 pr = xor_all<K>(x[c]);
-        sp.store(row(r), lane, pr);
-        // cell (r, j) lies on diagonal (r + j) % p; the P cell of row r on r - 1
+        for (int i = 0; i < M; ++i) acc[i] = u32x4{0, 0, 0, 0};
 #pragma unroll
         for (int j = 0; j < K; ++j) {
-            const int dg = (r + j) % P;
-            if (dg != P - 1) q[dg] ^= x[c][j];
+            Gf8Fields f[4];
+            gf8_fields16(x[j], f);
+#pragma unroll
+            for (int i = 0; i < M; ++i) acc[i] = gf8_fma16(acc[i], f, tab[i * K + j]);
+            // read each input's tables from LDS next to their use, rather
+            // than all k*m of them up front into registers
+            asm volatile("" ::: "memory");
         }
-        if (r >= 1) q[r - 1] ^= pr;
-        if constexpr (M > 0) {
-            u32x4 acc[M];
 #pragma unroll
-            for (int i = 0; i < M; ++i) acc[i] = u32x4{0, 0, 0, 0};
-#pragma unroll
-            for (int j = 0; j < K; ++j) {
-                Gf8Fields f[4];
-                gf8_fields16(x[c][j], f);
-#pragma unroll
-                for (int i = 0; i < M; ++i) acc[i] = gf8_fma16(acc[i], f, tab[i * K + j]);
-            }
-#pragma unroll
-            for (int i = 0; i < M; ++i)
-                ShardView<true>(par.p[2 + i], (wmask & (1u << (kWRs + i))) ? nb : 0)
-                    .store(row(r), lane, acc[i]);
-        }
-        asm volatile("" ::: "memory");
+        for (int i = 0; i < M; ++i) out(par.p[2 + i], 1u << (kWRs + i)).store(0, soff, acc[i]);
     }
-    const ShardView<true> sq(par.p[1], (wmask & kWQ) ? nb : 0);
-#pragma unroll
-    for (int r = 0; r < ROWS; ++r) sq.store(row(r), lane, q[r]);
+    __syncthreads();
+    out(par.p[1], kWQ).store(0, soff, u32x4{qacc[r][0][lane], qacc[r][1][lane], qacc[r][2][lane], qacc[r][3][lane]});
 }
 
 // ------------------------------------------------------------------ RS decode
@@ -353,21 +349,23 @@ __global__ __launch_bounds__(kCBS) void chunk_rdp_decode_fixed(PagedGeom g, Chun
 // ------------------------------------------------------------------ dispatch
 // Launch the encode instantiation <P, K, M> with a table sized for it.
 template <int P, int K, int M>
-static void launch_encode(dim3 grid, hipStream_t st, const PagedGeom& g, const ChunkGeom& cg,
+static void launch_encode(hipStream_t st, const PagedGeom& g, const ChunkGeom& cg,
                           const Ptrs<kChunkMaxK>& d, const Ptrs<2 + kChunkMaxM>& par,
                           const uint32_t (*tab)[6], uint32_t wmask) {
     Gf8Tab<(K * M > 0 ? K * M : 1)> t{};
     for (int i = 0; i < K * M; ++i)
         for (int e = 0; e < 6; ++e) t.t[i][e] = tab[i][e];
+    // one block of p-1 waves per 1 KiB column piece
+    const dim3 rgrid(cg.nwaves), rblock((P - 1) * 64);
     if (wmask & kWData)
-        hipLaunchKernelGGL((chunk_encode_kernel<P, K, M, true>), grid, dim3(kCBS), 0, st, g, cg, d, par,
+        hipLaunchKernelGGL((chunk_encode_rows_kernel<P, K, M, true>), rgrid, rblock, 0, st, g, cg, d, par,
                            t, wmask);
     else
-        hipLaunchKernelGGL((chunk_encode_kernel<P, K, M, false>), grid, dim3(kCBS), 0, st, g, cg, d, par,
+        hipLaunchKernelGGL((chunk_encode_rows_kernel<P, K, M, false>), rgrid, rblock, 0, st, g, cg, d, par,
                            t, wmask);
 }
 
-typedef void (*EncLauncher)(dim3, hipStream_t, const PagedGeom&, const ChunkGeom&,
+typedef void (*EncLauncher)(hipStream_t, const PagedGeom&, const ChunkGeom&,
                             const Ptrs<kChunkMaxK>&, const Ptrs<2 + kChunkMaxM>&,
                             const uint32_t (*)[6], uint32_t);
 
@@ -568,7 +566,7 @@ static int run_encode(const ChunkArgs& a, uint32_t wmask, hipStream_t st, const 
     cauchy(a.k, a.m, C);
     uint32_t tab[kChunkMaxK * kChunkMaxM][6];
     for (int i = 0; i < a.k * a.m; ++i) perm_tables(C[i], tab[i]);
-    L(chunk_grid(a.cg), st, a.g, a.cg, a.d, a.par, tab, wmask);
+    L(st, a.g, a.cg, a.d, a.par, tab, wmask);
     return check_launch(fn);
 }
 

@@ -74,6 +74,19 @@ struct Xor3Acc {
     __device__ __forceinline__ u32x4 get() const { return held ? a ^ pend : a; }
 };
 
+// Xor3Acc for one dword.
+struct Xor3Acc1 {
+    uint32_t a, pend;
+    bool held;
+    __device__ __forceinline__ Xor3Acc1() : a(0), pend(0), held(false) {}
+    __device__ __forceinline__ void add(uint32_t x) {
+        if (held) a = xor3(a, pend, x);
+        else pend = x;
+        held = !held;
+    }
+    __device__ __forceinline__ uint32_t get() const { return held ? a ^ pend : a; }
+};
+
 // The same interface with 2-input XORs and one register per accumulator, for
 // kernels whose accumulators alone would otherwise crowd the register file
 // (RDP over p >= 11 keeps 2(p-1) of them).

@@ -84,6 +84,27 @@ __device__ __forceinline__ CellRef cell_ref(const PagedGeom& g, uint32_t w) {
     return CellRef{valid ? layer * g.layer_recs + (t & ((1u << g.page_shift) - 1)) : kNoCell, page};
 }
 
+// cell_ref for the lanes of one wave whose records are rec0 + d, with rec0
+// wave-uniform and 0 <= d <= dmax per lane (the 16-byte cells of one 1 KiB
+// stream piece).  When the whole run lies in one sequence's tokens of one
+// layer and before the padding, the record's (layer, sequence, token) is
+// decomposed once for the wave in scalar registers and each lane only adds
+// its token offset; otherwise every lane decomposes its own record.
+__device__ __forceinline__ CellRef cell_ref_run(const PagedGeom& g, uint32_t rec0, uint32_t d,
+                                                uint32_t dmax) {
+    const uint32_t lb = fdiv(rec0, g.div_t);
+    const uint32_t t0 = rec0 - lb * g.div_t.d;
+    const uint32_t nrec = uint32_t(g.recs_total);  // < 2^32 (make_geom)
+    if (t0 + dmax < g.div_t.d && nrec > dmax && rec0 < nrec - dmax) {
+        const uint32_t layer = fdiv(lb, g.div_b);
+        const uint32_t b = lb - layer * g.div_b.d;
+        const uint32_t t = t0 + g.tok_off + d;
+        const int32_t* row = g.table + b * g.pps;
+        return CellRef{layer * g.layer_recs + (t & ((1u << g.page_shift) - 1)), uint32_t(row[t >> g.page_shift])};
+    }
+    return cell_ref(g, rec0 + d);
+}
+
 __device__ __forceinline__ bool cell_valid(const PagedGeom& g, const CellRef& c) {
     return c.base != kNoCell && c.page < g.pool_pages;
 }

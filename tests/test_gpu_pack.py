@@ -20,9 +20,11 @@ def _kv(B, H, T, D, dtype, seed):
     return k, v
 
 
-# (B, H, T, D): the single-parity stripe's shard shape (2 x 512 tokens x 1 head
-# x 128, bf16: 256 KiB of K||V), odd n and T, the reference demo's shape
-@pytest.mark.parametrize("B,H,T,D", [(1, 1, 512, 128), (1, 3, 7, 1), (2, 1, 5, 3), (1, 8, 512, 128)])
+# (B, H, T, D): one 256 KiB shard of the XOR k=4 stripe (512 tokens x 1 head x
+# 128 bf16, K||V), the whole k=4 stripe (4 x 256 KiB: 2048 tokens), odd n and
+# T, the reference demo's shape
+@pytest.mark.parametrize("B,H,T,D", [(1, 1, 512, 128), (1, 1, 2048, 128), (1, 3, 7, 1), (2, 1, 5, 3),
+                                     (1, 8, 512, 128)])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 def test_pack_unpack_match_oracle(pkg, ora, gpu, B, H, T, D, dtype):
     k, v = _kv(B, H, T, D, dtype, seed=B * 100 + H * 10 + T)
