@@ -33,9 +33,10 @@ What differs:
   * the H2D "probe" copy is made only when asked for (``probe_h2d=True``);
   * any backend with ``forward_extend`` is hooked, not only FlashInfer's
     (ROCm serving backends are not FlashInfer).
-The gather of rows to dst is the reference's; the exchange that replaces it
-across GPUs (each rank reducing its own share of the linear combinations) is
-not part of this one-GPU build.
+The gather of rows to dst is the reference's, and kept: dst receives one row
+per other rank, each over its own link of a fully connected node, whereas
+XOR-reducing per-rank parity contributions would bring it two rows (P's and
+Q's share) per rank.
 """
 from __future__ import annotations
 
