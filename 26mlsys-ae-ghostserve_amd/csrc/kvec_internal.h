@@ -115,8 +115,8 @@ __device__ __forceinline__ u32x4 xor_all(const u32x4* v) {
 
 // ------------------------------------------------------------- shard views
 // One shard buffer seen by a kernel.  Shards below 4 GiB use a buffer
-// resource: the row-plane offset rides in an SGPR (soffset), the lane offset
-// in one VGPR, and there is no 64-bit address arithmetic per access.  Larger
+// resource: a load's row offset rides in an SGPR (soffset), the lane offset in
+// one VGPR, and there is no 64-bit address arithmetic per access.  Larger
 // shards use 64-bit global addressing.  Loads and stores are non-temporal:
 // every byte is read or written once per launch.
 constexpr int kAuxLoadNT = 2;        // nt

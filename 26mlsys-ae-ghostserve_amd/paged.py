@@ -83,7 +83,8 @@ class PagedKV:
 
 
 def rdp_row_bytes_for(kv: PagedKV, k: int, p: int) -> int:
-    """Row-plane size for kv's stream: a multiple of one token record (K and V)."""
+    """RDP row size R (each shard is (p-1)*R bytes) for kv's stream: a
+    multiple of one token record (K and V)."""
     from .spec import rdp_row_bytes
     return rdp_row_bytes(kv.stream_bytes(), k, p, 2 * kv.token_bytes)
 

@@ -13,7 +13,8 @@ codes the shard tensor with textbook RDP (Corbett et al., FAST 2004) over the
 smallest prime p > num_data_shards (p = 7 for six data shards): the data rows
 are shards, row nd is P and row nd+1 is Q, and fused_recovery_full_kv then
 rebuilds any two lost rows (data, P or Q) byte-exact.  Its shard size is the
-reference's rounded up so that every row is p-1 whole 16-byte row planes.
+reference's rounded up so that every shard row splits into p-1 RDP rows of a
+whole number of 16-byte cells.
 
 K/V may be any 2-byte dtype (coded as raw bits; results come back in the input
 dtype).
@@ -73,8 +74,9 @@ def spec_prime(num_data_shards: int) -> int:
 
 
 def spec_shard_size_words(total_words: int, num_data_shards: int, p: int):
-    """The reference's shard size rounded up to whole row planes: p-1 rows of
-    a multiple of 16 bytes (8 words) each.  Returns (shard_size, pad_words)."""
+    """The reference's shard size rounded up so that a shard row splits into
+    p-1 RDP rows of a multiple of 16 bytes (8 words) each.  Returns
+    (shard_size, pad_words)."""
     S, _ = determine_shard_size_words(total_words, num_data_shards)
     q = 8 * (p - 1)
     S = -(-S // q) * q
