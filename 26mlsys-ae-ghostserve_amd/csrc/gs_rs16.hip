@@ -342,6 +342,11 @@ __device__ __forceinline__ void rs_horner_tail(const RsJob& j, uint32_t red2, ui
 }
 
 constexpr int kRsNW = 2;                              // windows per thread
+// Non-temporal stores of the encode's parity rows and the reconstruct's
+// rebuilt rows, as measured on the 512 MiB stream: plain for the encode (whose
+// data-row copy writes alongside; nt 1 % slower), nt for the reconstruct (2 %
+// faster).
+constexpr bool kRsEncNT = false, kRsRecNT = true;
 constexpr uint32_t kRsTile = kTileBytes * kRsNW;      // logical bytes per row per tile
 constexpr uint32_t kRsStage = kRsTile + 16;           // LDS staging row
 
@@ -352,7 +357,7 @@ constexpr uint32_t kRsStage = kRsTile + 16;           // LDS staging row
 // outputs in one group, accumulators in natural word order; red2 holds the
 // reduction word in both halves).  The two are separate loops: sharing one
 // loop made the encode kernel spill registers.
-template <bool HORNER>
+template <bool HORNER, bool NT>
 __device__ __forceinline__ void rs_run_tiles(const RsJob& j, const uint32_t (*ptab)[kRs16Tab],
                                              uint8_t* tile, uint32_t red2) {
     const uint64_t Sb = uint64_t(j.S) * 2;
@@ -400,7 +405,7 @@ __device__ __forceinline__ void rs_run_tiles(const RsJob& j, const uint32_t (*pt
                                : join_bytes(acc[n][g]);
             __syncthreads();
             for (int g = 0; g < G; ++g)
-                tile_store(reinterpret_cast<uint8_t*>(j.out_rows[og + g]) + t0b, tile + g * kRsStage,
+                tile_store<NT>(reinterpret_cast<uint8_t*>(j.out_rows[og + g]) + t0b, tile + g * kRsStage,
                            nbytes);
             __syncthreads();
         }
@@ -441,8 +446,8 @@ __global__ __launch_bounds__(kTB) __attribute__((amdgpu_waves_per_eu(4))) void r
         if (v != basis[t][b]) s_horner = 0;
     }
     __syncthreads();
-    if (s_horner) rs_run_tiles<true>(j, ptab, tile, uint32_t(s_red) * 0x10001u);
-    else rs_run_tiles<false>(j, ptab, tile, 0u);
+    if (s_horner) rs_run_tiles<true, kRsEncNT>(j, ptab, tile, uint32_t(s_red) * 0x10001u);
+    else rs_run_tiles<false, kRsEncNT>(j, ptab, tile, 0u);
 }
 
 // benchmark/rs/kernel.cu:105-222 with the right-hand side folded into the
@@ -556,7 +561,7 @@ __global__ __launch_bounds__(kTB) __attribute__((amdgpu_waves_per_eu(4))) void r
     __syncthreads();
     rs_build_perm_tables(ptab, basis, coef, m * nin, ex, lg);
     __syncthreads();
-    rs_run_tiles<false>(j, ptab, tile, 0u);
+    rs_run_tiles<false, kRsRecNT>(j, ptab, tile, 0u);
 }
 
 static int rs_grid(int64_t S) {

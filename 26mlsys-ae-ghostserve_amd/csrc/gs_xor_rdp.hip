@@ -95,8 +95,9 @@ __device__ __forceinline__ u32x4 xor_rows_batched(const uint8_t* in, uint32_t Sb
 
 // One tile of XOR-of-rows, written to up to two outputs (row base addresses).
 // With fc.dst set, rows lo..hi-1 of `in` (the whole flat range of fc, no
-// skip) are also copied to fc.dst by the same loads.
-template <int ND>
+// skip) are also copied to fc.dst by the same loads.  NT: non-temporal
+// stores of the outputs.
+template <int ND, bool NT = false>
 __device__ __forceinline__ void xor_rows_tile(const uint8_t* in, uint64_t Sb, uint32_t in_bytes,
                                               RowSet rs, uint8_t* out0, uint8_t* out1,
                                               const FlatCopy& fc, uint8_t* tile) {
@@ -137,8 +138,8 @@ __device__ __forceinline__ void xor_rows_tile(const uint8_t* in, uint64_t Sb, ui
     }
     *reinterpret_cast<u32x4*>(tile + 16 * threadIdx.x) = acc;
     __syncthreads();
-    if (out0) tile_store(out0 + t0, tile, nbytes);
-    if (out1) tile_store(out1 + t0, tile, nbytes);
+    if (out0) tile_store<NT>(out0 + t0, tile, nbytes);
+    if (out1) tile_store<NT>(out1 + t0, tile, nbytes);
 }
 
 template <int ND>
@@ -166,8 +167,9 @@ __global__ __launch_bounds__(kTB) void xor_reconstruct_kernel(const uint8_t* enc
         rs = RowSet{0, nd, -1, -1};
     else
         return;
-    xor_rows_tile<ND>(enc, Sb, in_bytes, rs, rec + uint64_t(m) * Sb, rec_missing,
-                      FlatCopy{nullptr, nullptr, 0}, tile);
+    // non-temporal output stores: 121.2 against 130.2 us on the 512 MiB stream
+    xor_rows_tile<ND, true>(enc, Sb, in_bytes, rs, rec + uint64_t(m) * Sb, rec_missing,
+                            FlatCopy{nullptr, nullptr, 0}, tile);
 }
 
 // ------------------------------------------------------- XOR encode from K, V
