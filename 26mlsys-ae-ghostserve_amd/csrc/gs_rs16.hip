@@ -23,6 +23,7 @@
 // zero-pivot skip included), from indices read on the device.
 #include "gf8.h"
 #include "tile_engine.h"
+#include "piece_walk.h"
 
 namespace kvec {
 
@@ -450,47 +451,67 @@ __global__ __launch_bounds__(kTB) __attribute__((amdgpu_waves_per_eu(4))) void r
     else rs_run_tiles<false, kRsEncNT>(j, ptab, tile, 0u);
 }
 
-// benchmark/rs/kernel.cu:105-222 with the right-hand side folded into the
-// coefficients.  Inputs: the k - m surviving data rows, then the m parity rows
-// of parity_used; outputs: the m missing data rows.
-__global__ __launch_bounds__(kTB) __attribute__((amdgpu_waves_per_eu(4))) void rs16_reconstruct_kernel(uint16_t* sh, int64_t S, int k,
-                                                               int mpar, int m,
-                                                               const int32_t* missing,
-                                                               const int32_t* pused,
-                                                               const uint16_t* ex,
-                                                               const uint16_t* lg) {
-    __shared__ __attribute__((aligned(16))) uint32_t ptab[kRsMaxTables][kRs16Tab];
-    __shared__ uint16_t basis[kRsMaxTables][16];
-    __shared__ uint16_t coef[kRsMaxTables];
-    __shared__ uint16_t inv[kRsMaxM * kRsMaxM];
-    __shared__ int s_miss[kRsMaxM], s_pu[kRsMaxM];
-    __shared__ int s_ok;
-    __shared__ __attribute__((aligned(16))) uint8_t tile[kRsGroup * kRsStage];
-    __shared__ RsJob j;
+// The reconstruct's plan, shared by its kernels: which rows are inputs and
+// outputs, and one coefficient per (output, input) pair.
+//   inputs  the k - m surviving data rows in index order, then the m parity
+//           rows of parity_used;
+//   outputs the m missing data rows.
+// benchmark/rs/kernel.cu:105-222 computes the right-hand side b (parity row
+// XOR the known data terms) and then x = V^-1 b; folding the two steps into
+// one coefficient per pair is exact in the field, so the bytes are those of
+// the two-step computation.
+struct RsRecPlan {
+    int miss[kRsMaxM], pu[kRsMaxM];
+    int in_row[kRsMaxTables];       // input i is row in_row[i] of the shard tensor
+    int nin;
+    int ok;
+    uint16_t inv[kRsMaxM * kRsMaxM];
+    uint16_t coef[kRsMaxTables];    // coefficient of input i for output c at [c * nin + i]
+    uint16_t basis[kRsMaxTables][16];
+};
+
+// First phase (all threads; ends with a barrier): the indices, read from
+// device memory, and the input rows.  A row index outside the tensor would be
+// an out-of-bounds write, and repeated indices would overflow the LDS tables,
+// so either leaves pl.ok = 0 and the call writes nothing.
+__device__ __forceinline__ void rs16_rec_rows(RsRecPlan& pl, int k, int mpar, int m, const int32_t* missing,
+                                              const int32_t* pused) {
     if (threadIdx.x < m) {
-        s_miss[threadIdx.x] = missing[threadIdx.x];
-        s_pu[threadIdx.x] = pused[threadIdx.x];
+        pl.miss[threadIdx.x] = missing[threadIdx.x];
+        pl.pu[threadIdx.x] = pused[threadIdx.x];
     }
     __syncthreads();
-    // Indices come from device memory: a row outside the tensor would be an
-    // out-of-bounds write, and repeated indices would overflow the LDS tables,
-    // so either makes the call write nothing.
     if (threadIdx.x == 0) {
         int ok = 1;
         for (int q = 0; q < m; ++q) {
-            ok &= (s_miss[q] >= 0 && s_miss[q] < k && s_pu[q] >= 0 && s_pu[q] < mpar);
-            for (int q2 = 0; q2 < q; ++q2) ok &= (s_miss[q2] != s_miss[q]);
+            ok &= (pl.miss[q] >= 0 && pl.miss[q] < k && pl.pu[q] >= 0 && pl.pu[q] < mpar);
+            for (int q2 = 0; q2 < q; ++q2) ok &= (pl.miss[q2] != pl.miss[q]);
         }
-        s_ok = ok;
+        pl.ok = ok;
+        int n = 0;
+        for (int i = 0; i < k; ++i) {
+            bool miss = false;
+            for (int q = 0; q < m; ++q) miss |= (pl.miss[q] == i);
+            if (!miss && n < kRsMaxTables) pl.in_row[n++] = i;
+        }
+        for (int r = 0; r < m && n < kRsMaxTables; ++r) pl.in_row[n++] = k + pl.pu[r];
+        pl.nin = n;
     }
     __syncthreads();
-    if (!s_ok) return;
+}
+
+// Second phase (all threads, pl.ok set; ends with a barrier): the inverse of
+// V[r][c] = alpha^((pu_r + 1) miss_c) by the reference's Gauss-Jordan (pivot
+// order and zero-pivot skip included), the folded coefficients and their
+// v_perm byte maps.
+__device__ __forceinline__ void rs16_rec_tables(RsRecPlan& pl, uint32_t (*ptab)[kRs16Tab], int k, int m,
+                                                const uint16_t* ex, const uint16_t* lg) {
     if (threadIdx.x == 0) {
         uint16_t V[kRsMaxM * kRsMaxM];
         for (int r = 0; r < m; ++r)
-            for (int c = 0; c < m; ++c) V[r * m + c] = ex[((s_pu[r] + 1) * s_miss[c]) % kGfOrder];
+            for (int c = 0; c < m; ++c) V[r * m + c] = ex[((pl.pu[r] + 1) * pl.miss[c]) % kGfOrder];
         for (int r = 0; r < m; ++r)
-            for (int c = 0; c < m; ++c) inv[r * m + c] = (r == c) ? 1 : 0;
+            for (int c = 0; c < m; ++c) pl.inv[r * m + c] = (r == c) ? 1 : 0;
         for (int i = 0; i < m; ++i) {
             int pr = i;
             while (pr < m && V[pr * m + i] == 0) ++pr;
@@ -500,16 +521,16 @@ __global__ __launch_bounds__(kTB) __attribute__((amdgpu_waves_per_eu(4))) void r
                     uint16_t t = V[i * m + c];
                     V[i * m + c] = V[pr * m + c];
                     V[pr * m + c] = t;
-                    t = inv[i * m + c];
-                    inv[i * m + c] = inv[pr * m + c];
-                    inv[pr * m + c] = t;
+                    t = pl.inv[i * m + c];
+                    pl.inv[i * m + c] = pl.inv[pr * m + c];
+                    pl.inv[pr * m + c] = t;
                 }
             const uint16_t piv = V[i * m + i];
             if (piv == 0) continue;
             const uint16_t ip = gf16_div_tab(1, piv, ex, lg);
             for (int c = 0; c < m; ++c) {
                 V[i * m + c] = gf16_mul_tab(V[i * m + c], ip, ex, lg);
-                inv[i * m + c] = gf16_mul_tab(inv[i * m + c], ip, ex, lg);
+                pl.inv[i * m + c] = gf16_mul_tab(pl.inv[i * m + c], ip, ex, lg);
             }
             for (int r = 0; r < m; ++r) {
                 if (r == i) continue;
@@ -517,51 +538,248 @@ __global__ __launch_bounds__(kTB) __attribute__((amdgpu_waves_per_eu(4))) void r
                 if (!f) continue;
                 for (int c = 0; c < m; ++c) {
                     V[r * m + c] ^= gf16_mul_tab(f, V[i * m + c], ex, lg);
-                    inv[r * m + c] ^= gf16_mul_tab(f, inv[i * m + c], ex, lg);
+                    pl.inv[r * m + c] ^= gf16_mul_tab(f, pl.inv[i * m + c], ex, lg);
                 }
             }
         }
     }
     __syncthreads();
-    // inputs: surviving data rows in index order, then the used parity rows
-    if (threadIdx.x == 0) {
-        j.S = S;
-        j.nout = m;
-        j.copy = FlatCopy{nullptr, nullptr, 0};
-        int n = 0;
-        for (int i = 0; i < k; ++i) {
-            bool miss = false;
-            for (int q = 0; q < m; ++q) miss |= (s_miss[q] == i);
-            if (!miss && n < kRsMaxTables) j.in_rows[n++] = sh + uint64_t(i) * S;
-        }
-        for (int r = 0; r < m && n < kRsMaxTables; ++r) j.in_rows[n++] = sh + uint64_t(k + s_pu[r]) * S;
-        j.nin = n;
-        for (int c = 0; c < m; ++c) j.out_rows[c] = sh + uint64_t(s_miss[c]) * S;
-    }
-    __syncthreads();
-    const int nin = j.nin, ndata = nin - m;
-    // coefficient of input `in` for output c
+    const int nin = pl.nin, ndata = nin - m;
     for (int t = threadIdx.x; t < m * nin; t += kTB) {
         const int c = t / nin, in = t % nin;
         uint16_t v = 0;
         if (in < ndata) {
-            int i = 0, seen = -1;
-            for (; i < k; ++i) {
-                bool miss = false;
-                for (int q = 0; q < m; ++q) miss |= (s_miss[q] == i);
-                if (!miss && ++seen == in) break;
-            }
+            const int i = pl.in_row[in];
             for (int r = 0; r < m; ++r)
-                v ^= gf16_mul_tab(inv[c * m + r], ex[((s_pu[r] + 1) * i) % kGfOrder], ex, lg);
+                v ^= gf16_mul_tab(pl.inv[c * m + r], ex[((pl.pu[r] + 1) * i) % kGfOrder], ex, lg);
         } else {
-            v = inv[c * m + (in - ndata)];
+            v = pl.inv[c * m + (in - ndata)];
         }
-        coef[t] = v;
+        pl.coef[t] = v;
     }
     __syncthreads();
-    rs_build_perm_tables(ptab, basis, coef, m * nin, ex, lg);
+    rs_build_perm_tables(ptab, pl.basis, pl.coef, m * nin, ex, lg);
+    __syncthreads();
+}
+
+// benchmark/rs/kernel.cu:105-222, tile engine: any k, m and row size.
+__global__ __launch_bounds__(kTB) __attribute__((amdgpu_waves_per_eu(4))) void rs16_reconstruct_kernel(uint16_t* sh, int64_t S, int k,
+                                                               int mpar, int m,
+                                                               const int32_t* missing,
+                                                               const int32_t* pused,
+                                                               const uint16_t* ex,
+                                                               const uint16_t* lg) {
+    __shared__ __attribute__((aligned(16))) uint32_t ptab[kRsMaxTables][kRs16Tab];
+    __shared__ RsRecPlan pl;
+    __shared__ __attribute__((aligned(16))) uint8_t tile[kRsGroup * kRsStage];
+    __shared__ RsJob j;
+    rs16_rec_rows(pl, k, mpar, m, missing, pused);
+    if (!pl.ok) return;
+    rs16_rec_tables(pl, ptab, k, m, ex, lg);
+    if (threadIdx.x == 0) {
+        j.S = S;
+        j.nout = m;
+        j.copy = FlatCopy{nullptr, nullptr, 0};
+        j.nin = pl.nin;
+        for (int i = 0; i < pl.nin; ++i) j.in_rows[i] = sh + uint64_t(pl.in_row[i]) * S;
+        for (int c = 0; c < m; ++c) j.out_rows[c] = sh + uint64_t(pl.miss[c]) * S;
+    }
     __syncthreads();
     rs_run_tiles<false, kRsRecNT>(j, ptab, tile, 0u);
+}
+
+// ------------------------------------------------------------ piece kernel
+// The reconstruct on the piece engine (piece_walk.h): waves walk pieces of
+// 64 windows of every row, loaded and stored at the rows' own alignment,
+// every input row's window of a piece requested at once and the next piece's
+// requested before the current one is coded; no LDS tiles and no block
+// barriers.  For up to kRsPieceMaxIn inputs, up to kRsGroup outputs and
+// tensors of fewer than 2^31 bytes.  Measured on the 512 MiB stream against
+// the tile kernel (same box): the reconstruct of 2 rows 165 against 168-196
+// us with the folded byte maps, 149.6 us with the syndromes by Horner's rule
+// below; the encode on pieces took 279-304 against 245-255 us (with aligned
+// or misaligned data-row stores alike), so the encode stays on the tiles.
+constexpr int kRsPieceMaxIn = 8;
+constexpr uint32_t kRsPieceBlocks = 1024;   // persistent: the tables are built once per block
+
+// Outputs of one piece by the byte maps: out[g] = XOR_i c(g, i) * x_i, the
+// coefficient of input i for output g at ptab[g * NIN + i].  One
+// coefficient's byte maps (24 dwords) and one input's fields are live at a
+// time: the LDS reads stay next to their use (memory clobber) and no product
+// moves to another coefficient (scheduling barrier).  Without the fences the
+// compiler reads every map of an input at once and spills.
+template <int NIN, int M>
+__device__ __forceinline__ void rs_piece_mix(const u32x4* x, const uint32_t (*ptab)[kRs16Tab], u32x4* out) {
+    uint32_t acc[M][4];
+#pragma unroll
+    for (int g = 0; g < M; ++g) acc[g][0] = acc[g][1] = acc[g][2] = acc[g][3] = 0;
+#pragma unroll
+    for (int i = 0; i < NIN; ++i) {
+        uint32_t by[4];
+        split_bytes(x[i], by);
+        Gf8Fields f[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) f[q] = gf8_fields(by[q]);
+#pragma unroll
+        for (int g = 0; g < M; ++g) {
+            const uint32_t* T = ptab[g * NIN + i];
+            acc[g][0] = gf16_fma2(acc[g][0], f[0], T + 0, f[1], T + 6);
+            acc[g][1] = gf16_fma2(acc[g][1], f[0], T + 12, f[1], T + 18);
+            acc[g][2] = gf16_fma2(acc[g][2], f[2], T + 0, f[3], T + 6);
+            acc[g][3] = gf16_fma2(acc[g][3], f[2], T + 12, f[3], T + 18);
+            // the accumulators pass through the asm, so the products are
+            // computed here rather than sunk towards the final join
+            asm volatile("" : "+v"(acc[g][0]), "+v"(acc[g][1]), "+v"(acc[g][2]), "+v"(acc[g][3]) :: "memory");
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+#pragma unroll
+    for (int g = 0; g < M; ++g) out[g] = join_bytes(acc[g]);
+}
+
+// Wave-uniform copy of an LDS int.
+__device__ __forceinline__ uint32_t lds_uniform(const int& v) {
+    return uint32_t(__builtin_amdgcn_readfirstlane(v));
+}
+
+// Multiply four packed word pairs by alpha^n (n doublings; n is wave-uniform).
+__device__ __forceinline__ u32x4 gf16_dbl_n(u32x4 v, uint32_t n, uint32_t red2) {
+    for (uint32_t t = 0; t < n; ++t)
+        v = u32x4{gf16_dbl2(v.x, red2), gf16_dbl2(v.y, red2), gf16_dbl2(v.z, red2), gf16_dbl2(v.w, red2)};
+    return v;
+}
+
+// The reconstruct by Horner's rule, for tables with alpha = 2.  The inputs
+// x[] are the ND = NIN - M surviving data rows (rows row[0] < row[1] < ...)
+// and the M parity rows of parity_used.  Each parity syndrome
+//     b_r = Par_{pu_r} ^ XOR_j D_{row[j]} * alpha^((pu_r + 1) row[j])
+// folds the data rows from the highest down, the accumulator multiplied by
+// alpha^((pu_r + 1) (row[j+1] - row[j])) between them (dbl[r][j] doublings;
+// dbl[r][ND-1] brings the lowest row to its power); then only
+// out_c = XOR_r inv[c][r] b_r takes byte maps (itab, M * M coefficients).
+// This is the same field arithmetic as the folded coefficients, so the bytes
+// are the reference's.
+template <int NIN, int M>
+__device__ __forceinline__ void rs_rec_horner(const u32x4* x, const uint32_t (*dbl)[NIN], uint32_t red2,
+                                              const uint32_t (*itab)[kRs16Tab], u32x4* out) {
+    constexpr int ND = NIN - M;
+    u32x4 b[M];
+#pragma unroll
+    for (int r = 0; r < M; ++r) {
+        u32x4 a = ND > 0 ? x[ND > 0 ? ND - 1 : 0] : u32x4{0, 0, 0, 0};
+#pragma unroll
+        for (int j = ND - 2; j >= 0; --j) a = gf16_dbl_n(a, dbl[r][j], red2) ^ x[j];
+        if (ND > 0) a = gf16_dbl_n(a, dbl[r][ND > 0 ? ND - 1 : 0], red2);
+        b[r] = a ^ x[ND + r];
+        asm volatile("" : "+v"(b[r].x), "+v"(b[r].y), "+v"(b[r].z), "+v"(b[r].w));
+    }
+    rs_piece_mix<M, M>(b, itab, out);
+}
+
+// reconstruct_rs_u16_inplace on the piece engine: NIN = k inputs, M = m
+// outputs.  The shard tensor starts b15 bytes past base_al (16-aligned); the
+// resource covers res_bytes from base_al.
+template <int NIN, int M>
+__global__ __launch_bounds__(kTB) __attribute__((amdgpu_waves_per_eu(4))) void rs16_reconstruct_piece_kernel(
+        uint8_t* base_al, uint32_t b15, uint32_t res_bytes, uint32_t Sb, int mpar,
+        const int32_t* missing, const int32_t* pused, const uint16_t* ex, const uint16_t* lg) {
+    constexpr int ND = NIN - M;
+    // the folded coefficients (M * NIN), then those of the inverse (M * M)
+    __shared__ __attribute__((aligned(16))) uint32_t ptab[M * NIN + M * M][kRs16Tab];
+    __shared__ RsRecPlan pl;
+    __shared__ int s_horner;
+    __shared__ uint16_t s_red;
+    rs16_rec_rows(pl, NIN, mpar, M, missing, pused);
+    if (!pl.ok) return;
+    const __amdgpu_buffer_rsrc_t rs = chunk_rsrc(base_al, res_bytes);
+    uint32_t in[NIN], lim[NIN], out[M];
+#pragma unroll
+    for (int i = 0; i < NIN; ++i) {
+        const uint32_t r = lds_uniform(pl.in_row[i]);
+        in[i] = b15 + r * Sb;
+        lim[i] = r + 1 == uint32_t(NIN + mpar) ? res_bytes - 16 : ~0u;
+    }
+#pragma unroll
+    for (int g = 0; g < M; ++g) out[g] = b15 + lds_uniform(pl.miss[g]) * Sb;
+    const PieceWalk wk = wave_walk();
+    const uint32_t lane16 = 16 * (threadIdx.x & 63);
+    // the first piece's windows are in flight while the tables are built
+    u32x4 c[NIN];
+    if (wk.first < Sb) {
+#pragma unroll
+        for (int i = 0; i < NIN; ++i) c[i] = piece_load(rs, in[i], wk.first + lane16, lim[i]);
+    }
+    rs16_rec_tables(pl, ptab, NIN, M, ex, lg);
+    rs_build_perm_tables(ptab + M * NIN, pl.basis, pl.inv, M * M, ex, lg);
+    // Horner's rule when every coefficient alpha^((pu_r + 1) i) of a surviving
+    // data row, as the caller's tables multiply by it, equals its chain of
+    // doublings on all sixteen basis symbols
+    if (threadIdx.x == 0) {
+        s_red = gf16_mul_tab(0x8000, 2, ex, lg);
+        s_horner = 1;
+    }
+    __syncthreads();
+    for (int e = threadIdx.x; e < M * ND * 16; e += kTB) {
+        const int r = e / (ND * 16), j = (e >> 4) % ND, b = e & 15;
+        const int n = (pl.pu[r] + 1) * pl.in_row[j];
+        const uint16_t cf = ex[n % kGfOrder];
+        uint16_t v = uint16_t(1u << b);
+        for (int d = 0; d < n; ++d) v = gf16_dbl(v, s_red);
+        if (v != gf16_mul_tab(uint16_t(1u << b), cf, ex, lg)) s_horner = 0;
+    }
+    __syncthreads();
+    const bool horner = __builtin_amdgcn_readfirstlane(s_horner) != 0;
+    const uint32_t red2 = uint32_t(s_red) * 0x10001u;
+    uint32_t dbl[M][NIN];
+#pragma unroll
+    for (int r = 0; r < M; ++r) {
+        const uint32_t f = lds_uniform(pl.pu[r]) + 1;
+#pragma unroll
+        for (int j = 0; j < NIN; ++j)
+            dbl[r][j] = j + 1 < ND ? f * (lds_uniform(pl.in_row[j + 1]) - lds_uniform(pl.in_row[j]))
+                                   : (j + 1 == ND ? f * lds_uniform(pl.in_row[0]) : 0u);
+    }
+    for (uint32_t P = wk.first; P < Sb; P += wk.stride) {
+        const bool last = P + wk.stride >= Sb;
+        u32x4 n[NIN];
+        if (!last) {
+#pragma unroll
+            for (int i = 0; i < NIN; ++i) n[i] = piece_load(rs, in[i], P + wk.stride + lane16, lim[i]);
+        }
+        // the byte maps are read from LDS at their use in every piece:
+        // hoisted out of the loop they would take 24 registers per coefficient
+        asm volatile("" ::: "memory");
+        u32x4 o[M];
+        if (horner) rs_rec_horner<NIN, M>(c, dbl, red2, ptab + M * NIN, o);
+        else rs_piece_mix<NIN, M>(c, ptab, o);
+#pragma unroll
+        for (int g = 0; g < M; ++g) piece_store<kRsRecNT>(rs, out[g], P + lane16, Sb, o[g]);
+        if (!last) {
+#pragma unroll
+            for (int i = 0; i < NIN; ++i) c[i] = n[i];
+        }
+    }
+}
+
+// Piece-kernel instances: [k - 1][m - 1] for k <= kRsPieceMaxIn, m <= kRsGroup.
+typedef void (*RsRecPieceFn)(uint8_t*, uint32_t, uint32_t, uint32_t, int, const int32_t*, const int32_t*,
+                           const uint16_t*, const uint16_t*);
+template <int... I>
+struct RsPieceTable {
+    static constexpr RsRecPieceFn rec[sizeof...(I)][kRsGroup] = {
+        {rs16_reconstruct_piece_kernel<I + 1, 1>, rs16_reconstruct_piece_kernel<I + 1, 2>}...};
+};
+using RsPiece = RsPieceTable<0, 1, 2, 3, 4, 5, 6, 7>;
+static_assert(kRsPieceMaxIn == 8 && kRsGroup == 2, "instance table");
+
+// Resource bytes from the 16-aligned address at or below p to the end of
+// [p, p + n), or 0 when that reaches 2^31 (the piece kernel's limit).
+static uint32_t piece_res_bytes(const void* p, uint64_t n) {
+    const uint64_t r = ((reinterpret_cast<uintptr_t>(p) & 15) + n + 15) & ~uint64_t(15);
+    return r < (uint64_t(1) << 31) ? uint32_t(r) : 0u;
+}
+static uint8_t* align_down16(const void* p) {
+    return reinterpret_cast<uint8_t*>(reinterpret_cast<uintptr_t>(p) & ~uintptr_t(15));
 }
 
 static int rs_grid(int64_t S) {
@@ -650,7 +868,6 @@ extern "C" int kvec_rs16_reconstruct(void* shards, int shard_size, int data_shar
                                      int parity_shards, const int32_t* missing_data, int m,
                                      const int32_t* parity_used, const uint16_t* gf_exp,
                                      const uint16_t* gf_log, void* stream) {
-    (void)parity_shards;
     if (m == 0) return KVEC_OK;
     if (m < 0 || m > kRsMaxM)
         return set_error(KVEC_EINVAL, "kvec_rs16_reconstruct: m=%d (must be <= %d)", m, kRsMaxM);
@@ -663,6 +880,14 @@ extern "C" int kvec_rs16_reconstruct(void* shards, int shard_size, int data_shar
         return set_error(KVEC_EUNSUPPORTED, "kvec_rs16_reconstruct: k*m=%d exceeds %d",
                          data_shards * m, kRsMaxTables);
     if (shard_size == 0) return KVEC_OK;
+    const uint64_t Sb = uint64_t(shard_size) * 2;
+    const uint32_t res = piece_res_bytes(shards, uint64_t(data_shards + parity_shards) * Sb);
+    if (data_shards <= kRsPieceMaxIn && m <= kRsGroup && res) {
+        hipLaunchKernelGGL(RsPiece::rec[data_shards - 1][m - 1], dim3(piece_grid(Sb, kRsPieceBlocks)), dim3(kTB), 0,
+                           as_stream(stream), align_down16(shards), uint32_t(reinterpret_cast<uintptr_t>(shards) & 15),
+                           res, uint32_t(Sb), parity_shards, missing_data, parity_used, gf_exp, gf_log);
+        return check_launch("kvec_rs16_reconstruct");
+    }
     hipLaunchKernelGGL(rs16_reconstruct_kernel, dim3(rs_grid(shard_size)), dim3(kTB), 0,
                        as_stream(stream), (uint16_t*)shards, int64_t(shard_size), data_shards,
                        parity_shards, m, missing_data, parity_used, gf_exp, gf_log);

@@ -379,10 +379,7 @@ def test_rs16_encode_other_generator(pkg, ora, gpu, k, m, S):
     encode must leave its Horner path and still give the reference's bytes for
     these tables."""
     ex0, lg0 = ora.gf16_tables()
-    n = np.arange(2 * 65535, dtype=np.int64)
-    ex = ex0[(2 * n) % 65535].astype(np.uint16)
-    lg = ((lg0.astype(np.int64) * 32768) % 65535).astype(np.uint16)   # 2 * 32768 = 1 mod 65535
-    lg[0] = 0
+    ex, lg = _gen4_tables(ora)
     assert ex[1] == 4 and all(ex[lg[x]] == x for x in (1, 2, 3, 0x8000, 0xFFFF))
     rng = np.random.default_rng(k * 7 + S)
     data = rng.integers(0, 65536, k * S, dtype=np.uint16)
@@ -433,6 +430,50 @@ def test_rs16_reconstruct_matches_oracle(pkg, ora, gpu, k, m, S):
                     d, S, k, m, torch.tensor(miss, dtype=torch.int32, device=gpu),
                     torch.tensor(pused, dtype=torch.int32, device=gpu), gex, glg)
                 assert np.array_equal(host(d), want), (miss, pused)
+
+
+def _gen4_tables(ora):
+    """Tables of the same field with generator alpha^2 = 4 (log base 4)."""
+    ex0, lg0 = ora.gf16_tables()
+    n = np.arange(2 * 65535, dtype=np.int64)
+    ex = ex0[(2 * n) % 65535].astype(np.uint16)
+    lg = ((lg0.astype(np.int64) * 32768) % 65535).astype(np.uint16)   # 2 * 32768 = 1 mod 65535
+    lg[0] = 0
+    return ex, lg
+
+
+@pytest.mark.parametrize("k,mp,S,soff,gen4", [(6, 2, 44741, 0, False), (6, 2, 44741, 3, False),
+                                              (6, 2, 44741, 5, True), (8, 3, 5003, 7, False),
+                                              (4, 2, 517, 1, True), (2, 2, 1000, 2, False),
+                                              (1, 1, 9, 0, False), (7, 4, 2048, 6, True)])
+def test_rs16_reconstruct_offsets_and_generators(pkg, ora, gpu, k, mp, S, soff, gen4):
+    """The reconstruct with the shard tensor at word offset soff of a larger
+    buffer (the bytes around it stay untouched), every data row of a small
+    code lost (k = m), the last parity row used, and tables with generator 4
+    (no chains of doublings: the byte maps of every coefficient)."""
+    ex, lg = _gen4_tables(ora) if gen4 else ora.gf16_tables()
+    rng = np.random.default_rng(k * 1000 + S + soff)
+    data = rng.integers(0, 65536, k * S, dtype=np.uint16)
+    ref = ora.rs16_encode(data, k, mp, S, ex, lg)
+    gex, glg = dev(ex, gpu), dev(lg, gpu)
+    cases = [((0,), (mp - 1,)), ((k - 1,), (0,))]
+    if k >= 2 and mp >= 2:
+        cases += [((0, k - 1), (mp - 2, mp - 1)), ((k - 1, 0), (mp - 1, 0))]
+    for miss, pused in cases:
+        sh = ref.copy()
+        sh[list(miss)] = rng.integers(0, 65536, (len(miss), S), dtype=np.uint16)
+        want = sh.copy()
+        ora.rs16_reconstruct(want, S, k, mp, list(miss), list(pused), ex, lg)
+        assert np.array_equal(want, ref)
+        buf = torch.full(((k + mp) * S + 16,), 0x2A2A, dtype=torch.int16, device=gpu)
+        buf[soff:soff + (k + mp) * S] = dev(sh.reshape(-1).view(np.int16), gpu)
+        d = buf[soff:soff + (k + mp) * S].view(k + mp, S).view(torch.uint16)
+        pkg.rs.rs_kernel.reconstruct_rs_u16_inplace(
+            d, S, k, mp, torch.tensor(miss, dtype=torch.int32, device=gpu),
+            torch.tensor(pused, dtype=torch.int32, device=gpu), gex, glg)
+        assert np.array_equal(host(d), want), (miss, pused)
+        rest = torch.cat([buf[:soff], buf[soff + (k + mp) * S:]])
+        assert bool((rest == 0x2A2A).all()), (miss, pused)
 
 
 def test_rs16_bad_device_indices_write_nothing(pkg, gpu):
