@@ -252,6 +252,33 @@ def test_gs_fused_backup_layouts(pkg, ora, gpu, T, n, nd, S_extra, koff, voff, s
     assert bool((rest == 0x3C3C).all())
 
 
+# The fused backup's batched tiles with K, V and the shard tensor 16-byte
+# aligned and rows of at least one 4 KiB tile, for every row count nd <= 8:
+# the K/V boundary inside a row, padding words holding the caller's bytes
+# (they enter P/Q as is and are never written), star bases inside, outside and
+# before the rows, guard words after the shard tensor.
+@pytest.mark.parametrize("nd", [1, 2, 3, 4, 5, 6, 7, 8])
+@pytest.mark.parametrize("S_extra,sb", [(0, 0), (3, -1), (7, 5), (1, 123457)])
+def test_gs_backup_aligned_every_nd(pkg, ora, gpu, nd, S_extra, sb):
+    T, n = 97, 136                      # K of 26,384 bytes
+    tn = T * n
+    S = -(-2 * tn // nd) + S_extra
+    rng = np.random.default_rng(nd * 100 + S_extra)
+    K = rng.integers(0, 65536, tn, dtype=np.uint16)
+    V = rng.integers(0, 65536, tn, dtype=np.uint16)
+    init = rng.integers(0, 65536, (nd + 2) * S, dtype=np.uint16).reshape(nd + 2, S)
+    want = init.copy()
+    ora.gs_pack(K.reshape(T, n), V.reshape(T, n), want, nd, S, T, n)
+    ora.gs_parity(want, nd, S, sb)
+    sbuf = torch.full(((nd + 2) * S + 64,), 0x3C3C, dtype=torch.int16, device=gpu)
+    sbuf[:(nd + 2) * S] = dev(init.reshape(-1).view(np.int16), gpu)
+    shards = sbuf[:(nd + 2) * S].view(nd + 2, S)
+    pkg.rdp.rdp_kernel.fused_backup_full_kv(dev(K.view(np.int16), gpu).view(T, n),
+                                            dev(V.view(np.int16), gpu).view(T, n), shards, nd, S, T, n, sb)
+    assert np.array_equal(host(shards).view(np.uint16), want)
+    assert bool((sbuf[(nd + 2) * S:] == 0x3C3C).all())
+
+
 @pytest.mark.parametrize("B,H,T,D,nd", [(1, 8, 512, 128, 8), (2, 1, 33, 128, 6), (1, 2, 5, 64, 3),
                                         (1, 1, 7, 3, 4)])
 def test_gs_backup_and_recovery(pkg, ora, gpu, B, H, T, D, nd):
