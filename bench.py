@@ -776,11 +776,22 @@ def bench_gs(pkg, torch, oracle, dev, seed, steps, warmup):
         par8(rows8[i % 2])
         torch.cuda.synchronize()
         one.append((time.perf_counter() - t0) * 1e6)
+    # The floor of that path: the same call on a one-word stripe (one block
+    # of one tile), launched and synchronized the same way.
+    tiny = torch.zeros((nd8 + 2, 1), dtype=torch.uint16, device=dev)
+    floor = []
+    for i in range(22):
+        t0 = time.perf_counter()
+        pkg.rdp_kv_ops.compute_rdp_parity(tiny, nd8, 1, 0)
+        torch.cuda.synchronize()
+        floor.append((time.perf_counter() - t0) * 1e6)
+    floor = floor[2:]
     alg8 = nd8 * S8 * 2 + 2 * S8 * 2
     out["plugin_step_pq_tp8"] = {"rows": [nd8 + 2, S8], "alg_bytes": alg8,
                                  "us_back_to_back": round(kms * 1e3, 2),
                                  "gbs_back_to_back": gbs(alg8, kms * 1e3),
-                                 "us_launch_and_sync_median": round(sorted(one)[len(one) // 2], 2)}
+                                 "us_launch_and_sync_median": round(sorted(one)[len(one) // 2], 2),
+                                 "us_launch_and_sync_one_word_median": round(sorted(floor)[len(floor) // 2], 2)}
     del rows8
     out["workload"] = "gs_family_nd6_llama3.1-8b_16x2048tok_512MiB"
     out["byte_exact_full"] = True
