@@ -146,3 +146,46 @@ def test_sweep_rs8_encode_decode(pkg, ora, gpu, k, m, S):
     pkg.spec.rs8_decode(sh, k, er)
     for a, b in zip(sh, want):
         assert torch.equal(a, b)
+
+
+# ------------------------------------------------------------------ gs RS16 reconstruct
+# Its own generator, so the draws above stay as they were.  k up to 10 and up
+# to 2 lost rows reach both the piece kernel (k <= 8, m <= 2) and the tile
+# kernel; any row length and tensor offset; erased rows and parity choices
+# drawn per case.
+_R2 = np.random.default_rng(20261)
+
+
+def _rs16_rec_case(i):
+    k = int(_R2.integers(1, 11))
+    mp = int(_R2.integers(1, 6))
+    nm = int(_R2.integers(1, min(k, mp, 3) + 1))
+    miss = sorted(_R2.choice(k, nm, replace=False).tolist())
+    pused = sorted(_R2.choice(mp, nm, replace=False).tolist())
+    return (k, mp, int(_R2.integers(1, 20000)), int(_R2.integers(0, 8)), miss, pused)
+
+
+RS16REC = [_rs16_rec_case(i) for i in range(20)]
+
+
+@pytest.mark.parametrize("k,mp,S,soff,miss,pused", RS16REC)
+def test_sweep_rs16_reconstruct(pkg, ora, gpu, k, mp, S, soff, miss, pused):
+    ex, lg = ora.gf16_tables()
+    rng = np.random.default_rng(k * 131 + mp * 17 + S)
+    data = rng.integers(0, 65536, k * S, dtype=np.uint16)
+    ref = ora.rs16_encode(data, k, mp, S, ex, lg)
+    sh = ref.copy()
+    sh[miss] = rng.integers(0, 65536, (len(miss), S), dtype=np.uint16)
+    # the oracle's rebuild (the original rows unless the reference's system is
+    # singular for these parity rows, where its Gauss-Jordan gives other bytes)
+    want = sh.copy()
+    ora.rs16_reconstruct(want, S, k, mp, list(miss), list(pused), ex, lg)
+    buf = torch.full(((k + mp) * S + 8,), 0x1B1B, dtype=torch.int16, device=gpu)
+    buf[soff:soff + (k + mp) * S] = dev(sh.reshape(-1).view(np.int16), gpu)
+    d = buf[soff:soff + (k + mp) * S].view(k + mp, S).view(torch.uint16)
+    gex, glg = pkg.rs.device_gf_tables(gpu)
+    pkg.rs.rs_kernel.reconstruct_rs_u16_inplace(
+        d, S, k, mp, torch.tensor(miss, dtype=torch.int32, device=gpu),
+        torch.tensor(pused, dtype=torch.int32, device=gpu), gex, glg)
+    assert np.array_equal(d.cpu().numpy(), want)
+    assert bool((torch.cat([buf[:soff], buf[soff + (k + mp) * S:]]) == 0x1B1B).all())
