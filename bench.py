@@ -71,13 +71,22 @@ def log(msg):
 
 
 def cpu_model():
+    """The CPU's model name with its family, model and stepping numbers (a
+    virtual machine may report only a generic name)."""
+    f = {}
     try:
         for line in open("/proc/cpuinfo"):
-            if line.startswith("model name"):
-                return line.split(":", 1)[1].strip()
+            if ":" in line:
+                k, v = (x.strip() for x in line.split(":", 1))
+                if k in ("model name", "cpu family", "model", "stepping") and k not in f:
+                    f[k] = v
+            if not line.strip() and f:
+                break
     except OSError:
         pass
-    return "unknown"
+    name = f.get("model name", "unknown")
+    ids = [f"{k} {f[k]}" for k in ("cpu family", "model", "stepping") if k in f]
+    return f"{name} ({', '.join(ids)})" if ids else name
 
 
 def host_cores():
