@@ -32,7 +32,13 @@ constexpr int kRsMaxM = 16;           // reference limit (benchmark/rs/kernel.cu
 constexpr int kRsMaxTables = 48;      // coefficients held in LDS
 constexpr int kRs16Tab = 24;          // dwords per coefficient: 4 byte maps x 6
 constexpr int kRsGroup = 2;           // outputs accumulated per pass over the inputs
-constexpr int kRsGrid = 1024;         // persistent blocks (4 per CU): tables are built once per block
+// The tile kernels (encode, and the reconstruct beyond the piece kernel's
+// limits) run blocks of kRsBS threads, two per CU, persistent: the tables are
+// built once per block.  Measured on the 512 MiB stream, RS(6,2) encode: 512
+// threads (16 KiB tiles) with 512 blocks 245 against 248 us for 256 threads
+// with 1024 blocks, and with the XCD-grouped tile order of rs_run_tiles 239 us.
+constexpr int kRsBS = 512;
+constexpr int kRsGrid = 512;
 
 __device__ __forceinline__ uint16_t gf16_mul_tab(uint16_t a, uint16_t b, const uint16_t* ex,
                                                  const uint16_t* lg) {
@@ -65,10 +71,10 @@ struct RsJob {
 __device__ __forceinline__ void rs_build_perm_tables(uint32_t (*ptab)[kRs16Tab], uint16_t (*basis)[16],
                                      const uint16_t* coef, int ncoef, const uint16_t* ex,
                                      const uint16_t* lg) {
-    for (int e = threadIdx.x; e < ncoef * 16; e += kTB)
+    for (int e = threadIdx.x; e < ncoef * 16; e += blockDim.x)
         basis[e >> 4][e & 15] = gf16_mul_tab(uint16_t(1u << (e & 15)), coef[e >> 4], ex, lg);
     __syncthreads();
-    for (int e = threadIdx.x; e < ncoef * kRs16Tab; e += kTB) {
+    for (int e = threadIdx.x; e < ncoef * kRs16Tab; e += blockDim.x) {
         const int t = e / kRs16Tab, d = e % kRs16Tab;
         const int map = d / 6, f = (d % 6) >> 1, half = d & 1;
         const int src = map & 1, dst = map >> 1;   // 0 = low byte, 1 = high byte
@@ -172,18 +178,18 @@ __device__ __forceinline__ void rs_mix_full(const RsJob& j, const uint32_t (*pta
     u32x4 lo[NW], hi[NW];
     RowWin rw = row_win(reinterpret_cast<const uint8_t*>(j.in_rows[0]) + t0b);
 #pragma unroll
-    for (int n = 0; n < NW; ++n) win_chunks(rw, 16 * (threadIdx.x + n * kTB), lo[n], hi[n]);
+    for (int n = 0; n < NW; ++n) win_chunks(rw, 16 * (threadIdx.x + n * kRsBS), lo[n], hi[n]);
     for (int i = 0; i < nin; ++i) {
         u32x4 x[NW];
 #pragma unroll
         for (int n = 0; n < NW; ++n) {
             x[n] = win_join(rw, lo[n], hi[n]);
-            if (copy) copy_owned<false>(j.copy, rw, 16 * (threadIdx.x + n * kTB), lo[n], hi[n]);
+            if (copy) copy_owned<false>(j.copy, rw, 16 * (threadIdx.x + n * kRsBS), lo[n], hi[n]);
         }
         if (i + 1 < nin) {
             rw = row_win(reinterpret_cast<const uint8_t*>(j.in_rows[i + 1]) + t0b);
 #pragma unroll
-            for (int n = 0; n < NW; ++n) win_chunks(rw, 16 * (threadIdx.x + n * kTB), lo[n], hi[n]);
+            for (int n = 0; n < NW; ++n) win_chunks(rw, 16 * (threadIdx.x + n * kRsBS), lo[n], hi[n]);
         }
         rs_mix_input<G, NW>(ptab, og, nin, i, x, acc);
     }
@@ -203,7 +209,7 @@ __device__ __forceinline__ void rs_mix_tail(const RsJob& j, const uint32_t (*pta
         u32x4 x[NW];
 #pragma unroll
         for (int n = 0; n < NW; ++n) {
-            const uint32_t off = 16 * (threadIdx.x + n * kTB);
+            const uint32_t off = 16 * (threadIdx.x + n * kRsBS);
             if (w0[n] + 8 <= j.S) {
                 u32x4 lo, hi;
                 win_chunks(rw, off, lo, hi);
@@ -295,18 +301,18 @@ __device__ __forceinline__ void rs_horner_full(const RsJob& j, uint32_t red2, ui
     u32x4 lo[NW], hi[NW];
     RowWin rw = row_win(reinterpret_cast<const uint8_t*>(j.in_rows[nin - 1]) + t0b);
 #pragma unroll
-    for (int n = 0; n < NW; ++n) win_chunks(rw, 16 * (threadIdx.x + n * kTB), lo[n], hi[n]);
+    for (int n = 0; n < NW; ++n) win_chunks(rw, 16 * (threadIdx.x + n * kRsBS), lo[n], hi[n]);
     for (int i = nin - 1; i >= 0; --i) {
         u32x4 x[NW];
 #pragma unroll
         for (int n = 0; n < NW; ++n) {
             x[n] = win_join(rw, lo[n], hi[n]);
-            if (copy) copy_owned<false>(j.copy, rw, 16 * (threadIdx.x + n * kTB), lo[n], hi[n]);
+            if (copy) copy_owned<false>(j.copy, rw, 16 * (threadIdx.x + n * kRsBS), lo[n], hi[n]);
         }
         if (i > 0) {
             rw = row_win(reinterpret_cast<const uint8_t*>(j.in_rows[i - 1]) + t0b);
 #pragma unroll
-            for (int n = 0; n < NW; ++n) win_chunks(rw, 16 * (threadIdx.x + n * kTB), lo[n], hi[n]);
+            for (int n = 0; n < NW; ++n) win_chunks(rw, 16 * (threadIdx.x + n * kRsBS), lo[n], hi[n]);
         }
         if (i == nin - 1) rs_horner_first<G, NW>(x, acc);
         else rs_horner_step<G, NW>(red2, x, acc);
@@ -322,7 +328,7 @@ __device__ __forceinline__ void rs_horner_tail(const RsJob& j, uint32_t red2, ui
         u32x4 x[NW];
 #pragma unroll
         for (int n = 0; n < NW; ++n) {
-            const uint32_t off = 16 * (threadIdx.x + n * kTB);
+            const uint32_t off = 16 * (threadIdx.x + n * kRsBS);
             if (w0[n] + 8 <= j.S) {
                 u32x4 lo, hi;
                 win_chunks(rw, off, lo, hi);
@@ -348,31 +354,43 @@ constexpr int kRsNW = 2;                              // windows per thread
 // data-row copy writes alongside; nt 1 % slower), nt for the reconstruct (2 %
 // faster).
 constexpr bool kRsEncNT = false, kRsRecNT = true;
-constexpr uint32_t kRsTile = kTileBytes * kRsNW;      // logical bytes per row per tile
+constexpr uint32_t kRsTile = 16 * kRsBS * kRsNW;     // logical bytes per row per tile
 constexpr uint32_t kRsStage = kRsTile + 16;           // LDS staging row
 
 // Stream every tile of the job through the tables already in LDS; `tile`
 // holds kRsGroup staging rows of kRsStage bytes.  Window n of thread t covers
-// logical bytes 16 (t + n kTB) .. +15 of the tile, so each window's loads are
-// contiguous across the block.  HORNER selects the Horner encode (all
+// logical bytes 16 (t + n kRsBS) .. +15 of the tile, so each window's loads
+// are contiguous across the block.  HORNER selects the Horner encode (all
 // outputs in one group, accumulators in natural word order; red2 holds the
 // reduction word in both halves).  The two are separate loops: sharing one
 // loop made the encode kernel spill registers.
+//
+// Tile order: blocks are dispatched round-robin over the eight XCDs (block b
+// on XCD b % 8), and the blocks of one XCD take consecutive tiles, so the
+// 128-byte lines that two neighbouring tiles of a misaligned row share are
+// mostly written through one XCD's L2.
 template <bool HORNER, bool NT>
 __device__ __forceinline__ void rs_run_tiles(const RsJob& j, const uint32_t (*ptab)[kRs16Tab],
                                              uint8_t* tile, uint32_t red2) {
     const uint64_t Sb = uint64_t(j.S) * 2;
     const uint64_t ntiles = (Sb + kRsTile - 1) / kRsTile;
-    for (uint64_t tt = blockIdx.x; tt < ntiles; tt += gridDim.x) {
+    // each row's head bytes up to its first 16-byte-aligned address, which no
+    // tile's aligned chunks cover: one lane per byte
+    if (j.copy.dst && blockIdx.x == 0)
+        for (int e = threadIdx.x; e < 16 * j.nin; e += kRsBS) {
+            const uint64_t o = uint64_t(reinterpret_cast<const uint8_t*>(j.in_rows[e >> 4]) - j.copy.src);
+            const uint32_t mis = uint32_t(reinterpret_cast<uintptr_t>(j.copy.src + o) & 15);
+            const uint32_t b = uint32_t(e & 15);
+            if (mis && b < 16 - mis && b < Sb) as_global(j.copy.dst)[o + b] = as_global(j.copy.src)[o + b];
+        }
+    const uint32_t G = gridDim.x;
+    const uint32_t first = G % 8 == 0 ? (blockIdx.x % 8) * (G / 8) + blockIdx.x / 8 : blockIdx.x;
+    for (uint64_t tt = first; tt < ntiles; tt += G) {
         const uint64_t t0b = tt * kRsTile;
         const uint32_t nbytes = uint32_t(Sb - t0b < uint64_t(kRsTile) ? Sb - t0b : kRsTile);
         int64_t w0[kRsNW];
 #pragma unroll
-        for (int n = 0; n < kRsNW; ++n) w0[n] = int64_t(t0b / 2) + 8 * (threadIdx.x + n * kTB);
-        if (j.copy.dst && tt == 0 && threadIdx.x == 0)
-            for (int i = 0; i < j.nin; ++i)
-                copy_row_head(j.copy,
-                              uint64_t(reinterpret_cast<const uint8_t*>(j.in_rows[i]) - j.copy.src), Sb);
+        for (int n = 0; n < kRsNW; ++n) w0[n] = int64_t(t0b / 2) + 8 * (threadIdx.x + n * kRsBS);
         for (int og = 0; og < j.nout; og += kRsGroup) {
             const bool copy = j.copy.dst != nullptr && og == 0;
             const int G = j.nout - og < kRsGroup ? j.nout - og : kRsGroup;
@@ -401,20 +419,20 @@ __device__ __forceinline__ void rs_run_tiles(const RsJob& j, const uint32_t (*pt
             }
             for (int g = 0; g < G; ++g)
                 for (int n = 0; n < kRsNW; ++n)
-                    *reinterpret_cast<u32x4*>(tile + g * kRsStage + 16 * (threadIdx.x + n * kTB)) =
+                    *reinterpret_cast<u32x4*>(tile + g * kRsStage + 16 * (threadIdx.x + n * kRsBS)) =
                         HORNER ? u32x4{acc[n][g][0], acc[n][g][1], acc[n][g][2], acc[n][g][3]}
                                : join_bytes(acc[n][g]);
             __syncthreads();
             for (int g = 0; g < G; ++g)
-                tile_store<NT>(reinterpret_cast<uint8_t*>(j.out_rows[og + g]) + t0b, tile + g * kRsStage,
-                           nbytes);
+                tile_store<NT, kRsBS>(reinterpret_cast<uint8_t*>(j.out_rows[og + g]) + t0b, tile + g * kRsStage,
+                                      nbytes);
             __syncthreads();
         }
     }
 }
 
 // benchmark/rs/kernel.cu:67-102 parity: Par_p = XOR_i D_i * alpha^((p+1) i mod 65535).
-__global__ __launch_bounds__(kTB) __attribute__((amdgpu_waves_per_eu(4))) void rs16_encode_kernel(RsJob job, const uint16_t* ex,
+__global__ __launch_bounds__(kRsBS) __attribute__((amdgpu_waves_per_eu(4))) void rs16_encode_kernel(RsJob job, const uint16_t* ex,
                                                           const uint16_t* lg) {
     __shared__ __attribute__((aligned(16))) uint32_t ptab[kRsMaxTables][kRs16Tab];
     __shared__ uint16_t basis[kRsMaxTables][16];
@@ -423,7 +441,7 @@ __global__ __launch_bounds__(kTB) __attribute__((amdgpu_waves_per_eu(4))) void r
     __shared__ RsJob j;
     if (threadIdx.x == 0) j = job;
     __syncthreads();
-    for (int t = threadIdx.x; t < j.nout * j.nin; t += kTB) {
+    for (int t = threadIdx.x; t < j.nout * j.nin; t += kRsBS) {
         const int p = t / j.nin, i = t % j.nin;
         coef[t] = ex[((p + 1) * i) % kGfOrder];
     }
@@ -439,7 +457,7 @@ __global__ __launch_bounds__(kTB) __attribute__((amdgpu_waves_per_eu(4))) void r
         s_horner = j.nout <= kRsGroup;
     }
     __syncthreads();
-    for (int e = threadIdx.x; e < j.nout * j.nin * 16; e += kTB) {
+    for (int e = threadIdx.x; e < j.nout * j.nin * 16; e += kRsBS) {
         const int t = e >> 4, b = e & 15;
         const int p = t / j.nin, i = t % j.nin;
         uint16_t v = uint16_t(1u << b);
@@ -545,7 +563,7 @@ __device__ __forceinline__ void rs16_rec_tables(RsRecPlan& pl, uint32_t (*ptab)[
     }
     __syncthreads();
     const int nin = pl.nin, ndata = nin - m;
-    for (int t = threadIdx.x; t < m * nin; t += kTB) {
+    for (int t = threadIdx.x; t < m * nin; t += blockDim.x) {
         const int c = t / nin, in = t % nin;
         uint16_t v = 0;
         if (in < ndata) {
@@ -563,7 +581,7 @@ __device__ __forceinline__ void rs16_rec_tables(RsRecPlan& pl, uint32_t (*ptab)[
 }
 
 // benchmark/rs/kernel.cu:105-222, tile engine: any k, m and row size.
-__global__ __launch_bounds__(kTB) __attribute__((amdgpu_waves_per_eu(4))) void rs16_reconstruct_kernel(uint16_t* sh, int64_t S, int k,
+__global__ __launch_bounds__(kRsBS) __attribute__((amdgpu_waves_per_eu(4))) void rs16_reconstruct_kernel(uint16_t* sh, int64_t S, int k,
                                                                int mpar, int m,
                                                                const int32_t* missing,
                                                                const int32_t* pused,
@@ -855,7 +873,7 @@ extern "C" int kvec_rs16_encode(const void* data_padded, void* shards, int data_
     for (int i = 0; i < data_shards; ++i) j.in_rows[i] = (const uint16_t*)data_padded + uint64_t(i) * S;
     for (int p = 0; p < parity_shards; ++p)
         j.out_rows[p] = (uint16_t*)shards + uint64_t(data_shards + p) * S;
-    hipLaunchKernelGGL(rs16_encode_kernel, dim3(rs_grid(S)), dim3(kTB), 0, st, j, gf_exp, gf_log);
+    hipLaunchKernelGGL(rs16_encode_kernel, dim3(rs_grid(S)), dim3(kRsBS), 0, st, j, gf_exp, gf_log);
     return check_launch("kvec_rs16_encode");
 }
 
@@ -888,7 +906,7 @@ extern "C" int kvec_rs16_reconstruct(void* shards, int shard_size, int data_shar
                            res, uint32_t(Sb), parity_shards, missing_data, parity_used, gf_exp, gf_log);
         return check_launch("kvec_rs16_reconstruct");
     }
-    hipLaunchKernelGGL(rs16_reconstruct_kernel, dim3(rs_grid(shard_size)), dim3(kTB), 0,
+    hipLaunchKernelGGL(rs16_reconstruct_kernel, dim3(rs_grid(shard_size)), dim3(kRsBS), 0,
                        as_stream(stream), (uint16_t*)shards, int64_t(shard_size), data_shards,
                        parity_shards, m, missing_data, parity_used, gf_exp, gf_log);
     return check_launch("kvec_rs16_reconstruct");

@@ -218,12 +218,12 @@ __device__ __forceinline__ void copy_row_head(const FlatCopy& fc, uint64_t o, ui
 }
 
 // Write logical bytes [0, nbytes) of the LDS tile `t` (16-byte aligned, with 16
-// bytes of slack after nbytes) to dst, any alignment.  All threads call it.
-// NT: the aligned 16-byte stores are non-temporal.  Which is faster depends on
-// the kernel's other traffic (measured per kernel on MI355X): the P/Q rows of
-// the star-diagonal code write 12 % faster with it, the XOR parity row next
-// to the fused data-row copy 7 % slower.
-template <bool NT = false>
+// bytes of slack after nbytes) to dst, any alignment.  All BS threads of the
+// block call it.  NT: the aligned 16-byte stores are non-temporal.  Which is
+// faster depends on the kernel's other traffic (measured per kernel on
+// MI355X): the P/Q rows of the star-diagonal code write 12 % faster with it,
+// the XOR parity row next to the fused data-row copy 7 % slower.
+template <bool NT = false, int BS = kTB>
 __device__ __forceinline__ void tile_store(uint8_t* dst, const uint8_t* t, uint32_t nbytes) {
     dst = wave_uniform(dst);
     nbytes = uint32_t(__builtin_amdgcn_readfirstlane(int(nbytes)));
@@ -235,7 +235,7 @@ __device__ __forceinline__ void tile_store(uint8_t* dst, const uint8_t* t, uint3
         const uint32_t delta = uint32_t(A0 - D0);
         const uint32_t dsh = delta & 15, dal = delta - dsh;   // uniform
         const uint32_t nch = uint32_t((A1 - A0) >> 4);
-        for (uint32_t k = threadIdx.x; k < nch; k += kTB) {
+        for (uint32_t k = threadIdx.x; k < nch; k += BS) {
             const uint32_t al = dal + 16 * k;
             u32x4 v = *reinterpret_cast<const u32x4*>(t + al);
             if (dsh) v = funnel16(v, *reinterpret_cast<const u32x4*>(t + al + 16), dsh);
@@ -250,7 +250,7 @@ __device__ __forceinline__ void tile_store(uint8_t* dst, const uint8_t* t, uint3
         else if (i >= 16 && i - 16 < nt) g[(A1 - D0) + (i - 16)] = t[(A1 - D0) + (i - 16)];
     } else {
         const gptr<uint8_t> g = as_global(dst);
-        for (uint32_t i = threadIdx.x; i < nbytes; i += kTB) g[i] = t[i];
+        for (uint32_t i = threadIdx.x; i < nbytes; i += BS) g[i] = t[i];
     }
 }
 
