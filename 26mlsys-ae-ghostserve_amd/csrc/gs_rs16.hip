@@ -698,7 +698,7 @@ __device__ __forceinline__ void rs_rec_horner(const u32x4* x, const uint32_t (*d
 // outputs.  The shard tensor starts b15 bytes past base_al (16-aligned); the
 // resource covers res_bytes from base_al.
 template <int NIN, int M>
-__global__ __launch_bounds__(kTB) __attribute__((amdgpu_waves_per_eu(4))) void rs16_reconstruct_piece_kernel(
+__global__ __launch_bounds__(kPieceBS) __attribute__((amdgpu_waves_per_eu(4))) void rs16_reconstruct_piece_kernel(
         uint8_t* base_al, uint32_t b15, uint32_t res_bytes, uint32_t Sb, int mpar,
         const int32_t* missing, const int32_t* pused, const uint16_t* ex, const uint16_t* lg) {
     constexpr int ND = NIN - M;
@@ -737,7 +737,7 @@ __global__ __launch_bounds__(kTB) __attribute__((amdgpu_waves_per_eu(4))) void r
         s_horner = 1;
     }
     __syncthreads();
-    for (int e = threadIdx.x; e < M * ND * 16; e += kTB) {
+    for (int e = threadIdx.x; e < M * ND * 16; e += kPieceBS) {
         const int r = e / (ND * 16), j = (e >> 4) % ND, b = e & 15;
         const int n = (pl.pu[r] + 1) * pl.in_row[j];
         const uint16_t cf = ex[n % kGfOrder];
@@ -901,7 +901,7 @@ extern "C" int kvec_rs16_reconstruct(void* shards, int shard_size, int data_shar
     const uint64_t Sb = uint64_t(shard_size) * 2;
     const uint32_t res = piece_res_bytes(shards, uint64_t(data_shards + parity_shards) * Sb);
     if (data_shards <= kRsPieceMaxIn && m <= kRsGroup && res) {
-        hipLaunchKernelGGL(RsPiece::rec[data_shards - 1][m - 1], dim3(piece_grid(Sb, kRsPieceBlocks)), dim3(kTB), 0,
+        hipLaunchKernelGGL(RsPiece::rec[data_shards - 1][m - 1], dim3(piece_grid(Sb, kRsPieceBlocks)), dim3(kPieceBS), 0,
                            as_stream(stream), align_down16(shards), uint32_t(reinterpret_cast<uintptr_t>(shards) & 15),
                            res, uint32_t(Sb), parity_shards, missing_data, parity_used, gf_exp, gf_log);
         return check_launch("kvec_rs16_reconstruct");

@@ -26,7 +26,8 @@
 namespace kvec {
 
 constexpr uint32_t kPieceBytes = 1024;               // logical bytes per row per piece
-constexpr int kPieceWaves = kTB / 64;                // waves per block
+constexpr int kPieceBS = 256;                        // threads per block
+constexpr int kPieceWaves = kPieceBS / 64;           // waves per block
 
 // Host: blocks for rows of Sb bytes, with at most max_blocks blocks.
 inline uint32_t piece_grid(uint64_t Sb, uint32_t max_blocks) {

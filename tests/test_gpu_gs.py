@@ -20,7 +20,8 @@ def host(t):
 
 # ------------------------------------------------------------------ XOR
 @pytest.mark.parametrize("nd,S", [(4, 262144), (8, 1000), (3, 17), (5, 1), (1, 33), (6, 4111),
-                                  (7, 16), (2, 4096 * 3 + 5)])
+                                  (7, 16), (2, 4096 * 3 + 5), (3, 8192), (6, 8192 + 15),
+                                  (5, 8192 * 3 + 1)])
 def test_xor_encode_matches_oracle(pkg, ora, gpu, nd, S):
     rng = np.random.default_rng(nd * 7 + S)
     data = rng.integers(0, 256, nd * S, dtype=np.uint8)
@@ -34,7 +35,8 @@ def test_xor_encode_matches_oracle(pkg, ora, gpu, nd, S):
 # disjoint and equally aligned modulo 16 bytes (else a separate copy): offsets
 # into guard-filled buffers cover both paths, misaligned row starts, whole
 # tiles and partial tails, and nothing outside the shard tensor may change.
-@pytest.mark.parametrize("nd,S", [(6, 8192), (3, 4096 * 2 + 10), (4, 1000), (2, 17), (1, 4096)])
+@pytest.mark.parametrize("nd,S", [(6, 8192), (3, 4096 * 2 + 10), (4, 1000), (2, 17), (1, 4096),
+                                  (2, 8192 * 2 + 3)])
 @pytest.mark.parametrize("doff,soff", [(0, 0), (5, 5), (3, 7), (0, 16), (11, 27)])
 def test_xor_encode_fused_copy_offsets(pkg, ora, gpu, nd, S, doff, soff):
     rng = np.random.default_rng(nd * 1000 + S + doff)
@@ -82,7 +84,7 @@ def test_xor_encode_kv_matches_oracle(pkg, ora, gpu, nd, kb, extra, koff, voff):
 # kvec_xor_recover_kv: a lost data row (one pass), a lost P, nothing lost, no
 # output bytes, and an output overlapping the shard tensor (the two-step path).
 @pytest.mark.parametrize("nd,S,out_bytes", [(6, 4096 * 3 + 37, 6 * (4096 * 3 + 37) - 5), (3, 1001, 2000),
-                                            (9, 5000, 9 * 5000)])
+                                            (9, 5000, 9 * 5000), (5, 8192 * 3 + 37, 5 * (8192 * 3 + 37) - 9)])
 def test_xor_recover_kv_matches_oracle(pkg, ora, gpu, nd, S, out_bytes):
     rng = np.random.default_rng(nd + S)
     enc = ora.xor_encode(rng.integers(0, 256, nd * S, dtype=np.uint8), nd, S)
@@ -120,7 +122,8 @@ def test_xor_encode_kv_rejects_short_shards(pkg, gpu):
                       pkg._lib.stream_handle(gpu))
 
 
-@pytest.mark.parametrize("nd,S", [(4, 262144), (8, 999), (3, 17), (5, 3), (6, 4096 * 3 + 37), (2, 5000)])
+@pytest.mark.parametrize("nd,S", [(4, 262144), (8, 999), (3, 17), (5, 3), (6, 4096 * 3 + 37), (2, 5000),
+                                  (6, 8192 * 3 + 37), (3, 8192)])
 def test_xor_reconstruct_matches_oracle(pkg, ora, gpu, nd, S):
     rng = np.random.default_rng(S)
     data = rng.integers(0, 256, nd * S, dtype=np.uint8)
@@ -179,6 +182,7 @@ def test_xor_forward_backward_round_trip(pkg, ora, gpu, dtype, nd):
 # ------------------------------------------------------------------ gs RDP
 @pytest.mark.parametrize("nd,S", [(8, 5000), (6, 101), (1, 9), (3, 2), (2, 1), (13, 4103),
                                   (8, 2048), (8, 2049), (4, 16), (5, 24577), (8, 7),
+                                  (8, 4096), (8, 4097), (6, 4096 * 6 + 1),
                                   # rows whose Q window starts more than one chunk
                                   # back (misalignment - 2 r < -16)
                                   (13, 4096), (11, 4100), (20, 4105), (16, 2000)])
@@ -384,7 +388,8 @@ def test_gs_pack_row(pkg, ora, gpu):
 
 
 # ------------------------------------------------------------------ gs RS16
-@pytest.mark.parametrize("k,m,S", [(8, 2, 4096), (6, 2, 44741), (5, 3, 1000), (4, 1, 3),
+@pytest.mark.parametrize("k,m,S", [(8, 2, 4096), (6, 2, 44741), (5, 3, 1000), (4, 1, 3), (6, 2, 8192),
+                                   (3, 2, 8192 * 3 + 5),
                                    (8, 0, 100), (10, 4, 2049), (1, 1, 77), (16, 3, 8),
                                    (6, 7, 1001), (3, 16, 513), (48, 1, 300)])
 def test_rs16_encode_matches_oracle(pkg, ora, gpu, k, m, S):
@@ -567,11 +572,13 @@ def test_gs_parity_interior_tiles(pkg, ora, gpu, nd, soff, S, sb):
 # Q words i < r of row r wrap to row r's last words.  star_base S - 6 puts the
 # skipped word of rows 3, 4 and 5 on a wrapped word (diagonals 0, 2 and 4),
 # star_base 0 puts it on unwrapped words of thread 0, -1 skips nothing in row
-# 0.  S = 2048 is a one-tile stripe; 524288 words is a Llama-3.1-8B TP8 prefill
-# step's [K | V] rows (2048 tokens x 128 words).
+# 0.  S = 4096 is a one-tile stripe (8 KiB rows) and S = 2048 half of one;
+# 524288 words is a Llama-3.1-8B TP8 prefill step's [K | V] rows (2048 tokens
+# x 128 words).
 @pytest.mark.parametrize("nd", range(1, 9))
 @pytest.mark.parametrize("soff", [0, 3])
-@pytest.mark.parametrize("S,sb", [(2048, 2042), (2048 * 3 + 5, 0), (6000, -1), (4096, 4095)])
+@pytest.mark.parametrize("S,sb", [(2048, 2042), (2048 * 3 + 5, 0), (6000, -1), (4096, 4095),
+                                  (4096 * 2 + 3, 4096 * 2 - 3)])
 def test_gs_parity_first_tile(pkg, ora, gpu, nd, soff, S, sb):
     rng = np.random.default_rng(nd * 29 + soff * 3 + S + sb)
     rows = rng.integers(0, 65536, (nd + 2, S), dtype=np.uint16)
@@ -601,7 +608,7 @@ def test_gs_parity_plugin_step_shape(pkg, ora, gpu, sb):
 @pytest.mark.parametrize("nd", range(1, 9))
 @pytest.mark.parametrize("soff,S_extra", [(0, 0), (5, 2500), (3, 7000)])
 def test_gs_backup_interior_tiles(pkg, ora, gpu, nd, soff, S_extra):
-    T, n, sb = 96, 211, 2050
+    T, n, sb = 192, 211, 2050     # rows of at least two 8 KiB tiles for every nd
     tn = T * n
     S = -(-2 * tn // nd) + S_extra
     koff, voff = soff, (soff + tn) % 8      # the alignment the fused pack needs
