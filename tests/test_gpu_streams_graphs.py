@@ -89,3 +89,73 @@ def test_encodes_on_concurrent_streams(pkg, gpu):
         pkg.spec.rdp_encode(data, Pe, Qe, p=p)
         torch.cuda.synchronize()
         assert torch.equal(P, Pe) and torch.equal(Q, Qe)
+
+
+def test_xor_and_rs16_encodes_in_hip_graph(pkg, gpu):
+    """encode_xor and encode_rs_u16 (each with its data-row copy) captured in
+    one graph on row sizes that end in partial tiles."""
+    nd, Sb = 6, 8192 * 5 + 37
+    k, m, S = 6, 2, 8192 * 3 + 5
+    ex, lg = pkg.rs.device_gf_tables(gpu)
+    xd = _bytes(nd * Sb, gpu, 1)
+    xs = torch.empty((nd + 1, Sb), dtype=torch.uint8, device=gpu)
+    rd = _bytes(k * S * 2, gpu, 2).view(torch.uint16)
+    rsh = torch.empty((k + m, S), dtype=torch.uint16, device=gpu)
+    xe, re = torch.empty_like(xs), torch.empty_like(rsh)
+
+    def both(xs_, rsh_):
+        pkg.xor.xor_kernel.encode_xor(xd, xs_, nd, Sb)
+        pkg.rs.rs_kernel.encode_rs_u16(rd, rsh_, k, m, S, ex, lg)
+
+    graph = _capture(lambda: both(xs, rsh))
+    for rep in range(4):
+        xd.random_(0, 256)
+        rd.view(torch.uint8).random_(0, 256)
+        torch.cuda.synchronize()
+        graph.replay()
+        both(xe, re)
+        torch.cuda.synchronize()
+        assert torch.equal(xs, xe) and torch.equal(rsh, re), rep
+
+
+def test_rs16_reconstruct_in_hip_graph(pkg, gpu):
+    """reconstruct_rs_u16_inplace captured once; before each replay the
+    tensor is re-encoded from new data and the lost rows are overwritten."""
+    k, m, S = 6, 2, 44741
+    ex, lg = pkg.rs.device_gf_tables(gpu)
+    data = _bytes(k * S * 2, gpu, 3).view(torch.uint16)
+    sh = torch.empty((k + m, S), dtype=torch.uint16, device=gpu)
+    md = torch.tensor([1, 4], dtype=torch.int32, device=gpu)
+    pu = torch.tensor([0, 1], dtype=torch.int32, device=gpu)
+    pkg.rs.rs_kernel.encode_rs_u16(data, sh, k, m, S, ex, lg)
+    graph = _capture(lambda: pkg.rs.rs_kernel.reconstruct_rs_u16_inplace(sh, S, k, m, md, pu, ex, lg))
+    for rep in range(4):
+        data.view(torch.uint8).random_(0, 256)
+        pkg.rs.rs_kernel.encode_rs_u16(data, sh, k, m, S, ex, lg)
+        want = sh.clone()
+        sh[1].fill_(0x1111 + rep)
+        sh[4].fill_(0x4444 + rep)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(sh, want), rep
+
+
+def test_fused_backup_in_hip_graph(pkg, gpu):
+    """fused_backup_full_kv (pack K || V into the rows + star-diagonal P/Q)
+    captured and replayed on new K and V."""
+    T, n, nd, sb = 64, 301, 6, 5        # 4 padding words after K || V
+    S = -(-2 * T * n // nd)
+    K = torch.empty((T, n), dtype=torch.int16, device=gpu)
+    V = torch.empty_like(K)
+    sh = torch.zeros((nd + 2, S), dtype=torch.uint16, device=gpu)
+    ref = torch.zeros_like(sh)
+    graph = _capture(lambda: pkg.rdp.rdp_kernel.fused_backup_full_kv(K, V, sh, nd, S, T, n, sb))
+    for rep in range(4):
+        K.view(torch.uint8).random_(0, 256)
+        V.view(torch.uint8).random_(0, 256)
+        torch.cuda.synchronize()
+        graph.replay()
+        pkg.rdp.rdp_kernel.fused_backup_full_kv(K, V, ref, nd, S, T, n, sb)
+        torch.cuda.synchronize()
+        assert torch.equal(sh, ref), rep
