@@ -486,10 +486,19 @@ __device__ __forceinline__ bool gs_pq_batched(uint16_t* sh, uint32_t Sb, uint32_
             // this lane's chunk into the data rows (rows read from the row
             // tensor itself lie past K||V, so their chunks fail the test); the
             // last thread also stores the chunk past the block, which the
-            // window's last mr bytes fall in
+            // window's last mr bytes fall in.  A wave's 64 chunks start at
+            // position `pre` of a 128-byte line: when pre != 0 its first and
+            // last lines are shared with the neighbouring waves, and their
+            // chunks go through L2 (the two parts merge there), the others
+            // non-temporal.  All non-temporal, the two parts of each such line
+            // were written separately: 235 against 219.5 us on the 512 MiB
+            // stream (rows misaligned by 86 bytes mod 128).
             const uint32_t X = row_x0(r) + 16 * threadIdx.x;
+            const uint32_t pre = uint32_t((reinterpret_cast<uintptr_t>(sh) + row_x0(r)) >> 4) & 7;
+            const bool edge = pre != 0 && (lane < 8 - pre || lane >= 64 - pre);
             if (X < copy_end) {
-                gs_store_chunk32(reinterpret_cast<uint8_t*>(sh), X, c0[r], copy_end);
+                if (edge && X + 16 <= copy_end) st16(reinterpret_cast<uint8_t*>(sh) + X, c0[r]);
+                else gs_store_chunk32(reinterpret_cast<uint8_t*>(sh), X, c0[r], copy_end);
                 if (mr > 0 && threadIdx.x == kTB - 1)
                     gs_store_chunk32(reinterpret_cast<uint8_t*>(sh), X + 16, c1, copy_end);
             }
