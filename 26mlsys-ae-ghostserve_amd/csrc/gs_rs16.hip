@@ -800,6 +800,135 @@ static uint8_t* align_down16(const void* p) {
     return reinterpret_cast<uint8_t*>(reinterpret_cast<uintptr_t>(p) & ~uintptr_t(15));
 }
 
+// ------------------------------------------------------ one-shot tile encode
+// encode_rs_u16 on one kTileBytes tile of every row per block, blocks in tile
+// order (the shape of the XOR encode), for m <= 2 parities and k <= 8 data
+// rows.  Each lane requests its aligned chunk of every data row at once (lane
+// 63 also the chunk after it, which a misaligned window reaches into), forms
+// its windows by a DPP lane shift, stores its owned chunks into the data rows
+// and folds the windows into the parities by Horner's rule; the parities go
+// through LDS to tile_store.
+//
+// The generator is read from the tables per block with scalar loads, whose
+// wait counter is not the vector loads': with gf_exp[1] == 2 (the tables of
+// init_gf_tables, or any field's exp/log pair whose generator is 2) the
+// coefficient alpha^((p+1) i) is (p+1) i doublings with the field's reduction
+// word 0x8000 * 2; for other tables each word is multiplied through the
+// tables.  (Like the byte maps, this takes the tables to be a field's.)
+//
+// Data-row copy stores are non-temporal, except the chunks in the two
+// 128-byte lines a wave shares with its neighbours, which go through L2
+// (copy_chunk_split); the parity rows' stores are non-temporal too.  On the
+// 512 MiB stream, RS(6,2), against the persistent tile kernel (plain stores)
+// on one box: 218.7-220.9 against 240.5-247.4 us; with plain parity stores
+// this kernel took 247-251 us.  Rows of at least one full tile take this path in every
+// tile: in a partial last tile the lanes past a row's end fold bytes that are
+// never stored, and their copied chunks carry the next row's bytes (the
+// values its own tile copies) or lie past the copy range, where they are
+// clipped.
+template <int ND, int M>
+__global__ __launch_bounds__(kTB) void rs16_encode_tiles_kernel(const uint8_t* in, uint32_t Sb, uint32_t in_bytes,
+                                                               FlatCopy fc, uint8_t* par,
+                                                               const uint16_t* __restrict__ ex,
+                                                               const uint16_t* __restrict__ lg) {
+    static_assert(ND >= 1 && ND <= 8 && M >= 1 && M <= 2, "instances");
+    __shared__ __attribute__((aligned(16))) uint8_t tile[M][kTileBytes + 16];
+    const uint32_t t0 = blockIdx.x * uint32_t(kTileBytes);
+    const uint32_t nbytes = Sb - t0 < uint32_t(kTileBytes) ? Sb - t0 : uint32_t(kTileBytes);
+    const uint32_t lane = threadIdx.x & 63;
+    const uint32_t b15 = uint32_t(reinterpret_cast<uintptr_t>(in)) & 15;
+    const uint8_t* in_al = in - b15;
+    const __amdgpu_buffer_rsrc_t rsin = chunk_rsrc(in_al, (b15 + in_bytes + 15) & ~15u);
+    auto row_a = [&](int i) { return b15 + uint32_t(i) * Sb + t0; };   // tile start of row i, from in_al
+    u32x4 lo[ND], e1[ND];
+#pragma unroll
+    for (int i = 0; i < ND; ++i) {
+        const uint32_t A = row_a(i), sh = A & 15, my = A - sh + 16 * threadIdx.x;
+        lo[i] = chunk_load(rsin, my);
+        e1[i] = chunk_load(rsin, lane == 63 && sh ? my + 16 : kNoLoad);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    // each row's head bytes before its first 16-byte-aligned address, which no
+    // tile's chunks cover: one lane per byte
+    if (fc.dst && t0 == 0 && threadIdx.x < 16 * ND) {
+        const uint32_t i = threadIdx.x >> 4, b = threadIdx.x & 15;
+        const uint64_t o = uint64_t(i) * Sb;
+        const uint32_t mis = uint32_t(reinterpret_cast<uintptr_t>(fc.src + o) & 15);
+        if (mis && b < 16 - mis && b < Sb) as_global(fc.dst)[o + b] = as_global(fc.src)[o + b];
+    }
+    const bool horner = ex[1] == 2;
+    const uint16_t red = gf16_mul_tab(0x8000, 2, ex, lg);
+    const uint32_t red2 = uint32_t(red) * 0x10001u;
+    u32x4 acc[M];
+    if (horner) {
+#pragma unroll
+        for (int i = ND - 1; i >= 0; --i) {
+            const uint32_t A = row_a(i), sh = A & 15;
+            const u32x4 hi = from_next_lane_or(lo[i], e1[i]);
+            const u32x4 x = sh ? funnel16(lo[i], hi, sh) : lo[i];
+            if (fc.dst) {
+                const uint8_t* c = in_al + (A - sh) + 16 * threadIdx.x + (sh ? 16 : 0);
+                copy_chunk_split(fc, c, sh ? hi : lo[i]);
+            }
+            const uint32_t xv[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+            for (int p = 0; p < M; ++p) {
+                uint32_t a[4] = {acc[p].x, acc[p].y, acc[p].z, acc[p].w};
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    if (i == ND - 1) {
+                        a[q] = xv[q];
+                    } else {
+                        uint32_t v = a[q];
+#pragma unroll
+                        for (int d = 0; d < p; ++d) v = gf16_dbl2(v, red2);
+                        a[q] = gf16_dbl2_xor(v, red2, xv[q]);
+                    }
+                }
+                acc[p] = u32x4{a[0], a[1], a[2], a[3]};
+            }
+        }
+    } else {
+        // tables with another generator: every word multiplied through them
+#pragma unroll
+        for (int p = 0; p < M; ++p) acc[p] = u32x4{0, 0, 0, 0};
+        for (int i = 0; i < ND; ++i) {
+            const uint32_t A = row_a(i), sh = A & 15;
+            const u32x4 hi = from_next_lane_or(lo[i], e1[i]);
+            const u32x4 x = sh ? funnel16(lo[i], hi, sh) : lo[i];
+            if (fc.dst) {
+                const uint8_t* c = in_al + (A - sh) + 16 * threadIdx.x + (sh ? 16 : 0);
+                copy_chunk_split(fc, c, sh ? hi : lo[i]);
+            }
+            for (int p = 0; p < M; ++p) {
+                const uint16_t cf = ex[((p + 1) * i) % kGfOrder];
+                const uint32_t xv[4] = {x.x, x.y, x.z, x.w};
+                uint32_t a[4] = {acc[p].x, acc[p].y, acc[p].z, acc[p].w};
+                for (int q = 0; q < 4; ++q) {
+                    const uint32_t w0 = gf16_mul_tab(uint16_t(xv[q]), cf, ex, lg);
+                    const uint32_t w1 = gf16_mul_tab(uint16_t(xv[q] >> 16), cf, ex, lg);
+                    a[q] ^= w0 | (w1 << 16);
+                }
+                acc[p] = u32x4{a[0], a[1], a[2], a[3]};
+            }
+        }
+    }
+#pragma unroll
+    for (int p = 0; p < M; ++p) *reinterpret_cast<u32x4*>(tile[p] + 16 * threadIdx.x) = acc[p];
+    __syncthreads();
+#pragma unroll
+    for (int p = 0; p < M; ++p) tile_store<true, kTB>(par + uint64_t(p) * Sb + t0, tile[p], nbytes);
+}
+
+typedef void (*RsEncTilesFn)(const uint8_t*, uint32_t, uint32_t, FlatCopy, uint8_t*, const uint16_t*,
+                             const uint16_t*);
+template <int... I>
+struct RsEncTilesTable {
+    static constexpr RsEncTilesFn fn[sizeof...(I)][2] = {
+        {rs16_encode_tiles_kernel<I + 1, 1>, rs16_encode_tiles_kernel<I + 1, 2>}...};
+};
+using RsEncTiles = RsEncTilesTable<0, 1, 2, 3, 4, 5, 6, 7>;
+
 static int rs_grid(int64_t S) {
     const int64_t tiles = (S * 2 + kRsTile - 1) / kRsTile;
     return int(tiles < kRsGrid ? tiles : kRsGrid);
@@ -873,6 +1002,15 @@ extern "C" int kvec_rs16_encode(const void* data_padded, void* shards, int data_
     for (int i = 0; i < data_shards; ++i) j.in_rows[i] = (const uint16_t*)data_padded + uint64_t(i) * S;
     for (int p = 0; p < parity_shards; ++p)
         j.out_rows[p] = (uint16_t*)shards + uint64_t(data_shards + p) * S;
+    const uint64_t Sb = uint64_t(S) * 2;
+    if (data_shards <= 8 && parity_shards <= 2 && Sb >= uint64_t(kTileBytes) &&
+        data_bytes < (uint64_t(1) << 31)) {
+        hipLaunchKernelGGL(RsEncTiles::fn[data_shards - 1][parity_shards - 1],
+                           dim3(uint32_t((Sb + kTileBytes - 1) / kTileBytes)), dim3(kTB), 0, st,
+                           (const uint8_t*)data_padded, uint32_t(Sb), uint32_t(data_bytes), j.copy,
+                           (uint8_t*)shards + uint64_t(data_shards) * Sb, gf_exp, gf_log);
+        return check_launch("kvec_rs16_encode");
+    }
     hipLaunchKernelGGL(rs16_encode_kernel, dim3(rs_grid(S)), dim3(kRsBS), 0, st, j, gf_exp, gf_log);
     return check_launch("kvec_rs16_encode");
 }

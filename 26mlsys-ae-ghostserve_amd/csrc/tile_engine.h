@@ -202,6 +202,24 @@ __device__ __forceinline__ void copy_chunk(const FlatCopy& fc, const uint8_t* c,
     for (int i = 0; i < 16 && o + i < fc.len; ++i) d[o + i] = byte_of(v, i);
 }
 
+// copy_chunk for a wave whose lanes store consecutive chunks: non-temporal,
+// except the chunks of the two 128-byte lines the wave shares with its
+// neighbours when its 1 KiB does not start on a line, which go through L2,
+// where the two parts of such a line merge (written non-temporally, the two
+// parts reach HBM separately).
+__device__ __forceinline__ void copy_chunk_split(const FlatCopy& fc, const uint8_t* c, u32x4 v) {
+    const uint64_t o = uint64_t(c - fc.src);
+    if (o + 16 <= fc.len) {
+        const uint32_t lane = threadIdx.x & 63;
+        const uint32_t pre = uint32_t((reinterpret_cast<uintptr_t>(fc.dst) + o - 16 * uint64_t(lane)) >> 4) & 7;
+        if (pre != 0 && (lane < 8 - pre || lane >= 64 - pre)) st16(fc.dst + o, v);
+        else st_stream(fc.dst, o, v);
+        return;
+    }
+    const gptr<uint8_t> d = as_global(fc.dst);
+    for (int i = 0; i < 16 && o + i < fc.len; ++i) d[o + i] = byte_of(v, i);
+}
+
 template <bool NT = true>
 __device__ __forceinline__ void copy_owned(const FlatCopy& fc, const RowWin& r, uint32_t off,
                                            u32x4 lo, u32x4 hi) {
