@@ -67,10 +67,36 @@ struct RsJob {
 // Byte maps of coefficient t, ptab[t][24]: dwords 0-5 lo->lo, 6-11 hi->lo,
 // 12-17 lo->hi, 18-23 hi->hi; within a map, the two dwords of field f (bits
 // 3f.. of the source byte) hold the images of the field values 0-3 and 4-7.
-// All threads call it.
+// The maps are built from basis[t][b] = coefficient t times 2^b, which the
+// caller has made visible to the threads that call it: dwords first,
+// first + stride, ... of the ncoef * kRs16Tab.
+__device__ __forceinline__ void rs_maps_from_basis(uint32_t (*ptab)[kRs16Tab], const uint16_t (*basis)[16],
+                                                   int ncoef, int first, int stride) {
+    for (int e = first; e < ncoef * kRs16Tab; e += stride) {
+        const int t = e / kRs16Tab, d = e % kRs16Tab;
+        const int map = d / 6, f = (d % 6) >> 1, half = d & 1;
+        const int src = map & 1, dst = map >> 1;   // 0 = low byte, 1 = high byte
+        uint32_t dw = 0;
+        for (int q = 0; q < 4; ++q) {
+            const int v = half * 4 + q;
+            if (f == 2 && v >= 4) continue;
+            const uint32_t x = uint32_t(v) << (3 * f);   // source byte value
+            uint32_t y = 0;
+            for (int b = 0; b < 8; ++b)
+                if (x & (1u << b)) y ^= basis[t][b + 8 * src];
+            dw |= ((y >> (8 * dst)) & 0xFFu) << (8 * q);
+        }
+        ptab[t][d] = dw;
+    }
+}
+
+// Byte maps of the coefficients coef[0 .. ncoef), their basis products read
+// from the tables (all threads).  The maps loop is written out here rather
+// than calling rs_maps_from_basis: the piece kernel compiled through the call
+// ran its two-row reconstruct in 165 instead of 151 us.
 __device__ __forceinline__ void rs_build_perm_tables(uint32_t (*ptab)[kRs16Tab], uint16_t (*basis)[16],
-                                     const uint16_t* coef, int ncoef, const uint16_t* ex,
-                                     const uint16_t* lg) {
+                                                     const uint16_t* coef, int ncoef, const uint16_t* ex,
+                                                     const uint16_t* lg) {
     for (int e = threadIdx.x; e < ncoef * 16; e += blockDim.x)
         basis[e >> 4][e & 15] = gf16_mul_tab(uint16_t(1u << (e & 15)), coef[e >> 4], ex, lg);
     __syncthreads();
@@ -929,6 +955,141 @@ struct RsEncTilesTable {
 };
 using RsEncTiles = RsEncTilesTable<0, 1, 2, 3, 4, 5, 6, 7>;
 
+// ------------------------------------------------- one-shot tile reconstruct
+// reconstruct_rs_u16_inplace of one lost data row (m = 1) on one kTileBytes
+// tile of every row per block, blocks in tile order, for k <= 8 data rows,
+// tensors below 2 GiB and rows of at least one tile.  A block reads the two
+// indices, requests its tile of every input row (the k - 1 surviving data rows
+// in order, then parity row pu), and forms the windows by a DPP lane shift;
+// the lost row goes through LDS to tile_store.
+//
+// With one lost row i and parity pu, the reference's 1 x 1 system
+// (benchmark/rs/kernel.cu:151-184) has V = g^((pu + 1) i) for the tables'
+// generator g, so its inverse is g^-((pu + 1) i) and its basis products
+// (inverse times 2^j, for the byte maps) are table reads at known exponents.
+// The syndrome Par_pu ^ XOR_r D_r g^((pu + 1) r) is Horner's rule over the
+// surviving rows when g = 2 (the piece kernel's fold); for tables of another
+// generator every input is multiplied through byte maps of its folded
+// coefficient.  Each product is the field's, as the reference's table
+// products are (the tables are taken to be a field's exp/log pair).
+//
+// Measured on the 512 MiB stream against the piece kernel (one box, lost row
+// 2 from parity 0): 103.7-104.8 against 119.6-120.6 us.  The same kernel with
+// two lost rows (the 2 x 2 inverse in closed form, one log-table read per
+// block) ran 151-157 against 147-158 us, and with 256- or 1024-thread blocks
+// slower still, so two lost rows stay on the piece kernel.
+template <int NIN, int BS = kTB>
+__global__ __launch_bounds__(BS) void rs16_reconstruct1_tiles_kernel(uint8_t* base_al, uint32_t b15,
+                                                                     uint32_t res_bytes, uint32_t Sb, int mpar,
+                                                                     const int32_t* __restrict__ missing,
+                                                                     const int32_t* __restrict__ pused,
+                                                                     const uint16_t* __restrict__ ex,
+                                                                     const uint16_t* __restrict__ lg) {
+    constexpr int ND = NIN - 1;
+    constexpr uint32_t G = kGfOrder;
+    constexpr uint32_t TB = 16 * BS;   // logical bytes per row per tile
+    __shared__ __attribute__((aligned(16))) uint8_t tile[TB + 16];
+    __shared__ __attribute__((aligned(16))) uint32_t itab[1][kRs16Tab];
+    __shared__ uint16_t basis[1][16];
+    const int miss = missing[0], pu = pused[0];
+    if (miss < 0 || miss >= NIN || pu < 0 || pu >= mpar) return;   // uniform: nothing is written
+    const bool horner = ex[1] == 2;
+    const uint32_t f = uint32_t(pu + 1);
+    auto row = [&](int j) { return j + (j >= miss ? 1 : 0); };   // surviving data row j
+    // input i's byte offset from base_al
+    auto in_off = [&](int i) { return b15 + uint32_t(i < ND ? row(i) : NIN + pu) * Sb; };
+    const uint32_t t0 = blockIdx.x * TB;
+    const uint32_t nbytes = Sb - t0 < TB ? Sb - t0 : TB;
+    const uint32_t lane = threadIdx.x & 63;
+    const __amdgpu_buffer_rsrc_t rs = chunk_rsrc(base_al, res_bytes);
+    const uint32_t linv = (G - (f * uint32_t(miss)) % G) % G;   // exponent of the inverse
+    u32x4 o;
+    if (horner) {
+        u32x4 lo[NIN], e1[NIN];
+        uint32_t shp = 0;   // the windows' shifts, 4 bits each
+#pragma unroll
+        for (int i = 0; i < NIN; ++i) {
+            const uint32_t A = in_off(i) + t0, sh = A & 15, my = A - sh + 16 * threadIdx.x;
+            lo[i] = chunk_load(rs, my);
+            e1[i] = chunk_load(rs, lane == 63 && sh ? my + 16 : kNoLoad);
+            shp |= sh << (4 * i);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        const uint32_t red2 = uint32_t(ex[16]) * 0x10001u;   // g^16 = 2^16 reduced, as g = 2
+        u32x4 x[NIN];
+#pragma unroll
+        for (int i = 0; i < NIN; ++i) {
+            const uint32_t sh = (shp >> (4 * i)) & 15;
+            const u32x4 hi = from_next_lane_or(lo[i], e1[i]);
+            x[i] = sh ? funnel16(lo[i], hi, sh) : lo[i];
+        }
+        u32x4 acc = ND > 0 ? x[ND > 0 ? ND - 1 : 0] : u32x4{0, 0, 0, 0};
+#pragma unroll
+        for (int j = ND - 2; j >= 0; --j) acc = gf16_dbl_n(acc, f * uint32_t(row(j + 1) - row(j)), red2) ^ x[j];
+        if (ND > 0) acc = gf16_dbl_n(acc, f * uint32_t(row(0)), red2);
+        const u32x4 syn = acc ^ x[ND];
+        // the inverse's basis products, read after the syndrome so that the
+        // first wave waits for them while its data arrives
+        if (threadIdx.x < 16) basis[0][threadIdx.x] = ex[(linv + uint32_t(lg[1u << threadIdx.x]) % G) % G];
+        __syncthreads();
+        rs_maps_from_basis(itab, basis, 1, threadIdx.x, blockDim.x);
+        __syncthreads();
+        u32x4 out[1];
+        rs_piece_mix<1, 1>(&syn, itab, out);
+        o = out[0];
+    } else {
+        // tables of another generator: input i's folded coefficient
+        // g^-((pu + 1) miss) g^((pu + 1) row(i)) (1 for the parity row) through
+        // byte maps, the windows read again one input at a time so that this
+        // path holds no more registers than the one above
+        __shared__ uint16_t fold[NIN];
+        __shared__ uint16_t fbasis[NIN][16];
+        __shared__ __attribute__((aligned(16))) uint32_t ftab[NIN][kRs16Tab];
+        if (threadIdx.x < NIN) {
+            const int i = threadIdx.x;
+            const uint32_t ei = i < ND ? (linv + (f * uint32_t(row(i))) % G) % G : linv;
+            fold[i] = ex[ei];
+        }
+        __syncthreads();
+        rs_build_perm_tables(ftab, fbasis, fold, NIN, ex, lg);
+        __syncthreads();
+        uint32_t acc[4] = {0, 0, 0, 0};
+#pragma unroll
+        for (int i = 0; i < NIN; ++i) {
+            const uint32_t A = in_off(i) + t0, sh = A & 15, my = A - sh + 16 * threadIdx.x;
+            const u32x4 l = chunk_load(rs, my);
+            const u32x4 h = from_next_lane_or(l, chunk_load(rs, lane == 63 && sh ? my + 16 : kNoLoad));
+            const u32x4 xi = sh ? funnel16(l, h, sh) : l;
+            uint32_t by[4];
+            split_bytes(xi, by);
+            Gf8Fields fl[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) fl[q] = gf8_fields(by[q]);
+            const uint32_t* T = ftab[i];
+            acc[0] = gf16_fma2(acc[0], fl[0], T + 0, fl[1], T + 6);
+            acc[1] = gf16_fma2(acc[1], fl[0], T + 12, fl[1], T + 18);
+            acc[2] = gf16_fma2(acc[2], fl[2], T + 0, fl[3], T + 6);
+            acc[3] = gf16_fma2(acc[3], fl[2], T + 12, fl[3], T + 18);
+            asm volatile("" : "+v"(acc[0]), "+v"(acc[1]), "+v"(acc[2]), "+v"(acc[3]) :: "memory");
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        o = join_bytes(acc);
+    }
+    *reinterpret_cast<u32x4*>(tile + 16 * threadIdx.x) = o;
+    __syncthreads();
+    tile_store<true, BS>(base_al + b15 + uint64_t(miss) * Sb + t0, tile, nbytes);
+}
+
+constexpr int kRsRecTB = kTB;                         // threads per block
+constexpr uint32_t kRsRecTile = 16 * kRsRecTB;        // logical bytes per row per tile
+typedef void (*RsRec1TilesFn)(uint8_t*, uint32_t, uint32_t, uint32_t, int, const int32_t*, const int32_t*,
+                              const uint16_t*, const uint16_t*);
+template <int... I>
+struct RsRec1TilesTable {
+    static constexpr RsRec1TilesFn fn[sizeof...(I)] = {rs16_reconstruct1_tiles_kernel<I + 1, kRsRecTB>...};
+};
+using RsRec1Tiles = RsRec1TilesTable<0, 1, 2, 3, 4, 5, 6, 7>;
+
 static int rs_grid(int64_t S) {
     const int64_t tiles = (S * 2 + kRsTile - 1) / kRsTile;
     return int(tiles < kRsGrid ? tiles : kRsGrid);
@@ -1038,6 +1199,13 @@ extern "C" int kvec_rs16_reconstruct(void* shards, int shard_size, int data_shar
     if (shard_size == 0) return KVEC_OK;
     const uint64_t Sb = uint64_t(shard_size) * 2;
     const uint32_t res = piece_res_bytes(shards, uint64_t(data_shards + parity_shards) * Sb);
+    if (data_shards <= kRsPieceMaxIn && m == 1 && res && Sb >= kRsRecTile) {
+        hipLaunchKernelGGL(RsRec1Tiles::fn[data_shards - 1], dim3(uint32_t((Sb + kRsRecTile - 1) / kRsRecTile)),
+                           dim3(kRsRecTB), 0, as_stream(stream), align_down16(shards),
+                           uint32_t(reinterpret_cast<uintptr_t>(shards) & 15), res, uint32_t(Sb), parity_shards,
+                           missing_data, parity_used, gf_exp, gf_log);
+        return check_launch("kvec_rs16_reconstruct");
+    }
     if (data_shards <= kRsPieceMaxIn && m <= kRsGroup && res) {
         hipLaunchKernelGGL(RsPiece::rec[data_shards - 1][m - 1], dim3(piece_grid(Sb, kRsPieceBlocks)), dim3(kPieceBS), 0,
                            as_stream(stream), align_down16(shards), uint32_t(reinterpret_cast<uintptr_t>(shards) & 15),

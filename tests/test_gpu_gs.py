@@ -508,6 +508,43 @@ def test_rs16_reconstruct_offsets_and_generators(pkg, ora, gpu, k, mp, S, soff, 
         assert bool((rest == 0x2A2A).all()), (miss, pused)
 
 
+@pytest.mark.parametrize("k", range(1, 9))
+@pytest.mark.parametrize("S,soff,gen4", [(4096, 0, False), (8192 * 2 + 7, 3, False), (4096 * 3 + 1, 5, True)])
+def test_rs16_reconstruct_tiles(pkg, ora, gpu, k, S, soff, gen4):
+    """Rows of at least one 8 KiB tile with k <= 8: one lost row takes the
+    one-shot tile reconstruct, two the piece kernel.  Every single and every
+    pair of lost rows, parity rows in either order and up to parity 2, a
+    repeated parity row (the reference's singular system, whose second
+    Gauss-Jordan step is skipped: the output is not the data but must still be
+    the reference's), the tensor at an odd word offset, and tables with
+    generator 4."""
+    mp = 3
+    ex, lg = _gen4_tables(ora) if gen4 else ora.gf16_tables()
+    rng = np.random.default_rng(k * 31 + S + soff)
+    data = rng.integers(0, 65536, k * S, dtype=np.uint16)
+    ref = ora.rs16_encode(data, k, mp, S, ex, lg)
+    gex, glg = dev(ex, gpu), dev(lg, gpu)
+    pairs = [(0, 1), (1, 0), (2, 0), (1, 2), (1, 1), (2, 2)]
+    cases = [((i,), (i % mp,)) for i in range(k)]
+    cases += [(mi, pairs[n % len(pairs)]) for n, mi in enumerate(itertools.combinations(range(k), 2))]
+    cases += [((k - 1, 0), (0, 1))] if k >= 2 else []
+    buf = torch.full(((k + mp) * S + 16,), 0x2A2A, dtype=torch.int16, device=gpu)
+    d = buf[soff:soff + (k + mp) * S].view(k + mp, S).view(torch.uint16)
+    for miss, pused in cases:
+        sh = ref.copy()
+        sh[list(miss)] = rng.integers(0, 65536, (len(miss), S), dtype=np.uint16)
+        want = sh.copy()
+        ora.rs16_reconstruct(want, S, k, mp, list(miss), list(pused), ex, lg)
+        assert np.array_equal(want, ref) == (len(set(pused)) == len(pused)), (miss, pused)
+        buf[soff:soff + (k + mp) * S] = dev(sh.reshape(-1).view(np.int16), gpu)
+        pkg.rs.rs_kernel.reconstruct_rs_u16_inplace(
+            d, S, k, mp, torch.tensor(miss, dtype=torch.int32, device=gpu),
+            torch.tensor(pused, dtype=torch.int32, device=gpu), gex, glg)
+        assert np.array_equal(host(d), want), (miss, pused)
+        rest = torch.cat([buf[:soff], buf[soff + (k + mp) * S:]])
+        assert bool((rest == 0x2A2A).all()), (miss, pused)
+
+
 def test_rs16_bad_device_indices_write_nothing(pkg, gpu):
     k, m, S = 6, 2, 100
     d = torch.zeros((k + m, S), dtype=torch.uint16, device=gpu)
