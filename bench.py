@@ -754,6 +754,22 @@ def bench_gs(pkg, torch, oracle, dev, seed, steps, warmup):
         raise RuntimeError("gs RS16 reconstruct did not restore the rows")
     del keep
     out["rs16_reconstruct_2lost"] = _entry(time_us(torch, rrec), nd * S * 2 + 2 * S * 2)
+
+    # one lost data row (row 2, from parity 0)
+    md1 = torch.tensor([2], dtype=torch.int32, device=dev)
+    pu1 = torch.tensor([0], dtype=torch.int32, device=dev)
+    keep = sh[2].clone()
+    sh[2].fill_(0x2222)
+
+    def rrec1(i):
+        pkg.rs.rs_kernel.reconstruct_rs_u16_inplace(sets[i % 2][1], S, nd, m, md1, pu1, ex, lg)
+
+    rrec1(0)
+    torch.cuda.synchronize()
+    if not torch.equal(sh[2], keep):
+        raise RuntimeError("gs RS16 reconstruct did not restore the row")
+    del keep
+    out["rs16_reconstruct_1lost"] = _entry(time_us(torch, rrec1), nd * S * 2 + S * 2)
     del sets, sh
 
     # The serving plugin's per-step parity (bench_ghostserve_rdp.py:334-360):
@@ -1049,7 +1065,8 @@ def main():
             f"{gs['xor_reconstruct_1lost']['us']:.1f} us, from K, V "
             f"{gs['xor_encode_from_kv']['us']:.1f} us, decode {gs['xor_decode_1lost']['us']:.1f} us), "
             f"RS16 {gs['rs16_encode']['us']:.1f} us (reconstruct "
-            f"{gs['rs16_reconstruct_2lost']['us']:.1f} us)")
+            f"{gs['rs16_reconstruct_2lost']['us']:.1f} us, one row "
+            f"{gs['rs16_reconstruct_1lost']['us']:.1f} us)")
         torch.cuda.empty_cache()
 
     c0 = None
