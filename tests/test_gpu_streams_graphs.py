@@ -118,23 +118,25 @@ def test_xor_and_rs16_encodes_in_hip_graph(pkg, gpu):
         assert torch.equal(xs, xe) and torch.equal(rsh, re), rep
 
 
-def test_rs16_reconstruct_in_hip_graph(pkg, gpu):
-    """reconstruct_rs_u16_inplace captured once; before each replay the
-    tensor is re-encoded from new data and the lost rows are overwritten."""
+@pytest.mark.parametrize("lost,used", [((1, 4), (0, 1)), ((2,), (1,))])
+def test_rs16_reconstruct_in_hip_graph(pkg, gpu, lost, used):
+    """reconstruct_rs_u16_inplace captured once (two lost rows: the piece
+    kernel; one: the tile kernel); before each replay the tensor is re-encoded
+    from new data and the lost rows are overwritten."""
     k, m, S = 6, 2, 44741
     ex, lg = pkg.rs.device_gf_tables(gpu)
     data = _bytes(k * S * 2, gpu, 3).view(torch.uint16)
     sh = torch.empty((k + m, S), dtype=torch.uint16, device=gpu)
-    md = torch.tensor([1, 4], dtype=torch.int32, device=gpu)
-    pu = torch.tensor([0, 1], dtype=torch.int32, device=gpu)
+    md = torch.tensor(lost, dtype=torch.int32, device=gpu)
+    pu = torch.tensor(used, dtype=torch.int32, device=gpu)
     pkg.rs.rs_kernel.encode_rs_u16(data, sh, k, m, S, ex, lg)
     graph = _capture(lambda: pkg.rs.rs_kernel.reconstruct_rs_u16_inplace(sh, S, k, m, md, pu, ex, lg))
     for rep in range(4):
         data.view(torch.uint8).random_(0, 256)
         pkg.rs.rs_kernel.encode_rs_u16(data, sh, k, m, S, ex, lg)
         want = sh.clone()
-        sh[1].fill_(0x1111 + rep)
-        sh[4].fill_(0x4444 + rep)
+        for r in lost:
+            sh[r].fill_(0x1111 * (r + 1) + rep)
         torch.cuda.synchronize()
         graph.replay()
         torch.cuda.synchronize()
