@@ -638,11 +638,13 @@ __global__ __launch_bounds__(kRsBS) __attribute__((amdgpu_waves_per_eu(4))) void
 // every input row's window of a piece requested at once and the next piece's
 // requested before the current one is coded; no LDS tiles and no block
 // barriers.  For up to kRsPieceMaxIn inputs, up to kRsGroup outputs and
-// tensors of fewer than 2^31 bytes.  Measured on the 512 MiB stream against
-// the tile kernel (same box): the reconstruct of 2 rows 165 against 168-196
-// us with the folded byte maps, 149.6 us with the syndromes by Horner's rule
-// below; the encode on pieces took 279-304 against 245-255 us (with aligned
-// or misaligned data-row stores alike), so the encode stays on the tiles.
+// tensors of fewer than 2^31 bytes; rows of at least one tile take the
+// one-shot tile reconstruct below instead.  Measured on the 512 MiB stream
+// against the persistent tile kernel (same box): the reconstruct of 2 rows 165
+// against 168-196 us with the folded byte maps, 149.6 us with the syndromes by
+// Horner's rule below; the encode on pieces took 279-304 against 245-255 us
+// (with aligned or misaligned data-row stores alike), so the encode stays on
+// the tiles.
 constexpr int kRsPieceMaxIn = 8;
 constexpr uint32_t kRsPieceBlocks = 1024;   // persistent: the tables are built once per block
 
@@ -956,139 +958,272 @@ struct RsEncTilesTable {
 using RsEncTiles = RsEncTilesTable<0, 1, 2, 3, 4, 5, 6, 7>;
 
 // ------------------------------------------------- one-shot tile reconstruct
-// reconstruct_rs_u16_inplace of one lost data row (m = 1) on one kTileBytes
-// tile of every row per block, blocks in tile order, for k <= 8 data rows,
-// tensors below 2 GiB and rows of at least one tile.  A block reads the two
-// indices, requests its tile of every input row (the k - 1 surviving data rows
-// in order, then parity row pu), and forms the windows by a DPP lane shift;
-// the lost row goes through LDS to tile_store.
+// reconstruct_rs_u16_inplace of m <= 2 lost data rows on one kTileBytes tile
+// of every row per block, blocks in tile order, for k <= 8 data rows, tensors
+// below 2 GiB and rows of at least one tile.  A block reads the indices,
+// requests its tile of every input row (the surviving data rows in order,
+// then the parity rows of parity_used) and forms the windows by a DPP lane
+// shift; the lost rows go through LDS to tile_store.
 //
-// With one lost row i and parity pu, the reference's 1 x 1 system
-// (benchmark/rs/kernel.cu:151-184) has V = g^((pu + 1) i) for the tables'
-// generator g, so its inverse is g^-((pu + 1) i) and its basis products
-// (inverse times 2^j, for the byte maps) are table reads at known exponents.
-// The syndrome Par_pu ^ XOR_r D_r g^((pu + 1) r) is Horner's rule over the
-// surviving rows when g = 2 (the piece kernel's fold); for tables of another
-// generator every input is multiplied through byte maps of its folded
-// coefficient.  Each product is the field's, as the reference's table
-// products are (the tables are taken to be a field's exp/log pair).
+// The inverse.  V[r][c] = g^((pu_r + 1) miss_c) for the tables' generator g,
+// so every entry is a power of g and the reference's Gauss-Jordan steps
+// (benchmark/rs/kernel.cu:151-184: pivot V[0][0], never zero; then the
+// remainder of V[1][1], skipped when zero) come down to sums of exponents and
+// at most one log-table read.  With a, b, c, d the exponents of V[0][0],
+// V[0][1], V[1][0], V[1][1] and e = b + c - a:
+//     m = 1:           inv = g^-a
+//     m = 2, d == e:   inv = [[g^-a, 0], [g^(c-a), 1]]       (singular, step 2 skipped)
+//     m = 2, d != e:   p = log(g^d ^ g^e),
+//                      inv = [[g^-a ^ g^(b+c-2a-p), g^(b-a-p)], [g^(c-a-p), g^-p]]
+// each product taken in the field the tables define, as the reference's
+// table products are (the tables are taken to be a field's exp/log pair).
 //
-// Measured on the 512 MiB stream against the piece kernel (one box, lost row
-// 2 from parity 0): 103.7-104.8 against 119.6-120.6 us.  The same kernel with
-// two lost rows (the 2 x 2 inverse in closed form, one log-table read per
-// block) ran 151-157 against 147-158 us, and with 256- or 1024-thread blocks
-// slower still, so two lost rows stay on the piece kernel.
-template <int NIN, int BS = kTB>
-__global__ __launch_bounds__(BS) void rs16_reconstruct1_tiles_kernel(uint8_t* base_al, uint32_t b15,
-                                                                     uint32_t res_bytes, uint32_t Sb, int mpar,
-                                                                     const int32_t* __restrict__ missing,
-                                                                     const int32_t* __restrict__ pused,
-                                                                     const uint16_t* __restrict__ ex,
-                                                                     const uint16_t* __restrict__ lg) {
-    constexpr int ND = NIN - 1;
-    constexpr uint32_t G = kGfOrder;
-    constexpr uint32_t TB = 16 * BS;   // logical bytes per row per tile
-    __shared__ __attribute__((aligned(16))) uint8_t tile[TB + 16];
-    __shared__ __attribute__((aligned(16))) uint32_t itab[1][kRs16Tab];
-    __shared__ uint16_t basis[1][16];
-    const int miss = missing[0], pu = pused[0];
-    if (miss < 0 || miss >= NIN || pu < 0 || pu >= mpar) return;   // uniform: nothing is written
-    const bool horner = ex[1] == 2;
-    const uint32_t f = uint32_t(pu + 1);
-    auto row = [&](int j) { return j + (j >= miss ? 1 : 0); };   // surviving data row j
-    // input i's byte offset from base_al
-    auto in_off = [&](int i) { return b15 + uint32_t(i < ND ? row(i) : NIN + pu) * Sb; };
-    const uint32_t t0 = blockIdx.x * TB;
-    const uint32_t nbytes = Sb - t0 < TB ? Sb - t0 : TB;
-    const uint32_t lane = threadIdx.x & 63;
-    const __amdgpu_buffer_rsrc_t rs = chunk_rsrc(base_al, res_bytes);
-    const uint32_t linv = (G - (f * uint32_t(miss)) % G) % G;   // exponent of the inverse
-    u32x4 o;
-    if (horner) {
-        u32x4 lo[NIN], e1[NIN];
-        uint32_t shp = 0;   // the windows' shifts, 4 bits each
-#pragma unroll
-        for (int i = 0; i < NIN; ++i) {
-            const uint32_t A = in_off(i) + t0, sh = A & 15, my = A - sh + 16 * threadIdx.x;
-            lo[i] = chunk_load(rs, my);
-            e1[i] = chunk_load(rs, lane == 63 && sh ? my + 16 : kNoLoad);
-            shp |= sh << (4 * i);
-        }
-        __builtin_amdgcn_sched_barrier(0);
-        const uint32_t red2 = uint32_t(ex[16]) * 0x10001u;   // g^16 = 2^16 reduced, as g = 2
-        u32x4 x[NIN];
-#pragma unroll
-        for (int i = 0; i < NIN; ++i) {
-            const uint32_t sh = (shp >> (4 * i)) & 15;
-            const u32x4 hi = from_next_lane_or(lo[i], e1[i]);
-            x[i] = sh ? funnel16(lo[i], hi, sh) : lo[i];
-        }
-        u32x4 acc = ND > 0 ? x[ND > 0 ? ND - 1 : 0] : u32x4{0, 0, 0, 0};
-#pragma unroll
-        for (int j = ND - 2; j >= 0; --j) acc = gf16_dbl_n(acc, f * uint32_t(row(j + 1) - row(j)), red2) ^ x[j];
-        if (ND > 0) acc = gf16_dbl_n(acc, f * uint32_t(row(0)), red2);
-        const u32x4 syn = acc ^ x[ND];
-        // the inverse's basis products, read after the syndrome so that the
-        // first wave waits for them while its data arrives
-        if (threadIdx.x < 16) basis[0][threadIdx.x] = ex[(linv + uint32_t(lg[1u << threadIdx.x]) % G) % G];
-        __syncthreads();
-        rs_maps_from_basis(itab, basis, 1, threadIdx.x, blockDim.x);
-        __syncthreads();
-        u32x4 out[1];
-        rs_piece_mix<1, 1>(&syn, itab, out);
-        o = out[0];
+// Every wave forms the inverse's byte maps itself, so no wave waits at a
+// block barrier for another's table reads: lane t * 16 + j reads entry t
+// times 2^j (the entry's basis products) from the tables into the wave's LDS,
+// and lanes below 6 m^2 span each 3-bit field's eight images from three of
+// them and pack the maps there too.  The syndromes are Horner's rule over the
+// surviving rows when g = 2 (the piece kernel's fold); tables of another
+// generator fold every input's coefficient into byte maps built by the block
+// and read the windows again one input at a time, so that path adds no
+// registers (58 VGPRs, 8 waves per SIMD).
+//
+// Measured on the 512 MiB stream against the piece kernel (one box, A/B,
+// byte-identical): rows 1 and 4 lost 132.5-136.6 against 151.3-156.6 us, rows
+// 0 and 5 129.2-129.6 against 146.5-148.1 us, row 2 101.9-102.7 against
+// 119.6-120.6 us.  Earlier forms: the maps built once per block behind two
+// block barriers, 151-157 us for two rows (104 us for one); every wave
+// building them with the generic map loop, 172-186 us.
+template <int NIN, int M, int BS = kTB>
+__global__ __launch_bounds__(BS) void rs16_reconstruct_tiles_kernel(uint8_t* base_al, uint32_t b15,
+                                                                    uint32_t res_bytes, uint32_t Sb, int mpar,
+                                                                    const int32_t* __restrict__ missing,
+                                                                    const int32_t* __restrict__ pused,
+                                                                    const uint16_t* __restrict__ ex,
+                                                                    const uint16_t* __restrict__ lg) {
+    if constexpr (M > NIN) {
+        return;   // no such code: the host requires k >= m
     } else {
-        // tables of another generator: input i's folded coefficient
-        // g^-((pu + 1) miss) g^((pu + 1) row(i)) (1 for the parity row) through
-        // byte maps, the windows read again one input at a time so that this
-        // path holds no more registers than the one above
-        __shared__ uint16_t fold[NIN];
-        __shared__ uint16_t fbasis[NIN][16];
-        __shared__ __attribute__((aligned(16))) uint32_t ftab[NIN][kRs16Tab];
-        if (threadIdx.x < NIN) {
-            const int i = threadIdx.x;
-            const uint32_t ei = i < ND ? (linv + (f * uint32_t(row(i))) % G) % G : linv;
-            fold[i] = ex[ei];
+        constexpr int ND = NIN - M, NW = BS / 64;
+        constexpr uint32_t G = kGfOrder;
+        constexpr uint32_t TB = 16 * BS;   // logical bytes per row per tile
+        __shared__ __attribute__((aligned(16))) uint8_t tile[M][TB + 16];
+        __shared__ __attribute__((aligned(16))) uint32_t wtab[NW][M * M][kRs16Tab];
+        __shared__ uint16_t wbasis[NW][M * M * 16];
+        int miss[M], pu[M];
+        bool ok = true;
+#pragma unroll
+        for (int q = 0; q < M; ++q) {
+            miss[q] = missing[q];
+            pu[q] = pused[q];
+            ok = ok && miss[q] >= 0 && miss[q] < NIN && pu[q] >= 0 && pu[q] < mpar;
         }
-        __syncthreads();
-        rs_build_perm_tables(ftab, fbasis, fold, NIN, ex, lg);
-        __syncthreads();
-        uint32_t acc[4] = {0, 0, 0, 0};
+        if (M == 2) ok = ok && miss[0] != miss[M - 1];
+        if (!ok) return;   // uniform: the whole grid writes nothing
+        const bool horner = ex[1] == 2;
+        const int m_lo = M == 2 ? min(miss[0], miss[M - 1]) : miss[0];
+        const int m_hi = M == 2 ? max(miss[0], miss[M - 1]) : NIN;
+        uint32_t rowp = 0;   // the surviving data rows, 4 bits each
 #pragma unroll
-        for (int i = 0; i < NIN; ++i) {
-            const uint32_t A = in_off(i) + t0, sh = A & 15, my = A - sh + 16 * threadIdx.x;
-            const u32x4 l = chunk_load(rs, my);
-            const u32x4 h = from_next_lane_or(l, chunk_load(rs, lane == 63 && sh ? my + 16 : kNoLoad));
-            const u32x4 xi = sh ? funnel16(l, h, sh) : l;
-            uint32_t by[4];
-            split_bytes(xi, by);
-            Gf8Fields fl[4];
+        for (int j = 0; j < ND; ++j) {
+            int r = j + (j >= m_lo ? 1 : 0);
+            if (M == 2) r += r >= m_hi ? 1 : 0;
+            rowp |= uint32_t(r) << (4 * j);
+        }
+        auto row = [&](int j) { return int((rowp >> (4 * j)) & 15); };
+        auto in_off = [&](int i) {
+            return b15 + uint32_t(i < ND ? row(i) : NIN + pu[i < ND ? 0 : i - ND]) * Sb;
+        };
+        const uint32_t t0 = blockIdx.x * TB;
+        const uint32_t nbytes = Sb - t0 < TB ? Sb - t0 : TB;
+        const uint32_t lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+        const __amdgpu_buffer_rsrc_t rs = chunk_rsrc(base_al, res_bytes);
+        auto add = [](uint32_t x, uint32_t y) { return x + y >= G ? x + y - G : x + y; };
+        auto neg = [](uint32_t x) { return x ? G - x : 0u; };
+        // the inverse's entries t = c * M + r as up to two powers of g
+        uint32_t L1[M * M], L2[M * M];
+        bool has1[M * M], has2[M * M];
+        auto inverse = [&]() {
+            const uint32_t a = uint32_t((pu[0] + 1) * miss[0]) % G;
 #pragma unroll
-            for (int q = 0; q < 4; ++q) fl[q] = gf8_fields(by[q]);
-            const uint32_t* T = ftab[i];
-            acc[0] = gf16_fma2(acc[0], fl[0], T + 0, fl[1], T + 6);
-            acc[1] = gf16_fma2(acc[1], fl[0], T + 12, fl[1], T + 18);
-            acc[2] = gf16_fma2(acc[2], fl[2], T + 0, fl[3], T + 6);
-            acc[3] = gf16_fma2(acc[3], fl[2], T + 12, fl[3], T + 18);
-            asm volatile("" : "+v"(acc[0]), "+v"(acc[1]), "+v"(acc[2]), "+v"(acc[3]) :: "memory");
+            for (int t = 0; t < M * M; ++t) has1[t] = true, has2[t] = false, L1[t] = L2[t] = 0;
+            L1[0] = neg(a);
+            if constexpr (M == 2) {
+                const uint32_t b = uint32_t((pu[0] + 1) * miss[1]) % G;
+                const uint32_t c = uint32_t((pu[1] + 1) * miss[0]) % G;
+                const uint32_t d = uint32_t((pu[1] + 1) * miss[1]) % G;
+                const uint32_t e = add(add(b, c), neg(a));
+                if (d == e) {
+                    has1[1] = false;
+                    L1[2] = add(c, neg(a));
+                } else {
+                    const uint32_t p = uint32_t(lg[uint16_t(ex[d] ^ ex[e])]) % G, np = neg(p);
+                    L2[0] = add(add(e, neg(a)), np);   // b + c - 2a - p
+                    has2[0] = true;
+                    L1[1] = add(add(b, neg(a)), np);
+                    L1[2] = add(add(c, neg(a)), np);
+                    L1[3] = np;
+                }
+            }
+        };
+        u32x4 o[M];
+        if (horner) {
+            u32x4 lo[NIN], e1[NIN];
+            uint32_t shp = 0;   // the windows' shifts, 4 bits each
+#pragma unroll
+            for (int i = 0; i < NIN; ++i) {
+                const uint32_t A = in_off(i) + t0, sh = A & 15, my = A - sh + 16 * threadIdx.x;
+                lo[i] = chunk_load(rs, my);
+                e1[i] = chunk_load(rs, lane == 63 && sh ? my + 16 : kNoLoad);
+                shp |= sh << (4 * i);
+            }
             __builtin_amdgcn_sched_barrier(0);
+            inverse();
+            // this lane's basis product (lanes below 16 M^2), in flight with
+            // the data; with g = 2, log(2^j) = j
+            uint32_t bv = 0;
+            {
+                const int t = int(lane >> 4);
+                const uint32_t j = lane & 15;
+                uint32_t l1 = L1[0], l2 = L2[0];
+                bool h1 = has1[0], h2 = has2[0];
+#pragma unroll
+                for (int q = 1; q < M * M; ++q)
+                    if (t == q) l1 = L1[q], l2 = L2[q], h1 = has1[q], h2 = has2[q];
+                if (t < M * M) {
+                    bv = h1 ? ex[add(l1, j)] : 0u;
+                    if (h2) bv ^= ex[add(l2, j)];
+                }
+            }
+            const uint32_t red2 = uint32_t(ex[16]) * 0x10001u;   // g^16 = 2^16 reduced, as g = 2
+            u32x4 x[NIN];
+#pragma unroll
+            for (int i = 0; i < NIN; ++i) {
+                const uint32_t sh = (shp >> (4 * i)) & 15;
+                const u32x4 hi = from_next_lane_or(lo[i], e1[i]);
+                x[i] = sh ? funnel16(lo[i], hi, sh) : lo[i];
+            }
+            u32x4 bsyn[M];
+#pragma unroll
+            for (int r = 0; r < M; ++r) {
+                const uint32_t f = uint32_t(pu[r] + 1);
+                u32x4 acc = ND > 0 ? x[ND > 0 ? ND - 1 : 0] : u32x4{0, 0, 0, 0};
+#pragma unroll
+                for (int j = ND - 2; j >= 0; --j)
+                    acc = gf16_dbl_n(acc, f * uint32_t(row(j + 1) - row(j)), red2) ^ x[j];
+                if (ND > 0) acc = gf16_dbl_n(acc, f * uint32_t(row(0)), red2);
+                bsyn[r] = acc ^ x[ND + r];
+            }
+            // byte maps: lane g < 6 M^2 takes coefficient g / 6, source byte
+            // (g % 6) / 3 and field g % 3; its three basis products are those
+            // of the field's bits (none for bit 8 of the 2-bit field)
+            auto wave_lds_sync = []() {
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                __builtin_amdgcn_wave_barrier();
+                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            };
+            if (lane < M * M * 16) wbasis[wv][lane] = uint16_t(bv);
+            wave_lds_sync();
+            {
+                const int g = int(lane), t = g / 6, src = (g % 6) / 3, f = g % 3;
+                const int b0 = t * 16 + 8 * src + 3 * f;
+                if (g < 6 * M * M) {
+                    const uint32_t B0 = wbasis[wv][b0], B1 = wbasis[wv][b0 + 1], B2 = f < 2 ? wbasis[wv][b0 + 2] : 0u;
+                    const uint32_t e[8] = {0u, B0, B1, B0 ^ B1, B2, B0 ^ B2, B1 ^ B2, B0 ^ B1 ^ B2};
+#pragma unroll
+                    for (int dst = 0; dst < 2; ++dst) {
+#pragma unroll
+                        for (int half = 0; half < 2; ++half) {
+                            uint32_t dw = 0;
+#pragma unroll
+                            for (int q = 0; q < 4; ++q) dw |= ((e[4 * half + q] >> (8 * dst)) & 0xFFu) << (8 * q);
+                            if (f == 2 && half) dw = 0;   // the 2-bit field has four images
+                            wtab[wv][t][(2 * dst + src) * 6 + 2 * f + half] = dw;
+                        }
+                    }
+                }
+            }
+            wave_lds_sync();
+            rs_piece_mix<M, M>(bsyn, wtab[wv], o);
+        } else {
+            // tables of another generator: the byte maps of the folded
+            // coefficients, output c's coefficient of input i at
+            // fold[c * NIN + i], built by the block; the windows are read again
+            // one input at a time so that this path holds no more registers
+            // than the one above
+            __shared__ uint16_t fold[M * NIN];
+            __shared__ uint16_t fbasis[M * NIN][16];
+            __shared__ __attribute__((aligned(16))) uint32_t ftab[M * NIN][kRs16Tab];
+            inverse();
+            if (threadIdx.x < M * NIN) {
+                const int c = threadIdx.x / NIN, in = threadIdx.x % NIN;
+                auto inv = [&](int r) {
+                    uint16_t v = 0;
+#pragma unroll
+                    for (int t = 0; t < M * M; ++t)
+                        if (t == c * M + r) v = (has1[t] ? ex[L1[t]] : 0) ^ (has2[t] ? ex[L2[t]] : 0);
+                    return v;
+                };
+                uint16_t v = 0;
+                if (in < ND) {
+#pragma unroll
+                    for (int r = 0; r < M; ++r)
+                        v ^= gf16_mul_tab(inv(r), ex[(uint32_t(pu[r] + 1) * uint32_t(row(in))) % G], ex, lg);
+                } else {
+                    v = inv(in - ND);
+                }
+                fold[threadIdx.x] = v;
+            }
+            __syncthreads();
+            rs_build_perm_tables(ftab, fbasis, fold, M * NIN, ex, lg);
+            __syncthreads();
+            uint32_t acc[M][4];
+#pragma unroll
+            for (int c = 0; c < M; ++c) acc[c][0] = acc[c][1] = acc[c][2] = acc[c][3] = 0;
+#pragma unroll
+            for (int i = 0; i < NIN; ++i) {
+                const uint32_t A = in_off(i) + t0, sh = A & 15, my = A - sh + 16 * threadIdx.x;
+                const u32x4 l = chunk_load(rs, my);
+                const u32x4 h = from_next_lane_or(l, chunk_load(rs, lane == 63 && sh ? my + 16 : kNoLoad));
+                const u32x4 xi = sh ? funnel16(l, h, sh) : l;
+                uint32_t by[4];
+                split_bytes(xi, by);
+                Gf8Fields fl[4];
+#pragma unroll
+                for (int q = 0; q < 4; ++q) fl[q] = gf8_fields(by[q]);
+#pragma unroll
+                for (int c = 0; c < M; ++c) {
+                    const uint32_t* T = ftab[c * NIN + i];
+                    acc[c][0] = gf16_fma2(acc[c][0], fl[0], T + 0, fl[1], T + 6);
+                    acc[c][1] = gf16_fma2(acc[c][1], fl[0], T + 12, fl[1], T + 18);
+                    acc[c][2] = gf16_fma2(acc[c][2], fl[2], T + 0, fl[3], T + 6);
+                    acc[c][3] = gf16_fma2(acc[c][3], fl[2], T + 12, fl[3], T + 18);
+                    asm volatile("" : "+v"(acc[c][0]), "+v"(acc[c][1]), "+v"(acc[c][2]), "+v"(acc[c][3]) :: "memory");
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+            }
+#pragma unroll
+            for (int c = 0; c < M; ++c) o[c] = join_bytes(acc[c]);
         }
-        o = join_bytes(acc);
+#pragma unroll
+        for (int c = 0; c < M; ++c) *reinterpret_cast<u32x4*>(tile[c] + 16 * threadIdx.x) = o[c];
+        __syncthreads();
+#pragma unroll
+        for (int c = 0; c < M; ++c)
+            tile_store<true, BS>(base_al + b15 + uint64_t(miss[c]) * Sb + t0, tile[c], nbytes);
     }
-    *reinterpret_cast<u32x4*>(tile + 16 * threadIdx.x) = o;
-    __syncthreads();
-    tile_store<true, BS>(base_al + b15 + uint64_t(miss) * Sb + t0, tile, nbytes);
 }
 
 constexpr int kRsRecTB = kTB;                         // threads per block
 constexpr uint32_t kRsRecTile = 16 * kRsRecTB;        // logical bytes per row per tile
-typedef void (*RsRec1TilesFn)(uint8_t*, uint32_t, uint32_t, uint32_t, int, const int32_t*, const int32_t*,
-                              const uint16_t*, const uint16_t*);
+typedef void (*RsRecTilesFn)(uint8_t*, uint32_t, uint32_t, uint32_t, int, const int32_t*, const int32_t*,
+                             const uint16_t*, const uint16_t*);
 template <int... I>
-struct RsRec1TilesTable {
-    static constexpr RsRec1TilesFn fn[sizeof...(I)] = {rs16_reconstruct1_tiles_kernel<I + 1, kRsRecTB>...};
+struct RsRecTilesTable {
+    static constexpr RsRecTilesFn fn[sizeof...(I)][2] = {
+        {rs16_reconstruct_tiles_kernel<I + 1, 1, kRsRecTB>, rs16_reconstruct_tiles_kernel<I + 1, 2, kRsRecTB>}...};
 };
-using RsRec1Tiles = RsRec1TilesTable<0, 1, 2, 3, 4, 5, 6, 7>;
+using RsRecTiles = RsRecTilesTable<0, 1, 2, 3, 4, 5, 6, 7>;
 
 static int rs_grid(int64_t S) {
     const int64_t tiles = (S * 2 + kRsTile - 1) / kRsTile;
@@ -1199,8 +1334,8 @@ extern "C" int kvec_rs16_reconstruct(void* shards, int shard_size, int data_shar
     if (shard_size == 0) return KVEC_OK;
     const uint64_t Sb = uint64_t(shard_size) * 2;
     const uint32_t res = piece_res_bytes(shards, uint64_t(data_shards + parity_shards) * Sb);
-    if (data_shards <= kRsPieceMaxIn && m == 1 && res && Sb >= kRsRecTile) {
-        hipLaunchKernelGGL(RsRec1Tiles::fn[data_shards - 1], dim3(uint32_t((Sb + kRsRecTile - 1) / kRsRecTile)),
+    if (data_shards <= kRsPieceMaxIn && m <= kRsGroup && res && Sb >= kRsRecTile) {
+        hipLaunchKernelGGL(RsRecTiles::fn[data_shards - 1][m - 1], dim3(uint32_t((Sb + kRsRecTile - 1) / kRsRecTile)),
                            dim3(kRsRecTB), 0, as_stream(stream), align_down16(shards),
                            uint32_t(reinterpret_cast<uintptr_t>(shards) & 15), res, uint32_t(Sb), parity_shards,
                            missing_data, parity_used, gf_exp, gf_log);

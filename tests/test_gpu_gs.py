@@ -511,9 +511,9 @@ def test_rs16_reconstruct_offsets_and_generators(pkg, ora, gpu, k, mp, S, soff, 
 @pytest.mark.parametrize("k", range(1, 9))
 @pytest.mark.parametrize("S,soff,gen4", [(4096, 0, False), (8192 * 2 + 7, 3, False), (4096 * 3 + 1, 5, True)])
 def test_rs16_reconstruct_tiles(pkg, ora, gpu, k, S, soff, gen4):
-    """Rows of at least one 8 KiB tile with k <= 8: one lost row takes the
-    one-shot tile reconstruct, two the piece kernel.  Every single and every
-    pair of lost rows, parity rows in either order and up to parity 2, a
+    """Rows of at least one 8 KiB tile with k <= 8 take the one-shot tile
+    reconstruct (each wave building the inverse's byte maps).  Every single
+    and every pair of lost rows, parity rows in either order and up to parity 2, a
     repeated parity row (the reference's singular system, whose second
     Gauss-Jordan step is skipped: the output is not the data but must still be
     the reference's), the tensor at an odd word offset, and tables with

@@ -120,8 +120,8 @@ def test_xor_and_rs16_encodes_in_hip_graph(pkg, gpu):
 
 @pytest.mark.parametrize("lost,used", [((1, 4), (0, 1)), ((2,), (1,))])
 def test_rs16_reconstruct_in_hip_graph(pkg, gpu, lost, used):
-    """reconstruct_rs_u16_inplace captured once (two lost rows: the piece
-    kernel; one: the tile kernel); before each replay the tensor is re-encoded
+    """reconstruct_rs_u16_inplace (the one-shot tile kernel) captured once, for
+    two lost rows and for one; before each replay the tensor is re-encoded
     from new data and the lost rows are overwritten."""
     k, m, S = 6, 2, 44741
     ex, lg = pkg.rs.device_gf_tables(gpu)
