@@ -841,8 +841,10 @@ static uint8_t* align_down16(const void* p) {
 // wait counter is not the vector loads': with gf_exp[1] == 2 (the tables of
 // init_gf_tables, or any field's exp/log pair whose generator is 2) the
 // coefficient alpha^((p+1) i) is (p+1) i doublings with the field's reduction
-// word 0x8000 * 2; for other tables each word is multiplied through the
-// tables.  (Like the byte maps, this takes the tables to be a field's.)
+// word gf_exp[16] = 2^16 reduced (one table read; 0x8000 * 2 through the log
+// table took two dependent reads and ran 217.5-221.5 against 220.4-229.9 us);
+// for other tables each word is multiplied through the tables.  (Like the
+// byte maps, this takes the tables to be a field's.)
 //
 // Data-row copy stores are non-temporal, except the chunks in the two
 // 128-byte lines a wave shares with its neighbours, which go through L2
@@ -885,8 +887,7 @@ __global__ __launch_bounds__(kTB) void rs16_encode_tiles_kernel(const uint8_t* i
         if (mis && b < 16 - mis && b < Sb) as_global(fc.dst)[o + b] = as_global(fc.src)[o + b];
     }
     const bool horner = ex[1] == 2;
-    const uint16_t red = gf16_mul_tab(0x8000, 2, ex, lg);
-    const uint32_t red2 = uint32_t(red) * 0x10001u;
+    const uint32_t red2 = uint32_t(ex[16]) * 0x10001u;   // g^16 = 2^16 reduced, when g = 2
     u32x4 acc[M];
     if (horner) {
 #pragma unroll

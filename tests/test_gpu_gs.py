@@ -545,15 +545,20 @@ def test_rs16_reconstruct_tiles(pkg, ora, gpu, k, S, soff, gen4):
         assert bool((rest == 0x2A2A).all()), (miss, pused)
 
 
-def test_rs16_bad_device_indices_write_nothing(pkg, gpu):
-    k, m, S = 6, 2, 100
+@pytest.mark.parametrize("S", [100, 4096 * 2 + 3])
+def test_rs16_bad_device_indices_write_nothing(pkg, gpu, S):
+    """A lost row outside the data rows, a repeated lost row, a parity row
+    outside the tensor or a negative index: nothing is written (rows under one
+    tile on the piece kernel, longer rows on the tile kernel)."""
+    k, m = 6, 2
     d = torch.zeros((k + m, S), dtype=torch.uint16, device=gpu)
     d.view(torch.int16).fill_(7)
     gex, glg = pkg.rs.device_gf_tables(gpu)
-    pkg.rs.rs_kernel.reconstruct_rs_u16_inplace(
-        d, S, k, m, torch.tensor([0, 9], dtype=torch.int32, device=gpu),
-        torch.tensor([0, 1], dtype=torch.int32, device=gpu), gex, glg)
-    assert bool((d.view(torch.int16) == 7).all())
+    for miss, pu in [([0, 9], [0, 1]), ([3, 3], [0, 1]), ([1, 2], [0, 2]), ([-1], [0]), ([2], [-1]), ([6], [0])]:
+        pkg.rs.rs_kernel.reconstruct_rs_u16_inplace(
+            d, S, k, m, torch.tensor(miss, dtype=torch.int32, device=gpu),
+            torch.tensor(pu, dtype=torch.int32, device=gpu), gex, glg)
+        assert bool((d.view(torch.int16) == 7).all()), (miss, pu)
 
 
 @pytest.mark.parametrize("k,m", [(8, 2), (6, 2), (5, 3)])
