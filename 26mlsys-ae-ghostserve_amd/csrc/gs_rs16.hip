@@ -287,6 +287,30 @@ __device__ __forceinline__ uint32_t gf16_dbl2_xor(uint32_t x, uint32_t red2, uin
     return xor3(sh, top & red2, y);
 }
 
+// Times 4 in one step: a word v = t * 2^14 + low is v * 4 = (low << 2) ^ T[t]
+// with T[t] = t * 2^16 reduced, t the two bits shifted out.  T fits the eight
+// bytes one v_perm_b32 indexes: lo = T[0] | T[1] << 16, hi = T[2] | T[3] << 16,
+// with T[1] = 2^16 reduced (the reduction word) and T[2] = 2^17 reduced (its
+// double, reduced again when its top bit is set).
+struct Gf16Quad {
+    uint32_t lo, hi;
+};
+__host__ __device__ __forceinline__ Gf16Quad gf16_quad_table(uint16_t red) {
+    const uint16_t r2 = gf16_dbl(red, red);
+    return Gf16Quad{uint32_t(red) << 16, uint32_t(r2) | (uint32_t(uint16_t(red ^ r2)) << 16)};
+}
+
+// (x * 4) ^ y for two packed words: shift, the two top bits' byte selectors
+// (2t, 2t + 1) by one packed multiply-add, the table lookup and a 3-input XOR
+// (five VALU ops; two doublings and the XOR take seven).
+__device__ __forceinline__ uint32_t gf16_quad2_xor(uint32_t x, Gf16Quad q, uint32_t y) {
+    const u16x2 v = __builtin_bit_cast(u16x2, x);
+    const uint32_t sh = __builtin_bit_cast(uint32_t, u16x2(v << 2));
+    const u16x2 t = v >> 14;
+    const uint32_t sel = __builtin_bit_cast(uint32_t, u16x2(t * u16x2{0x0202, 0x0202} + u16x2{0x0100, 0x0100}));
+    return xor3(sh, __builtin_amdgcn_perm(q.hi, q.lo, sel), y);
+}
+
 // acc[n][g] = acc[n][g] * alpha^(g+1) ^ x[n]; acc in natural word order.
 template <int G, int NW>
 __device__ __forceinline__ void rs_horner_step(uint32_t red2, const u32x4* x, uint32_t (*acc)[kRsGroup][4]) {
@@ -695,6 +719,15 @@ __device__ __forceinline__ u32x4 gf16_dbl_n(u32x4 v, uint32_t n, uint32_t red2) 
     return v;
 }
 
+// The same product by n / 2 steps of gf16_quad2_xor and, for odd n, one doubling.
+__device__ __forceinline__ u32x4 gf16_dbl_n(u32x4 v, uint32_t n, uint32_t red2, Gf16Quad q) {
+    for (; n >= 2; n -= 2)
+        v = u32x4{gf16_quad2_xor(v.x, q, 0u), gf16_quad2_xor(v.y, q, 0u), gf16_quad2_xor(v.z, q, 0u),
+                  gf16_quad2_xor(v.w, q, 0u)};
+    if (n) v = u32x4{gf16_dbl2(v.x, red2), gf16_dbl2(v.y, red2), gf16_dbl2(v.z, red2), gf16_dbl2(v.w, red2)};
+    return v;
+}
+
 // The reconstruct by Horner's rule, for tables with alpha = 2.  The inputs
 // x[] are the ND = NIN - M surviving data rows (rows row[0] < row[1] < ...)
 // and the M parity rows of parity_used.  Each parity syndrome
@@ -887,7 +920,9 @@ __global__ __launch_bounds__(kTB) void rs16_encode_tiles_kernel(const uint8_t* i
         if (mis && b < 16 - mis && b < Sb) as_global(fc.dst)[o + b] = as_global(fc.src)[o + b];
     }
     const bool horner = ex[1] == 2;
-    const uint32_t red2 = uint32_t(ex[16]) * 0x10001u;   // g^16 = 2^16 reduced, when g = 2
+    const uint16_t red = ex[16];   // g^16 = 2^16 reduced, when g = 2
+    const uint32_t red2 = uint32_t(red) * 0x10001u;
+    const Gf16Quad quad = gf16_quad_table(red);
     u32x4 acc[M];
     if (horner) {
 #pragma unroll
@@ -907,11 +942,10 @@ __global__ __launch_bounds__(kTB) void rs16_encode_tiles_kernel(const uint8_t* i
                 for (int q = 0; q < 4; ++q) {
                     if (i == ND - 1) {
                         a[q] = xv[q];
+                    } else if (p == 0) {
+                        a[q] = gf16_dbl2_xor(a[q], red2, xv[q]);
                     } else {
-                        uint32_t v = a[q];
-#pragma unroll
-                        for (int d = 0; d < p; ++d) v = gf16_dbl2(v, red2);
-                        a[q] = gf16_dbl2_xor(v, red2, xv[q]);
+                        a[q] = gf16_quad2_xor(a[q], quad, xv[q]);   // g_1 = alpha^2 = 4
                     }
                 }
                 acc[p] = u32x4{a[0], a[1], a[2], a[3]};
@@ -1096,7 +1130,9 @@ __global__ __launch_bounds__(BS) void rs16_reconstruct_tiles_kernel(uint8_t* bas
                     if (h2) bv ^= ex[add(l2, j)];
                 }
             }
-            const uint32_t red2 = uint32_t(ex[16]) * 0x10001u;   // g^16 = 2^16 reduced, as g = 2
+            const uint16_t red = ex[16];   // g^16 = 2^16 reduced, as g = 2
+            const uint32_t red2 = uint32_t(red) * 0x10001u;
+            const Gf16Quad quad = gf16_quad_table(red);
             u32x4 x[NIN];
 #pragma unroll
             for (int i = 0; i < NIN; ++i) {
@@ -1111,8 +1147,8 @@ __global__ __launch_bounds__(BS) void rs16_reconstruct_tiles_kernel(uint8_t* bas
                 u32x4 acc = ND > 0 ? x[ND > 0 ? ND - 1 : 0] : u32x4{0, 0, 0, 0};
 #pragma unroll
                 for (int j = ND - 2; j >= 0; --j)
-                    acc = gf16_dbl_n(acc, f * uint32_t(row(j + 1) - row(j)), red2) ^ x[j];
-                if (ND > 0) acc = gf16_dbl_n(acc, f * uint32_t(row(0)), red2);
+                    acc = gf16_dbl_n(acc, f * uint32_t(row(j + 1) - row(j)), red2, quad) ^ x[j];
+                if (ND > 0) acc = gf16_dbl_n(acc, f * uint32_t(row(0)), red2, quad);
                 bsyn[r] = acc ^ x[ND + r];
             }
             // byte maps: lane g < 6 M^2 takes coefficient g / 6, source byte

@@ -474,6 +474,51 @@ def _gen4_tables(ora):
     return ex, lg
 
 
+def _poly_tables(poly):
+    """exp/log tables of GF(2^16) with the primitive polynomial `poly`, generator 2."""
+    ex = np.zeros(2 * 65535, np.uint16)
+    lg = np.zeros(65536, np.uint16)
+    x = 1
+    for i in range(65535):
+        ex[i] = x
+        lg[x] = i
+        x <<= 1
+        if x & 0x10000:
+            x ^= poly
+    ex[65535:] = ex[:65535]
+    return ex, lg
+
+
+@pytest.mark.parametrize("k,S", [(6, 44741), (3, 4096 * 2 + 5)])
+def test_rs16_horner_field_with_top_reduction_bit(pkg, ora, gpu, k, S):
+    """Tables of GF(2^16) over x^16 + x^15 + x^4 + x + 1 (0x18013, generator
+    2): the reduction word 2^16 = 0x8013 has its top bit set, so 2^17 needs a
+    second reduction, which the times-4 steps of the encode's second parity
+    and of the reconstruct's syndromes (a table of the two shifted-out bits)
+    must apply."""
+    m = 2
+    ex, lg = _poly_tables(0x18013)
+    assert ex[1] == 2 and ex[16] == 0x8013 and len(set(ex[:65535].tolist())) == 65535
+    rng = np.random.default_rng(k + S)
+    data = rng.integers(0, 65536, k * S, dtype=np.uint16)
+    want = ora.rs16_encode(data, k, m, S, ex, lg)
+    gex, glg = dev(ex, gpu), dev(lg, gpu)
+    shards = torch.zeros((k + m, S), dtype=torch.uint16, device=gpu)
+    pkg.rs.rs_kernel.encode_rs_u16(dev(data, gpu), shards, k, m, S, gex, glg)
+    assert np.array_equal(host(shards), want)
+    for miss, pused in [((0, k - 1), (0, 1)), ((1,), (1,)), ((k - 1,), (0,)), ((0, 1), (1, 0))]:
+        sh = want.copy()
+        sh[list(miss)] = 0x1234
+        expect = sh.copy()
+        ora.rs16_reconstruct(expect, S, k, m, list(miss), list(pused), ex, lg)
+        assert np.array_equal(expect, want)
+        d = dev(sh, gpu)
+        pkg.rs.rs_kernel.reconstruct_rs_u16_inplace(
+            d, S, k, m, torch.tensor(miss, dtype=torch.int32, device=gpu),
+            torch.tensor(pused, dtype=torch.int32, device=gpu), gex, glg)
+        assert np.array_equal(host(d), expect), (miss, pused)
+
+
 @pytest.mark.parametrize("k,mp,S,soff,gen4", [(6, 2, 44741, 0, False), (6, 2, 44741, 3, False),
                                               (6, 2, 44741, 5, True), (8, 3, 5003, 7, False),
                                               (4, 2, 517, 1, True), (2, 2, 1000, 2, False),
