@@ -32,9 +32,9 @@ constexpr int kRsMaxM = 16;           // reference limit (benchmark/rs/kernel.cu
 constexpr int kRsMaxTables = 48;      // coefficients held in LDS
 constexpr int kRs16Tab = 24;          // dwords per coefficient: 4 byte maps x 6
 constexpr int kRsGroup = 2;           // outputs accumulated per pass over the inputs
-// The tile kernels (encode, and the reconstruct beyond the piece kernel's
-// limits) run blocks of kRsBS threads, two per CU, persistent: the tables are
-// built once per block.  Measured on the 512 MiB stream, RS(6,2) encode: 512
+// The persistent tile kernels (the encode and the reconstruct for shapes the
+// one-shot tile kernels and the piece kernel do not take) run blocks of kRsBS
+// threads, two per CU: the tables are built once per block.  Measured on the 512 MiB stream, RS(6,2) encode: 512
 // threads (16 KiB tiles) with 512 blocks 245 against 248 us for 256 threads
 // with 1024 blocks, and with the XCD-grouped tile order of rs_run_tiles 239 us.
 constexpr int kRsBS = 512;
