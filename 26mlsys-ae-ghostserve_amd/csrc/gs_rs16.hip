@@ -1267,6 +1267,343 @@ static int rs_grid(int64_t S) {
     return int(tiles < kRsGrid ? tiles : kRsGrid);
 }
 
+// ------------------------------------------- any k and m: Horner over byte maps
+// The shapes whose k * m coefficient maps do not fit the kernels above
+// (k * m > kRsMaxTables).  Parity p of the encode is Horner's rule over the
+// data rows from the last to the first,
+//     acc = acc * g_p ^ D_i,   g_p = gf_exp[p + 1] = alpha^(p+1),
+// which leaves D_i multiplied by g_p^i = alpha^((p+1) i) = gf_exp[((p+1) i) mod
+// 65535], the reference's coefficient (benchmark/rs/kernel.cu:88-95): one
+// multiplier per output whatever k is, applied through its byte maps.  The
+// reconstruct's syndromes
+//     b_r = Par_{pu_r} ^ XOR_{j not lost} D_j * alpha^((pu_r+1) j)
+// (benchmark/rs/kernel.cu:190-207) are the same rule over all k data rows, a
+// lost row adding nothing but its multiplication; the lost rows are then
+// x_c = XOR_r inv[c][r] b_r (:209-219), the inverse by the reference's
+// Gauss-Jordan with one thread per matrix entry.  Both take the tables to be a
+// field's exp/log pair, as the byte maps everywhere in this file do.
+//
+// Accumulators are byte-transposed (split_bytes order); a product costs the
+// four fields of the accumulator and four gf16_fma2.  Rows are read through
+// 16-byte windows at any alignment (RowWin), outputs staged in LDS one row at
+// a time and written by tile_store, so every row alignment and length is
+// taken.  The encode runs one block row per group of G parities
+// (blockIdx.y), each block building its G maps once and walking tiles; the
+// reconstruct keeps all M lost rows of a tile in registers.
+constexpr int kRsHBS = 256;      // threads per block
+constexpr int kRsHGrid = 1024;   // blocks per output group (tiles are walked)
+constexpr int kRsHMaxG = 8;      // encode parities per block; reconstruct syndromes per pass
+
+// Keeps one coefficient's byte maps live at a time: the accumulators pass
+// through the asm (their products are formed here), the memory clobber keeps
+// the next maps' LDS reads after it and the scheduling barrier keeps them
+// from moving up.  Without it the compiler reads every loop-invariant map
+// into registers ahead of the loops and spills.
+__device__ __forceinline__ void rs_h_fence(uint32_t acc[4]) {
+    asm volatile("" : "+v"(acc[0]), "+v"(acc[1]), "+v"(acc[2]), "+v"(acc[3]) :: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+}
+
+// acc = acc * c ^ y (byte-transposed words; T = c's byte maps).
+__device__ __forceinline__ void gf16_mul_split_xor(uint32_t acc[4], const uint32_t* T, const uint32_t y[4]) {
+    Gf8Fields f[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) f[q] = gf8_fields(acc[q]);
+    acc[0] = gf16_fma2(y[0], f[0], T + 0, f[1], T + 6);
+    acc[1] = gf16_fma2(y[1], f[0], T + 12, f[1], T + 18);
+    acc[2] = gf16_fma2(y[2], f[2], T + 0, f[3], T + 6);
+    acc[3] = gf16_fma2(y[3], f[2], T + 12, f[3], T + 18);
+    rs_h_fence(acc);
+}
+
+// acc ^= x * c, with x given by its fields.
+__device__ __forceinline__ void gf16_fma_split(uint32_t acc[4], const Gf8Fields f[4], const uint32_t* T) {
+    acc[0] = gf16_fma2(acc[0], f[0], T + 0, f[1], T + 6);
+    acc[1] = gf16_fma2(acc[1], f[0], T + 12, f[1], T + 18);
+    acc[2] = gf16_fma2(acc[2], f[2], T + 0, f[3], T + 6);
+    acc[3] = gf16_fma2(acc[3], f[2], T + 12, f[3], T + 18);
+    rs_h_fence(acc);
+}
+
+// Window n of this thread in a tile at logical byte t0b of `row`: 16 bytes
+// starting at word w0, zero past the row's end S (words); `full` when the
+// tile lies wholly inside the row (the aligned-chunk path, RowWin rules).
+template <int NW>
+__device__ __forceinline__ void rs_h_windows(const uint16_t* row, uint64_t t0b, int64_t S, bool full,
+                                             u32x4* x) {
+    if (full) {
+        const RowWin rw = row_win(reinterpret_cast<const uint8_t*>(row) + t0b);
+#pragma unroll
+        for (int n = 0; n < NW; ++n) {
+            u32x4 lo, hi;
+            win_chunks(rw, 16 * (threadIdx.x + n * kRsHBS), lo, hi);
+            x[n] = win_join(rw, lo, hi);
+        }
+    } else {
+#pragma unroll
+        for (int n = 0; n < NW; ++n)
+            x[n] = rs_window(row, int64_t(t0b / 2) + 8 * (threadIdx.x + n * kRsHBS), S);
+    }
+}
+
+// Stage one output row's windows (byte-transposed) and write them to dst.
+template <int NW>
+__device__ __forceinline__ void rs_h_store(uint8_t* stage, const uint32_t (*acc)[4], uint8_t* dst,
+                                           uint32_t nbytes) {
+#pragma unroll
+    for (int n = 0; n < NW; ++n)
+        *reinterpret_cast<u32x4*>(stage + 16 * (threadIdx.x + n * kRsHBS)) = join_bytes(acc[n]);
+    __syncthreads();
+    tile_store<true, kRsHBS>(dst, stage, nbytes);
+    __syncthreads();
+}
+
+// encode_rs_u16's parity rows og .. og + G - 1 (og = blockIdx.y * G; those at
+// or past m are computed and not stored).  in: the k data rows of S words;
+// par: parity row 0.
+template <int G, int NW>
+__global__ __launch_bounds__(kRsHBS) void rs16_encode_horner_kernel(const uint16_t* in, uint16_t* par, int64_t S,
+                                                                    int k, int m, const uint16_t* ex,
+                                                                    const uint16_t* lg) {
+    constexpr uint32_t TB = 16 * kRsHBS * NW;
+    __shared__ __attribute__((aligned(16))) uint32_t ptab[G][kRs16Tab];
+    __shared__ uint16_t basis[G][16];
+    __shared__ uint16_t coef[G];
+    __shared__ __attribute__((aligned(16))) uint8_t stage[TB + 16];
+    const int og = int(blockIdx.y) * G;
+    if (threadIdx.x < G) {
+        const int p = og + int(threadIdx.x);
+        coef[threadIdx.x] = p < m ? ex[uint32_t(p + 1) % kGfOrder] : uint16_t(0);
+    }
+    __syncthreads();
+    rs_build_perm_tables(ptab, basis, coef, G, ex, lg);
+    __syncthreads();
+    const int nout = m - og < G ? m - og : G;
+    const uint64_t Sb = uint64_t(S) * 2;
+    const uint64_t ntiles = (Sb + TB - 1) / TB;
+    for (uint64_t tt = blockIdx.x; tt < ntiles; tt += gridDim.x) {
+        const uint64_t t0b = tt * TB;
+        const uint32_t nbytes = uint32_t(Sb - t0b < TB ? Sb - t0b : TB);
+        const bool full = nbytes == TB;
+        uint32_t acc[NW][G][4];
+        u32x4 x[NW], nx[NW];
+        rs_h_windows<NW>(in + uint64_t(k - 1) * S, t0b, S, full, x);
+        for (int i = k - 1; i >= 0; --i) {
+            if (i > 0) rs_h_windows<NW>(in + uint64_t(i - 1) * S, t0b, S, full, nx);
+#pragma unroll
+            for (int n = 0; n < NW; ++n) {
+                uint32_t y[4];
+                split_bytes(x[n], y);
+#pragma unroll
+                for (int g = 0; g < G; ++g) {
+                    if (i == k - 1) {
+                        acc[n][g][0] = y[0], acc[n][g][1] = y[1], acc[n][g][2] = y[2], acc[n][g][3] = y[3];
+                    } else {
+                        gf16_mul_split_xor(acc[n][g], ptab[g], y);
+                    }
+                }
+            }
+            if (i > 0) {
+#pragma unroll
+                for (int n = 0; n < NW; ++n) x[n] = nx[n];
+            }
+        }
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            if (g >= nout) break;
+            uint32_t o[NW][4];
+#pragma unroll
+            for (int n = 0; n < NW; ++n)
+#pragma unroll
+                for (int q = 0; q < 4; ++q) o[n][q] = acc[n][g][q];
+            rs_h_store<NW>(stage, o, reinterpret_cast<uint8_t*>(par + uint64_t(og + g) * S) + t0b, nbytes);
+        }
+    }
+}
+
+// The inverse of V[r][c] = gf_exp[((pu_r + 1) miss_c) mod 65535] by
+// benchmark/rs/kernel.cu:135-185 (pivot order, zero-pivot skip), one thread
+// per entry: within a step the rows r != i change only from row i and their
+// own factor V[r][i], read by every thread of row r before any writes it, so
+// each entry sees the serial loop's sequence of products.  All threads of the
+// block call it; inv (m x m) is left in LDS, followed by a barrier.
+__device__ __forceinline__ void rs16_gauss_jordan(int m, const int* miss, const int* pu, uint16_t* V, uint16_t* inv,
+                                                  const uint16_t* ex, const uint16_t* lg) {
+    const int t = int(threadIdx.x), r = t / m, c = t % m;
+    const bool mine = t < m * m;
+    if (mine) {
+        V[t] = ex[uint32_t((pu[r] + 1) * miss[c]) % kGfOrder];
+        inv[t] = r == c ? 1 : 0;
+    }
+    __syncthreads();
+    for (int i = 0; i < m; ++i) {
+        int pr = i;
+        while (pr < m && V[pr * m + i] == 0) ++pr;
+        if (pr == m) continue;   // uniform: every thread read the same V
+        if (pr != i && t < m) {
+            uint16_t s = V[i * m + t];
+            V[i * m + t] = V[pr * m + t];
+            V[pr * m + t] = s;
+            s = inv[i * m + t];
+            inv[i * m + t] = inv[pr * m + t];
+            inv[pr * m + t] = s;
+        }
+        __syncthreads();
+        const uint16_t ip = gf16_div_tab(1, V[i * m + i], ex, lg);   // V[i][i] != 0 here
+        __syncthreads();
+        if (t < m) {
+            V[i * m + t] = gf16_mul_tab(V[i * m + t], ip, ex, lg);
+            inv[i * m + t] = gf16_mul_tab(inv[i * m + t], ip, ex, lg);
+        }
+        __syncthreads();
+        const uint16_t f = mine && r != i ? V[r * m + i] : uint16_t(0);
+        __syncthreads();
+        if (f) {
+            V[r * m + c] ^= gf16_mul_tab(f, V[i * m + c], ex, lg);
+            inv[r * m + c] ^= gf16_mul_tab(f, inv[i * m + c], ex, lg);
+        }
+        __syncthreads();
+    }
+}
+
+// reconstruct_rs_u16_inplace of M lost data rows, any k (inputs: the
+// surviving data rows and the parity rows of parity_used).  sh: the shard
+// tensor, rows of S words.  Out-of-range or repeated lost rows, or parity rows
+// outside the tensor, write nothing.
+template <int M>
+__global__ __launch_bounds__(kRsHBS) void rs16_reconstruct_horner_kernel(uint16_t* sh, int64_t S, int k, int mpar,
+                                                                         const int32_t* missing,
+                                                                         const int32_t* pused,
+                                                                         const uint16_t* ex,
+                                                                         const uint16_t* lg) {
+    constexpr int NW = 1, G = M < kRsHMaxG ? M : kRsHMaxG, NT = M + M * M;
+    constexpr uint32_t TB = 16 * kRsHBS * NW;
+    static_assert(M * M <= kRsHBS, "one thread per inverse entry");
+    // maps: syndrome multipliers g_r = gf_exp[pu_r + 1] at [r], inverse entry
+    // inv[c][r] at [M + c * M + r]
+    __shared__ __attribute__((aligned(16))) uint32_t ptab[NT][kRs16Tab];
+    __shared__ uint16_t basis[NT][16];
+    __shared__ uint16_t coef[NT];
+    __shared__ uint16_t sV[M * M], sInv[M * M];
+    __shared__ int s_miss[M], s_pu[M], s_desc[M], s_ok;
+    __shared__ __attribute__((aligned(16))) uint8_t stage[TB + 16];
+    if (threadIdx.x < M) {
+        s_miss[threadIdx.x] = missing[threadIdx.x];
+        s_pu[threadIdx.x] = pused[threadIdx.x];
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        int ok = 1;
+        for (int q = 0; q < M; ++q) {
+            ok &= s_miss[q] >= 0 && s_miss[q] < k && s_pu[q] >= 0 && s_pu[q] < mpar;
+            for (int q2 = 0; q2 < q; ++q2) ok &= s_miss[q2] != s_miss[q];
+        }
+        s_ok = ok;
+        // the lost rows from the highest down, the order the syndromes meet them
+        for (int q = 0; q < M; ++q) {
+            int v = s_miss[q], at = q;
+            while (at > 0 && s_desc[at - 1] < v) s_desc[at] = s_desc[at - 1], --at;
+            s_desc[at] = v;
+        }
+    }
+    __syncthreads();
+    if (!s_ok) return;   // uniform: the whole grid writes nothing
+    rs16_gauss_jordan(M, s_miss, s_pu, sV, sInv, ex, lg);
+    for (int e = threadIdx.x; e < NT; e += kRsHBS)
+        coef[e] = e < M ? ex[uint32_t(s_pu[e] + 1) % kGfOrder] : sInv[e - M];
+    __syncthreads();
+    rs_build_perm_tables(ptab, basis, coef, NT, ex, lg);
+    __syncthreads();
+    // indices stay in LDS and are read where used (2 M of them held in scalar
+    // registers beside the loop's own spilled SGPRs for M >= 8)
+    auto desc = [&](int q) { return q < M ? int(lds_uniform(s_desc[q])) : -1; };
+    const uint64_t Sb = uint64_t(S) * 2;
+    const uint64_t ntiles = (Sb + TB - 1) / TB;
+    for (uint64_t tt = blockIdx.x; tt < ntiles; tt += gridDim.x) {
+        const uint64_t t0b = tt * TB;
+        const uint32_t nbytes = uint32_t(Sb - t0b < TB ? Sb - t0b : TB);
+        const bool full = nbytes == TB;
+        uint32_t out[M][NW][4];
+#pragma unroll
+        for (int c = 0; c < M; ++c)
+#pragma unroll
+            for (int n = 0; n < NW; ++n) out[c][n][0] = out[c][n][1] = out[c][n][2] = out[c][n][3] = 0;
+#pragma unroll
+        for (int og = 0; og < M; og += G) {
+            constexpr int GG = G;
+            const int ng = M - og < GG ? M - og : GG;
+            uint32_t acc[GG][NW][4];
+#pragma unroll
+            for (int g = 0; g < GG; ++g)
+#pragma unroll
+                for (int n = 0; n < NW; ++n) acc[g][n][0] = acc[g][n][1] = acc[g][n][2] = acc[g][n][3] = 0;
+            u32x4 x[NW], nx[NW];
+            // nxt: the highest lost row below the rows passed (nl of them lost)
+            int nl = 0, nxt = desc(0);
+            bool have = k - 1 != nxt;
+            if (!have) nxt = desc(++nl);
+            if (have) rs_h_windows<NW>(sh + uint64_t(k - 1) * S, t0b, S, full, x);
+            for (int j = k - 1; j >= 0; --j) {
+                const bool next = j > 0 && j - 1 != nxt;
+                if (j > 0 && !next) nxt = desc(++nl);
+                if (next) rs_h_windows<NW>(sh + uint64_t(j - 1) * S, t0b, S, full, nx);
+                uint32_t y[NW][4];
+#pragma unroll
+                for (int n = 0; n < NW; ++n) {
+                    if (have) split_bytes(x[n], y[n]);
+                    else y[n][0] = y[n][1] = y[n][2] = y[n][3] = 0;
+                }
+#pragma unroll
+                for (int g = 0; g < GG; ++g) {
+                    if (g >= ng) break;
+#pragma unroll
+                    for (int n = 0; n < NW; ++n) gf16_mul_split_xor(acc[g][n], ptab[og + g], y[n]);
+                }
+                if (next) {
+#pragma unroll
+                    for (int n = 0; n < NW; ++n) x[n] = nx[n];
+                }
+                have = next;
+            }
+            // b_r = acc ^ Par_{pu_r}, then out_c ^= inv[c][r] b_r
+#pragma unroll
+            for (int g = 0; g < GG; ++g) {
+                if (g >= ng) break;
+                u32x4 pw[NW];
+                rs_h_windows<NW>(sh + uint64_t(k + int(lds_uniform(s_pu[og + g]))) * S, t0b, S, full, pw);
+#pragma unroll
+                for (int n = 0; n < NW; ++n) {
+                    uint32_t y[4];
+                    split_bytes(pw[n], y);
+                    Gf8Fields f[4];
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) f[q] = gf8_fields(acc[g][n][q] ^ y[q]);
+#pragma unroll
+                    for (int c = 0; c < M; ++c) gf16_fma_split(out[c][n], f, ptab[M + c * M + og + g]);
+                }
+            }
+        }
+#pragma unroll
+        for (int c = 0; c < M; ++c)
+            rs_h_store<NW>(stage, out[c], reinterpret_cast<uint8_t*>(sh + uint64_t(lds_uniform(s_miss[c])) * S) + t0b,
+                           nbytes);
+    }
+}
+
+typedef void (*RsRecHornerFn)(uint16_t*, int64_t, int, int, const int32_t*, const int32_t*, const uint16_t*,
+                              const uint16_t*);
+template <int... I>
+struct RsRecHornerTable {
+    static constexpr RsRecHornerFn fn[sizeof...(I)] = {rs16_reconstruct_horner_kernel<I + 1>...};
+};
+using RsRecHorner = RsRecHornerTable<0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11, 12, 13, 14, 15>;
+static_assert(kRsMaxM == 16, "instance table");
+
+static unsigned rs_h_grid(int64_t S, uint32_t tile) {
+    const uint64_t tiles = (uint64_t(S) * 2 + tile - 1) / tile;
+    return unsigned(tiles < uint64_t(kRsHGrid) ? tiles : uint64_t(kRsHGrid));
+}
+
 }  // namespace kvec
 
 using namespace kvec;
@@ -1305,9 +1642,12 @@ extern "C" int kvec_rs16_encode(const void* data_padded, void* shards, int data_
     if (data_shards < 1 || parity_shards < 0 || shard_size < 0)
         return set_error(KVEC_EINVAL, "kvec_rs16_encode: k=%d m=%d S=%d", data_shards, parity_shards,
                          shard_size);
-    if (parity_shards > kRsMaxM || data_shards * parity_shards > kRsMaxTables)
-        return set_error(KVEC_EUNSUPPORTED, "kvec_rs16_encode: k*m=%d exceeds %d (m <= %d)",
-                         data_shards * parity_shards, kRsMaxTables, kRsMaxM);
+    // every k and m whose exponents (p + 1) i the reference's int arithmetic
+    // holds (benchmark/rs/kernel.cu:93), with at most 65535 groups of parities
+    if (int64_t(data_shards - 1) * parity_shards >= (int64_t(1) << 31) ||
+        int64_t(parity_shards) > int64_t(65535) * kRsHMaxG)
+        return set_error(KVEC_EUNSUPPORTED, "kvec_rs16_encode: k=%d m=%d out of range", data_shards,
+                         parity_shards);
     hipStream_t st = as_stream(stream);
     const int64_t S = shard_size;
     if (S == 0) return KVEC_OK;
@@ -1320,12 +1660,29 @@ extern "C" int kvec_rs16_encode(const void* data_padded, void* shards, int data_
     if (ranges_overlap(data_padded, data_bytes, (uint16_t*)shards + uint64_t(data_shards) * S,
                        uint64_t(parity_shards) * S * 2))
         return set_error(KVEC_EINVAL, "kvec_rs16_encode: data overlaps the parity rows");
-    const bool fuse = parity_shards > 0 && fused_copy_ok(data_padded, shards, data_bytes);
+    // k * m maps beyond the LDS tables: Horner over byte maps, data rows copied apart
+    const bool general = int64_t(data_shards) * parity_shards > kRsMaxTables;
+    const bool fuse = !general && parity_shards > 0 && fused_copy_ok(data_padded, shards, data_bytes);
     if (!fuse) {
         int rc = copy_d2d(shards, data_padded, data_bytes, st, "kvec_rs16_encode");
         if (rc) return rc;
     }
     if (parity_shards == 0) return KVEC_OK;
+    if (general) {
+        const uint16_t* in = (const uint16_t*)data_padded;
+        uint16_t* par = (uint16_t*)shards + uint64_t(data_shards) * S;
+        constexpr uint32_t TB = 16 * kRsHBS * 2;
+        auto launch = [&](auto kern, int G) {
+            const unsigned groups = unsigned((parity_shards + G - 1) / G);
+            hipLaunchKernelGGL(kern, dim3(rs_h_grid(S, TB), groups), dim3(kRsHBS), 0, st, in, par, S, data_shards,
+                               parity_shards, gf_exp, gf_log);
+        };
+        if (parity_shards <= 1) launch(rs16_encode_horner_kernel<1, 2>, 1);
+        else if (parity_shards <= 2) launch(rs16_encode_horner_kernel<2, 2>, 2);
+        else if (parity_shards <= 4) launch(rs16_encode_horner_kernel<4, 2>, 4);
+        else launch(rs16_encode_horner_kernel<kRsHMaxG, 2>, kRsHMaxG);
+        return check_launch("kvec_rs16_encode");
+    }
     RsJob j{};
     j.copy = fuse ? FlatCopy{(const uint8_t*)data_padded, (uint8_t*)shards, data_bytes}
                   : FlatCopy{nullptr, nullptr, 0};
@@ -1365,10 +1722,14 @@ extern "C" int kvec_rs16_reconstruct(void* shards, int shard_size, int data_shar
     if (data_shards < m || parity_shards < m || shard_size < 0)
         return set_error(KVEC_EINVAL, "kvec_rs16_reconstruct: k=%d parity=%d m=%d S=%d", data_shards,
                          parity_shards, m, shard_size);
-    if (data_shards * m > kRsMaxTables)
-        return set_error(KVEC_EUNSUPPORTED, "kvec_rs16_reconstruct: k*m=%d exceeds %d",
-                         data_shards * m, kRsMaxTables);
     if (shard_size == 0) return KVEC_OK;
+    if (int64_t(data_shards) * m > kRsMaxTables) {
+        // k * m maps beyond the LDS tables: syndromes by Horner over byte maps
+        hipLaunchKernelGGL(RsRecHorner::fn[m - 1], dim3(rs_h_grid(shard_size, 16 * kRsHBS)), dim3(kRsHBS), 0,
+                           as_stream(stream), (uint16_t*)shards, int64_t(shard_size), data_shards, parity_shards,
+                           missing_data, parity_used, gf_exp, gf_log);
+        return check_launch("kvec_rs16_reconstruct");
+    }
     const uint64_t Sb = uint64_t(shard_size) * 2;
     const uint32_t res = piece_res_bytes(shards, uint64_t(data_shards + parity_shards) * Sb);
     if (data_shards <= kRsPieceMaxIn && m <= kRsGroup && res && Sb >= kRsRecTile) {

@@ -262,14 +262,17 @@ int kvec_rs16_pack(const void* k, const void* v, void* out, int64_t N_k, int64_t
 int kvec_rs16_split(const void* in, void* k_out, void* v_out, int64_t N_k, int64_t N_v,
                     void* stream);
 /* encode_rs_u16, :265-285: copy data rows; Par_p = XOR_i D_i * alpha^((p+1) i).
- * Limits: parity_shards <= 16, data_shards * parity_shards <= 48. */
+ * Any data_shards >= 1 and parity_shards >= 0 with (k - 1) * m < 2^31 (the
+ * reference's int exponent) and m <= 524280; KVEC_EUNSUPPORTED beyond.  The
+ * tables must be a GF(2^16) exp/log pair (as init_gf_tables() gives). */
 int kvec_rs16_encode(const void* data_padded, void* shards, int data_shards, int parity_shards,
                      int shard_size, const uint16_t* gf_exp, const uint16_t* gf_log,
                      void* stream);
 /* reconstruct_rs_u16_inplace, :287-312: rebuild the m data rows listed in the
  * device int32 array missing_data from the parity rows in parity_used (device,
- * m entries).  Parity rows are not rewritten.  Indices outside the tensor, or a
- * repeated missing index, make the call write nothing. */
+ * m entries; m <= 16 as the reference's, any data_shards >= m).  Parity rows
+ * are not rewritten.  Indices outside the tensor, or a repeated missing index,
+ * make the call write nothing. */
 int kvec_rs16_reconstruct(void* shards, int shard_size, int data_shards, int parity_shards,
                           const int32_t* missing_data, int m, const int32_t* parity_used,
                           const uint16_t* gf_exp, const uint16_t* gf_log, void* stream);

@@ -142,6 +142,22 @@ def test_copy_entries_reject_partial_overlap(pkg, fake_ptrs):
     assert b"overlap" in L.kvec_last_error()
 
 
+def test_rs16_encode_limits(pkg, fake_ptrs):
+    """The GF(2^16) encode takes every k >= 1 and m >= 0 whose exponents
+    (p + 1) i fit the reference's int (benchmark/rs/kernel.cu:93); beyond that,
+    KVEC_EUNSUPPORTED before any launch.  (k * m beyond 48 is no limit.)"""
+    L = pkg._lib.lib()
+    base, S = 1 << 20, 8
+    ex = lg = 4096
+    assert L.kvec_rs16_encode(base, base + (1 << 30), (1 << 16) + 1, 1 << 15, S, ex, lg, None) == -2
+    assert b"out of range" in L.kvec_last_error()
+    assert L.kvec_rs16_encode(base, base + (1 << 30), 2, 524281, S, ex, lg, None) == -2
+    assert L.kvec_rs16_encode(base, base + (1 << 30), 0, 2, S, ex, lg, None) == -1
+    # a valid shape with nothing to code (S = 0) returns before any launch
+    assert L.kvec_rs16_encode(base, base + (1 << 30), 25, 2, 0, ex, lg, None) == 0
+    assert L.kvec_rs16_encode(base, base + (1 << 30), 16, 16, 0, ex, lg, None) == 0
+
+
 def test_product_fails_loudly_without_library(pkg, monkeypatch, tmp_path):
     monkeypatch.setattr(pkg._lib, "LIB_PATH", str(tmp_path / "missing.so"))
     monkeypatch.setattr(pkg._lib, "_lib", None)

@@ -590,16 +590,123 @@ def test_rs16_reconstruct_tiles(pkg, ora, gpu, k, S, soff, gen4):
         assert bool((rest == 0x2A2A).all()), (miss, pused)
 
 
-@pytest.mark.parametrize("S", [100, 4096 * 2 + 3])
-def test_rs16_bad_device_indices_write_nothing(pkg, gpu, S):
+# ------------------------------------------- RS16 at k * m beyond 48 maps
+# The reference's encode takes any k and m and its reconstruct any k with
+# m <= 16 (benchmark/rs/kernel.cu:67-102, :105-222): these shapes run the
+# Horner kernels (one multiplier per output, the inverse by a thread per entry).
+@pytest.mark.parametrize("k,m,S", [(10, 5, 8192 * 2 + 3), (16, 4, 4096), (25, 2, 30001), (7, 7, 9),
+                                   (49, 1, 1000), (5, 20, 517), (3, 17, 2048 * 5)])
+@pytest.mark.parametrize("doff,soff", [(0, 0), (3, 5)])
+def test_rs16_encode_any_k_m(pkg, ora, gpu, k, m, S, doff, soff):
+    """Offsets in u16 words: the data and shard tensors at any alignment;
+    the words around the shard tensor stay untouched."""
+    ex, lg = ora.gf16_tables()
+    rng = np.random.default_rng(k * 1000 + m * 10 + S)
+    data = rng.integers(0, 65536, k * S, dtype=np.uint16)
+    data[rng.integers(0, k * S, k * S // 7)] = 0
+    want = ora.rs16_encode(data, k, m, S, ex, lg)
+    dbuf = torch.zeros(k * S + 16, dtype=torch.int16, device=gpu)
+    dbuf[doff:doff + k * S] = dev(data.view(np.int16), gpu)
+    sbuf = torch.full(((k + m) * S + 16,), 0x1234, dtype=torch.int16, device=gpu)
+    shards = sbuf[soff:soff + (k + m) * S].view(k + m, S)
+    gex, glg = pkg.rs.device_gf_tables(gpu)
+    pkg.rs.rs_kernel.encode_rs_u16(dbuf[doff:doff + k * S].view(torch.uint16), shards.view(torch.uint16),
+                                   k, m, S, gex, glg)
+    assert np.array_equal(host(shards).view(np.uint16), want)
+    rest = torch.cat([sbuf[:soff], sbuf[soff + (k + m) * S:]])
+    assert bool((rest == 0x1234).all())
+
+
+def test_rs16_encode_any_k_m_other_generator(pkg, ora, gpu):
+    """Tables with generator 4: the per-output multiplier is gf_exp[p + 1]
+    of those tables, and the bytes are still the reference's for them."""
+    k, m, S = 12, 5, 5003
+    ex, lg = _gen4_tables(ora)
+    rng = np.random.default_rng(5)
+    data = rng.integers(0, 65536, k * S, dtype=np.uint16)
+    want = ora.rs16_encode(data, k, m, S, ex, lg)
+    shards = torch.zeros((k + m, S), dtype=torch.uint16, device=gpu)
+    pkg.rs.rs_kernel.encode_rs_u16(dev(data, gpu), shards, k, m, S, dev(ex, gpu), dev(lg, gpu))
+    assert np.array_equal(host(shards), want)
+
+
+@pytest.mark.parametrize("k,mp,S,soff,gen4", [(16, 4, 4096 * 2 + 5, 0, False), (20, 3, 1000, 3, False),
+                                              (25, 2, 8192 + 1, 1, False), (13, 4, 517, 0, True),
+                                              (20, 16, 300, 2, False), (17, 16, 2048 * 3, 0, True)])
+def test_rs16_reconstruct_any_k(pkg, ora, gpu, k, mp, S, soff, gen4):
+    """Lost sets of m rows with k * m > 48 (up to all 16 parities): first,
+    last and scattered rows, parity rows in any order, a repeated parity row
+    (the reference's singular system: Gauss-Jordan skips a step, the output is
+    not the data but must still be the reference's), the tensor at a word
+    offset with the words around it untouched."""
+    ex, lg = _gen4_tables(ora) if gen4 else ora.gf16_tables()
+    rng = np.random.default_rng(k * 100 + mp + S)
+    data = rng.integers(0, 65536, k * S, dtype=np.uint16)
+    ref = ora.rs16_encode(data, k, mp, S, ex, lg)
+    gex, glg = dev(ex, gpu), dev(lg, gpu)
+    cases = []
+    for nm in sorted({mp, max(1, mp - 1), mp // 2 + 1}):
+        if k * nm <= 48:
+            continue
+        rows = list(range(k))
+        cases.append((tuple(rows[:nm]), tuple(range(nm))))
+        cases.append((tuple(rows[-nm:]), tuple(reversed(range(mp - nm, mp)))))
+        pick = rng.choice(k, nm, replace=False)
+        cases.append((tuple(int(x) for x in pick), tuple(int(x) for x in rng.permutation(mp)[:nm])))
+        if nm >= 2:
+            cases.append((tuple(int(x) for x in rng.choice(k, nm, replace=False)), (0,) * 2 + tuple(range(2, nm))))
+    assert cases
+    buf = torch.full(((k + mp) * S + 16,), 0x2A2A, dtype=torch.int16, device=gpu)
+    d = buf[soff:soff + (k + mp) * S].view(k + mp, S).view(torch.uint16)
+    for miss, pused in cases:
+        sh = ref.copy()
+        sh[list(miss)] = rng.integers(0, 65536, (len(miss), S), dtype=np.uint16)
+        want = sh.copy()
+        ora.rs16_reconstruct(want, S, k, mp, list(miss), list(pused), ex, lg)
+        assert np.array_equal(want, ref) == (len(set(pused)) == len(pused)), (miss, pused)
+        buf[soff:soff + (k + mp) * S] = dev(sh.reshape(-1).view(np.int16), gpu)
+        pkg.rs.rs_kernel.reconstruct_rs_u16_inplace(
+            d, S, k, mp, torch.tensor(miss, dtype=torch.int32, device=gpu),
+            torch.tensor(pused, dtype=torch.int32, device=gpu), gex, glg)
+        assert np.array_equal(host(d), want), (miss, pused)
+        rest = torch.cat([buf[:soff], buf[soff + (k + mp) * S:]])
+        assert bool((rest == 0x2A2A).all()), (miss, pused)
+
+
+def test_rs16_any_k_m_round_trip_and_refusals(pkg, gpu):
+    """forward_encode_kv / backwards_decode_kv at (k, m) = (16, 4) with four
+    lost data shards, and the reference's m <= 16 limit on the reconstruct."""
+    K = torch.randn(1, 4, 100, 128, device=gpu).to(torch.float16)
+    V = torch.randn(1, 4, 100, 128, device=gpu).to(torch.float16)
+    shards, meta = pkg.rs.forward_encode_kv(K, V, 16, 4)
+    er = shards.clone()
+    for x in (0, 5, 9, 15):
+        er[x].view(torch.int16).fill_(-1)
+    kr, vr = pkg.rs.backwards_decode_kv(er, meta, [0, 5, 9, 15])
+    assert torch.equal(kr.view(torch.int16), K.view(torch.int16))
+    assert torch.equal(vr.view(torch.int16), V.view(torch.int16))
+    gex, glg = pkg.rs.device_gf_tables(gpu)
+    idx = torch.arange(17, dtype=torch.int32, device=gpu)
+    with pytest.raises(RuntimeError, match="<= 16"):
+        pkg.rs.rs_kernel.reconstruct_rs_u16_inplace(torch.zeros((40, 8), dtype=torch.uint16, device=gpu), 8, 20,
+                                                    20, idx, idx, gex, glg)
+
+
+@pytest.mark.parametrize("k,S", [(6, 100), (6, 4096 * 2 + 3), (25, 300)])
+def test_rs16_bad_device_indices_write_nothing(pkg, gpu, k, S):
     """A lost row outside the data rows, a repeated lost row, a parity row
-    outside the tensor or a negative index: nothing is written (rows under one
-    tile on the piece kernel, longer rows on the tile kernel)."""
-    k, m = 6, 2
+    outside the tensor or a negative index: nothing is written (k = 6: rows
+    under one tile on the piece kernel, longer rows on the tile kernel; k = 25
+    with two lost rows: the Horner kernel)."""
+    m = 2
     d = torch.zeros((k + m, S), dtype=torch.uint16, device=gpu)
     d.view(torch.int16).fill_(7)
     gex, glg = pkg.rs.device_gf_tables(gpu)
-    for miss, pu in [([0, 9], [0, 1]), ([3, 3], [0, 1]), ([1, 2], [0, 2]), ([-1], [0]), ([2], [-1]), ([6], [0])]:
+    cases = [([0, k + 3], [0, 1]), ([3, 3], [0, 1]), ([1, 2], [0, 2]), ([-1, 0], [0, 1]), ([2, 0], [-1, 1]),
+             ([k, 1], [0, 1])]
+    if k <= 8:
+        cases += [([-1], [0]), ([2], [-1]), ([k], [0])]
+    for miss, pu in cases:
         pkg.rs.rs_kernel.reconstruct_rs_u16_inplace(
             d, S, k, m, torch.tensor(miss, dtype=torch.int32, device=gpu),
             torch.tensor(pu, dtype=torch.int32, device=gpu), gex, glg)
