@@ -98,6 +98,9 @@ SIGNATURES = {
     "kvec_gf16_tables": (_i, [_vp, _vp]),
 }
 
+# major number of the include/kvec.h these signatures mirror (KVEC_VERSION / 10000)
+ABI_MAJOR = 1
+
 _lib = None
 
 
@@ -116,6 +119,10 @@ def lib():
             f = getattr(L, name)
             f.restype = res
             f.argtypes = args
+        ver = L.kvec_version()
+        if ver // 10000 != ABI_MAJOR:
+            raise RuntimeError(f"{LIB_PATH} has ABI version {ver}; these bindings need major "
+                               f"version {ABI_MAJOR} (rebuild with __graft_entry__.build())")
         _lib = L
     return _lib
 

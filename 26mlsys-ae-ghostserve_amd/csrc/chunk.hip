@@ -119,16 +119,19 @@ __global__ __launch_bounds__((P - 1) * 64) void chunk_encode_rows_kernel(
     const int r = int(__builtin_amdgcn_readfirstlane(threadIdx.x >> 6));
     const uint32_t lane = threadIdx.x & 63;
     const RdpWave w = rdp_wave(cg.geo, ROWS, blockIdx.x, lane);
-    // Lanes past a short last stripe's row end take offset 0 of the row: they
-    // compute lane 0's values and store them to lane 0's addresses (lane 0 is
-    // always inside the row), and they still reach the barrier.
+    // A short last stripe's rows end before the pieces its unit spans: a piece
+    // that starts past the end codes nothing (every wave of the block leaves
+    // here).  In the piece that holds the end, lanes past it take offset 0 of
+    // the row: they compute lane 0's values and store them to lane 0's
+    // addresses (lane 0 is inside the row), and they still reach the barrier.
+    const uint32_t piece = uint32_t(__builtin_amdgcn_readfirstlane(w.within));  // lane 0: the piece's start
+    if (piece >= w.g) return;
     const uint32_t o = w.within < w.g ? w.within : 0u;
     const uint32_t w0 = fdiv(o, g.div_rec);
     const uint32_t inner = o - w0 * g.rec;
     // cell (j, r) is record j*recs_per_shard + rbase + w0: rbase is the
     // wave's, w0 <= dmax the lane's record within the 1 KiB piece
     const uint32_t rbase = uint32_t(r) * fdiv(uint32_t(w.g), g.div_rec) + fdiv(uint32_t(w.base), g.div_rec);
-    const uint32_t piece = uint32_t(__builtin_amdgcn_readfirstlane(w.within));  // lane 0: the piece's start
     const uint32_t dmax = fdiv(piece + kRdpWaveBytes - 16, g.div_rec);
     CellRef ref[K];
 #pragma unroll

@@ -1054,11 +1054,20 @@ extern "C" int kvec_gs_rdp_backup(const void* K_TN, const void* V_TN, void* shar
 // :305-345), words past row nd-1 reading 0.
 extern "C" int kvec_gs_rdp_recover(void* shards, void* out_TN, int nd, int S, int T, int n,
                                    int star_base, int missing_a, int missing_b, void* stream) {
-    (void)star_base;
     if (!shards) return set_error(KVEC_EINVAL, "kvec_gs_rdp_recover: null shards");
     hipStream_t st = as_stream(stream);
     int a = (missing_a >= 0 && missing_a < nd) ? missing_a : -1;
     int b = (missing_b >= 0 && missing_b < nd) ? missing_b : -1;
+    // Two rows lost: the reference's fill_a_star_from_P (benchmark/rdp/kernel.cu:268-282,
+    // launched at :466) reads P and the other rows at column (star_base + a) % S and writes
+    // row a there, a the lower row.  A negative remainder (C's %) addresses the row before
+    // each one, and before the tensor for row 0: undefined, so refused.  Otherwise that
+    // write lands in row a, which rebuild_row_from_P rewrites, and star_base changes no
+    // output byte.
+    if (a >= 0 && b >= 0 && a != b && S > 0 && (int64_t(star_base) + (a < b ? a : b)) % S < 0)
+        return set_error(KVEC_EINVAL,
+                         "kvec_gs_rdp_recover: (star_base + a) %% S < 0 for lost rows %d and %d (star_base=%d): "
+                         "the reference addresses outside row a", a < b ? a : b, a < b ? b : a, star_base);
     int t = -1;
     if (a >= 0 && b >= 0 && a != b)
         t = a < b ? a : b;

@@ -46,7 +46,7 @@ int check_no_alias(const Span* w, int nw, const Span* r, int nr, const char* fn)
 
 }  // namespace kvec
 
-extern "C" int kvec_version(void) { return 100; }
+extern "C" int kvec_version(void) { return KVEC_VERSION; }
 
 extern "C" const char* kvec_strerror(int code) {
     switch (code) {

@@ -34,7 +34,14 @@ extern "C" {
 #define KVEC_EHIP (-3)        /* HIP launch/runtime error */
 #define KVEC_EDECODE (-4)     /* erasure pattern cannot be decoded */
 
-/* Library version, as 10000*major + 100*minor + patch. */
+/* Library version, as 10000*major + 100*minor + patch.  The major number
+ * changes with every incompatible change of the entry points or structs
+ * below; a caller built against this header checks
+ * kvec_version() / 10000 == KVEC_VERSION / 10000 before its first call.
+ * 1.0.0: kvec_rdp_encode / kvec_rdp_decode / kvec_rdp_encode_paged take
+ * unit_bytes, kvec_chunk_stripe has region_off and unit_bytes (0.1.0 had
+ * neither). */
+#define KVEC_VERSION 10000
 int kvec_version(void);
 /* Static description of a KVEC_E* code. */
 const char* kvec_strerror(int code);
@@ -240,7 +247,9 @@ int kvec_gs_rdp_backup(const void* K_TN, const void* V_TN, void* shards, int nd,
 /* fused_recovery_full_kv_launcher, :397-521: observable semantics of the
  * reference (indices outside [0, nd) ignored; one data row is rebuilt from P;
  * for two, the lower row is rebuilt from P and the other keeps its bytes),
- * then out_TN [2*T*n] words = the data rows. */
+ * then out_TN [2*T*n] words = the data rows.  For two lost rows with
+ * (star_base + a) % S < 0 (a the lower row, C's %) the reference reads and
+ * writes outside row a (:268-282); that case returns KVEC_EINVAL. */
 int kvec_gs_rdp_recover(void* shards, void* out_TN, int nd, int S, int T, int n, int star_base,
                         int missing_a, int missing_b, void* stream);
 /* pack_row_from_block_launcher, bench_ghostserve_rdp.py:152-175:

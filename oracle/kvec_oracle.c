@@ -233,7 +233,13 @@ static void gs_rebuild_from_P(uint16_t* sh, int nd, int S, int t) {
  * every column of row a, then rebuild_row_from_P(b) (:482-490).  Only the last
  * two writes are observable, so they are what is restated here. */
 void kvo_gs_recover(uint16_t* sh, int nd, int S, int star_base, int a, int b) {
-    (void)star_base; /* only read by the ring-walk kernels whose output is dead */
+    /* star_base is read by the ring-walk kernels, whose output is dead, and by
+     * fill_a_star_from_P (:268-282), which writes row a at column
+     * (star_base + a) % S: for a non-negative remainder a cell that the
+     * rebuild of row a rewrites, for a negative one (star_base + a < 0 and
+     * not a multiple of S) an address outside row a, which the library
+     * refuses and which is not restated here. */
+    (void)star_base;
     a = (a >= 0 && a < nd) ? a : -1;
     b = (b >= 0 && b < nd) ? b : -1;
     if (a >= 0 && b >= 0 && a != b) {

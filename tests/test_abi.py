@@ -40,7 +40,10 @@ def test_header_symbols_exported(pkg):
 
 def test_status_strings(pkg):
     L = pkg._lib.lib()
-    assert L.kvec_version() >= 100
+    hdr = open(os.path.join(ROOT, "include", "kvec.h")).read()
+    want = int(re.search(r"#define KVEC_VERSION (\d+)", hdr).group(1))
+    assert L.kvec_version() == want
+    assert pkg._lib.ABI_MAJOR == want // 10000
     assert L.kvec_strerror(0) == b"success"
     assert L.kvec_strerror(-1) == b"invalid argument"
 
@@ -156,6 +159,27 @@ def test_rs16_encode_limits(pkg, fake_ptrs):
     # a valid shape with nothing to code (S = 0) returns before any launch
     assert L.kvec_rs16_encode(base, base + (1 << 30), 25, 2, 0, ex, lg, None) == 0
     assert L.kvec_rs16_encode(base, base + (1 << 30), 16, 16, 0, ex, lg, None) == 0
+
+
+def test_gs_recover_refuses_negative_star_column(pkg, fake_ptrs):
+    """Two lost rows with (star_base + a) % S < 0 (C's %, a the lower row):
+    the reference's fill_a_star_from_P (benchmark/rdp/kernel.cu:268-282)
+    would read and write outside row a, so the call is refused before any
+    launch, whatever order the two rows are given in."""
+    L = pkg._lib.lib()
+    base, nd, S = 1 << 20, 6, 1000
+    for sb, a, b in [(-1, 0, 3), (-3, 2, 1), (-1001, 4, 5), (-5, 5, 4)]:
+        assert L.kvec_gs_rdp_recover(base, None, nd, S, 0, 0, sb, a, b, None) == -1, (sb, a, b)
+        assert b"star_base" in L.kvec_last_error()
+
+
+def test_loader_refuses_other_abi_major(pkg, monkeypatch):
+    """A library whose major version differs from the one the bindings mirror
+    is refused at load, before any call with mismatched arguments."""
+    monkeypatch.setattr(pkg._lib, "_lib", None)
+    monkeypatch.setattr(pkg._lib, "ABI_MAJOR", pkg._lib.ABI_MAJOR + 1)
+    with pytest.raises(RuntimeError, match="ABI version"):
+        pkg._lib.lib()
 
 
 def test_product_fails_loudly_without_library(pkg, monkeypatch, tmp_path):

@@ -16,7 +16,7 @@ def fp8_pool(L, npages, pt, H, D, seed):
     return torch.from_numpy(b).view(torch.float8_e4m3fn)
 
 
-def setup(pkg, gpu, L, B, pps, pt, H, D, k, p, m, chunk_tokens, keep_data, seed):
+def setup(pkg, gpu, L, B, pps, pt, H, D, k, p, m, chunk_tokens, keep_data, seed, unit_bytes=None):
     npages = B * pps + 3
     pool = fp8_pool(L, npages, pt, H, D, seed)
     rng = np.random.default_rng(seed + 1)
@@ -26,7 +26,8 @@ def setup(pkg, gpu, L, B, pps, pt, H, D, k, p, m, chunk_tokens, keep_data, seed)
     kv0 = pkg.chunked.chunk_kv(pool_d, table_d, 0, chunk_tokens)
     scales = torch.rand(L, dtype=torch.float32, device=gpu)
     st = pkg.chunked.ChunkedStripes(kv0.stream_bytes(), 2 * kv0.token_bytes, n_chunks, gpu,
-                                    k=k, p=p, m=m, keep_data=keep_data, scales=scales)
+                                    k=k, p=p, m=m, keep_data=keep_data, scales=scales,
+                                    unit_bytes=unit_bytes)
     return pool, table, pool_d, table_d, n_chunks, st
 
 
@@ -71,6 +72,26 @@ def test_chunked_encode_matches_oracle(pkg, ora, gpu, cfg, keep_data):
     for n, g_, w_ in zip(names, got, want):
         assert np.array_equal(g_, w_), n
     assert st.scales is not None and st.scales.shape == (L,)
+
+
+@pytest.mark.parametrize("unit", [1024, 2048, 4096])
+def test_chunked_encode_short_last_stripe(pkg, ora, gpu, unit):
+    """Rows of 4608 bytes in stripes of `unit` bytes: the last stripe's rows
+    (512 bytes at 4096) end before the 1 KiB pieces its unit spans, and the
+    pieces past the end must write nothing; two chunks, data kept."""
+    cfg = (2, 4, 8, 16, 1, 128, 5, 7, 3, 64)
+    L, B, pps, pt, H, D, k, p, m, ct = cfg
+    pool, table, pool_d, table_d, nc, st = setup(pkg, gpu, L, B, pps, pt, H, D, k, p, m, ct, True,
+                                                 seed=7 + unit, unit_bytes=unit)
+    assert st.width == 4608 and st.width % unit != 0 and nc == 2
+    W, data, P, Q, rs = ora.chunked_encode(pool_u8(pool), table.numpy(), pt, ct, nc, k, p, m, unit)
+    for t in st.shards():
+        t.fill_(0xA5)
+    for c in range(nc):
+        st.encode(pkg.chunked.chunk_kv(pool_d, table_d, c, ct), c)
+    torch.cuda.synchronize()
+    for n, g_, w_ in zip(range(k + 2 + m), [t.cpu().numpy() for t in st.shards()], data + [P, Q] + rs):
+        assert np.array_equal(g_, w_), n
 
 
 def erase(pkg, st, kv, c, erased, gen):

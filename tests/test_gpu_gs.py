@@ -317,6 +317,44 @@ def test_gs_backup_and_recovery(pkg, ora, gpu, B, H, T, D, nd):
         assert "recover_ms" in st
 
 
+@pytest.mark.parametrize("sb", [-2, 3, -7])
+def test_gs_recovery_star_base(pkg, ora, gpu, sb):
+    """A backup with star_base sb and recoveries under it: one lost row for
+    any sb; two lost rows when (sb + a) % S >= 0 for the lower row a, where
+    star_base changes no output byte (the reference's star-cell write lands
+    in row a, which is rebuilt); (sb + a) % S < 0 addresses outside row a in
+    the reference and is refused, the shards left as they were."""
+    B, H, T, D, nd = 1, 2, 40, 64, 6
+    g = torch.Generator(device="cpu").manual_seed(11)
+    K = torch.randn(B, H, T, D, generator=g).half()
+    V = torch.randn(B, H, T, D, generator=g).half()
+    n = B * H * D
+    pk = pkg.rdp.fused_backup_full_kv(K.to(gpu), V.to(gpu), nd, star_base=sb)
+    K_TN = K.permute(2, 0, 1, 3).contiguous().view(T, n).view(torch.uint16).numpy()
+    V_TN = V.permute(2, 0, 1, 3).contiguous().view(T, n).view(torch.uint16).numpy()
+    want = ora.gs_backup(K_TN, V_TN, nd, sb)
+    assert np.array_equal(host(pk["shards_KV"]), want)
+    S = pk["shard_size"]
+    for a, b in [(0, 3), (2, 4), (5, 1), (3, -1), (-1, 0), (4, 4)]:
+        sh = want.copy()
+        for x in (a, b):
+            if 0 <= x < nd:
+                sh[x] = 0x5A5A
+        pk2 = dict(pk)
+        pk2["shards_KV"] = dev(sh, gpu)
+        lo = min(x for x in (a, b) if x >= 0) if (a >= 0 or b >= 0) else -1
+        two = a >= 0 and b >= 0 and a != b
+        if two and sb + lo < 0 and (sb + lo) % S != 0:
+            with pytest.raises(RuntimeError, match="star_base"):
+                pkg.rdp.fused_recovery_full_kv(pk2, a, b)
+            assert np.array_equal(host(pk2["shards_KV"]), sh), (a, b)
+            continue
+        exp = sh.copy()
+        ora.gs_recover(exp, nd, S, sb, a, b)
+        kr, vr, _ = pkg.rdp.fused_recovery_full_kv(pk2, a, b)
+        assert np.array_equal(host(pk2["shards_KV"]), exp), (a, b)
+
+
 # The recovery's rebuild and copy-out run as one pass: shard tensors 0 or 10
 # bytes past alignment, outputs misaligned differently, rows of odd length
 # (partial last tiles), padding words in the last data row, nd up to 10 (the
