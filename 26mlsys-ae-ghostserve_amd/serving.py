@@ -97,12 +97,92 @@ class MetricsLog:
             f.write(json.dumps(entry) + "\n")
 
 
+class _StepPlan:
+    """Resources of one step shape (active slots, heads, head_dim, dtype,
+    pool, group size, star_base), reused while the shape repeats: two row
+    buffers [world + 2, S] used in turn and, with graphs, a static slot
+    buffer, the paged-gather descriptor over it and one HIP graph per row
+    buffer for the gather of this rank's delta and one for P/Q.
+
+    A step's P/Q rows are read by its host copies on the side stream, so
+    before a buffer is written again (two steps later) the current stream
+    waits, on the device, for the event that marks those copies done."""
+
+    def __init__(self, kv_pool: torch.Tensor, n: int, world: int, rank: int, star_base: int,
+                 graphs: bool):
+        dev = kv_pool.device
+        T, _, H, D = kv_pool.shape
+        self.world, self.rank, self.star_base = world, rank, star_base
+        self.elems = n * H * D          # words of K (and of V) in one rank's delta
+        self.S = 2 * self.elems         # words per row: K then V
+        self.rows = [torch.empty((world + 2, self.S), dtype=torch.int16, device=dev) for _ in range(2)]
+        self.pool6 = kv_pool.view(1, T, 1, 2, H, D)
+        self.n = n
+        if graphs:
+            self.slots = torch.empty(n, dtype=torch.int32, device=dev)
+            self.kv = paged.PagedKV(self.pool6, self.slots.view(1, n), 0, n)
+        self.freed = [None, None]
+        self.graphs = graphs
+        self.g_gather = [None, None]
+        self.g_parity = [None, None]
+        self.turn = 0
+
+    def _gather(self, b: int, kv: paged.PagedKV):
+        mine = self.rows[b][self.rank]
+        kv.gather_split(mine[:self.elems], mine[self.elems:])
+
+    def _parity(self, b: int):
+        rdp_kv_ops.compute_rdp_parity(self.rows[b].view(torch.uint16), self.world, self.S, self.star_base)
+
+    def _replay(self, which: list, fn, b: int):
+        if which[b] is None:
+            # captured on torch.cuda.graph's side stream; replays are ordered
+            # on the current one
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                fn(b)
+            which[b] = g
+        which[b].replay()
+
+    def begin(self, active: torch.Tensor) -> int:
+        """Take the next row buffer (after the host copies that last read
+        it) and, with graphs, load this step's slots; returns the buffer."""
+        b = self.turn
+        self.turn ^= 1
+        if self.freed[b] is not None:
+            torch.cuda.current_stream(active.device).wait_event(self.freed[b])
+        self.active = active
+        if self.graphs:
+            self.slots.copy_(active, non_blocking=True)
+        return b
+
+    def gather(self, b: int):
+        if self.graphs:
+            self._replay(self.g_gather, lambda bb: self._gather(bb, self.kv), b)
+        else:
+            self._gather(b, paged.PagedKV(self.pool6, self.active.view(1, self.n), 0, self.n))
+
+    def parity(self, b: int):
+        if self.graphs:
+            self._replay(self.g_parity, self._parity, b)
+        else:
+            self._parity(b)
+
+
 class KVParityHook:
     """Per-step parity of the KV delta; call :meth:`on_extend` after each
-    ``forward_extend`` (or let :func:`install` do it)."""
+    ``forward_extend`` (or let :func:`install` do it).
+
+    ``graphs``: replay each step's gather and P/Q kernels from HIP graphs
+    captured once per step shape (the first step of a shape captures them)
+    instead of launching them through the C calls.  Off by default: on
+    MI355X with torch 2.10 a graph replay costs the host about as much as
+    the two launches it replaces, plus a device copy of the slots, and the
+    owner's step at TP8 took 219 against 203 us per step."""
 
     def __init__(self, star_base: Optional[int] = None, metrics_file: Optional[str] = None,
-                 prog_start_mono: Optional[float] = None, probe_h2d: bool = False):
+                 prog_start_mono: Optional[float] = None, probe_h2d: bool = False,
+                 graphs: bool = False):
         env = os.environ
         self.star_base = int(env.get("RDP_STAR_BASE", "0")) if star_base is None else int(star_base)
         self.metrics = MetricsLog(env.get("FT_METRICS_FILE") if metrics_file is None else metrics_file)
@@ -110,77 +190,133 @@ class KVParityHook:
             prog_start_mono = float(env.get("FT_PROG_START_MONO", "nan"))
         self.prog_start_mono = prog_start_mono
         self.probe_h2d = probe_h2d
+        self.graphs = graphs
         self.counter = ChunkCounter()
         self.first_chunk_wall_ms: Optional[float] = None
         self._stream: Optional[torch.cuda.Stream] = None
         self._pending: list = []
+        self._plans: dict = {}
         self.last_parity = None   # (P, Q) host tensors of the newest finished chunk
 
     # ------------------------------------------------------------ per step
+    @staticmethod
+    def _check_pool(kv_pool: torch.Tensor) -> None:
+        if kv_pool.dim() != 4 or kv_pool.shape[1] != 2 or kv_pool.element_size() != 2:
+            raise ValueError("kv_pool must be [max_tokens, 2, kv_heads, head_dim] of a 2-byte dtype")
+        if not kv_pool.is_contiguous():
+            raise ValueError("kv_pool must be contiguous")
+
+    @staticmethod
+    def _active(slot_mapping, dev) -> torch.Tensor:
+        """The slots written this step (-1 entries dropped), int32 on the
+        device.  The count is needed on the host (it sizes the rows), so a
+        device slot_mapping costs one synchronization here, as in the
+        reference (bench_ghostserve_rdp.py:449-451); a host one costs none."""
+        slots = torch.as_tensor(slot_mapping).reshape(-1)
+        if slots.device.type == "cpu":
+            # pinned, so the upload is queued behind the device's work
+            # instead of waiting for it
+            return slots[slots != -1].to(torch.int32).pin_memory().to(dev, non_blocking=True)
+        slots = slots.to(dev)
+        return slots[slots != -1].to(torch.int32)
+
+    MAX_PLANS = 8   # step shapes kept (prefill chunks of a few sizes repeat)
+
+    def _plan(self, kv_pool: torch.Tensor, n: int, world: int, rank: int) -> _StepPlan:
+        key = (kv_pool.data_ptr(), tuple(kv_pool.shape), kv_pool.dtype, n, world, rank, self.star_base)
+        plan = self._plans.pop(key, None)
+        if plan is None:
+            if len(self._plans) >= self.MAX_PLANS:
+                # the least recently used shape: its rows go back to the
+                # allocator only once the copies queued on the side stream
+                # have read them
+                old = self._plans.pop(next(iter(self._plans)))
+                if self._stream is not None:
+                    for r in old.rows:
+                        r.record_stream(self._stream)
+            plan = _StepPlan(kv_pool, n, world, rank, self.star_base, self.graphs)
+        self._plans[key] = plan   # most recently used last
+        return plan
+
     def on_extend(self, kv_pool: torch.Tensor, slot_mapping) -> Optional[int]:
         """Code this step's delta.  ``kv_pool``: [max_tokens, 2, kv_heads,
         head_dim] of a 2-byte dtype; ``slot_mapping``: the slots written this
         step, -1 for none.  Returns the chunk id, or None for an empty step."""
         self.poll()
-        if kv_pool.dim() != 4 or kv_pool.shape[1] != 2 or kv_pool.element_size() != 2:
-            raise ValueError("kv_pool must be [max_tokens, 2, kv_heads, head_dim] of a 2-byte dtype")
-        if not kv_pool.is_contiguous():
-            raise ValueError("kv_pool must be contiguous")
+        self._check_pool(kv_pool)
         dev = kv_pool.device
-        slots = torch.as_tensor(slot_mapping, device=dev).reshape(-1)
-        active = slots[slots != -1].to(torch.int32)
+        active = self._active(slot_mapping, dev)
         n = int(active.numel())
         if n == 0:
             return None
         cid, dst = self.counter.next(dev)
         if self.first_chunk_wall_ms is None and not math.isnan(self.prog_start_mono):
             self.first_chunk_wall_ms = (time.perf_counter() - self.prog_start_mono) * 1000.0
-
-        T, _, H, D = kv_pool.shape
-        elems = n * H * D            # words of K (and of V) in this rank's delta
-        S = 2 * elems                # words per row: K then V
         dist = _dist()
         world = dist.get_world_size() if dist is not None else 1
         rank = dist.get_rank() if dist is not None else 0
-        rows = torch.empty((world + 2, S), dtype=torch.int16, device=dev) if rank == dst else None
-        mine = rows[rank] if rows is not None else torch.empty(S, dtype=torch.int16, device=dev)
-        kv = paged.PagedKV(kv_pool.view(1, T, 1, 2, H, D), active.view(1, n), 0, n)
-        kv.gather_split(mine[:elems], mine[elems:])
+        plan = self._plan(kv_pool, n, world, rank)
+        b = plan.begin(active)
+        plan.gather(b)
         if world > 1:
-            self._gather_rows(dist, mine, rows, dst, dev)
-        if rank != dst:
-            return cid
+            self._gather_rows(dist, plan.rows[b][rank], plan.rows[b] if rank == dst else None, dst, dev)
+        if rank == dst:
+            self._code_owner(plan, b, cid, dst)
+        return cid
 
+    def step_as_owner(self, kv_pool: torch.Tensor, slot_mapping, world: int) -> Optional[int]:
+        """The parity owner's work of one step in a group of ``world`` ranks,
+        in one process: this rank's delta gathered into row 0, P/Q of the
+        ``world`` rows and their copies to host memory.  The other ranks'
+        rows are whatever the row buffer holds (the exchange that would
+        bring them is not part of it): a single-GPU measurement of the
+        owner's step at a real group size."""
+        self.poll()
+        self._check_pool(kv_pool)
+        active = self._active(slot_mapping, kv_pool.device)
+        n = int(active.numel())
+        if n == 0:
+            return None
+        self.counter.count += 1
+        plan = self._plan(kv_pool, n, int(world), 0)
+        b = plan.begin(active)
+        plan.gather(b)
+        self._code_owner(plan, b, self.counter.count, 0)
+        return self.counter.count
+
+    def _code_owner(self, plan: _StepPlan, b: int, cid: int, dst: int) -> None:
+        """P/Q of the row buffer and their copy to pinned host memory on a
+        side stream (the two rows are adjacent: one copy); the JSONL record
+        waits for that copy."""
+        dev = plan.rows[b].device
+        rows, world, S = plan.rows[b], plan.world, plan.S
         t0 = torch.cuda.Event(enable_timing=True)
         t1 = torch.cuda.Event(enable_timing=True)
         t0.record()
-        rdp_kv_ops.compute_rdp_parity(rows.view(torch.uint16), world, S, self.star_base)
+        plan.parity(b)
         t1.record()
         # P/Q to pinned host memory on a side stream, after the parity kernel
         if self._stream is None:
             self._stream = torch.cuda.Stream(device=dev)
-        P_h = torch.empty(S, dtype=torch.int16, pin_memory=True)
-        Q_h = torch.empty(S, dtype=torch.int16, pin_memory=True)
+        PQ_h = torch.empty((2, S), dtype=torch.int16, pin_memory=True)
+        P_h, Q_h = PQ_h[0], PQ_h[1]
         c0 = torch.cuda.Event(enable_timing=True)
         c1 = torch.cuda.Event(enable_timing=True)
         self._stream.wait_event(t1)
         with torch.cuda.stream(self._stream):
             c0.record(self._stream)
-            P_h.copy_(rows[world], non_blocking=True)
-            Q_h.copy_(rows[world + 1], non_blocking=True)
+            PQ_h.copy_(rows[world:world + 2], non_blocking=True)
             c1.record(self._stream)
-            rows.record_stream(self._stream)
             h0 = h1 = None
             if self.probe_h2d:
                 h0 = torch.cuda.Event(enable_timing=True)
                 h1 = torch.cuda.Event(enable_timing=True)
                 probe = torch.empty((2, S), dtype=torch.int16, device=dev)
                 h0.record(self._stream)
-                probe[0].copy_(P_h, non_blocking=True)
-                probe[1].copy_(Q_h, non_blocking=True)
+                probe.copy_(PQ_h, non_blocking=True)
                 h1.record(self._stream)
+        plan.freed[b] = c1
         self._pending.append((cid, dst, (t0, t1), (c0, c1), (h0, h1), P_h, Q_h))
-        return cid
 
     def _gather_rows(self, dist, mine, rows, dst, dev):
         """Every rank's row to dst (bench_ghostserve_rdp.py:302-332).  gloo

@@ -465,13 +465,23 @@ def bench_chunked(pkg, torch, oracle, dev, seed, warmup):
     torch.cuda.synchronize()
     tp = time.perf_counter()
     evs_off = []
+    evs_enc = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+               for _ in range(NCH)]
     for c in range(NCH):
+        evs_enc[c][0].record(stream)
         st.encode(kvs[c], c)
+        evs_enc[c][1].record(stream)
         evs_off.append(off.to_host(st.region(c), nr))
     for e in evs_off:
         e.synchronize()
     torch.cuda.synchronize()
     pipe_us = (time.perf_counter() - tp) * 1e6 / NCH
+    # encodes 1.. run while an earlier chunk's copies are in flight
+    beside = [a.elapsed_time(b) * 1e3 for a, b in evs_enc[1:]]
+    ok_off = all(torch.equal(d.view(torch.uint8).view(-1)[st.region(0):st.region(NCH - 1) + nr].cpu(),
+                             h[st.region(0):st.region(NCH - 1) + nr]) for d, h in zip(par, off.host))
+    if not ok_off:
+        raise RuntimeError("parity offload: host mirrors differ from the device parity")
     t1 = torch.cuda.Event(enable_timing=True)
     t2 = torch.cuda.Event(enable_timing=True)
     t1.record(off.stream)
@@ -484,7 +494,13 @@ def bench_chunked(pkg, torch, oracle, dev, seed, warmup):
         "d2h_ms_per_chunk": round(d2h_ms, 3),
         "d2h_gbs": round(parity_w / d2h_ms / 1e6, 2),
         "pipelined_encode_plus_d2h_us_per_chunk": round(pipe_us, 1),
+        "encode_us_beside_d2h_mean": round(float(np.mean(beside)), 2),
+        "encode_us_beside_d2h_max": round(float(np.max(beside)), 2),
+        "encode_us_alone": round(enc_us, 2),
+        "encode_beside_d2h_vs_alone": round(float(np.mean(beside)) / enc_us, 3),
         "host_buffers": "pinned",
+        "copy_engine": "DMA (hipMemcpyAsync device-to-host into pinned memory)",
+        "mirrors_byte_exact": ok_off,
     }
     del off, par
 
@@ -823,6 +839,116 @@ def bench_gs(pkg, torch, oracle, dev, seed, steps, warmup):
     return out
 
 
+def bench_hook(pkg, torch, oracle, dev, seed, steps=100, warmup=10):
+    """The parity owner's step of the serving hook at the plugin shape
+    (Llama-3.1-8B at TP8: a 2048-token prefill step, 1 KV head x 128 bf16 per
+    rank, 8 + 2 rows of 524,288 words): this rank's delta gathered into its
+    row, P/Q of the 8 rows, the pinned copies to the host, and the JSONL
+    timings the reference records (rdp_encode_ms, gpu_to_cpu_ms;
+    bench_ghostserve_rdp.py:334-392).  The other 7 rows stand for the rows the
+    exchange brings.  Eager C calls against HIP graphs replayed per shape,
+    with the slot mapping on the device (one synchronization per step for
+    its length, as in the reference) and on the host (none)."""
+    import json as _json
+    import tempfile
+    import numpy as np
+    world, H, D, NTOK, MAXT = 8, 1, 128, 2048, 1 << 17
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed + 77)
+    pool = torch.randn((MAXT, 2, H, D), generator=g, device=dev).to(torch.bfloat16)
+    rng = np.random.default_rng(seed + 78)
+    slot_sets = [rng.permutation(MAXT)[:NTOK].astype(np.int64) for _ in range(8)]
+    dslots = [torch.from_numpy(x).to(dev) for x in slot_sets]
+    hslots = [torch.from_numpy(x) for x in slot_sets]
+    out = {"world": world, "tokens": NTOK, "rows": [world + 2, 2 * NTOK * H * D], "kv_dtype": "bf16"}
+    for graphs in (False, True):
+        tag = "graph" if graphs else "eager"
+        with tempfile.TemporaryDirectory() as tmp:
+            path = os.path.join(tmp, "m.jsonl")
+            hook = pkg.serving.KVParityHook(star_base=0, metrics_file=path, graphs=graphs)
+            for i in range(warmup):
+                hook.step_as_owner(pool, dslots[i % 8], world)
+            hook.flush()
+            plan = next(iter(hook._plans.values()))
+            for b in range(2):
+                plan.rows[b][1:world].copy_(torch.randint(-32768, 32767, (world - 1, plan.S), generator=g,
+                                                          device=dev, dtype=torch.int16))
+            torch.cuda.synchronize()
+            open(path, "w").close()
+            res = {}
+            for kind, sl in (("device_slots", dslots), ("host_slots", hslots)):
+                torch.cuda.synchronize()
+                t0 = time.perf_counter()
+                for i in range(steps):
+                    hook.step_as_owner(pool, sl[i % 8], world)
+                t1 = time.perf_counter()
+                torch.cuda.synchronize()
+                t2 = time.perf_counter()
+                hook.flush()
+                res[kind] = {"issue_us_per_step": round((t1 - t0) * 1e6 / steps, 2),
+                             "us_per_step": round((t2 - t0) * 1e6 / steps, 2)}
+            recs = [_json.loads(x) for x in open(path).read().splitlines()]
+            # the last step checked against the oracle's P/Q of the buffer's rows
+            b = plan.turn ^ 1
+            rows_h = plan.rows[b].cpu().numpy().view(np.uint16).copy()
+            P, Q = hook.last_parity
+            want = rows_h.copy()
+            want[world:] = 0
+            oracle.gs_parity(want, world, plan.S, 0)
+            host_pool = pool.view(torch.int16).cpu().numpy().view(np.uint16)
+            last = slot_sets[(steps - 1) % 8]
+            own = np.concatenate([host_pool[last, 0].reshape(-1), host_pool[last, 1].reshape(-1)])
+            if not (np.array_equal(rows_h[0], own) and np.array_equal(P.numpy().view(np.uint16), want[world])
+                    and np.array_equal(Q.numpy().view(np.uint16), want[world + 1])):
+                raise RuntimeError(f"hook step ({tag}) P/Q mismatch vs oracle")
+        res["records"] = len(recs)
+        res["rdp_encode_ms_mean"] = round(float(np.mean([r["timings"]["rdp_encode_ms"] for r in recs])), 4)
+        res["gpu_to_cpu_ms_mean"] = round(float(np.mean([r["timings"]["gpu_to_cpu_ms"] for r in recs])), 4)
+        out[tag] = res
+        del hook, plan
+    # The reference's step on this GPU (bench_ghostserve_rdp.py:445-458,
+    # :334-374), the exchange left out as above: the delta by advanced
+    # indexing, per rank an fp16 copy of K and V and pack_row_from_block,
+    # P/Q, then the host copies and the device-to-host-to-device probe, each
+    # followed by a synchronize.
+    elems = NTOK * H * D
+    S = 2 * elems
+    k_all = torch.zeros(elems * world, dtype=torch.bfloat16, device=dev)
+    v_all = torch.zeros_like(k_all)
+
+    def ref_step(slots):
+        active = slots != -1
+        if int(active.sum().item()) == 0:
+            return
+        act = slots[active].to(dtype=torch.long)
+        k_all[:elems].copy_(pool[act, 0].reshape(-1))
+        v_all[:elems].copy_(pool[act, 1].reshape(-1))
+        rows = torch.empty((world + 2, S), dtype=torch.uint16, device=dev)
+        for r in range(world):
+            k = k_all.narrow(0, r * elems, elems).to(torch.float16)
+            v = v_all.narrow(0, r * elems, elems).to(torch.float16)
+            pkg.rdp_kv_ops.pack_row_from_block(k.view(1, 1, elems, 1), v.view(1, 1, elems, 1), rows, r)
+        pkg.rdp_kv_ops.compute_rdp_parity(rows, nd=world, S=S, star_base=0)
+        torch.cuda.synchronize()
+        P_cpu = rows[world].to("cpu", non_blocking=True).contiguous()
+        Q_cpu = rows[world + 1].to("cpu", non_blocking=True).contiguous()
+        torch.cuda.synchronize()
+        _ = P_cpu.to(dev, non_blocking=True)
+        _ = Q_cpu.to(dev, non_blocking=True)
+        torch.cuda.synchronize()
+
+    for i in range(warmup):
+        ref_step(dslots[i % 8])
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        ref_step(dslots[i % 8])
+    torch.cuda.synchronize()
+    out["reference_sequence_us_per_step"] = round((time.perf_counter() - t0) * 1e6 / steps, 2)
+    out["byte_exact_last_step"] = True
+    return out
+
+
 C0_K, C0_SHARD = 4, 2 * 512 * 1 * 128 * 2          # 262,144 B: [2, 512 tok, 1, 128] bf16
 C0_ALG = C0_K * C0_SHARD + C0_SHARD                  # 1,310,720 B
 
@@ -968,6 +1094,7 @@ def main():
     ap.add_argument("--no-chunked", action="store_true")
     ap.add_argument("--no-gs", action="store_true")
     ap.add_argument("--no-c0", action="store_true")
+    ap.add_argument("--no-hook", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=10.0,
                     help="seconds of CPU work for the main CPU baseline (others take less)")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -1069,6 +1196,17 @@ def main():
             f"{gs['rs16_reconstruct_1lost']['us']:.1f} us)")
         torch.cuda.empty_cache()
 
+    hook = None
+    if not args.no_hook:
+        log("[bench] serving hook: the parity owner's step at TP8 (2048 tokens), eager and graphs")
+        hook = bench_hook(pkg, torch, oracle, dev, args.seed)
+        log(f"[bench] hook step: eager {hook['eager']['device_slots']['us_per_step']:.1f} / "
+            f"graph {hook['graph']['device_slots']['us_per_step']:.1f} us per step (device slots; "
+            f"the reference's sequence {hook['reference_sequence_us_per_step']:.1f}), "
+            f"issue {hook['eager']['host_slots']['issue_us_per_step']:.1f} / "
+            f"{hook['graph']['host_slots']['issue_us_per_step']:.1f} us (host slots)")
+        torch.cuda.empty_cache()
+
     c0 = None
     if not args.no_c0:
         log("[bench] XOR k=4 single parity, 256 KiB bf16 shards (CPU path, and the GPU)")
@@ -1124,6 +1262,7 @@ def main():
         "paged_gather_rdp": fused,
         "chunked_fp8_rdp_rs": chunked,
         "gs_family": gs,
+        "hook_step_tp8": hook,
         "c0_xor_cpu_path": c0,
     }
     print(json.dumps(out), flush=True)

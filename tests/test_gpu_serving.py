@@ -81,3 +81,72 @@ def test_hook_steps_match_oracle(pkg, ora, gpu, tmp_path, star_base):
         assert np.array_equal(P.numpy().view(np.uint16), rows[1])
         assert np.array_equal(Q.numpy().view(np.uint16), rows[2])
         assert rec["timings"]["parity_bytes"] == 2 * S * 2
+
+
+def _row_of(host, slots):
+    act = [s for s in slots if s != -1]
+    return np.concatenate([host[act, 0].reshape(-1), host[act, 1].reshape(-1)])
+
+
+@pytest.mark.parametrize("graphs", [True, False])
+def test_hook_repeated_shapes_and_host_slots(pkg, ora, gpu, monkeypatch, graphs):
+    """Steps of two shapes in turn, each repeated with new slots (the graphs
+    of a shape are captured once and replayed on both row buffers; a plan
+    is evicted and rebuilt when only one is kept), the slots given as a
+    device tensor, a host tensor or a list: every chunk's P/Q is the
+    oracle's."""
+    monkeypatch.setattr(pkg.serving.KVParityHook, "MAX_PLANS", 1)
+    pool = _pool(gpu, T=400, seed=3)
+    host = pool.cpu().view(torch.int16).numpy().view(np.uint16)
+    hook = pkg.serving.KVParityHook(star_base=2, graphs=graphs)
+    rng = np.random.default_rng(4)
+    for i in range(7):
+        n = 5 if i % 3 else 9
+        sl = [int(x) for x in rng.choice(400, n, replace=False)]
+        if i == 2:
+            sl[1] = -1
+        arg = [torch.tensor(sl, device=gpu), torch.tensor(sl), sl][i % 3]
+        assert hook.on_extend(pool, arg) == i + 1
+        hook.flush()
+        P, Q = hook.last_parity
+        row = _row_of(host, sl)
+        rows = np.zeros((3, row.size), np.uint16)
+        rows[0] = row
+        ora.gs_parity(rows, 1, row.size, 2)
+        assert np.array_equal(P.numpy().view(np.uint16), rows[1]), i
+        assert np.array_equal(Q.numpy().view(np.uint16), rows[2]), i
+
+
+@pytest.mark.parametrize("graphs", [True, False])
+def test_owner_step_at_group_of_eight(pkg, ora, gpu, graphs):
+    """The parity owner's step in a group of 8 ranks, in one process: row 0
+    is this rank's delta, rows 1-7 whatever the buffer holds (set here), and
+    P/Q are those of all 8 rows; three steps, so both row buffers are
+    reused."""
+    pool = _pool(gpu, T=500, H=1, D=128, seed=5)
+    host = pool.cpu().view(torch.int16).numpy().view(np.uint16)
+    hook = pkg.serving.KVParityHook(star_base=0, graphs=graphs)
+    rng = np.random.default_rng(6)
+    for i in range(3):
+        sl = [int(x) for x in rng.choice(500, 64, replace=False)]
+        if i == 0:
+            hook.step_as_owner(pool, torch.tensor(sl, device=gpu), 8)
+            hook.flush()
+            plan = next(iter(hook._plans.values()))
+            for b in range(2):
+                plan.rows[b][1:8].view(torch.uint16).copy_(
+                    torch.from_numpy(rng.integers(0, 65536, (7, plan.S), dtype=np.uint16)).to(gpu))
+            torch.cuda.synchronize()
+        b = plan.turn if i else None
+        others = plan.rows[plan.turn][1:8].cpu().numpy().view(np.uint16).copy() if i else None
+        hook.step_as_owner(pool, torch.tensor(sl, device=gpu), 8)
+        hook.flush()
+        if not i:
+            continue
+        P, Q = hook.last_parity
+        rows = np.zeros((10, plan.S), np.uint16)
+        rows[0] = _row_of(host, sl)
+        rows[1:8] = others
+        ora.gs_parity(rows, 8, plan.S, 0)
+        assert np.array_equal(P.numpy().view(np.uint16), rows[8]), (i, b)
+        assert np.array_equal(Q.numpy().view(np.uint16), rows[9]), (i, b)
