@@ -1016,35 +1016,54 @@ def bench_c0(pkg, torch, oracle, dev, seed, budget_s):
     }
 
 
-def _rate(fn, nbytes, budget_s):
+def _rate(fn, nbytes, budget_s, runs=None):
+    """GB/s over as many runs as fit in budget_s (at least one); each run's
+    own duration is appended to `runs` when given."""
     n, t0 = 0, time.perf_counter()
     while True:
+        a = time.perf_counter()
         fn()
+        b = time.perf_counter()
+        if runs is not None:
+            runs.append(b - a)
         n += 1
-        t = time.perf_counter() - t0
+        t = b - t0
         if t >= budget_s:
             return nbytes * n / t / 1e9, n, t
+
+
+def _cpu_entry(oracle, fn, nbytes, budget_s, threads):
+    """One CPU baseline at `threads` OpenMP threads: GB/s, runs, and the
+    spread of the single runs' rates (min, median, max)."""
+    import numpy as np
+    prev = oracle.num_threads()
+    oracle.set_num_threads(threads)
+    try:
+        runs = []
+        v, n, t = _rate(fn, nbytes, budget_s, runs)
+    finally:
+        oracle.set_num_threads(prev)
+    r = sorted(nbytes / x / 1e9 for x in runs)
+    return {"gbs": round(v, 3), "threads": threads, "runs": n,
+            "gbs_spread_min_median_max": [round(r[0], 3), round(float(np.median(r)), 3), round(r[-1], 3)]}, t
 
 
 def cpu_baselines(oracle, c1_host, R, rs8_host, chunk_case, budget_s):
     """The oracle (C, OpenMP over stripe columns) on the same full workloads:
     C1 encode and C2 decode (all 28 pairs cycled) on the 512 MiB stripe set,
-    RS(6,2) encode, and one chunk of the fp8 chunked coder; all host cores, and
-    the C1 encode on one core too."""
+    RS(6,2) encode, and one chunk of the fp8 chunked coder; each on all host
+    cores and on one core, with the spread of the single runs."""
     import numpy as np
     all_cores = oracle.num_threads()
     out = {"cpu_model": cpu_model(), "cores": all_cores, "kind": "port"}
     par = (np.zeros_like(c1_host[0]), np.zeros_like(c1_host[0]))    # written in place
-    v, n, t = _rate(lambda: oracle.rdp_encode(c1_host, P_RDP, unit=UNIT, out=par), ALG_BYTES, budget_s)
-    out["c1_rdp_encode"] = {"gbs": round(v, 3), "threads": all_cores, "runs": n}
-    main = {"value": round(v, 3), "unit": "GB/s", "cores": all_cores, "kind": "port",
+    c1 = lambda: oracle.rdp_encode(c1_host, P_RDP, unit=UNIT, out=par)
+    out["c1_rdp_encode"], t = _cpu_entry(oracle, c1, ALG_BYTES, budget_s, all_cores)
+    v, n = out["c1_rdp_encode"]["gbs"], out["c1_rdp_encode"]["runs"]
+    main = {"value": v, "unit": "GB/s", "cores": all_cores, "kind": "port",
             "sample": f"oracle RDP p=7 k=6 encode (64 KiB stripe rows) of the full 512 MiB chunk "
                       f"stripe set, {n} runs in {t:.1f} s (C, OpenMP over stripe columns)"}
-    oracle.set_num_threads(1)
-    v1, n1, _ = _rate(lambda: oracle.rdp_encode(c1_host, P_RDP, unit=UNIT, out=par), ALG_BYTES,
-                      budget_s / 2)
-    out["c1_rdp_encode_1core"] = {"gbs": round(v1, 3), "threads": 1, "runs": n1}
-    oracle.set_num_threads(all_cores)
+    out["c1_rdp_encode_1core"], _ = _cpu_entry(oracle, c1, ALG_BYTES, budget_s / 2, 1)
     full = list(c1_host) + list(par)
     pairs = list(itertools.combinations(range(K_RDP + 2), 2))
     it = iter(itertools.cycle(pairs))
@@ -1053,13 +1072,14 @@ def cpu_baselines(oracle, c1_host, R, rs8_host, chunk_case, budget_s):
         a, b = next(it)
         oracle.rdp_decode(full, P_RDP, a, b, unit=UNIT)
 
-    v, n, _ = _rate(dec, ALG_BYTES, budget_s / 2)
-    out["c2_rdp_decode_pairs"] = {"gbs": round(v, 3), "threads": all_cores, "runs": n}
+    out["c2_rdp_decode_pairs"], _ = _cpu_entry(oracle, dec, ALG_BYTES, budget_s / 2, all_cores)
+    out["c2_rdp_decode_pairs_1core"], _ = _cpu_entry(oracle, dec, ALG_BYTES, budget_s / 4, 1)
     del full
     if rs8_host is not None:
         rpar = [np.zeros_like(rs8_host[0]) for _ in range(2)]
-        v, n, _ = _rate(lambda: oracle.rs8_encode(rs8_host, 2, out=rpar), ALG_BYTES, budget_s / 2)
-        out["c3_rs8_encode"] = {"gbs": round(v, 3), "threads": all_cores, "runs": n}
+        c3 = lambda: oracle.rs8_encode(rs8_host, 2, out=rpar)
+        out["c3_rs8_encode"], _ = _cpu_entry(oracle, c3, ALG_BYTES, budget_s / 2, all_cores)
+        out["c3_rs8_encode_1core"], _ = _cpu_entry(oracle, c3, ALG_BYTES, budget_s / 4, 1)
     if chunk_case is not None:
         pool_h, table, page_tokens, ct, k, p, m, W, U = chunk_case
         cpar = [np.zeros((p - 1) * W, np.uint8) for _ in range(2 + m)]
@@ -1074,10 +1094,12 @@ def cpu_baselines(oracle, c1_host, R, rs8_host, chunk_case, budget_s):
 
         sb = one_chunk()
         alg = 2 * sb + (2 + m) * (p - 1) * W    # pool read + cells written, parity written
-        v, n, _ = _rate(one_chunk, alg, budget_s / 2)
-        out["c4_chunk_encode"] = {"gbs": round(v, 3), "threads": all_cores, "runs": n,
-                                  "us_per_chunk": round(alg / v / 1e3, 1),
-                                  "note": "gather into cells, then RDP + RS(5,3)"}
+        for key, thr, bud in (("c4_chunk_encode", all_cores, budget_s / 2), ("c4_chunk_encode_1core", 1,
+                                                                             budget_s / 4)):
+            e, _ = _cpu_entry(oracle, one_chunk, alg, bud, thr)
+            e["us_per_chunk"] = round(alg / e["gbs"] / 1e3, 1)
+            e["note"] = "gather into cells, then RDP + RS(5,3)"
+            out[key] = e
     return main, out
 
 
