@@ -56,6 +56,19 @@ __device__ __forceinline__ uint16_t gf16_div_tab(uint16_t a, uint16_t b, const u
     return ex[d];
 }
 
+// Table word i (0 <= i < 131069) by a scalar load of the dword holding it,
+// through the constant address space: the tables do not change during a
+// launch, and the scalar cache answers a block's read of the generator in a
+// fraction of a vector load's round trip, which a block otherwise waits for
+// before issuing its data loads.  The dword read starts at an even word of
+// the 2-byte-aligned table, so it never leaves the table.
+__device__ __forceinline__ uint32_t table_word_s(const uint16_t* tab, uint32_t i) {
+    const uintptr_t a = reinterpret_cast<uintptr_t>(tab + i);
+    const uintptr_t d = a & ~uintptr_t(3);
+    const uint32_t w = *reinterpret_cast<const __attribute__((address_space(4))) uint32_t*>(d);
+    return (a & 2) ? (w >> 16) : (w & 0xFFFFu);
+}
+
 struct RsJob {
     const uint16_t* in_rows[kRsMaxTables];  // k input rows (u16, logical column 0)
     uint16_t* out_rows[kRsMaxM];            // output rows
@@ -870,8 +883,9 @@ static uint8_t* align_down16(const void* p) {
 // and folds the windows into the parities by Horner's rule; the parities go
 // through LDS to tile_store.
 //
-// The generator is read from the tables per block with scalar loads, whose
-// wait counter is not the vector loads': with gf_exp[1] == 2 (the tables of
+// The generator is read from the tables per block with scalar loads
+// (table_word_s), whose wait counter is not the vector loads': with
+// gf_exp[1] == 2 (the tables of
 // init_gf_tables, or any field's exp/log pair whose generator is 2) the
 // coefficient alpha^((p+1) i) is (p+1) i doublings with the field's reduction
 // word gf_exp[16] = 2^16 reduced (one table read; 0x8000 * 2 through the log
@@ -919,8 +933,8 @@ __global__ __launch_bounds__(kTB) void rs16_encode_tiles_kernel(const uint8_t* i
         const uint32_t mis = uint32_t(reinterpret_cast<uintptr_t>(fc.src + o) & 15);
         if (mis && b < 16 - mis && b < Sb) as_global(fc.dst)[o + b] = as_global(fc.src)[o + b];
     }
-    const bool horner = ex[1] == 2;
-    const uint16_t red = ex[16];   // g^16 = 2^16 reduced, when g = 2
+    const bool horner = table_word_s(ex, 1) == 2;
+    const uint16_t red = uint16_t(table_word_s(ex, 16));   // g^16 = 2^16 reduced, when g = 2
     const uint32_t red2 = uint32_t(red) * 0x10001u;
     const Gf16Quad quad = gf16_quad_table(red);
     u32x4 acc[M];
@@ -1013,6 +1027,14 @@ using RsEncTiles = RsEncTilesTable<0, 1, 2, 3, 4, 5, 6, 7>;
 // each product taken in the field the tables define, as the reference's
 // table products are (the tables are taken to be a field's exp/log pair).
 //
+// The generator and the inverse's uniform table reads (gf_exp[d], gf_exp[e],
+// the log of their sum) are scalar loads: read as vector loads, the
+// generator's round trip came before the block's data loads and the other
+// two chained two more round trips after the data had arrived (A/B on one
+// box, byte-identical: rows 1 and 4 lost 131.2-132.6 against 122.8-125.3 us,
+// rows 0 and 5 126.9-128.6 against 118.8-119.4 us; the encode, whose
+// generator read already followed its data loads, 218.3 against 213.1 us).
+//
 // Every wave forms the inverse's byte maps itself, so no wave waits at a
 // block barrier for another's table reads: lane t * 16 + j reads entry t
 // times 2^j (the entry's basis products) from the tables into the wave's LDS,
@@ -1055,7 +1077,7 @@ __global__ __launch_bounds__(BS) void rs16_reconstruct_tiles_kernel(uint8_t* bas
         }
         if (M == 2) ok = ok && miss[0] != miss[M - 1];
         if (!ok) return;   // uniform: the whole grid writes nothing
-        const bool horner = ex[1] == 2;
+        const bool horner = table_word_s(ex, 1) == 2;
         const int m_lo = M == 2 ? min(miss[0], miss[M - 1]) : miss[0];
         const int m_hi = M == 2 ? max(miss[0], miss[M - 1]) : NIN;
         uint32_t rowp = 0;   // the surviving data rows, 4 bits each
@@ -1092,7 +1114,9 @@ __global__ __launch_bounds__(BS) void rs16_reconstruct_tiles_kernel(uint8_t* bas
                     has1[1] = false;
                     L1[2] = add(c, neg(a));
                 } else {
-                    const uint32_t p = uint32_t(lg[uint16_t(ex[d] ^ ex[e])]) % G, np = neg(p);
+                    // uniform table reads on the scalar cache, while the
+                    // data loads are in flight
+                    const uint32_t p = table_word_s(lg, table_word_s(ex, d) ^ table_word_s(ex, e)) % G, np = neg(p);
                     L2[0] = add(add(e, neg(a)), np);   // b + c - 2a - p
                     has2[0] = true;
                     L1[1] = add(add(b, neg(a)), np);
@@ -1130,7 +1154,7 @@ __global__ __launch_bounds__(BS) void rs16_reconstruct_tiles_kernel(uint8_t* bas
                     if (h2) bv ^= ex[add(l2, j)];
                 }
             }
-            const uint16_t red = ex[16];   // g^16 = 2^16 reduced, as g = 2
+            const uint16_t red = uint16_t(table_word_s(ex, 16));   // g^16 = 2^16 reduced, as g = 2
             const uint32_t red2 = uint32_t(red) * 0x10001u;
             const Gf16Quad quad = gf16_quad_table(red);
             u32x4 x[NIN];
