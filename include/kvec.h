@@ -262,7 +262,10 @@ int kvec_gs_rdp_parity(void* rows, int nd, int S, int star_base, void* stream);
 
 /* ======== gs family: RS over GF(2^16) (benchmark/rs/kernel.cu, main.py) ======= */
 /* u16 symbols, packed: shards = [(k + m), shard_size].  gf_exp / gf_log are
- * the device tables of init_gf_tables() (poly 0x1100B). */
+ * device tables: those of init_gf_tables() (poly 0x1100B), or any exp/log pair
+ * of GF(2^16) (any primitive polynomial, any generator), for which every
+ * kernel gives the reference's bytes.  Tables that are not a field's make the
+ * bytes unspecified (they may differ between shapes). */
 
 /* pack_fp16_pair_to_u16, benchmark/rs/kernel.cu:225-243: out = K || V words. */
 int kvec_rs16_pack(const void* k, const void* v, void* out, int64_t N_k, int64_t N_v,
@@ -272,8 +275,7 @@ int kvec_rs16_split(const void* in, void* k_out, void* v_out, int64_t N_k, int64
                     void* stream);
 /* encode_rs_u16, :265-285: copy data rows; Par_p = XOR_i D_i * alpha^((p+1) i).
  * Any data_shards >= 1 and parity_shards >= 0 with (k - 1) * m < 2^31 (the
- * reference's int exponent) and m <= 524280; KVEC_EUNSUPPORTED beyond.  The
- * tables must be a GF(2^16) exp/log pair (as init_gf_tables() gives). */
+ * reference's int exponent) and m <= 524280; KVEC_EUNSUPPORTED beyond. */
 int kvec_rs16_encode(const void* data_padded, void* shards, int data_shards, int parity_shards,
                      int shard_size, const uint16_t* gf_exp, const uint16_t* gf_log,
                      void* stream);
