@@ -788,6 +788,47 @@ def bench_gs(pkg, torch, oracle, dev, seed, steps, warmup):
     out["rs16_reconstruct_1lost"] = _entry(time_us(torch, rrec1), nd * S * 2 + S * 2)
     del sets, sh
 
+    # Shapes past the 48 coefficient maps (k * m > 48): (k, m) = (16, 4) on the
+    # same stream, the data rows in the shard tensor as forward_encode_kv lays
+    # them out; the encode checked against the oracle on the first 2^20
+    # columns (each column is its own codeword), 4 lost rows at full size.
+    k16, m16 = 16, 4
+    S16 = -(-(STREAM_BYTES // 2) // k16)
+    sh16 = [torch.empty((k16 + m16, S16), dtype=torch.uint16, device=dev) for _ in range(2)]
+    for t in sh16:
+        t[:k16].view(torch.int16).copy_(torch.randint(-32768, 32767, (k16, S16), generator=g, device=dev,
+                                                      dtype=torch.int16))
+
+    def renc16(t):
+        pkg.rs.rs_kernel.encode_rs_u16(t.view(-1)[:k16 * S16], t, k16, m16, S16, ex, lg)
+
+    renc16(sh16[0])
+    renc16(sh16[1])
+    torch.cuda.synchronize()
+    cols = 1 << 20
+    head = np.ascontiguousarray(u16(sh16[0]).reshape(k16 + m16, S16)[:, :cols])
+    if not np.array_equal(head, oracle.rs16_encode(head[:k16].reshape(-1), k16, m16, cols, exh, lgh)):
+        raise RuntimeError("gs RS16 (16, 4) encode mismatch vs oracle")
+    wall, kms = time_kernel(torch, renc16, [(t,) for t in sh16], steps, warmup)
+    out["rs16_encode_k16m4"] = _entry(kms * 1e3, k16 * S16 * 2 + m16 * S16 * 2)
+    lost = [1, 5, 9, 14]
+    md4 = torch.tensor(lost, dtype=torch.int32, device=dev)
+    pu4 = torch.tensor([0, 1, 2, 3], dtype=torch.int32, device=dev)
+    v16 = sh16[0].view(torch.int16)
+    keep = v16[lost].clone()
+    v16[lost] = 0x1234
+
+    def rrec4(i):
+        pkg.rs.rs_kernel.reconstruct_rs_u16_inplace(sh16[i % 2], S16, k16, m16, md4, pu4, ex, lg)
+
+    rrec4(0)
+    torch.cuda.synchronize()
+    if not torch.equal(v16[lost], keep):
+        raise RuntimeError("gs RS16 (16, 4) reconstruct did not restore the rows")
+    del keep, v16
+    out["rs16_reconstruct_k16_4lost"] = _entry(time_us(torch, rrec4), k16 * S16 * 2 + len(lost) * S16 * 2)
+    del sh16
+
     # The serving plugin's per-step parity (bench_ghostserve_rdp.py:334-360):
     # Llama-3.1-8B at TP8, a 2048-token prefill step, one [K | V] row per rank
     # of w = 2048 x 1 KV head x 128 words each, so rows [(8+2), 2w] u16.  A small
@@ -1215,7 +1256,8 @@ def main():
             f"{gs['xor_encode_from_kv']['us']:.1f} us, decode {gs['xor_decode_1lost']['us']:.1f} us), "
             f"RS16 {gs['rs16_encode']['us']:.1f} us (reconstruct "
             f"{gs['rs16_reconstruct_2lost']['us']:.1f} us, one row "
-            f"{gs['rs16_reconstruct_1lost']['us']:.1f} us)")
+            f"{gs['rs16_reconstruct_1lost']['us']:.1f} us; (16, 4) encode "
+            f"{gs['rs16_encode_k16m4']['us']:.1f} us, 4 lost {gs['rs16_reconstruct_k16_4lost']['us']:.1f} us)")
         torch.cuda.empty_cache()
 
     hook = None
