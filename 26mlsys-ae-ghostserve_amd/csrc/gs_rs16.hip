@@ -1382,27 +1382,22 @@ __device__ __forceinline__ void rs_h_store(uint8_t* stage, const uint32_t (*acc)
     __syncthreads();
 }
 
-// encode_rs_u16's parity rows og .. og + G - 1 (og = blockIdx.y * G; those at
-// or past m are computed and not stored).  in: the k data rows of S words;
-// par: parity row 0.
-template <int G, int NW>
-__global__ __launch_bounds__(kRsHBS) void rs16_encode_horner_kernel(const uint16_t* in, uint16_t* par, int64_t S,
-                                                                    int k, int m, const uint16_t* ex,
-                                                                    const uint16_t* lg) {
+// With gf_exp[1] == 2 (the tables' generator is 2, the rule of the tile
+// kernels), parity p's multiplier alpha^(p+1) is p + 1 doublings: up to
+// kRsHChainMax of them (times-4 steps and at most one doubling, 5 VALU ops
+// per two doublings of a dword) cost less than a byte-map product (about 14
+// per dword).
+constexpr int kRsHChainMax = 6;
+
+// The tiles of rs16_encode_horner_kernel.  CHAINS (group 0 only): accumulators
+// in natural word order, parity g multiplied by its chain of g + 1 doublings
+// (a compile-time length, unrolled), parities past nout skipped; else
+// byte-transposed, multiplied through the byte maps ptab.
+template <int G, int NW, bool CHAINS>
+__device__ __forceinline__ void rs_h_encode_tiles(const uint16_t* in, uint16_t* par, int64_t S, int k, int og,
+                                                  int nout, const uint32_t (*ptab)[kRs16Tab], uint32_t red2,
+                                                  Gf16Quad quad, uint8_t* stage) {
     constexpr uint32_t TB = 16 * kRsHBS * NW;
-    __shared__ __attribute__((aligned(16))) uint32_t ptab[G][kRs16Tab];
-    __shared__ uint16_t basis[G][16];
-    __shared__ uint16_t coef[G];
-    __shared__ __attribute__((aligned(16))) uint8_t stage[TB + 16];
-    const int og = int(blockIdx.y) * G;
-    if (threadIdx.x < G) {
-        const int p = og + int(threadIdx.x);
-        coef[threadIdx.x] = p < m ? ex[uint32_t(p + 1) % kGfOrder] : uint16_t(0);
-    }
-    __syncthreads();
-    rs_build_perm_tables(ptab, basis, coef, G, ex, lg);
-    __syncthreads();
-    const int nout = m - og < G ? m - og : G;
     const uint64_t Sb = uint64_t(S) * 2;
     const uint64_t ntiles = (Sb + TB - 1) / TB;
     for (uint64_t tt = blockIdx.x; tt < ntiles; tt += gridDim.x) {
@@ -1417,11 +1412,21 @@ __global__ __launch_bounds__(kRsHBS) void rs16_encode_horner_kernel(const uint16
 #pragma unroll
             for (int n = 0; n < NW; ++n) {
                 uint32_t y[4];
-                split_bytes(x[n], y);
+                if (CHAINS) y[0] = x[n].x, y[1] = x[n].y, y[2] = x[n].z, y[3] = x[n].w;
+                else split_bytes(x[n], y);
 #pragma unroll
                 for (int g = 0; g < G; ++g) {
+                    if (CHAINS && g >= nout) continue;
                     if (i == k - 1) {
                         acc[n][g][0] = y[0], acc[n][g][1] = y[1], acc[n][g][2] = y[2], acc[n][g][3] = y[3];
+                    } else if (CHAINS) {
+#pragma unroll
+                        for (int q = 0; q < 4; ++q) {
+                            uint32_t a = acc[n][g][q];
+#pragma unroll
+                            for (int d = 0; d + 2 <= g + 1; d += 2) a = gf16_quad2_xor(a, quad, 0u);
+                            acc[n][g][q] = (g + 1) & 1 ? gf16_dbl2_xor(a, red2, y[q]) : a ^ y[q];
+                        }
                     } else {
                         gf16_mul_split_xor(acc[n][g], ptab[g], y);
                     }
@@ -1437,12 +1442,46 @@ __global__ __launch_bounds__(kRsHBS) void rs16_encode_horner_kernel(const uint16
             if (g >= nout) break;
             uint32_t o[NW][4];
 #pragma unroll
-            for (int n = 0; n < NW; ++n)
-#pragma unroll
-                for (int q = 0; q < 4; ++q) o[n][q] = acc[n][g][q];
+            for (int n = 0; n < NW; ++n) {
+                if (CHAINS) split_bytes(u32x4{acc[n][g][0], acc[n][g][1], acc[n][g][2], acc[n][g][3]}, o[n]);
+                else o[n][0] = acc[n][g][0], o[n][1] = acc[n][g][1], o[n][2] = acc[n][g][2], o[n][3] = acc[n][g][3];
+            }
             rs_h_store<NW>(stage, o, reinterpret_cast<uint8_t*>(par + uint64_t(og + g) * S) + t0b, nbytes);
         }
     }
+}
+
+// encode_rs_u16's parity rows og .. og + G - 1 (og = blockIdx.y * G; those at
+// or past m are computed and not stored).  in: the k data rows of S words;
+// par: parity row 0.
+template <int G, int NW>
+__global__ __launch_bounds__(kRsHBS) void rs16_encode_horner_kernel(const uint16_t* in, uint16_t* par, int64_t S,
+                                                                    int k, int m, const uint16_t* ex,
+                                                                    const uint16_t* lg) {
+    constexpr uint32_t TB = 16 * kRsHBS * NW;
+    __shared__ __attribute__((aligned(16))) uint32_t ptab[G][kRs16Tab];
+    __shared__ uint16_t basis[G][16];
+    __shared__ uint16_t coef[G];
+    __shared__ __attribute__((aligned(16))) uint8_t stage[TB + 16];
+    const int og = int(blockIdx.y) * G;
+    const int nout = m - og < G ? m - og : G;
+    // (the chains with eight parities held spilled SGPRs: m <= 6 only)
+    if constexpr (G <= kRsHChainMax) {
+        if (og == 0 && nout <= kRsHChainMax && table_word_s(ex, 1) == 2) {
+            const uint16_t red = uint16_t(table_word_s(ex, 16));   // 2^16 reduced
+            rs_h_encode_tiles<G, NW, true>(in, par, S, k, og, nout, ptab, uint32_t(red) * 0x10001u,
+                                           gf16_quad_table(red), stage);
+            return;
+        }
+    }
+    if (threadIdx.x < G) {
+        const int p = og + int(threadIdx.x);
+        coef[threadIdx.x] = p < m ? ex[uint32_t(p + 1) % kGfOrder] : uint16_t(0);
+    }
+    __syncthreads();
+    rs_build_perm_tables(ptab, basis, coef, G, ex, lg);
+    __syncthreads();
+    rs_h_encode_tiles<G, NW, false>(in, par, S, k, og, nout, ptab, 0u, Gf16Quad{0, 0}, stage);
 }
 
 // The inverse of V[r][c] = gf_exp[((pu_r + 1) miss_c) mod 65535] by
@@ -1701,10 +1740,17 @@ extern "C" int kvec_rs16_encode(const void* data_padded, void* shards, int data_
             hipLaunchKernelGGL(kern, dim3(rs_h_grid(S, TB), groups), dim3(kRsHBS), 0, st, in, par, S, data_shards,
                                parity_shards, gf_exp, gf_log);
         };
-        if (parity_shards <= 1) launch(rs16_encode_horner_kernel<1, 2>, 1);
-        else if (parity_shards <= 2) launch(rs16_encode_horner_kernel<2, 2>, 2);
-        else if (parity_shards <= 4) launch(rs16_encode_horner_kernel<4, 2>, 4);
-        else launch(rs16_encode_horner_kernel<kRsHMaxG, 2>, kRsHMaxG);
+        // one group of exactly m parities up to kRsHMaxG, else groups of kRsHMaxG
+        switch (parity_shards) {
+            case 1: launch(rs16_encode_horner_kernel<1, 2>, 1); break;
+            case 2: launch(rs16_encode_horner_kernel<2, 2>, 2); break;
+            case 3: launch(rs16_encode_horner_kernel<3, 2>, 3); break;
+            case 4: launch(rs16_encode_horner_kernel<4, 2>, 4); break;
+            case 5: launch(rs16_encode_horner_kernel<5, 2>, 5); break;
+            case 6: launch(rs16_encode_horner_kernel<6, 2>, 6); break;
+            case 7: launch(rs16_encode_horner_kernel<7, 2>, 7); break;
+            default: launch(rs16_encode_horner_kernel<kRsHMaxG, 2>, kRsHMaxG); break;
+        }
         return check_launch("kvec_rs16_encode");
     }
     RsJob j{};

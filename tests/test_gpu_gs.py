@@ -655,11 +655,15 @@ def test_rs16_encode_any_k_m(pkg, ora, gpu, k, m, S, doff, soff):
     assert bool((rest == 0x1234).all())
 
 
-def test_rs16_encode_any_k_m_other_generator(pkg, ora, gpu):
-    """Tables with generator 4: the per-output multiplier is gf_exp[p + 1]
-    of those tables, and the bytes are still the reference's for them."""
-    k, m, S = 12, 5, 5003
-    ex, lg = _gen4_tables(ora)
+@pytest.mark.parametrize("k,m,S,poly", [(12, 5, 5003, None), (20, 3, 4099, None), (25, 3, 2 * 8192 + 9, 0x18013),
+                                         (49, 1, 777, 0x18013)])
+def test_rs16_encode_any_k_m_other_generator(pkg, ora, gpu, k, m, S, poly):
+    """Tables with generator 4 (poly None): the per-output multiplier is
+    gf_exp[p + 1] of those tables, through its byte maps even where
+    generator-2 tables take doubling chains (m <= 4); and generator-2 tables
+    of x^16 + x^15 + x^4 + x + 1, whose reduction word has its top bit set,
+    through the chains.  The bytes are the reference's for those tables."""
+    ex, lg = _gen4_tables(ora) if poly is None else _poly_tables(poly)
     rng = np.random.default_rng(5)
     data = rng.integers(0, 65536, k * S, dtype=np.uint16)
     want = ora.rs16_encode(data, k, m, S, ex, lg)
