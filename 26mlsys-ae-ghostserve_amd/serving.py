@@ -319,18 +319,20 @@ class KVParityHook:
         self._pending.append((cid, dst, (t0, t1), (c0, c1), (h0, h1), P_h, Q_h))
 
     def _gather_rows(self, dist, mine, rows, dst, dev):
-        """Every rank's row to dst (bench_ghostserve_rdp.py:302-332).  gloo
+        """Every rank's row to dst (bench_ghostserve_rdp.py:302-332), as bytes:
+        neither gloo nor NCCL/RCCL has a 16-bit integer type.  gloo
         collectives take host tensors, copied synchronously both ways."""
         world = dist.get_world_size()
+        mine = mine.view(torch.uint8)
         if dist.get_backend() == "gloo":
             h = mine.cpu()
             glist = [torch.empty_like(h) for _ in range(world)] if rows is not None else None
             dist.gather(h, gather_list=glist, dst=dst)
             if rows is not None:
                 for r in range(world):
-                    rows[r].copy_(glist[r].to(dev))
+                    rows[r].view(torch.uint8).copy_(glist[r].to(dev))
         else:
-            glist = [rows[r] for r in range(world)] if rows is not None else None
+            glist = [rows[r].view(torch.uint8) for r in range(world)] if rows is not None else None
             dist.gather(mine, gather_list=glist, dst=dst)
 
     # ------------------------------------------------------------ records

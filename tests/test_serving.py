@@ -58,6 +58,51 @@ def test_chunk_counter_two_ranks_agree_and_rotate():
         assert out[0] == want and out[1] == want
 
 
+def _rows_rank(rank, world, port, out):
+    """The hook's exchange of one step: every rank's [K | V] row to the
+    rotating owner dst = (chunk_id - 1) % world (bench_ghostserve_rdp.py:
+    302-332), over gloo with host tensors; three chunks, so the owner moves."""
+    import torch.distributed as dist
+    dist.init_process_group("gloo", init_method=f"tcp://127.0.0.1:{port}", rank=rank,
+                            world_size=world)
+    try:
+        serving = load_pkg().serving
+        hook = serving.KVParityHook(star_base=0, metrics_file=None)
+        got = []
+        for _ in range(3):
+            cid, dst = hook.counter.next(torch.device("cpu"))
+            S = 6
+            mine = torch.arange(S, dtype=torch.int16) + 100 * (rank + 1) + cid
+            rows = torch.full((world + 2, S), -1, dtype=torch.int16) if rank == dst else None
+            hook._gather_rows(dist, mine, rows, dst, torch.device("cpu"))
+            got.append((cid, dst, rows[:world].tolist() if rows is not None else None))
+        out[rank] = got
+    finally:
+        dist.destroy_process_group()
+
+
+def test_row_exchange_two_ranks_reaches_the_rotating_owner():
+    with socket.socket() as s:
+        s.bind(("127.0.0.1", 0))
+        port = s.getsockname()[1]
+    ctx = mp.get_context("spawn")
+    with ctx.Manager() as m:
+        out = m.dict()
+        procs = [ctx.Process(target=_rows_rank, args=(r, 2, port, out)) for r in range(2)]
+        for p in procs:
+            p.start()
+        for p in procs:
+            p.join(120)
+            assert p.exitcode == 0
+        for cid in (1, 2, 3):
+            dst = (cid - 1) % 2
+            want = [[100 * (r + 1) + cid + i for i in range(6)] for r in range(2)]
+            for rank in range(2):
+                c, d, rows = out[rank][cid - 1]
+                assert (c, d) == (cid, dst)
+                assert rows == (want if rank == dst else None), (cid, rank)
+
+
 class _Hook:
     def __init__(self, fail=False):
         self.calls, self.fail = [], fail
