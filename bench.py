@@ -538,7 +538,49 @@ def bench_chunked(pkg, torch, oracle, dev, seed, warmup):
         del ref, ref_sh
     cpu_case = (host(pool).reshape(CL, npages, page_tokens, 2, -1), table.cpu().numpy(), page_tokens,
                 ct, k, p, m, W, U)
-    del st, pool, kvs
+    del st, kvs
+
+    # the same pool coded as 8 chunks of 4096 tokens: a launch moves twice the
+    # bytes, so its ramp and tail weigh half as much per token; checked by a
+    # full-size round trip (3 data shards of one chunk erased in the pool,
+    # decoded back, pool compared)
+    ct2, nch2 = 2 * ct, NCH // 2
+    kvs2 = [pkg.chunked.chunk_kv(pool, table, c, ct2) for c in range(nch2)]
+    st2 = pkg.chunked.ChunkedStripes(kvs2[0].stream_bytes(), 2 * kvs2[0].token_bytes, nch2, dev, k=k, p=p,
+                                     m=m, keep_data=False)
+    alg2 = kvs2[0].stream_bytes() + (2 + m) * st2.region_bytes
+    for c in range(nch2):
+        st2.encode(kvs2[c], c)
+    ref = pool.view(torch.uint8).clone()
+    sbytes = kvs2[1].gather()
+    for e in (0, 2, 4):
+        sbytes[e * st2.region_bytes:min((e + 1) * st2.region_bytes, sbytes.numel())] = 0
+    kvs2[1].scatter(sbytes)
+    del sbytes
+    st2.decode(kvs2[1], 1, [0, 2, 4])
+    torch.cuda.synchronize()
+    if not torch.equal(pool.view(torch.uint8), ref):
+        raise RuntimeError("chunked decode at 4096-token chunks: pool not restored")
+    del ref
+    for _ in range(warmup):
+        for c in range(nch2):
+            st2.encode(kvs2[c], c)
+    ev2 = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+    ev2[0].record(stream)
+    for _ in range(PASSES):
+        for c in range(nch2):
+            st2.encode(kvs2[c], c)
+    ev2[1].record(stream)
+    torch.cuda.synchronize()
+    enc2_us = ev2[0].elapsed_time(ev2[1]) * 1e3 / (nch2 * PASSES)
+    longer = {
+        "chunk_tokens": ct2, "chunks": nch2, "alg_bytes_per_chunk": alg2,
+        "encode_us_per_chunk": round(enc2_us, 2),
+        "encode_us_per_2048_tokens": round(enc2_us * ct / ct2, 2),
+        "encode_frac_hbm_peak": frac(alg2, enc2_us),
+        "round_trip_byte_exact": True,
+    }
+    del st2, kvs2, pool
     return {
         "workload": "chunked_fp8_rdp_p7_k5_rs_k5m3_16x32768tok_16chunks",
         "chunk_tokens": ct, "chunks": NCH, "chunk_stream_bytes": chunk_bytes,
@@ -555,6 +597,7 @@ def bench_chunked(pkg, torch, oracle, dev, seed, warmup):
         "decode_us": dec,
         "decode_byte_exact": True,
         "parity_offload": offload,
+        "encode_at_4096_token_chunks": longer,
     }, cpu_case
 
 
@@ -1242,7 +1285,8 @@ def main():
         chunked, chunk_case = bench_chunked(pkg, torch, oracle, dev, args.seed,
                                             max(1, args.warmup // 2))
         log(f"[bench] chunked: {chunked['encode_us_per_chunk']:.1f} us/chunk "
-            f"({chunked['encode_gbs']:.0f} GB/s), decode {chunked['decode_us']}")
+            f"({chunked['encode_gbs']:.0f} GB/s), decode {chunked['decode_us']}; at 4096-token chunks "
+            f"{chunked['encode_at_4096_token_chunks']['encode_us_per_2048_tokens']:.1f} us per 2048 tokens")
         torch.cuda.empty_cache()
 
     rs8, rs8_host = None, None
