@@ -69,6 +69,16 @@ __device__ __forceinline__ uint32_t table_word_s(const uint16_t* tab, uint32_t i
     return (a & 2) ? (w >> 16) : (w & 0xFFFFu);
 }
 
+// The rule by which every GF(2^16) kernel here chooses Horner's rule (each
+// multiplication by 2 a shift and an XOR of the reduction word) over the byte
+// maps: the tables' generator is 2 (gf_exp[1] == 2), and the reduction word is
+// gf_exp[16] = 2^16 in the field.  For any field's exp/log pair with generator
+// 2 this is exactly the tables' multiplication, so both ways give the same
+// bytes; and since every kernel applies the same test, the kernel that serves a
+// call's shape never decides which way its bytes are computed.
+__device__ __forceinline__ bool horner_tables(const uint16_t* ex) { return table_word_s(ex, 1) == 2; }
+__device__ __forceinline__ uint32_t horner_red2(const uint16_t* ex) { return table_word_s(ex, 16) * 0x10001u; }
+
 struct RsJob {
     const uint16_t* in_rows[kRsMaxTables];  // k input rows (u16, logical column 0)
     uint16_t* out_rows[kRsMaxM];            // output rows
@@ -510,25 +520,9 @@ __global__ __launch_bounds__(kRsBS) __attribute__((amdgpu_waves_per_eu(4))) void
     }
     __syncthreads();
     rs_build_perm_tables(ptab, basis, coef, j.nout * j.nin, ex, lg);
-    // Horner's order when every basis product c(p, i) * 2^b the tables give
-    // equals 2^b doubled (p + 1) i times, the reduction word being 0x8000 * 2
-    // from the tables.
-    __shared__ int s_horner;
-    __shared__ uint16_t s_red;
-    if (threadIdx.x == 0) {
-        s_red = gf16_mul_tab(0x8000, 2, ex, lg);
-        s_horner = j.nout <= kRsGroup;
-    }
-    __syncthreads();
-    for (int e = threadIdx.x; e < j.nout * j.nin * 16; e += kRsBS) {
-        const int t = e >> 4, b = e & 15;
-        const int p = t / j.nin, i = t % j.nin;
-        uint16_t v = uint16_t(1u << b);
-        for (int d = 0; d < (p + 1) * i; ++d) v = gf16_dbl(v, s_red);
-        if (v != basis[t][b]) s_horner = 0;
-    }
-    __syncthreads();
-    if (s_horner) rs_run_tiles<true, kRsEncNT>(j, ptab, tile, uint32_t(s_red) * 0x10001u);
+    __syncthreads();   // the maps, written by every thread, before any use
+    // Horner's order by horner_tables (up to kRsGroup parities)
+    if (j.nout <= kRsGroup && horner_tables(ex)) rs_run_tiles<true, kRsEncNT>(j, ptab, tile, horner_red2(ex));
     else rs_run_tiles<false, kRsEncNT>(j, ptab, tile, 0u);
 }
 
@@ -779,8 +773,6 @@ __global__ __launch_bounds__(kPieceBS) __attribute__((amdgpu_waves_per_eu(4))) v
     // the folded coefficients (M * NIN), then those of the inverse (M * M)
     __shared__ __attribute__((aligned(16))) uint32_t ptab[M * NIN + M * M][kRs16Tab];
     __shared__ RsRecPlan pl;
-    __shared__ int s_horner;
-    __shared__ uint16_t s_red;
     rs16_rec_rows(pl, NIN, mpar, M, missing, pused);
     if (!pl.ok) return;
     const __amdgpu_buffer_rsrc_t rs = chunk_rsrc(base_al, res_bytes);
@@ -803,25 +795,11 @@ __global__ __launch_bounds__(kPieceBS) __attribute__((amdgpu_waves_per_eu(4))) v
     }
     rs16_rec_tables(pl, ptab, NIN, M, ex, lg);
     rs_build_perm_tables(ptab + M * NIN, pl.basis, pl.inv, M * M, ex, lg);
-    // Horner's rule when every coefficient alpha^((pu_r + 1) i) of a surviving
-    // data row, as the caller's tables multiply by it, equals its chain of
-    // doublings on all sixteen basis symbols
-    if (threadIdx.x == 0) {
-        s_red = gf16_mul_tab(0x8000, 2, ex, lg);
-        s_horner = 1;
-    }
+    // syndromes by Horner's rule by horner_tables (the barrier after the
+    // tables orders them before their use)
     __syncthreads();
-    for (int e = threadIdx.x; e < M * ND * 16; e += kPieceBS) {
-        const int r = e / (ND * 16), j = (e >> 4) % ND, b = e & 15;
-        const int n = (pl.pu[r] + 1) * pl.in_row[j];
-        const uint16_t cf = ex[n % kGfOrder];
-        uint16_t v = uint16_t(1u << b);
-        for (int d = 0; d < n; ++d) v = gf16_dbl(v, s_red);
-        if (v != gf16_mul_tab(uint16_t(1u << b), cf, ex, lg)) s_horner = 0;
-    }
-    __syncthreads();
-    const bool horner = __builtin_amdgcn_readfirstlane(s_horner) != 0;
-    const uint32_t red2 = uint32_t(s_red) * 0x10001u;
+    const bool horner = horner_tables(ex);
+    const uint32_t red2 = horner_red2(ex);
     uint32_t dbl[M][NIN];
 #pragma unroll
     for (int r = 0; r < M; ++r) {
@@ -933,7 +911,7 @@ __global__ __launch_bounds__(kTB) void rs16_encode_tiles_kernel(const uint8_t* i
         const uint32_t mis = uint32_t(reinterpret_cast<uintptr_t>(fc.src + o) & 15);
         if (mis && b < 16 - mis && b < Sb) as_global(fc.dst)[o + b] = as_global(fc.src)[o + b];
     }
-    const bool horner = table_word_s(ex, 1) == 2;
+    const bool horner = horner_tables(ex);
     const uint16_t red = uint16_t(table_word_s(ex, 16));   // g^16 = 2^16 reduced, when g = 2
     const uint32_t red2 = uint32_t(red) * 0x10001u;
     const Gf16Quad quad = gf16_quad_table(red);
@@ -1077,7 +1055,7 @@ __global__ __launch_bounds__(BS) void rs16_reconstruct_tiles_kernel(uint8_t* bas
         }
         if (M == 2) ok = ok && miss[0] != miss[M - 1];
         if (!ok) return;   // uniform: the whole grid writes nothing
-        const bool horner = table_word_s(ex, 1) == 2;
+        const bool horner = horner_tables(ex);
         const int m_lo = M == 2 ? min(miss[0], miss[M - 1]) : miss[0];
         const int m_hi = M == 2 ? max(miss[0], miss[M - 1]) : NIN;
         uint32_t rowp = 0;   // the surviving data rows, 4 bits each
@@ -1467,7 +1445,7 @@ __global__ __launch_bounds__(kRsHBS) void rs16_encode_horner_kernel(const uint16
     const int nout = m - og < G ? m - og : G;
     // (the chains with eight parities held spilled SGPRs: m <= 6 only)
     if constexpr (G <= kRsHChainMax) {
-        if (og == 0 && nout <= kRsHChainMax && table_word_s(ex, 1) == 2) {
+        if (og == 0 && nout <= kRsHChainMax && horner_tables(ex)) {
             const uint16_t red = uint16_t(table_word_s(ex, 16));   // 2^16 reduced
             rs_h_encode_tiles<G, NW, true>(in, par, S, k, og, nout, ptab, uint32_t(red) * 0x10001u,
                                            gf16_quad_table(red), stage);
