@@ -91,6 +91,7 @@ SIGNATURES = {
     "kvec_gs_rdp_recover": (_i, [_vp, _vp, _i, _i, _i, _i, _i, _i, _i, _vp]),
     "kvec_gs_pack_row": (_i, [_vp, _vp, _vp, _i64, _i, _i64, _vp]),
     "kvec_gs_rdp_parity": (_i, [_vp, _i, _i, _i, _vp]),
+    "kvec_hook_step": (_i, [_kvp, _vp, _vp, _i, _i, _i, _i, _vp, _vp, _vp, _vp, _pp]),
     "kvec_rs16_pack": (_i, [_vp, _vp, _vp, _i64, _i64, _vp]),
     "kvec_rs16_split": (_i, [_vp, _vp, _vp, _i64, _i64, _vp]),
     "kvec_rs16_encode": (_i, [_vp, _vp, _i, _i, _i, _vp, _vp, _vp]),

@@ -30,6 +30,9 @@ What differs:
     record is written once that copy has finished (checked at the next step
     or at ``flush()``), instead of a device-wide synchronize per chunk; its
     gpu_to_cpu_ms is the copy's own duration on the GPU;
+  * the step's device work (slot upload, gather, P/Q, the copy and the
+    events that time them) is enqueued by one native call, kvec_hook_step,
+    over buffers and events made once per step shape;
   * the H2D "probe" copy is made only when asked for (``probe_h2d=True``);
   * any backend with ``forward_extend`` is hooked, not only FlashInfer's
     (ROCm serving backends are not FlashInfer).
@@ -40,6 +43,7 @@ Q's share) per rank.
 """
 from __future__ import annotations
 
+import ctypes
 import functools
 import json
 import math
@@ -47,9 +51,10 @@ import os
 import time
 from typing import Callable, Optional
 
+import numpy as np
 import torch
 
-from . import paged, rdp_kv_ops
+from . import _lib, paged
 
 
 def _dist():
@@ -85,104 +90,86 @@ class ChunkCounter:
 
 class MetricsLog:
     """Append-only JSONL file (bench_ghostserve_rdp.py:232-244); no file, no
-    output."""
+    output.  The reference opens the file for every record; here it stays
+    open in append mode and each line is flushed as it is written, so a
+    reader sees the same file, without an open and a close per chunk."""
 
     def __init__(self, path: Optional[str]):
         self.path = path
+        self._f = None
 
     def append(self, entry: dict) -> None:
         if not self.path:
             return
-        with open(self.path, "a", encoding="utf-8") as f:
-            f.write(json.dumps(entry) + "\n")
+        if self._f is None:
+            self._f = open(self.path, "a", encoding="utf-8")
+        self._f.write(json.dumps(entry) + "\n")
+        self._f.flush()
+
+    def close(self) -> None:
+        if self._f is not None:
+            self._f.close()
+            self._f = None
+
+    def __del__(self):
+        self.close()
 
 
 class _StepPlan:
     """Resources of one step shape (active slots, heads, head_dim, dtype,
-    pool, group size, star_base), reused while the shape repeats: two row
-    buffers [world + 2, S] used in turn and, with graphs, a static slot
-    buffer, the paged-gather descriptor over it and one HIP graph per row
-    buffer for the gather of this rank's delta and one for P/Q.
+    pool, group size, rank, star_base), made once and reused while the shape
+    repeats:
 
-    A step's P/Q rows are read by its host copies on the side stream, so
-    before a buffer is written again (two steps later) the current stream
-    waits, on the device, for the event that marks those copies done."""
+      * two row buffers [world + 2, S], used in turn;
+      * the device slot buffer, the paged-gather descriptor over it, and two
+        pinned staging buffers for slot maps given on the host;
+      * a ring of pinned [2, S] buffers for the copies of P and Q, each with
+        the four events of its step (P/Q start and end, copy start and end).
 
-    def __init__(self, kv_pool: torch.Tensor, n: int, world: int, rank: int, star_base: int,
-                 graphs: bool):
+    A step's P/Q rows are read by its copy on the side stream, so before a row
+    buffer is written again (two steps later) the current stream waits, on the
+    device, for the event that marks that copy done; and a step's slots are
+    uploaded from a staging buffer that is refilled only after that upload."""
+
+    RING = 4
+
+    def __init__(self, kv_pool: torch.Tensor, n: int, world: int, rank: int, star_base: int):
         dev = kv_pool.device
         T, _, H, D = kv_pool.shape
-        self.world, self.rank, self.star_base = world, rank, star_base
+        self.world, self.rank, self.star_base, self.n = world, rank, star_base, n
         self.elems = n * H * D          # words of K (and of V) in one rank's delta
         self.S = 2 * self.elems         # words per row: K then V
         self.rows = [torch.empty((world + 2, self.S), dtype=torch.int16, device=dev) for _ in range(2)]
-        self.pool6 = kv_pool.view(1, T, 1, 2, H, D)
-        self.n = n
-        if graphs:
-            self.slots = torch.empty(n, dtype=torch.int32, device=dev)
-            self.kv = paged.PagedKV(self.pool6, self.slots.view(1, n), 0, n)
-        self.freed = [None, None]
-        self.graphs = graphs
-        self.g_gather = [None, None]
-        self.g_parity = [None, None]
+        self.slots = torch.empty(n, dtype=torch.int32, device=dev)
+        self.kv = paged.PagedKV(kv_pool.view(1, T, 1, 2, H, D), self.slots.view(1, n), 0, n)
+        self.staging = [torch.empty(n, dtype=torch.int32, pin_memory=True) for _ in range(2)]
+        self.staging_np = [t.numpy() for t in self.staging]
+        self.staged = [None, None]      # event after the upload out of staging[i]
+        self.pq = [torch.empty((2, self.S), dtype=torch.int16, pin_memory=True) for _ in range(self.RING)]
+        self.events = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(self.RING)]
+        self.stage_ev = [torch.cuda.Event() for _ in range(2)]
+        for e in [x for ev in self.events for x in ev] + self.stage_ev:
+            e.record()                  # the HIP events exist from here on: the step records them by handle
+        self.ev_args = [(ctypes.c_void_p * 4)(*[e.cuda_event for e in ev]) for ev in self.events]
+        self.busy = [False] * self.RING  # ring slot of a step whose record is not written yet
+        self.slot = 0
+        self.freed = [None, None]       # copy-done event of each row buffer's last step
         self.turn = 0
-
-    def _gather(self, b: int, kv: paged.PagedKV):
-        mine = self.rows[b][self.rank]
-        kv.gather_split(mine[:self.elems], mine[self.elems:])
-
-    def _parity(self, b: int):
-        rdp_kv_ops.compute_rdp_parity(self.rows[b].view(torch.uint16), self.world, self.S, self.star_base)
-
-    def _replay(self, which: list, fn, b: int):
-        if which[b] is None:
-            # captured on torch.cuda.graph's side stream; replays are ordered
-            # on the current one
-            g = torch.cuda.CUDAGraph()
-            with torch.cuda.graph(g):
-                fn(b)
-            which[b] = g
-        which[b].replay()
-
-    def begin(self, active: torch.Tensor) -> int:
-        """Take the next row buffer (after the host copies that last read
-        it) and, with graphs, load this step's slots; returns the buffer."""
-        b = self.turn
-        self.turn ^= 1
-        if self.freed[b] is not None:
-            torch.cuda.current_stream(active.device).wait_event(self.freed[b])
-        self.active = active
-        if self.graphs:
-            self.slots.copy_(active, non_blocking=True)
-        return b
-
-    def gather(self, b: int):
-        if self.graphs:
-            self._replay(self.g_gather, lambda bb: self._gather(bb, self.kv), b)
-        else:
-            self._gather(b, paged.PagedKV(self.pool6, self.active.view(1, self.n), 0, self.n))
-
-    def parity(self, b: int):
-        if self.graphs:
-            self._replay(self.g_parity, self._parity, b)
-        else:
-            self._parity(b)
 
 
 class KVParityHook:
     """Per-step parity of the KV delta; call :meth:`on_extend` after each
     ``forward_extend`` (or let :func:`install` do it).
 
-    ``graphs``: replay each step's gather and P/Q kernels from HIP graphs
-    captured once per step shape (the first step of a shape captures them)
-    instead of launching them through the C calls.  Off by default: on
-    MI355X with torch 2.10 a graph replay costs the host about as much as
-    the two launches it replaces, plus a device copy of the slots, and the
-    owner's step at TP8 took 219 against 203 us per step."""
+    A step is one native call (kvec_hook_step) that enqueues the slot upload,
+    the gather of this rank's delta into its row, P/Q and the copy of P and Q
+    to pinned host memory, with the events the JSONL timings come from; the
+    plan of a step shape (buffers, descriptor, events) is made once.
+    ``last_parity`` holds (P, Q) of the newest chunk whose record was written:
+    host tensors that stay valid for the next RING - 1 steps of that shape."""
 
     def __init__(self, star_base: Optional[int] = None, metrics_file: Optional[str] = None,
-                 prog_start_mono: Optional[float] = None, probe_h2d: bool = False,
-                 graphs: bool = False):
+                 prog_start_mono: Optional[float] = None, probe_h2d: bool = False):
         env = os.environ
         self.star_base = int(env.get("RDP_STAR_BASE", "0")) if star_base is None else int(star_base)
         self.metrics = MetricsLog(env.get("FT_METRICS_FILE") if metrics_file is None else metrics_file)
@@ -190,7 +177,6 @@ class KVParityHook:
             prog_start_mono = float(env.get("FT_PROG_START_MONO", "nan"))
         self.prog_start_mono = prog_start_mono
         self.probe_h2d = probe_h2d
-        self.graphs = graphs
         self.counter = ChunkCounter()
         self.first_chunk_wall_ms: Optional[float] = None
         self._stream: Optional[torch.cuda.Stream] = None
@@ -207,18 +193,18 @@ class KVParityHook:
             raise ValueError("kv_pool must be contiguous")
 
     @staticmethod
-    def _active(slot_mapping, dev) -> torch.Tensor:
-        """The slots written this step (-1 entries dropped), int32 on the
-        device.  The count is needed on the host (it sizes the rows), so a
-        device slot_mapping costs one synchronization here, as in the
-        reference (bench_ghostserve_rdp.py:449-451); a host one costs none."""
-        slots = torch.as_tensor(slot_mapping).reshape(-1)
-        if slots.device.type == "cpu":
-            # pinned, so the upload is queued behind the device's work
-            # instead of waiting for it
-            return slots[slots != -1].to(torch.int32).pin_memory().to(dev, non_blocking=True)
-        slots = slots.to(dev)
-        return slots[slots != -1].to(torch.int32)
+    def _active(slot_mapping):
+        """The slots written this step (-1 entries dropped): an int32 device
+        tensor for a device slot_mapping, an int32 numpy array otherwise.  The
+        count is needed on the host (it sizes the rows), so a device
+        slot_mapping costs one synchronization here, as in the reference
+        (bench_ghostserve_rdp.py:449-451); a host one costs none."""
+        if isinstance(slot_mapping, torch.Tensor) and slot_mapping.device.type != "cpu":
+            slots = slot_mapping.reshape(-1)
+            return slots[slots != -1].to(torch.int32)
+        a = slot_mapping.numpy() if isinstance(slot_mapping, torch.Tensor) else np.asarray(slot_mapping)
+        a = a.reshape(-1)
+        return a[a != -1].astype(np.int32, copy=False)
 
     MAX_PLANS = 8   # step shapes kept (prefill chunks of a few sizes repeat)
 
@@ -229,14 +215,69 @@ class KVParityHook:
             if len(self._plans) >= self.MAX_PLANS:
                 # the least recently used shape: its rows go back to the
                 # allocator only once the copies queued on the side stream
-                # have read them
+                # have read them (its host buffers stay referenced by the
+                # pending records)
                 old = self._plans.pop(next(iter(self._plans)))
                 if self._stream is not None:
                     for r in old.rows:
                         r.record_stream(self._stream)
-            plan = _StepPlan(kv_pool, n, world, rank, self.star_base, self.graphs)
+            plan = _StepPlan(kv_pool, n, world, rank, self.star_base)
         self._plans[key] = plan   # most recently used last
         return plan
+
+    def _begin(self, plan: _StepPlan, act):
+        """Take the next row buffer and stage this step's slots: a host array
+        goes to a pinned staging buffer (refilled only once its last upload
+        has run), a device tensor straight into the plan's slot buffer.
+        Returns the row buffer and the staging buffer's address (None)."""
+        b = plan.turn
+        plan.turn ^= 1
+        if isinstance(act, np.ndarray):
+            if plan.staged[b] is not None:
+                plan.staged[b].synchronize()
+            plan.staging_np[b][:] = act
+            return b, plan.staging[b].data_ptr()
+        plan.slots.copy_(act)
+        return b, None
+
+    def _issue(self, plan: _StepPlan, b: int, staging, gather: bool, code: bool, cid: int, dst: int):
+        """One kvec_hook_step: [the wait for the row buffer, the slot upload
+        and the gather of this rank's row] and/or [P/Q and their copy to the
+        next pinned ring buffer on the side stream]."""
+        dev = plan.rows[b].device
+        stream = torch.cuda.current_stream(dev).cuda_stream
+        pq = side = evs = None
+        if code:
+            if self._stream is None:
+                self._stream = torch.cuda.Stream(device=dev)
+            s = plan.slot
+            plan.slot = (s + 1) % plan.RING
+            if plan.busy[s]:
+                # the ring came round to a step whose record is not written
+                plan.events[s][3].synchronize()
+                self.poll()
+            pq, side, evs = plan.pq[s].data_ptr(), self._stream.cuda_stream, plan.ev_args[s]
+        freed = plan.freed[b] if gather else None
+        _lib.call("kvec_hook_step", plan.kv.c if gather else None, staging, plan.rows[b].data_ptr(), plan.rank,
+                  plan.world, plan.S, plan.star_base, pq, stream, side,
+                  freed.cuda_event if freed is not None else None, evs)
+        if staging is not None:
+            plan.stage_ev[b].record()
+            plan.staged[b] = plan.stage_ev[b]
+        if not code:
+            return
+        plan.busy[s] = True
+        plan.freed[b] = plan.events[s][3]
+        h = None
+        if self.probe_h2d:
+            # the reference's device-host-device round trip of P/Q (:370-374)
+            h = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+            with torch.cuda.stream(self._stream):
+                probe = torch.empty((2, plan.S), dtype=torch.int16, device=dev)
+                h[0].record(self._stream)
+                probe.copy_(plan.pq[s], non_blocking=True)
+                h[1].record(self._stream)
+        self._pending.append((cid, dst, plan, s, h))
 
     def on_extend(self, kv_pool: torch.Tensor, slot_mapping) -> Optional[int]:
         """Code this step's delta.  ``kv_pool``: [max_tokens, 2, kv_heads,
@@ -245,8 +286,8 @@ class KVParityHook:
         self.poll()
         self._check_pool(kv_pool)
         dev = kv_pool.device
-        active = self._active(slot_mapping, dev)
-        n = int(active.numel())
+        act = self._active(slot_mapping)
+        n = int(act.shape[0])
         if n == 0:
             return None
         cid, dst = self.counter.next(dev)
@@ -256,12 +297,14 @@ class KVParityHook:
         world = dist.get_world_size() if dist is not None else 1
         rank = dist.get_rank() if dist is not None else 0
         plan = self._plan(kv_pool, n, world, rank)
-        b = plan.begin(active)
-        plan.gather(b)
-        if world > 1:
-            self._gather_rows(dist, plan.rows[b][rank], plan.rows[b] if rank == dst else None, dst, dev)
+        b, staging = self._begin(plan, act)
+        if world == 1:
+            self._issue(plan, b, staging, True, True, cid, dst)
+            return cid
+        self._issue(plan, b, staging, True, False, cid, dst)
+        self._gather_rows(dist, plan.rows[b][rank], plan.rows[b] if rank == dst else None, dst, dev)
         if rank == dst:
-            self._code_owner(plan, b, cid, dst)
+            self._issue(plan, b, None, False, True, cid, dst)
         return cid
 
     def step_as_owner(self, kv_pool: torch.Tensor, slot_mapping, world: int) -> Optional[int]:
@@ -273,50 +316,15 @@ class KVParityHook:
         owner's step at a real group size."""
         self.poll()
         self._check_pool(kv_pool)
-        active = self._active(slot_mapping, kv_pool.device)
-        n = int(active.numel())
+        act = self._active(slot_mapping)
+        n = int(act.shape[0])
         if n == 0:
             return None
         self.counter.count += 1
         plan = self._plan(kv_pool, n, int(world), 0)
-        b = plan.begin(active)
-        plan.gather(b)
-        self._code_owner(plan, b, self.counter.count, 0)
+        b, staging = self._begin(plan, act)
+        self._issue(plan, b, staging, True, True, self.counter.count, 0)
         return self.counter.count
-
-    def _code_owner(self, plan: _StepPlan, b: int, cid: int, dst: int) -> None:
-        """P/Q of the row buffer and their copy to pinned host memory on a
-        side stream (the two rows are adjacent: one copy); the JSONL record
-        waits for that copy."""
-        dev = plan.rows[b].device
-        rows, world, S = plan.rows[b], plan.world, plan.S
-        t0 = torch.cuda.Event(enable_timing=True)
-        t1 = torch.cuda.Event(enable_timing=True)
-        t0.record()
-        plan.parity(b)
-        t1.record()
-        # P/Q to pinned host memory on a side stream, after the parity kernel
-        if self._stream is None:
-            self._stream = torch.cuda.Stream(device=dev)
-        PQ_h = torch.empty((2, S), dtype=torch.int16, pin_memory=True)
-        P_h, Q_h = PQ_h[0], PQ_h[1]
-        c0 = torch.cuda.Event(enable_timing=True)
-        c1 = torch.cuda.Event(enable_timing=True)
-        self._stream.wait_event(t1)
-        with torch.cuda.stream(self._stream):
-            c0.record(self._stream)
-            PQ_h.copy_(rows[world:world + 2], non_blocking=True)
-            c1.record(self._stream)
-            h0 = h1 = None
-            if self.probe_h2d:
-                h0 = torch.cuda.Event(enable_timing=True)
-                h1 = torch.cuda.Event(enable_timing=True)
-                probe = torch.empty((2, S), dtype=torch.int16, device=dev)
-                h0.record(self._stream)
-                probe.copy_(PQ_h, non_blocking=True)
-                h1.record(self._stream)
-        plan.freed[b] = c1
-        self._pending.append((cid, dst, (t0, t1), (c0, c1), (h0, h1), P_h, Q_h))
 
     def _gather_rows(self, dist, mine, rows, dst, dev):
         """Every rank's row to dst (bench_ghostserve_rdp.py:302-332), as bytes:
@@ -341,27 +349,29 @@ class KVParityHook:
         them with ``wait``); returns how many were written."""
         done = 0
         while self._pending:
-            cid, dst, enc, d2h, h2d, P_h, Q_h = self._pending[0]
-            last = h2d[1] if h2d[1] is not None else d2h[1]
+            cid, dst, plan, s, h = self._pending[0]
+            ev = plan.events[s]
+            last = h[1] if h is not None else ev[3]
             if wait:
                 last.synchronize()
             elif not last.query():
                 break
             self._pending.pop(0)
-            self.last_parity = (P_h, Q_h)
-            self.metrics.append({
-                "chunk_id": int(cid),
-                "dst_rank": int(dst),
-                "first_chunk_wall_ms": self.first_chunk_wall_ms,
-                "timings": {
-                    "rdp_encode_ms": float(enc[0].elapsed_time(enc[1])),
-                    "rdp_decode_ms": None,
-                    "gpu_to_cpu_ms": float(d2h[0].elapsed_time(d2h[1])),
-                    "cpu_to_gpu_ms": (float(h2d[0].elapsed_time(h2d[1]))
-                                      if h2d[0] is not None else None),
-                    "parity_bytes": int(2 * P_h.numel() * 2),
-                },
-            })
+            plan.busy[s] = False
+            self.last_parity = (plan.pq[s][0], plan.pq[s][1])
+            if self.metrics.path:
+                self.metrics.append({
+                    "chunk_id": int(cid),
+                    "dst_rank": int(dst),
+                    "first_chunk_wall_ms": self.first_chunk_wall_ms,
+                    "timings": {
+                        "rdp_encode_ms": float(ev[0].elapsed_time(ev[1])),
+                        "rdp_decode_ms": None,
+                        "gpu_to_cpu_ms": float(ev[2].elapsed_time(ev[3])),
+                        "cpu_to_gpu_ms": float(h[0].elapsed_time(h[1])) if h is not None else None,
+                        "parity_bytes": int(2 * plan.S * 2),
+                    },
+                })
             done += 1
         return done
 

@@ -938,9 +938,10 @@ def bench_hook(pkg, torch, oracle, dev, seed, steps=100, warmup=10):
     row, P/Q of the 8 rows, the pinned copies to the host, and the JSONL
     timings the reference records (rdp_encode_ms, gpu_to_cpu_ms;
     bench_ghostserve_rdp.py:334-392).  The other 7 rows stand for the rows the
-    exchange brings.  Eager C calls against HIP graphs replayed per shape,
-    with the slot mapping on the device (one synchronization per step for
-    its length, as in the reference) and on the host (none)."""
+    exchange brings.  The step is one native call (kvec_hook_step), with the
+    slot mapping on the device (one synchronization per step for its
+    length, as in the reference) and on the host (none); beside it, the
+    reference's own sequence of torch calls on this GPU."""
     import json as _json
     import tempfile
     import numpy as np
@@ -953,51 +954,54 @@ def bench_hook(pkg, torch, oracle, dev, seed, steps=100, warmup=10):
     dslots = [torch.from_numpy(x).to(dev) for x in slot_sets]
     hslots = [torch.from_numpy(x) for x in slot_sets]
     out = {"world": world, "tokens": NTOK, "rows": [world + 2, 2 * NTOK * H * D], "kv_dtype": "bf16"}
-    for graphs in (False, True):
-        tag = "graph" if graphs else "eager"
-        with tempfile.TemporaryDirectory() as tmp:
-            path = os.path.join(tmp, "m.jsonl")
-            hook = pkg.serving.KVParityHook(star_base=0, metrics_file=path, graphs=graphs)
+    with tempfile.TemporaryDirectory() as tmp:
+        path = os.path.join(tmp, "m.jsonl")
+        hook = pkg.serving.KVParityHook(star_base=0, metrics_file=path)
+        for i in range(warmup):
+            hook.step_as_owner(pool, dslots[i % 8], world)
+        hook.flush()
+        plan = next(iter(hook._plans.values()))
+        for b in range(2):
+            plan.rows[b][1:world].copy_(torch.randint(-32768, 32767, (world - 1, plan.S), generator=g,
+                                                      device=dev, dtype=torch.int16))
+        torch.cuda.synchronize()
+        res = {}
+        for kind, sl in (("device_slots", dslots), ("host_slots", hslots)):
             for i in range(warmup):
-                hook.step_as_owner(pool, dslots[i % 8], world)
+                hook.step_as_owner(pool, sl[i % 8], world)
             hook.flush()
-            plan = next(iter(hook._plans.values()))
-            for b in range(2):
-                plan.rows[b][1:world].copy_(torch.randint(-32768, 32767, (world - 1, plan.S), generator=g,
-                                                          device=dev, dtype=torch.int16))
             torch.cuda.synchronize()
-            open(path, "w").close()
-            res = {}
-            for kind, sl in (("device_slots", dslots), ("host_slots", hslots)):
-                torch.cuda.synchronize()
-                t0 = time.perf_counter()
-                for i in range(steps):
-                    hook.step_as_owner(pool, sl[i % 8], world)
-                t1 = time.perf_counter()
-                torch.cuda.synchronize()
-                t2 = time.perf_counter()
-                hook.flush()
-                res[kind] = {"issue_us_per_step": round((t1 - t0) * 1e6 / steps, 2),
-                             "us_per_step": round((t2 - t0) * 1e6 / steps, 2)}
-            recs = [_json.loads(x) for x in open(path).read().splitlines()]
-            # the last step checked against the oracle's P/Q of the buffer's rows
-            b = plan.turn ^ 1
-            rows_h = plan.rows[b].cpu().numpy().view(np.uint16).copy()
-            P, Q = hook.last_parity
-            want = rows_h.copy()
-            want[world:] = 0
-            oracle.gs_parity(want, world, plan.S, 0)
-            host_pool = pool.view(torch.int16).cpu().numpy().view(np.uint16)
-            last = slot_sets[(steps - 1) % 8]
-            own = np.concatenate([host_pool[last, 0].reshape(-1), host_pool[last, 1].reshape(-1)])
-            if not (np.array_equal(rows_h[0], own) and np.array_equal(P.numpy().view(np.uint16), want[world])
-                    and np.array_equal(Q.numpy().view(np.uint16), want[world + 1])):
-                raise RuntimeError(f"hook step ({tag}) P/Q mismatch vs oracle")
-        res["records"] = len(recs)
-        res["rdp_encode_ms_mean"] = round(float(np.mean([r["timings"]["rdp_encode_ms"] for r in recs])), 4)
-        res["gpu_to_cpu_ms_mean"] = round(float(np.mean([r["timings"]["gpu_to_cpu_ms"] for r in recs])), 4)
-        out[tag] = res
-        del hook, plan
+            open(path, "w").close()     # the records of the timed steps only (the log appends)
+            t0 = time.perf_counter()
+            for i in range(steps):
+                hook.step_as_owner(pool, sl[i % 8], world)
+            t1 = time.perf_counter()
+            torch.cuda.synchronize()
+            t2 = time.perf_counter()
+            hook.flush()
+            res[kind] = {"issue_us_per_step": round((t1 - t0) * 1e6 / steps, 2),
+                         "us_per_step": round((t2 - t0) * 1e6 / steps, 2)}
+        hook.metrics.close()
+        recs = [_json.loads(x) for x in open(path).read().splitlines()]
+        # the last step checked against the oracle's P/Q of the buffer's rows
+        b = plan.turn ^ 1
+        rows_h = plan.rows[b].cpu().numpy().view(np.uint16).copy()
+        P, Q = hook.last_parity
+        want = rows_h.copy()
+        want[world:] = 0
+        oracle.gs_parity(want, world, plan.S, 0)
+        host_pool = pool.view(torch.int16).cpu().numpy().view(np.uint16)
+        last = slot_sets[(steps - 1) % 8]
+        own = np.concatenate([host_pool[last, 0].reshape(-1), host_pool[last, 1].reshape(-1)])
+        if not (np.array_equal(rows_h[0], own) and np.array_equal(P.numpy().view(np.uint16), want[world])
+                and np.array_equal(Q.numpy().view(np.uint16), want[world + 1])):
+            raise RuntimeError("hook step P/Q mismatch vs oracle")
+    res["records"] = len(recs)
+    res["rdp_encode_ms_mean"] = round(float(np.mean([r["timings"]["rdp_encode_ms"] for r in recs])), 4)
+    res["gpu_to_cpu_ms_mean"] = round(float(np.mean([r["timings"]["gpu_to_cpu_ms"] for r in recs])), 4)
+    res["d2h_bytes_per_step"] = 2 * plan.S * 2
+    out["native_step"] = res
+    del hook, plan
     # The reference's step on this GPU (bench_ghostserve_rdp.py:445-458,
     # :334-374), the exchange left out as above: the delta by advanced
     # indexing, per rank an fp16 copy of K and V and pack_row_from_block,
@@ -1314,13 +1318,13 @@ def main():
 
     hook = None
     if not args.no_hook:
-        log("[bench] serving hook: the parity owner's step at TP8 (2048 tokens), eager and graphs")
+        log("[bench] serving hook: the parity owner's step at TP8 (2048 tokens), one native call per step")
         hook = bench_hook(pkg, torch, oracle, dev, args.seed)
-        log(f"[bench] hook step: eager {hook['eager']['device_slots']['us_per_step']:.1f} / "
-            f"graph {hook['graph']['device_slots']['us_per_step']:.1f} us per step (device slots; "
-            f"the reference's sequence {hook['reference_sequence_us_per_step']:.1f}), "
-            f"issue {hook['eager']['host_slots']['issue_us_per_step']:.1f} / "
-            f"{hook['graph']['host_slots']['issue_us_per_step']:.1f} us (host slots)")
+        nat = hook["native_step"]
+        log(f"[bench] hook step: {nat['device_slots']['us_per_step']:.1f} us per step with device slots, "
+            f"{nat['host_slots']['us_per_step']:.1f} with host slots (issue "
+            f"{nat['host_slots']['issue_us_per_step']:.1f}); the reference's sequence "
+            f"{hook['reference_sequence_us_per_step']:.1f}")
         torch.cuda.empty_cache()
 
     c0 = None

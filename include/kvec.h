@@ -40,8 +40,8 @@ extern "C" {
  * kvec_version() / 10000 == KVEC_VERSION / 10000 before its first call.
  * 1.0.0: kvec_rdp_encode / kvec_rdp_decode / kvec_rdp_encode_paged take
  * unit_bytes, kvec_chunk_stripe has region_off and unit_bytes (0.1.0 had
- * neither). */
-#define KVEC_VERSION 10000
+ * neither).  1.1.0: kvec_hook_step added. */
+#define KVEC_VERSION 10100
 int kvec_version(void);
 /* Static description of a KVEC_E* code. */
 const char* kvec_strerror(int code);
@@ -259,6 +259,25 @@ int kvec_gs_pack_row(const void* k_blk, const void* v_blk, void* rows, int64_t w
 /* compute_rdp_parity_launcher, bench_ghostserve_rdp.py:177-199: P, Q of the
  * first nd rows of `rows` (row stride S words) into rows nd and nd+1. */
 int kvec_gs_rdp_parity(void* rows, int nd, int S, int star_base, void* stream);
+/* No reference counterpart: the serving plugin's per-step parity
+ * (bench_ghostserve_rdp.py:334-374 with the delta gather of :440-458), the
+ * work its Python issues as separate torch calls, enqueued by one call.
+ * rows: [world + 2, S] u16 on the device; kv: the step's delta, its page
+ * table the device slot buffer ([1][n] with 1-token pages over a
+ * [1][T][1][2][H][D] view of the pool).  On `stream`, in order:
+ *   - wait for the event `freed` (if not NULL: the last copy out of rows);
+ *   - if kv is not NULL: copy n int32 slots from slots_host (host, pinned;
+ *     skipped when NULL) into kv->page_table, then gather the delta's K
+ *     words and V words into row `row` (kvec_kv_gather_split);
+ *   - if pq_host is not NULL: record ev[0], P and Q of rows 0..world-1 into
+ *     rows world and world+1 (kvec_gs_rdp_parity), record ev[1]; then on
+ *     copy_stream (NULL: `stream`), after ev[1]: record ev[2], copy the two
+ *     rows (4*S bytes) to pq_host (host, pinned), record ev[3].
+ * ev: 4 hipEvent_t (any may be NULL; ev[1] is required when copy_stream is
+ * another stream).  Host copies make it unfit for graph capture. */
+int kvec_hook_step(const kvec_paged_kv* kv, const int32_t* slots_host, void* rows, int row, int world, int S,
+                   int star_base, void* pq_host, void* stream, void* copy_stream, void* freed,
+                   void* const* ev);
 
 /* ======== gs family: RS over GF(2^16) (benchmark/rs/kernel.cu, main.py) ======= */
 /* u16 symbols, packed: shards = [(k + m), shard_size].  gf_exp / gf_log are

@@ -88,17 +88,14 @@ def _row_of(host, slots):
     return np.concatenate([host[act, 0].reshape(-1), host[act, 1].reshape(-1)])
 
 
-@pytest.mark.parametrize("graphs", [True, False])
-def test_hook_repeated_shapes_and_host_slots(pkg, ora, gpu, monkeypatch, graphs):
-    """Steps of two shapes in turn, each repeated with new slots (the graphs
-    of a shape are captured once and replayed on both row buffers; a plan
-    is evicted and rebuilt when only one is kept), the slots given as a
-    device tensor, a host tensor or a list: every chunk's P/Q is the
-    oracle's."""
+def test_hook_repeated_shapes_and_host_slots(pkg, ora, gpu, monkeypatch):
+    """Steps of two shapes in turn, each repeated with new slots (a plan is
+    evicted and rebuilt when only one is kept), the slots given as a device
+    tensor, a host tensor or a list: every chunk's P/Q is the oracle's."""
     monkeypatch.setattr(pkg.serving.KVParityHook, "MAX_PLANS", 1)
     pool = _pool(gpu, T=400, seed=3)
     host = pool.cpu().view(torch.int16).numpy().view(np.uint16)
-    hook = pkg.serving.KVParityHook(star_base=2, graphs=graphs)
+    hook = pkg.serving.KVParityHook(star_base=2)
     rng = np.random.default_rng(4)
     for i in range(7):
         n = 5 if i % 3 else 9
@@ -117,15 +114,14 @@ def test_hook_repeated_shapes_and_host_slots(pkg, ora, gpu, monkeypatch, graphs)
         assert np.array_equal(Q.numpy().view(np.uint16), rows[2]), i
 
 
-@pytest.mark.parametrize("graphs", [True, False])
-def test_owner_step_at_group_of_eight(pkg, ora, gpu, graphs):
+def test_owner_step_at_group_of_eight(pkg, ora, gpu):
     """The parity owner's step in a group of 8 ranks, in one process: row 0
     is this rank's delta, rows 1-7 whatever the buffer holds (set here), and
     P/Q are those of all 8 rows; three steps, so both row buffers are
     reused."""
     pool = _pool(gpu, T=500, H=1, D=128, seed=5)
     host = pool.cpu().view(torch.int16).numpy().view(np.uint16)
-    hook = pkg.serving.KVParityHook(star_base=0, graphs=graphs)
+    hook = pkg.serving.KVParityHook(star_base=0)
     rng = np.random.default_rng(6)
     for i in range(3):
         sl = [int(x) for x in rng.choice(500, 64, replace=False)]
@@ -150,3 +146,55 @@ def test_owner_step_at_group_of_eight(pkg, ora, gpu, graphs):
         ora.gs_parity(rows, 8, plan.S, 0)
         assert np.array_equal(P.numpy().view(np.uint16), rows[8]), (i, b)
         assert np.array_equal(Q.numpy().view(np.uint16), rows[9]), (i, b)
+
+
+def test_hook_step_split_calls_and_checks(pkg, ora, gpu):
+    """kvec_hook_step through the C ABI in the two halves a multi-rank step
+    uses: the gather of this rank's row alone (no host copy), then, after the
+    rows have arrived, P/Q and their copy to pinned memory on a second stream
+    with the four events; P, Q and the row against the oracle.  Then the
+    argument checks: a row outside the group, a delta that is not a row's
+    size, a separate copy stream without event 1."""
+    import ctypes
+    lib = pkg._lib
+    pool = _pool(gpu, T=300, H=1, D=64, seed=9)
+    T, _, H, D = pool.shape
+    host = pool.cpu().view(torch.int16).numpy().view(np.uint16)
+    world, rank, n = 4, 2, 24
+    rng = np.random.default_rng(10)
+    sl = rng.choice(T, n, replace=False).astype(np.int32)
+    slots_dev = torch.empty(n, dtype=torch.int32, device=gpu)
+    staging = torch.from_numpy(sl.copy()).pin_memory()
+    kv = pkg.paged.PagedKV(pool.view(1, T, 1, 2, H, D), slots_dev.view(1, n), 0, n)
+    S = 2 * n * H * D
+    rows = torch.from_numpy(rng.integers(0, 65536, (world + 2, S), dtype=np.uint16).view(np.int16)).to(gpu)
+    stream = torch.cuda.current_stream(gpu).cuda_stream
+    lib.call("kvec_hook_step", kv.c, staging.data_ptr(), rows.data_ptr(), rank, world, S, 3, None, stream,
+             None, None, None)
+    side = torch.cuda.Stream(device=gpu)
+    evs = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
+    for e in evs:
+        e.record()
+    ev_arr = (ctypes.c_void_p * 4)(*[e.cuda_event for e in evs])
+    pq = torch.empty((2, S), dtype=torch.int16, pin_memory=True)
+    lib.call("kvec_hook_step", None, None, rows.data_ptr(), 0, world, S, 3, pq.data_ptr(), stream,
+             side.cuda_stream, None, ev_arr)
+    evs[3].synchronize()
+    torch.cuda.synchronize()
+    got = rows.cpu().numpy().view(np.uint16)
+    assert np.array_equal(got[rank], _row_of(host, sl.tolist()))
+    want = got.copy()
+    want[world:] = 0
+    ora.gs_parity(want, world, S, 3)
+    assert np.array_equal(got[world:], want[world:])
+    assert np.array_equal(pq.numpy().view(np.uint16), want[world:])
+    assert evs[0].elapsed_time(evs[1]) >= 0 and evs[2].elapsed_time(evs[3]) >= 0
+    bad = [
+        (kv.c, None, rows.data_ptr(), world, world, S, 0, None, stream, None, None, None),
+        (kv.c, None, rows.data_ptr(), 0, world, S + 8, 0, None, stream, None, None, None),
+        (None, None, rows.data_ptr(), 0, world, S, 0, pq.data_ptr(), stream, side.cuda_stream, None, None),
+    ]
+    for args in bad:
+        with pytest.raises(lib.KvecError, match="kvec_hook_step"):
+            lib.call("kvec_hook_step", *args)
+    torch.cuda.synchronize()
