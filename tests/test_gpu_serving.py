@@ -198,3 +198,30 @@ def test_hook_step_split_calls_and_checks(pkg, ora, gpu):
         with pytest.raises(lib.KvecError, match="kvec_hook_step"):
             lib.call("kvec_hook_step", *args)
     torch.cuda.synchronize()
+
+
+def test_hook_ring_wraps_with_steps_in_flight(pkg, ora, gpu, tmp_path):
+    """Eleven steps issued without a flush between them (the pinned P/Q ring
+    holds four): every step gets its record, in chunk order, and the last
+    step's P/Q is the oracle's; the host slot maps alternate between the two
+    staging buffers while earlier uploads may still be queued."""
+    import json
+    pool = _pool(gpu, T=600, H=1, D=128, seed=12)
+    host = pool.cpu().view(torch.int16).numpy().view(np.uint16)
+    path = tmp_path / "m.jsonl"
+    hook = pkg.serving.KVParityHook(star_base=1, metrics_file=str(path))
+    rng = np.random.default_rng(13)
+    sets = [rng.choice(600, 40, replace=False).tolist() for _ in range(11)]
+    for sl in sets:
+        hook.on_extend(pool, torch.tensor(sl))
+    hook.flush()
+    hook.metrics.close()
+    recs = [json.loads(x) for x in path.read_text().splitlines()]
+    assert [r["chunk_id"] for r in recs] == list(range(1, 12))
+    P, Q = hook.last_parity
+    row = _row_of(host, sets[-1])
+    rows = np.zeros((3, row.size), np.uint16)
+    rows[0] = row
+    ora.gs_parity(rows, 1, row.size, 1)
+    assert np.array_equal(P.numpy().view(np.uint16), rows[1])
+    assert np.array_equal(Q.numpy().view(np.uint16), rows[2])
