@@ -221,6 +221,12 @@ class KVParityHook:
                 if self._stream is not None:
                     for r in old.rows:
                         r.record_stream(self._stream)
+                # its staging buffers go back to torch's pinned-memory cache,
+                # which does not know of the uploads kvec_hook_step queued
+                # from them: those must have run first
+                for e in old.staged:
+                    if e is not None:
+                        e.synchronize()
             plan = _StepPlan(kv_pool, n, world, rank, self.star_base)
         self._plans[key] = plan   # most recently used last
         return plan
