@@ -1371,18 +1371,116 @@ constexpr int kRsHChainMax = 6;
 // in natural word order, parity g multiplied by its chain of g + 1 doublings
 // (a compile-time length, unrolled), parities past nout skipped; else
 // byte-transposed, multiplied through the byte maps ptab.
+// Fold one input's windows x (natural word order) into the accumulators:
+// the first input (i == k - 1) starts them, every later one is
+// acc = acc * g ^ x, by doubling chains (CHAINS) or the byte maps.
 template <int G, int NW, bool CHAINS>
+__device__ __forceinline__ void rs_h_fold(uint32_t (*acc)[G][4], const u32x4* x, bool first, int nout,
+                                          const uint32_t (*ptab)[kRs16Tab], uint32_t red2, Gf16Quad quad) {
+#pragma unroll
+    for (int n = 0; n < NW; ++n) {
+        uint32_t y[4];
+        if (CHAINS) y[0] = x[n].x, y[1] = x[n].y, y[2] = x[n].z, y[3] = x[n].w;
+        else split_bytes(x[n], y);
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            if (CHAINS && g >= nout) continue;
+            if (first) {
+                acc[n][g][0] = y[0], acc[n][g][1] = y[1], acc[n][g][2] = y[2], acc[n][g][3] = y[3];
+            } else if (CHAINS) {
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    uint32_t a = acc[n][g][q];
+#pragma unroll
+                    for (int d = 0; d + 2 <= g + 1; d += 2) a = gf16_quad2_xor(a, quad, 0u);
+                    acc[n][g][q] = (g + 1) & 1 ? gf16_dbl2_xor(a, red2, y[q]) : a ^ y[q];
+                }
+            } else {
+                gf16_mul_split_xor(acc[n][g], ptab[g], y);
+            }
+        }
+    }
+}
+
+// The parities of one tile from the accumulators: natural word order (chains)
+// back to the byte-transposed form rs_h_store writes.
+template <int G, int NW, bool CHAINS>
+__device__ __forceinline__ void rs_h_store_all(uint16_t* par, int64_t S, int og, int nout, uint64_t t0b,
+                                               uint32_t nbytes, uint32_t (*acc)[G][4], uint8_t* stage) {
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+        if (g >= nout) break;
+        uint32_t o[NW][4];
+#pragma unroll
+        for (int n = 0; n < NW; ++n) {
+            if (CHAINS) split_bytes(u32x4{acc[n][g][0], acc[n][g][1], acc[n][g][2], acc[n][g][3]}, o[n]);
+            else o[n][0] = acc[n][g][0], o[n][1] = acc[n][g][1], o[n][2] = acc[n][g][2], o[n][3] = acc[n][g][3];
+        }
+        rs_h_store<NW>(stage, o, reinterpret_cast<uint8_t*>(par + uint64_t(og + g) * S) + t0b, nbytes);
+    }
+}
+
+// A full tile of 16-byte-aligned rows (each window one aligned load):
+// inputs from the last to the first, each one's loads issued two inputs ahead
+// into a ring of three window sets, the loop unrolled by three so that no set
+// is copied (a copy would wait for its loads).  Past row 0 the ring loads row
+// 0 again (cache hits), so every load is unconditional: the compiler then
+// waits for an input's windows with the next two inputs' loads still in
+// flight, on the first pass through the loop as on the others.  Used for
+// three and four parities, where an input's doubling chains give the loads
+// ahead of it the most time to arrive; with one or two parities it cost a
+// wave per SIMD and ran slower ((25, 2): 118.9 against 111.5 us), with five
+// and more its registers spilled SGPRs.  It runs as a kernel instance of its
+// own (RING) over the full tiles: beside the general tile loop in one kernel
+// it spilled SGPRs too.
+template <int G, int NW, bool CHAINS>
+__device__ __forceinline__ void rs_h_ring(const uint16_t* in, int64_t S, int k, uint64_t t0b, int nout,
+                                          const uint32_t (*ptab)[kRs16Tab], uint32_t red2, Gf16Quad quad,
+                                          uint32_t (*acc)[G][4]) {
+    u32x4 wa[NW], wb[NW], wc[NW];
+    auto load = [&](int i, u32x4* w) {
+        const uint8_t* r = reinterpret_cast<const uint8_t*>(in + uint64_t(i > 0 ? i : 0) * S) + t0b;
+#pragma unroll
+        for (int n = 0; n < NW; ++n) w[n] = ld16(r + 16 * (threadIdx.x + n * kRsHBS));
+    };
+    int i = k - 1;
+    load(i, wa);
+    load(i - 1, wb);
+    load(i - 2, wc);
+    rs_h_fold<G, NW, CHAINS>(acc, wa, true, nout, ptab, red2, quad);
+    // from here on, the set after the one just folded holds row i, the next row i - 1
+    while (i > 0) {
+        --i;
+        load(i - 2, wa);
+        rs_h_fold<G, NW, CHAINS>(acc, wb, false, nout, ptab, red2, quad);
+        if (i == 0) break;
+        --i;
+        load(i - 2, wb);
+        rs_h_fold<G, NW, CHAINS>(acc, wc, false, nout, ptab, red2, quad);
+        if (i == 0) break;
+        --i;
+        load(i - 2, wc);
+        rs_h_fold<G, NW, CHAINS>(acc, wa, false, nout, ptab, red2, quad);
+    }
+}
+
+template <int G, int NW, bool CHAINS, bool RING>
 __device__ __forceinline__ void rs_h_encode_tiles(const uint16_t* in, uint16_t* par, int64_t S, int k, int og,
                                                   int nout, const uint32_t (*ptab)[kRs16Tab], uint32_t red2,
-                                                  Gf16Quad quad, uint8_t* stage) {
+                                                  Gf16Quad quad, uint8_t* stage, uint64_t t_begin,
+                                                  uint64_t t_end) {
     constexpr uint32_t TB = 16 * kRsHBS * NW;
     const uint64_t Sb = uint64_t(S) * 2;
-    const uint64_t ntiles = (Sb + TB - 1) / TB;
-    for (uint64_t tt = blockIdx.x; tt < ntiles; tt += gridDim.x) {
+    for (uint64_t tt = t_begin + blockIdx.x; tt < t_end; tt += gridDim.x) {
         const uint64_t t0b = tt * TB;
         const uint32_t nbytes = uint32_t(Sb - t0b < TB ? Sb - t0b : TB);
-        const bool full = nbytes == TB;
         uint32_t acc[NW][G][4];
+        if constexpr (RING) {
+            rs_h_ring<G, NW, CHAINS>(in, S, k, t0b, nout, ptab, red2, quad, acc);
+            rs_h_store_all<G, NW, CHAINS>(par, S, og, nout, t0b, nbytes, acc, stage);
+            continue;
+        }
+        const bool full = nbytes == TB;
         u32x4 x[NW], nx[NW];
         rs_h_windows<NW>(in + uint64_t(k - 1) * S, t0b, S, full, x);
         for (int i = k - 1; i >= 0; --i) {
@@ -1415,27 +1513,18 @@ __device__ __forceinline__ void rs_h_encode_tiles(const uint16_t* in, uint16_t* 
                 for (int n = 0; n < NW; ++n) x[n] = nx[n];
             }
         }
-#pragma unroll
-        for (int g = 0; g < G; ++g) {
-            if (g >= nout) break;
-            uint32_t o[NW][4];
-#pragma unroll
-            for (int n = 0; n < NW; ++n) {
-                if (CHAINS) split_bytes(u32x4{acc[n][g][0], acc[n][g][1], acc[n][g][2], acc[n][g][3]}, o[n]);
-                else o[n][0] = acc[n][g][0], o[n][1] = acc[n][g][1], o[n][2] = acc[n][g][2], o[n][3] = acc[n][g][3];
-            }
-            rs_h_store<NW>(stage, o, reinterpret_cast<uint8_t*>(par + uint64_t(og + g) * S) + t0b, nbytes);
-        }
+        rs_h_store_all<G, NW, CHAINS>(par, S, og, nout, t0b, nbytes, acc, stage);
     }
 }
 
 // encode_rs_u16's parity rows og .. og + G - 1 (og = blockIdx.y * G; those at
 // or past m are computed and not stored).  in: the k data rows of S words;
 // par: parity row 0.
-template <int G, int NW>
+template <int G, int NW, bool RING>
 __global__ __launch_bounds__(kRsHBS) void rs16_encode_horner_kernel(const uint16_t* in, uint16_t* par, int64_t S,
                                                                     int k, int m, const uint16_t* ex,
-                                                                    const uint16_t* lg) {
+                                                                    const uint16_t* lg, uint64_t t_begin,
+                                                                    uint64_t t_end) {
     constexpr uint32_t TB = 16 * kRsHBS * NW;
     __shared__ __attribute__((aligned(16))) uint32_t ptab[G][kRs16Tab];
     __shared__ uint16_t basis[G][16];
@@ -1447,8 +1536,8 @@ __global__ __launch_bounds__(kRsHBS) void rs16_encode_horner_kernel(const uint16
     if constexpr (G <= kRsHChainMax) {
         if (og == 0 && nout <= kRsHChainMax && horner_tables(ex)) {
             const uint16_t red = uint16_t(table_word_s(ex, 16));   // 2^16 reduced
-            rs_h_encode_tiles<G, NW, true>(in, par, S, k, og, nout, ptab, uint32_t(red) * 0x10001u,
-                                           gf16_quad_table(red), stage);
+            rs_h_encode_tiles<G, NW, true, RING>(in, par, S, k, og, nout, ptab, uint32_t(red) * 0x10001u,
+                                                 gf16_quad_table(red), stage, t_begin, t_end);
             return;
         }
     }
@@ -1459,7 +1548,7 @@ __global__ __launch_bounds__(kRsHBS) void rs16_encode_horner_kernel(const uint16
     __syncthreads();
     rs_build_perm_tables(ptab, basis, coef, G, ex, lg);
     __syncthreads();
-    rs_h_encode_tiles<G, NW, false>(in, par, S, k, og, nout, ptab, 0u, Gf16Quad{0, 0}, stage);
+    rs_h_encode_tiles<G, NW, false, RING>(in, par, S, k, og, nout, ptab, 0u, Gf16Quad{0, 0}, stage, t_begin, t_end);
 }
 
 // The inverse of V[r][c] = gf_exp[((pu_r + 1) miss_c) mod 65535] by
@@ -1713,21 +1802,35 @@ extern "C" int kvec_rs16_encode(const void* data_padded, void* shards, int data_
         const uint16_t* in = (const uint16_t*)data_padded;
         uint16_t* par = (uint16_t*)shards + uint64_t(data_shards) * S;
         constexpr uint32_t TB = 16 * kRsHBS * 2;
-        auto launch = [&](auto kern, int G) {
+        const uint64_t Sb = uint64_t(S) * 2, ntiles = (Sb + TB - 1) / TB;
+        // three or four parities over 16-byte-aligned rows: the full tiles on
+        // the ring kernel, a partial last tile on the other
+        const bool aligned = (reinterpret_cast<uintptr_t>(in) & 15) == 0 && Sb % 16 == 0;
+        const uint64_t nring = (parity_shards == 3 || parity_shards == 4) && aligned ? Sb / TB : 0;
+        auto range = [&](auto kern, int G, uint64_t t0, uint64_t t1) {
+            if (t1 <= t0) return;
+            const uint64_t n = t1 - t0;
             const unsigned groups = unsigned((parity_shards + G - 1) / G);
-            hipLaunchKernelGGL(kern, dim3(rs_h_grid(S, TB), groups), dim3(kRsHBS), 0, st, in, par, S, data_shards,
-                               parity_shards, gf_exp, gf_log);
+            hipLaunchKernelGGL(kern, dim3(unsigned(n < uint64_t(kRsHGrid) ? n : uint64_t(kRsHGrid)), groups),
+                               dim3(kRsHBS), 0, st, in, par, S, data_shards, parity_shards, gf_exp, gf_log, t0, t1);
         };
+        auto launch = [&](auto kern, int G) { range(kern, G, nring, ntiles); };
         // one group of exactly m parities up to kRsHMaxG, else groups of kRsHMaxG
         switch (parity_shards) {
-            case 1: launch(rs16_encode_horner_kernel<1, 2>, 1); break;
-            case 2: launch(rs16_encode_horner_kernel<2, 2>, 2); break;
-            case 3: launch(rs16_encode_horner_kernel<3, 2>, 3); break;
-            case 4: launch(rs16_encode_horner_kernel<4, 2>, 4); break;
-            case 5: launch(rs16_encode_horner_kernel<5, 2>, 5); break;
-            case 6: launch(rs16_encode_horner_kernel<6, 2>, 6); break;
-            case 7: launch(rs16_encode_horner_kernel<7, 2>, 7); break;
-            default: launch(rs16_encode_horner_kernel<kRsHMaxG, 2>, kRsHMaxG); break;
+            case 1: launch(rs16_encode_horner_kernel<1, 2, false>, 1); break;
+            case 2: launch(rs16_encode_horner_kernel<2, 2, false>, 2); break;
+            case 3:
+                range(rs16_encode_horner_kernel<3, 2, true>, 3, 0, nring);
+                launch(rs16_encode_horner_kernel<3, 2, false>, 3);
+                break;
+            case 4:
+                range(rs16_encode_horner_kernel<4, 2, true>, 4, 0, nring);
+                launch(rs16_encode_horner_kernel<4, 2, false>, 4);
+                break;
+            case 5: launch(rs16_encode_horner_kernel<5, 2, false>, 5); break;
+            case 6: launch(rs16_encode_horner_kernel<6, 2, false>, 6); break;
+            case 7: launch(rs16_encode_horner_kernel<7, 2, false>, 7); break;
+            default: launch(rs16_encode_horner_kernel<kRsHMaxG, 2, false>, kRsHMaxG); break;
         }
         return check_launch("kvec_rs16_encode");
     }

@@ -633,11 +633,16 @@ def test_rs16_reconstruct_tiles(pkg, ora, gpu, k, S, soff, gen4):
 # m <= 16 (benchmark/rs/kernel.cu:67-102, :105-222): these shapes run the
 # Horner kernels (one multiplier per output, the inverse by a thread per entry).
 @pytest.mark.parametrize("k,m,S", [(10, 5, 8192 * 2 + 3), (16, 4, 4096), (25, 2, 30001), (7, 7, 9),
-                                   (49, 1, 1000), (5, 20, 517), (3, 17, 2048 * 5)])
-@pytest.mark.parametrize("doff,soff", [(0, 0), (3, 5)])
+                                   (49, 1, 1000), (5, 20, 517), (3, 17, 2048 * 5),
+                                   (16, 4, 4096 * 3 + 8), (17, 3, 6168), (13, 4, 4096 * 4)])
+@pytest.mark.parametrize("doff,soff", [(0, 0), (3, 5), (8, 0)])
 def test_rs16_encode_any_k_m(pkg, ora, gpu, k, m, S, doff, soff):
     """Offsets in u16 words: the data and shard tensors at any alignment;
-    the words around the shard tensor stay untouched."""
+    the words around the shard tensor stay untouched.  With three or four
+    parities over 16-byte-aligned data rows (doff 0 or 8, S a multiple of 8)
+    the full tiles run on the ring kernel and a partial last tile on the
+    general one (S = 4096 * 3 + 8: three full tiles and 16 bytes; 6168: one
+    and 4,144 bytes); otherwise every tile runs on the general kernel."""
     ex, lg = ora.gf16_tables()
     rng = np.random.default_rng(k * 1000 + m * 10 + S)
     data = rng.integers(0, 65536, k * S, dtype=np.uint16)
@@ -656,7 +661,7 @@ def test_rs16_encode_any_k_m(pkg, ora, gpu, k, m, S, doff, soff):
 
 
 @pytest.mark.parametrize("k,m,S,poly", [(12, 5, 5003, None), (20, 3, 4099, None), (25, 3, 2 * 8192 + 9, 0x18013),
-                                         (49, 1, 777, 0x18013)])
+                                         (49, 1, 777, 0x18013), (20, 4, 8192 + 8, None), (18, 4, 4096 * 2, 0x18013)])
 def test_rs16_encode_any_k_m_other_generator(pkg, ora, gpu, k, m, S, poly):
     """Tables with generator 4 (poly None): the per-output multiplier is
     gf_exp[p + 1] of those tables, through its byte maps even where
