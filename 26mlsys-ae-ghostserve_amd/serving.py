@@ -259,8 +259,14 @@ class KVParityHook:
             s = plan.slot
             plan.slot = (s + 1) % plan.RING
             if plan.busy[s]:
-                # the ring came round to a step whose record is not written
-                plan.events[s][3].synchronize()
+                # the ring came round to a step whose record is not written:
+                # wait for that step's last copy (its probe's, if it made
+                # one); the records before it finished earlier on the same
+                # side stream, so the poll writes them all
+                for ent in self._pending:
+                    if ent[2] is plan and ent[3] == s:
+                        (ent[4][1] if ent[4] is not None else plan.events[s][3]).synchronize()
+                        break
                 self.poll()
             pq, side, evs = plan.pq[s].data_ptr(), self._stream.cuda_stream, plan.ev_args[s]
         freed = plan.freed[b] if gather else None

@@ -200,16 +200,19 @@ def test_hook_step_split_calls_and_checks(pkg, ora, gpu):
     torch.cuda.synchronize()
 
 
-def test_hook_ring_wraps_with_steps_in_flight(pkg, ora, gpu, tmp_path):
+@pytest.mark.parametrize("probe", [False, True])
+def test_hook_ring_wraps_with_steps_in_flight(pkg, ora, gpu, tmp_path, probe):
     """Eleven steps issued without a flush between them (the pinned P/Q ring
     holds four): every step gets its record, in chunk order, and the last
     step's P/Q is the oracle's; the host slot maps alternate between the two
-    staging buffers while earlier uploads may still be queued."""
+    staging buffers while earlier uploads may still be queued.  With the
+    reference's host-to-device probe, a ring slot is reused only after its
+    step's probe copy too."""
     import json
     pool = _pool(gpu, T=600, H=1, D=128, seed=12)
     host = pool.cpu().view(torch.int16).numpy().view(np.uint16)
     path = tmp_path / "m.jsonl"
-    hook = pkg.serving.KVParityHook(star_base=1, metrics_file=str(path))
+    hook = pkg.serving.KVParityHook(star_base=1, metrics_file=str(path), probe_h2d=probe)
     rng = np.random.default_rng(13)
     sets = [rng.choice(600, 40, replace=False).tolist() for _ in range(11)]
     for sl in sets:
@@ -218,6 +221,7 @@ def test_hook_ring_wraps_with_steps_in_flight(pkg, ora, gpu, tmp_path):
     hook.metrics.close()
     recs = [json.loads(x) for x in path.read_text().splitlines()]
     assert [r["chunk_id"] for r in recs] == list(range(1, 12))
+    assert all((r["timings"]["cpu_to_gpu_ms"] is not None) == probe for r in recs)
     P, Q = hook.last_parity
     row = _row_of(host, sets[-1])
     rows = np.zeros((3, row.size), np.uint16)
