@@ -735,6 +735,39 @@ __device__ __forceinline__ u32x4 gf16_dbl_n(u32x4 v, uint32_t n, uint32_t red2, 
     return v;
 }
 
+// Four packed word pairs times alpha^e for alpha = 2 and 1 <= e <= 4 (e
+// wave-uniform): one times-4 step when e >= 3, then one doubling (e odd) or
+// one more times-4 step; straight-line code under two uniform branches.
+__device__ __forceinline__ void gf16_step_pow(uint32_t (&a)[4], int e, uint32_t red2, Gf16Quad q) {
+    if (e >= 3) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) a[i] = gf16_quad2_xor(a[i], q, 0u);
+    }
+    if (e & 1) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) a[i] = gf16_dbl2(a[i], red2);
+    } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) a[i] = gf16_quad2_xor(a[i], q, 0u);
+    }
+}
+
+// a = a * alpha^e ^ y, as gf16_step_pow with the XOR in the last step.
+__device__ __forceinline__ void gf16_step_pow_xor(uint32_t (&a)[4], int e, const uint32_t (&y)[4], uint32_t red2,
+                                                  Gf16Quad q) {
+    if (e >= 3) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) a[i] = gf16_quad2_xor(a[i], q, 0u);
+    }
+    if (e & 1) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) a[i] = gf16_dbl2_xor(a[i], red2, y[i]);
+    } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) a[i] = gf16_quad2_xor(a[i], q, y[i]);
+    }
+}
+
 // The reconstruct by Horner's rule, for tables with alpha = 2.  The inputs
 // x[] are the ND = NIN - M surviving data rows (rows row[0] < row[1] < ...)
 // and the M parity rows of parity_used.  Each parity syndrome
@@ -1596,6 +1629,199 @@ __device__ __forceinline__ void rs16_gauss_jordan(int m, const int* miss, const 
     }
 }
 
+// Whether the reconstruct of M <= 4 lost rows runs its syndromes as doubling
+// chains on rs16_reconstruct_ring_kernel: tables with generator 2
+// (horner_tables) and every parity row used below 4, so each syndrome's
+// multiplier alpha^(pu + 1) is at most four doublings per row.  The general
+// kernel evaluates the same test and leaves the ring's tiles alone when it
+// holds.  s_pu in LDS; uniform.
+template <int M>
+__device__ __forceinline__ bool rs_rec_ring_ok(const int* s_pu, const uint16_t* ex) {
+    bool ok = M <= 4 && horner_tables(ex);
+#pragma unroll
+    for (int r = 0; r < M; ++r) ok = ok && lds_uniform(s_pu[r]) <= 3;
+    return ok;
+}
+
+// reconstruct_rs_u16_inplace of M <= 4 lost data rows, any k, on the tiles
+// [0, t_end) of 16-byte-aligned rows whose length is a multiple of 16 bytes
+// (tiles of NW windows of 16 bytes per thread; the last may be partial), when
+// rs_rec_ring_ok holds (else it writes nothing and the general kernel codes
+// every tile).  Syndrome r is b_r = Par_{pu_r} ^ XOR over surviving rows j of
+// D_j * g_r^j, g_r = alpha^(pu_r + 1), by Horner's rule over the surviving
+// rows only (highest first): between consecutive survivors j > j' the
+// accumulator is multiplied by g_r^(j - j') -- j - j' steps of gf16_step_pow,
+// in natural word order -- and after the lowest survivor by g_r^(j_min).
+// Each surviving row's windows are loaded two survivors ahead into a ring of
+// three window sets (no register copies; past the last survivor the ring
+// loads parity row pu_0's windows, which the tile reads again at its end), so
+// a row is waited for with the next two rows' loads in flight.  The lost rows
+// come from the syndromes through the inverse's byte maps, out_c = XOR_r
+// inv[c][r] * b_r, as in the general kernel, and are stored straight from
+// registers (each thread's 16-byte windows, aligned).
+template <int M, int NW>
+__global__ __launch_bounds__(kRsHBS) void rs16_reconstruct_ring_kernel(uint16_t* sh, int64_t S, int k, int mpar,
+                                                                       const int32_t* missing,
+                                                                       const int32_t* pused,
+                                                                       const uint16_t* ex, const uint16_t* lg,
+                                                                       uint64_t t_end) {
+    static_assert(M >= 1 && M <= 4, "ring reconstruct: at most four lost rows");
+    constexpr uint32_t TB = 16 * kRsHBS * NW;
+    __shared__ __attribute__((aligned(16))) uint32_t ptab[M * M][kRs16Tab];   // inv[c][r] at [c * M + r]
+    __shared__ uint16_t basis[M * M][16];
+    __shared__ uint16_t coef[M * M];
+    __shared__ uint16_t sV[M * M], sInv[M * M];
+    __shared__ int s_miss[M], s_pu[M], s_desc[M], s_ok;
+    if (threadIdx.x < M) {
+        s_miss[threadIdx.x] = missing[threadIdx.x];
+        s_pu[threadIdx.x] = pused[threadIdx.x];
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        int ok = 1;
+        for (int q = 0; q < M; ++q) {
+            ok &= s_miss[q] >= 0 && s_miss[q] < k && s_pu[q] >= 0 && s_pu[q] < mpar;
+            for (int q2 = 0; q2 < q; ++q2) ok &= s_miss[q2] != s_miss[q];
+        }
+        s_ok = ok;
+        for (int q = 0; q < M; ++q) {
+            int v = s_miss[q], at = q;
+            while (at > 0 && s_desc[at - 1] < v) s_desc[at] = s_desc[at - 1], --at;
+            s_desc[at] = v;
+        }
+    }
+    __syncthreads();
+    if (!s_ok || !rs_rec_ring_ok<M>(s_pu, ex)) return;   // uniform over the grid
+    rs16_gauss_jordan(M, s_miss, s_pu, sV, sInv, ex, lg);
+    for (int e = threadIdx.x; e < M * M; e += kRsHBS) coef[e] = sInv[e];
+    __syncthreads();
+    rs_build_perm_tables(ptab, basis, coef, M * M, ex, lg);
+    __syncthreads();
+    const uint16_t red = uint16_t(table_word_s(ex, 16));
+    const uint32_t red2 = uint32_t(red) * 0x10001u;
+    const Gf16Quad quad = gf16_quad_table(red);
+    auto desc = [&](int q) { return q < M ? int(lds_uniform(s_desc[q])) : -1; };
+    auto pu = [&](int r) { return int(lds_uniform(s_pu[r])); };
+    const int dummy = k + pu(0);
+    const uint64_t Sb = uint64_t(S) * 2;
+    for (uint64_t tt = blockIdx.x; tt < t_end; tt += gridDim.x) {
+        const uint64_t t0b = tt * TB;
+        // window n at byte lo[n] of the tile; windows past the row's end (the
+        // last tile may be partial) read the tile's first window and store nothing
+        uint32_t lo[NW];
+        bool in[NW];
+#pragma unroll
+        for (int n = 0; n < NW; ++n) {
+            const uint32_t o = 16 * (threadIdx.x + n * kRsHBS);
+            in[n] = t0b + o < Sb;
+            lo[n] = in[n] ? o : 0u;
+        }
+        auto load = [&](int row, u32x4 (&w)[NW]) {
+            const uint8_t* rp =
+                    reinterpret_cast<const uint8_t*>(sh + uint64_t(row >= 0 ? row : dummy) * uint64_t(S)) + t0b;
+#pragma unroll
+            for (int n = 0; n < NW; ++n) w[n] = ld16(rp + lo[n]);
+        };
+        // the next surviving row below j (-1 when none): nl counts the lost
+        // rows passed, all of them above the rows still to come
+        int nl = 0;
+        auto next = [&](int j) {
+            if (j <= 0) return -1;
+            int r = j - 1;
+            while (nl < M && desc(nl) == r) {
+                --r;
+                ++nl;
+            }
+            return r;
+        };
+        uint32_t acc[M][NW][4];
+        // acc = acc * g^gap ^ w (acc = w for gap 0): gap - 1 plain steps, then
+        // one step with the XOR
+        auto fold = [&](const u32x4 (&w)[NW], int gap) {
+#pragma unroll
+            for (int n = 0; n < NW; ++n) {
+                const uint32_t y[4] = {w[n].x, w[n].y, w[n].z, w[n].w};
+#pragma unroll
+                for (int r = 0; r < M; ++r) {
+                    if (gap == 0) {
+#pragma unroll
+                        for (int q = 0; q < 4; ++q) acc[r][n][q] = y[q];
+                    } else {
+                        const int e = pu(r) + 1;
+                        for (int t = 1; t < gap; ++t) gf16_step_pow(acc[r][n], e, red2, quad);
+                        gf16_step_pow_xor(acc[r][n], e, y, red2, quad);
+                    }
+                }
+            }
+        };
+        u32x4 wa[NW], wb[NW], wc[NW];
+        int ra = next(k);
+        load(ra, wa);
+        int rb = next(ra);
+        load(rb, wb);
+        int rc = next(rb);
+        load(rc, wc);
+        if (ra >= 0) {
+            fold(wa, 0);
+        } else {   // every data row lost: the syndromes are the parity rows
+#pragma unroll
+            for (int r = 0; r < M; ++r)
+#pragma unroll
+                for (int n = 0; n < NW; ++n) acc[r][n][0] = acc[r][n][1] = acc[r][n][2] = acc[r][n][3] = 0;
+        }
+        int prev = ra;
+        for (;;) {
+            if (rb < 0) break;
+            ra = next(rc);
+            load(ra, wa);
+            fold(wb, prev - rb);
+            prev = rb;
+            if (rc < 0) break;
+            rb = next(ra);
+            load(rb, wb);
+            fold(wc, prev - rc);
+            prev = rc;
+            if (ra < 0) break;
+            rc = next(rb);
+            load(rc, wc);
+            fold(wa, prev - ra);
+            prev = ra;
+        }
+        // the lowest survivor's power, the parity rows, then the inverse
+        u32x4 pw[M][NW];
+#pragma unroll
+        for (int r = 0; r < M; ++r) load(k + pu(r), pw[r]);
+        uint32_t out[M][NW][4];
+#pragma unroll
+        for (int c = 0; c < M; ++c)
+#pragma unroll
+            for (int n = 0; n < NW; ++n) out[c][n][0] = out[c][n][1] = out[c][n][2] = out[c][n][3] = 0;
+#pragma unroll
+        for (int r = 0; r < M; ++r) {
+#pragma unroll
+            for (int n = 0; n < NW; ++n) {
+                for (int t = 0; t < prev; ++t) gf16_step_pow(acc[r][n], pu(r) + 1, red2, quad);
+                uint32_t b[4];
+                split_bytes(u32x4{acc[r][n][0] ^ pw[r][n].x, acc[r][n][1] ^ pw[r][n].y, acc[r][n][2] ^ pw[r][n].z,
+                                  acc[r][n][3] ^ pw[r][n].w},
+                            b);
+                Gf8Fields f[4];
+#pragma unroll
+                for (int q = 0; q < 4; ++q) f[q] = gf8_fields(b[q]);
+#pragma unroll
+                for (int c = 0; c < M; ++c) gf16_fma_split(out[c][n], f, ptab[c * M + r]);
+            }
+        }
+#pragma unroll
+        for (int c = 0; c < M; ++c) {
+            uint8_t* dst = reinterpret_cast<uint8_t*>(sh + uint64_t(lds_uniform(s_miss[c])) * uint64_t(S)) + t0b;
+#pragma unroll
+            for (int n = 0; n < NW; ++n)
+                if (in[n]) st16(dst + lo[n], join_bytes(out[c][n]));
+        }
+    }
+}
+
 // reconstruct_rs_u16_inplace of M lost data rows, any k (inputs: the
 // surviving data rows and the parity rows of parity_used).  sh: the shard
 // tensor, rows of S words.  Out-of-range or repeated lost rows, or parity rows
@@ -1605,7 +1831,8 @@ __global__ __launch_bounds__(kRsHBS) void rs16_reconstruct_horner_kernel(uint16_
                                                                          const int32_t* missing,
                                                                          const int32_t* pused,
                                                                          const uint16_t* ex,
-                                                                         const uint16_t* lg) {
+                                                                         const uint16_t* lg,
+                                                                         uint64_t ring_tiles) {
     constexpr int NW = 1, G = M < kRsHMaxG ? M : kRsHMaxG, NT = M + M * M;
     constexpr uint32_t TB = 16 * kRsHBS * NW;
     static_assert(M * M <= kRsHBS, "one thread per inverse entry");
@@ -1638,6 +1865,12 @@ __global__ __launch_bounds__(kRsHBS) void rs16_reconstruct_horner_kernel(uint16_
     }
     __syncthreads();
     if (!s_ok) return;   // uniform: the whole grid writes nothing
+    const uint64_t Sb = uint64_t(S) * 2;
+    const uint64_t ntiles = (Sb + TB - 1) / TB;
+    // the tiles [0, ring_tiles) are rs16_reconstruct_ring_kernel's when it runs
+    // (ring_tiles may pass the last tile: then this kernel writes nothing)
+    const uint64_t t_first = rs_rec_ring_ok<M>(s_pu, ex) ? ring_tiles : 0;
+    if (blockIdx.x + t_first >= ntiles) return;
     rs16_gauss_jordan(M, s_miss, s_pu, sV, sInv, ex, lg);
     for (int e = threadIdx.x; e < NT; e += kRsHBS)
         coef[e] = e < M ? ex[uint32_t(s_pu[e] + 1) % kGfOrder] : sInv[e - M];
@@ -1647,9 +1880,7 @@ __global__ __launch_bounds__(kRsHBS) void rs16_reconstruct_horner_kernel(uint16_
     // indices stay in LDS and are read where used (2 M of them held in scalar
     // registers beside the loop's own spilled SGPRs for M >= 8)
     auto desc = [&](int q) { return q < M ? int(lds_uniform(s_desc[q])) : -1; };
-    const uint64_t Sb = uint64_t(S) * 2;
-    const uint64_t ntiles = (Sb + TB - 1) / TB;
-    for (uint64_t tt = blockIdx.x; tt < ntiles; tt += gridDim.x) {
+    for (uint64_t tt = blockIdx.x + t_first; tt < ntiles; tt += gridDim.x) {
         const uint64_t t0b = tt * TB;
         const uint32_t nbytes = uint32_t(Sb - t0b < TB ? Sb - t0b : TB);
         const bool full = nbytes == TB;
@@ -1721,7 +1952,7 @@ __global__ __launch_bounds__(kRsHBS) void rs16_reconstruct_horner_kernel(uint16_
 }
 
 typedef void (*RsRecHornerFn)(uint16_t*, int64_t, int, int, const int32_t*, const int32_t*, const uint16_t*,
-                              const uint16_t*);
+                              const uint16_t*, uint64_t);
 template <int... I>
 struct RsRecHornerTable {
     static constexpr RsRecHornerFn fn[sizeof...(I)] = {rs16_reconstruct_horner_kernel<I + 1>...};
@@ -1875,10 +2106,36 @@ extern "C" int kvec_rs16_reconstruct(void* shards, int shard_size, int data_shar
                          parity_shards, m, shard_size);
     if (shard_size == 0) return KVEC_OK;
     if (int64_t(data_shards) * m > kRsMaxTables) {
-        // k * m maps beyond the LDS tables: syndromes by Horner over byte maps
-        hipLaunchKernelGGL(RsRecHorner::fn[m - 1], dim3(rs_h_grid(shard_size, 16 * kRsHBS)), dim3(kRsHBS), 0,
-                           as_stream(stream), (uint16_t*)shards, int64_t(shard_size), data_shards, parity_shards,
-                           missing_data, parity_used, gf_exp, gf_log);
+        // k * m maps beyond the LDS tables: syndromes by Horner's rule.  Up to
+        // four lost rows over 16-byte-aligned rows: the full tiles on the ring
+        // kernel (doubling chains, when the tables and parity rows allow them;
+        // both kernels evaluate that test), the rest on the byte-map kernel.
+        // Windows per thread of the ring tiles by M (measured on the 512 MiB
+        // stream: one for two lost rows, 121-123 against 123-127 us; two for
+        // the others, four lost rows 217 against 225 us).  The ring takes
+        // every tile, a partial last one included.
+        constexpr uint32_t TB = 16 * kRsHBS;
+        const uint32_t ring_nw = m == 2 ? 1 : 2;
+        const uint64_t Sb = uint64_t(shard_size) * 2;
+        const bool aligned = (reinterpret_cast<uintptr_t>(shards) & 15) == 0 && Sb % 16 == 0;
+        const uint64_t nring = m <= 4 && aligned ? (Sb + TB * ring_nw - 1) / (TB * ring_nw) : 0;
+        hipStream_t st = as_stream(stream);
+        hipLaunchKernelGGL(RsRecHorner::fn[m - 1], dim3(rs_h_grid(shard_size, TB)), dim3(kRsHBS), 0, st,
+                           (uint16_t*)shards, int64_t(shard_size), data_shards, parity_shards, missing_data,
+                           parity_used, gf_exp, gf_log, nring * ring_nw);
+        if (nring) {
+            const dim3 grid(unsigned(nring < uint64_t(kRsHGrid) ? nring : uint64_t(kRsHGrid)));
+            auto ring = [&](auto kern) {
+                hipLaunchKernelGGL(kern, grid, dim3(kRsHBS), 0, st, (uint16_t*)shards, int64_t(shard_size),
+                                   data_shards, parity_shards, missing_data, parity_used, gf_exp, gf_log, nring);
+            };
+            switch (m) {
+                case 1: ring(rs16_reconstruct_ring_kernel<1, 2>); break;
+                case 2: ring(rs16_reconstruct_ring_kernel<2, 1>); break;
+                case 3: ring(rs16_reconstruct_ring_kernel<3, 2>); break;
+                default: ring(rs16_reconstruct_ring_kernel<4, 2>); break;
+            }
+        }
         return check_launch("kvec_rs16_reconstruct");
     }
     const uint64_t Sb = uint64_t(shard_size) * 2;

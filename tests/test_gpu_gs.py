@@ -720,6 +720,61 @@ def test_rs16_reconstruct_any_k(pkg, ora, gpu, k, mp, S, soff, gen4):
         assert bool((rest == 0x2A2A).all()), (miss, pused)
 
 
+@pytest.mark.parametrize("k,mp,S,soff,gen", [(16, 4, 2048 * 3 + 8, 0, 2), (25, 4, 2048 * 2, 8, 2),
+                                             (13, 6, 2048 * 4 + 16, 0, 2), (20, 4, 2048 * 3, 0, 0x18013),
+                                             (14, 4, 2048 * 2 + 8, 0, 4), (30, 4, 2048 + 8, 8, 2),
+                                             (50, 4, 2048 * 2 + 8, 0, 2)])
+def test_rs16_reconstruct_ring(pkg, ora, gpu, k, mp, S, soff, gen):
+    """Up to four lost rows with k * m > 48 over 16-byte-aligned rows (soff
+    and S multiples of 8 words): every tile on the ring kernel (syndromes by
+    doubling chains over the surviving rows, each loaded two survivors
+    ahead), partial last tiles included (S = 2048 * 3 + 8: a last tile of 16
+    bytes in one-window tiles, 4,112 in two-window ones; 2048 * 4 + 16: 32
+    bytes; 2048 * 3 with three lost rows: a two-window tile's first window
+    only; k = 50: one lost row).  Lost rows at both ends and in runs (one
+    chain then spans several rows), a repeated parity row (the reference's
+    singular system), parity rows up to 3 and, with six parities, beyond 3
+    (no chains: every tile on the byte-map kernel); generator-2 tables of
+    x^16 + x^15 + x^4 + x + 1 (the reduction word's top bit set) and
+    generator-4 tables (no chains)."""
+    ex, lg = (ora.gf16_tables() if gen == 2 else _gen4_tables(ora) if gen == 4 else _poly_tables(gen))
+    rng = np.random.default_rng(k * 7 + mp + S + gen)
+    data = rng.integers(0, 65536, k * S, dtype=np.uint16)
+    ref = ora.rs16_encode(data, k, mp, S, ex, lg)
+    gex, glg = dev(ex, gpu), dev(lg, gpu)
+    cases = []
+    for nm in range(1, 5):
+        if k * nm <= 48:
+            continue
+        cases.append((tuple(range(nm)), tuple(range(nm))))
+        cases.append((tuple(range(k - nm, k)), tuple(reversed(range(nm)))))
+        cases.append(((0, k - 1, 5, 6)[:nm], tuple(rng.permutation(4)[:nm].tolist())))
+        cases.append(((8, 9, 10, 11)[:nm], (3, 1, 0, 2)[:nm]))
+        cases.append((tuple(rng.choice(k, nm, replace=False).tolist()), tuple(rng.permutation(4)[:nm].tolist())))
+        if nm >= 2:
+            cases.append((tuple(rng.choice(k, nm, replace=False).tolist()), (0, 0, 2, 3)[:nm]))
+        if mp > 4:
+            cases.append((tuple(rng.choice(k, nm, replace=False).tolist()), (5, 2, 4, 0)[:nm]))
+            cases.append(((0, 3, 4, k - 1)[:nm], (4, 3, 1, 0)[:nm]))
+    assert cases
+    buf = torch.full(((k + mp) * S + 16,), 0x2A2A, dtype=torch.int16, device=gpu)
+    d = buf[soff:soff + (k + mp) * S].view(k + mp, S).view(torch.uint16)
+    assert d.data_ptr() % 16 == 0
+    for miss, pused in cases:
+        sh = ref.copy()
+        sh[list(miss)] = rng.integers(0, 65536, (len(miss), S), dtype=np.uint16)
+        want = sh.copy()
+        ora.rs16_reconstruct(want, S, k, mp, list(miss), list(pused), ex, lg)
+        assert np.array_equal(want, ref) == (len(set(pused)) == len(pused)), (miss, pused)
+        buf[soff:soff + (k + mp) * S] = dev(sh.reshape(-1).view(np.int16), gpu)
+        pkg.rs.rs_kernel.reconstruct_rs_u16_inplace(
+            d, S, k, mp, torch.tensor(miss, dtype=torch.int32, device=gpu),
+            torch.tensor(pused, dtype=torch.int32, device=gpu), gex, glg)
+        assert np.array_equal(host(d), want), (miss, pused)
+        rest = torch.cat([buf[:soff], buf[soff + (k + mp) * S:]])
+        assert bool((rest == 0x2A2A).all()), (miss, pused)
+
+
 def test_rs16_any_k_m_round_trip_and_refusals(pkg, gpu):
     """forward_encode_kv / backwards_decode_kv at (k, m) = (16, 4) with four
     lost data shards, and the reference's m <= 16 limit on the reconstruct."""
