@@ -1632,9 +1632,8 @@ __device__ __forceinline__ void rs16_gauss_jordan(int m, const int* miss, const 
 // Whether the reconstruct of M <= 4 lost rows runs its syndromes as doubling
 // chains on rs16_reconstruct_ring_kernel: tables with generator 2
 // (horner_tables) and every parity row used below 4, so each syndrome's
-// multiplier alpha^(pu + 1) is at most four doublings per row.  The general
-// kernel evaluates the same test and leaves the ring's tiles alone when it
-// holds.  s_pu in LDS; uniform.
+// multiplier alpha^(pu + 1) is at most four doublings per row.  s_pu in LDS;
+// uniform.
 template <int M>
 __device__ __forceinline__ bool rs_rec_ring_ok(const int* s_pu, const uint16_t* ex) {
     bool ok = M <= 4 && horner_tables(ex);
@@ -1643,11 +1642,142 @@ __device__ __forceinline__ bool rs_rec_ring_ok(const int* s_pu, const uint16_t* 
     return ok;
 }
 
+// reconstruct_rs_u16_inplace of M lost data rows, any k (inputs: the
+// surviving data rows and the parity rows of parity_used).  sh: the shard
+// tensor, rows of S words.  Out-of-range or repeated lost rows, or parity rows
+// outside the tensor, write nothing.
+template <int M>
+__device__ __forceinline__ void rs_rec_general(uint16_t* sh, int64_t S, int k, int mpar, const int32_t* missing,
+                                               const int32_t* pused, const uint16_t* ex, const uint16_t* lg) {
+    constexpr int NW = 1, G = M < kRsHMaxG ? M : kRsHMaxG, NT = M + M * M;
+    constexpr uint32_t TB = 16 * kRsHBS * NW;
+    static_assert(M * M <= kRsHBS, "one thread per inverse entry");
+    // maps: syndrome multipliers g_r = gf_exp[pu_r + 1] at [r], inverse entry
+    // inv[c][r] at [M + c * M + r]
+    __shared__ __attribute__((aligned(16))) uint32_t ptab[NT][kRs16Tab];
+    __shared__ uint16_t basis[NT][16];
+    __shared__ uint16_t coef[NT];
+    __shared__ uint16_t sV[M * M], sInv[M * M];
+    __shared__ int s_miss[M], s_pu[M], s_desc[M], s_ok;
+    __shared__ __attribute__((aligned(16))) uint8_t stage[TB + 16];
+    if (threadIdx.x < M) {
+        s_miss[threadIdx.x] = missing[threadIdx.x];
+        s_pu[threadIdx.x] = pused[threadIdx.x];
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        int ok = 1;
+        for (int q = 0; q < M; ++q) {
+            ok &= s_miss[q] >= 0 && s_miss[q] < k && s_pu[q] >= 0 && s_pu[q] < mpar;
+            for (int q2 = 0; q2 < q; ++q2) ok &= s_miss[q2] != s_miss[q];
+        }
+        s_ok = ok;
+        // the lost rows from the highest down, the order the syndromes meet them
+        for (int q = 0; q < M; ++q) {
+            int v = s_miss[q], at = q;
+            while (at > 0 && s_desc[at - 1] < v) s_desc[at] = s_desc[at - 1], --at;
+            s_desc[at] = v;
+        }
+    }
+    __syncthreads();
+    if (!s_ok) return;   // uniform: the whole grid writes nothing
+    const uint64_t Sb = uint64_t(S) * 2;
+    const uint64_t ntiles = (Sb + TB - 1) / TB;
+    if (blockIdx.x >= ntiles) return;
+    rs16_gauss_jordan(M, s_miss, s_pu, sV, sInv, ex, lg);
+    for (int e = threadIdx.x; e < NT; e += kRsHBS)
+        coef[e] = e < M ? ex[uint32_t(s_pu[e] + 1) % kGfOrder] : sInv[e - M];
+    __syncthreads();
+    rs_build_perm_tables(ptab, basis, coef, NT, ex, lg);
+    __syncthreads();
+    // indices stay in LDS and are read where used (2 M of them held in scalar
+    // registers beside the loop's own spilled SGPRs for M >= 8)
+    auto desc = [&](int q) { return q < M ? int(lds_uniform(s_desc[q])) : -1; };
+    for (uint64_t tt = blockIdx.x; tt < ntiles; tt += gridDim.x) {
+        const uint64_t t0b = tt * TB;
+        const uint32_t nbytes = uint32_t(Sb - t0b < TB ? Sb - t0b : TB);
+        const bool full = nbytes == TB;
+        uint32_t out[M][NW][4];
+#pragma unroll
+        for (int c = 0; c < M; ++c)
+#pragma unroll
+            for (int n = 0; n < NW; ++n) out[c][n][0] = out[c][n][1] = out[c][n][2] = out[c][n][3] = 0;
+#pragma unroll
+        for (int og = 0; og < M; og += G) {
+            constexpr int GG = G;
+            const int ng = M - og < GG ? M - og : GG;
+            uint32_t acc[GG][NW][4];
+#pragma unroll
+            for (int g = 0; g < GG; ++g)
+#pragma unroll
+                for (int n = 0; n < NW; ++n) acc[g][n][0] = acc[g][n][1] = acc[g][n][2] = acc[g][n][3] = 0;
+            u32x4 x[NW], nx[NW];
+            // nxt: the highest lost row below the rows passed (nl of them lost)
+            int nl = 0, nxt = desc(0);
+            bool have = k - 1 != nxt;
+            if (!have) nxt = desc(++nl);
+            if (have) rs_h_windows<NW>(sh + uint64_t(k - 1) * S, t0b, S, full, x);
+            for (int j = k - 1; j >= 0; --j) {
+                const bool next = j > 0 && j - 1 != nxt;
+                if (j > 0 && !next) nxt = desc(++nl);
+                if (next) rs_h_windows<NW>(sh + uint64_t(j - 1) * S, t0b, S, full, nx);
+                uint32_t y[NW][4];
+#pragma unroll
+                for (int n = 0; n < NW; ++n) {
+                    if (have) split_bytes(x[n], y[n]);
+                    else y[n][0] = y[n][1] = y[n][2] = y[n][3] = 0;
+                }
+#pragma unroll
+                for (int g = 0; g < GG; ++g) {
+                    if (g >= ng) break;
+#pragma unroll
+                    for (int n = 0; n < NW; ++n) gf16_mul_split_xor(acc[g][n], ptab[og + g], y[n]);
+                }
+                if (next) {
+#pragma unroll
+                    for (int n = 0; n < NW; ++n) x[n] = nx[n];
+                }
+                have = next;
+            }
+            // b_r = acc ^ Par_{pu_r}, then out_c ^= inv[c][r] b_r
+#pragma unroll
+            for (int g = 0; g < GG; ++g) {
+                if (g >= ng) break;
+                u32x4 pw[NW];
+                rs_h_windows<NW>(sh + uint64_t(k + int(lds_uniform(s_pu[og + g]))) * S, t0b, S, full, pw);
+#pragma unroll
+                for (int n = 0; n < NW; ++n) {
+                    uint32_t y[4];
+                    split_bytes(pw[n], y);
+                    Gf8Fields f[4];
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) f[q] = gf8_fields(acc[g][n][q] ^ y[q]);
+#pragma unroll
+                    for (int c = 0; c < M; ++c) gf16_fma_split(out[c][n], f, ptab[M + c * M + og + g]);
+                }
+            }
+        }
+#pragma unroll
+        for (int c = 0; c < M; ++c)
+            rs_h_store<NW>(stage, out[c], reinterpret_cast<uint8_t*>(sh + uint64_t(lds_uniform(s_miss[c])) * S) + t0b,
+                           nbytes);
+    }
+}
+
+template <int M>
+__global__ __launch_bounds__(kRsHBS) void rs16_reconstruct_horner_kernel(uint16_t* sh, int64_t S, int k, int mpar,
+                                                                         const int32_t* missing,
+                                                                         const int32_t* pused,
+                                                                         const uint16_t* ex,
+                                                                         const uint16_t* lg) {
+    rs_rec_general<M>(sh, S, k, mpar, missing, pused, ex, lg);
+}
+
 // reconstruct_rs_u16_inplace of M <= 4 lost data rows, any k, on the tiles
 // [0, t_end) of 16-byte-aligned rows whose length is a multiple of 16 bytes
 // (tiles of NW windows of 16 bytes per thread; the last may be partial), when
-// rs_rec_ring_ok holds (else it writes nothing and the general kernel codes
-// every tile).  Syndrome r is b_r = Par_{pu_r} ^ XOR over surviving rows j of
+// rs_rec_ring_ok holds (else the block codes the general kernel's tiles
+// instead, through rs_rec_general: one launch serves either way).  Syndrome r is b_r = Par_{pu_r} ^ XOR over surviving rows j of
 // D_j * g_r^j, g_r = alpha^(pu_r + 1), by Horner's rule over the surviving
 // rows only (highest first): between consecutive survivors j > j' the
 // accumulator is multiplied by g_r^(j - j') -- j - j' steps of gf16_step_pow,
@@ -1691,7 +1821,11 @@ __global__ __launch_bounds__(kRsHBS) void rs16_reconstruct_ring_kernel(uint16_t*
         }
     }
     __syncthreads();
-    if (!s_ok || !rs_rec_ring_ok<M>(s_pu, ex)) return;   // uniform over the grid
+    if (!s_ok) return;   // uniform: the whole grid writes nothing
+    if (!rs_rec_ring_ok<M>(s_pu, ex)) {   // uniform: every tile through the byte maps
+        rs_rec_general<M>(sh, S, k, mpar, missing, pused, ex, lg);
+        return;
+    }
     rs16_gauss_jordan(M, s_miss, s_pu, sV, sInv, ex, lg);
     for (int e = threadIdx.x; e < M * M; e += kRsHBS) coef[e] = sInv[e];
     __syncthreads();
@@ -1822,137 +1956,8 @@ __global__ __launch_bounds__(kRsHBS) void rs16_reconstruct_ring_kernel(uint16_t*
     }
 }
 
-// reconstruct_rs_u16_inplace of M lost data rows, any k (inputs: the
-// surviving data rows and the parity rows of parity_used).  sh: the shard
-// tensor, rows of S words.  Out-of-range or repeated lost rows, or parity rows
-// outside the tensor, write nothing.
-template <int M>
-__global__ __launch_bounds__(kRsHBS) void rs16_reconstruct_horner_kernel(uint16_t* sh, int64_t S, int k, int mpar,
-                                                                         const int32_t* missing,
-                                                                         const int32_t* pused,
-                                                                         const uint16_t* ex,
-                                                                         const uint16_t* lg,
-                                                                         uint64_t ring_tiles) {
-    constexpr int NW = 1, G = M < kRsHMaxG ? M : kRsHMaxG, NT = M + M * M;
-    constexpr uint32_t TB = 16 * kRsHBS * NW;
-    static_assert(M * M <= kRsHBS, "one thread per inverse entry");
-    // maps: syndrome multipliers g_r = gf_exp[pu_r + 1] at [r], inverse entry
-    // inv[c][r] at [M + c * M + r]
-    __shared__ __attribute__((aligned(16))) uint32_t ptab[NT][kRs16Tab];
-    __shared__ uint16_t basis[NT][16];
-    __shared__ uint16_t coef[NT];
-    __shared__ uint16_t sV[M * M], sInv[M * M];
-    __shared__ int s_miss[M], s_pu[M], s_desc[M], s_ok;
-    __shared__ __attribute__((aligned(16))) uint8_t stage[TB + 16];
-    if (threadIdx.x < M) {
-        s_miss[threadIdx.x] = missing[threadIdx.x];
-        s_pu[threadIdx.x] = pused[threadIdx.x];
-    }
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        int ok = 1;
-        for (int q = 0; q < M; ++q) {
-            ok &= s_miss[q] >= 0 && s_miss[q] < k && s_pu[q] >= 0 && s_pu[q] < mpar;
-            for (int q2 = 0; q2 < q; ++q2) ok &= s_miss[q2] != s_miss[q];
-        }
-        s_ok = ok;
-        // the lost rows from the highest down, the order the syndromes meet them
-        for (int q = 0; q < M; ++q) {
-            int v = s_miss[q], at = q;
-            while (at > 0 && s_desc[at - 1] < v) s_desc[at] = s_desc[at - 1], --at;
-            s_desc[at] = v;
-        }
-    }
-    __syncthreads();
-    if (!s_ok) return;   // uniform: the whole grid writes nothing
-    const uint64_t Sb = uint64_t(S) * 2;
-    const uint64_t ntiles = (Sb + TB - 1) / TB;
-    // the tiles [0, ring_tiles) are rs16_reconstruct_ring_kernel's when it runs
-    // (ring_tiles may pass the last tile: then this kernel writes nothing)
-    const uint64_t t_first = rs_rec_ring_ok<M>(s_pu, ex) ? ring_tiles : 0;
-    if (blockIdx.x + t_first >= ntiles) return;
-    rs16_gauss_jordan(M, s_miss, s_pu, sV, sInv, ex, lg);
-    for (int e = threadIdx.x; e < NT; e += kRsHBS)
-        coef[e] = e < M ? ex[uint32_t(s_pu[e] + 1) % kGfOrder] : sInv[e - M];
-    __syncthreads();
-    rs_build_perm_tables(ptab, basis, coef, NT, ex, lg);
-    __syncthreads();
-    // indices stay in LDS and are read where used (2 M of them held in scalar
-    // registers beside the loop's own spilled SGPRs for M >= 8)
-    auto desc = [&](int q) { return q < M ? int(lds_uniform(s_desc[q])) : -1; };
-    for (uint64_t tt = blockIdx.x + t_first; tt < ntiles; tt += gridDim.x) {
-        const uint64_t t0b = tt * TB;
-        const uint32_t nbytes = uint32_t(Sb - t0b < TB ? Sb - t0b : TB);
-        const bool full = nbytes == TB;
-        uint32_t out[M][NW][4];
-#pragma unroll
-        for (int c = 0; c < M; ++c)
-#pragma unroll
-            for (int n = 0; n < NW; ++n) out[c][n][0] = out[c][n][1] = out[c][n][2] = out[c][n][3] = 0;
-#pragma unroll
-        for (int og = 0; og < M; og += G) {
-            constexpr int GG = G;
-            const int ng = M - og < GG ? M - og : GG;
-            uint32_t acc[GG][NW][4];
-#pragma unroll
-            for (int g = 0; g < GG; ++g)
-#pragma unroll
-                for (int n = 0; n < NW; ++n) acc[g][n][0] = acc[g][n][1] = acc[g][n][2] = acc[g][n][3] = 0;
-            u32x4 x[NW], nx[NW];
-            // nxt: the highest lost row below the rows passed (nl of them lost)
-            int nl = 0, nxt = desc(0);
-            bool have = k - 1 != nxt;
-            if (!have) nxt = desc(++nl);
-            if (have) rs_h_windows<NW>(sh + uint64_t(k - 1) * S, t0b, S, full, x);
-            for (int j = k - 1; j >= 0; --j) {
-                const bool next = j > 0 && j - 1 != nxt;
-                if (j > 0 && !next) nxt = desc(++nl);
-                if (next) rs_h_windows<NW>(sh + uint64_t(j - 1) * S, t0b, S, full, nx);
-                uint32_t y[NW][4];
-#pragma unroll
-                for (int n = 0; n < NW; ++n) {
-                    if (have) split_bytes(x[n], y[n]);
-                    else y[n][0] = y[n][1] = y[n][2] = y[n][3] = 0;
-                }
-#pragma unroll
-                for (int g = 0; g < GG; ++g) {
-                    if (g >= ng) break;
-#pragma unroll
-                    for (int n = 0; n < NW; ++n) gf16_mul_split_xor(acc[g][n], ptab[og + g], y[n]);
-                }
-                if (next) {
-#pragma unroll
-                    for (int n = 0; n < NW; ++n) x[n] = nx[n];
-                }
-                have = next;
-            }
-            // b_r = acc ^ Par_{pu_r}, then out_c ^= inv[c][r] b_r
-#pragma unroll
-            for (int g = 0; g < GG; ++g) {
-                if (g >= ng) break;
-                u32x4 pw[NW];
-                rs_h_windows<NW>(sh + uint64_t(k + int(lds_uniform(s_pu[og + g]))) * S, t0b, S, full, pw);
-#pragma unroll
-                for (int n = 0; n < NW; ++n) {
-                    uint32_t y[4];
-                    split_bytes(pw[n], y);
-                    Gf8Fields f[4];
-#pragma unroll
-                    for (int q = 0; q < 4; ++q) f[q] = gf8_fields(acc[g][n][q] ^ y[q]);
-#pragma unroll
-                    for (int c = 0; c < M; ++c) gf16_fma_split(out[c][n], f, ptab[M + c * M + og + g]);
-                }
-            }
-        }
-#pragma unroll
-        for (int c = 0; c < M; ++c)
-            rs_h_store<NW>(stage, out[c], reinterpret_cast<uint8_t*>(sh + uint64_t(lds_uniform(s_miss[c])) * S) + t0b,
-                           nbytes);
-    }
-}
-
 typedef void (*RsRecHornerFn)(uint16_t*, int64_t, int, int, const int32_t*, const int32_t*, const uint16_t*,
-                              const uint16_t*, uint64_t);
+                              const uint16_t*);
 template <int... I>
 struct RsRecHornerTable {
     static constexpr RsRecHornerFn fn[sizeof...(I)] = {rs16_reconstruct_horner_kernel<I + 1>...};
@@ -2107,34 +2112,38 @@ extern "C" int kvec_rs16_reconstruct(void* shards, int shard_size, int data_shar
     if (shard_size == 0) return KVEC_OK;
     if (int64_t(data_shards) * m > kRsMaxTables) {
         // k * m maps beyond the LDS tables: syndromes by Horner's rule.  Up to
-        // four lost rows over 16-byte-aligned rows: the full tiles on the ring
-        // kernel (doubling chains, when the tables and parity rows allow them;
-        // both kernels evaluate that test), the rest on the byte-map kernel.
+        // four lost rows over 16-byte-aligned rows: the ring kernel, whose
+        // blocks take the byte-map tiles instead when the tables or parity rows
+        // do not allow doubling chains; otherwise the byte-map kernel.
         // Windows per thread of the ring tiles by M (measured on the 512 MiB
         // stream: one for two lost rows, 121-123 against 123-127 us; two for
-        // the others, four lost rows 217 against 225 us).  The ring takes
-        // every tile, a partial last one included.
+        // the others, four lost rows 217 against 225 us).
         constexpr uint32_t TB = 16 * kRsHBS;
         const uint32_t ring_nw = m == 2 ? 1 : 2;
         const uint64_t Sb = uint64_t(shard_size) * 2;
         const bool aligned = (reinterpret_cast<uintptr_t>(shards) & 15) == 0 && Sb % 16 == 0;
-        const uint64_t nring = m <= 4 && aligned ? (Sb + TB * ring_nw - 1) / (TB * ring_nw) : 0;
         hipStream_t st = as_stream(stream);
-        hipLaunchKernelGGL(RsRecHorner::fn[m - 1], dim3(rs_h_grid(shard_size, TB)), dim3(kRsHBS), 0, st,
-                           (uint16_t*)shards, int64_t(shard_size), data_shards, parity_shards, missing_data,
-                           parity_used, gf_exp, gf_log, nring * ring_nw);
-        if (nring) {
-            const dim3 grid(unsigned(nring < uint64_t(kRsHGrid) ? nring : uint64_t(kRsHGrid)));
-            auto ring = [&](auto kern) {
-                hipLaunchKernelGGL(kern, grid, dim3(kRsHBS), 0, st, (uint16_t*)shards, int64_t(shard_size),
-                                   data_shards, parity_shards, missing_data, parity_used, gf_exp, gf_log, nring);
-            };
-            switch (m) {
-                case 1: ring(rs16_reconstruct_ring_kernel<1, 2>); break;
-                case 2: ring(rs16_reconstruct_ring_kernel<2, 1>); break;
-                case 3: ring(rs16_reconstruct_ring_kernel<3, 2>); break;
-                default: ring(rs16_reconstruct_ring_kernel<4, 2>); break;
-            }
+        if (m > 4 || !aligned) {
+            hipLaunchKernelGGL(RsRecHorner::fn[m - 1], dim3(rs_h_grid(shard_size, TB)), dim3(kRsHBS), 0, st,
+                               (uint16_t*)shards, int64_t(shard_size), data_shards, parity_shards, missing_data,
+                               parity_used, gf_exp, gf_log);
+            return check_launch("kvec_rs16_reconstruct");
+        }
+        // the ring's tiles, a partial last one included; its grid also serves
+        // the byte-map tiles (walked by grid stride)
+        const uint64_t nring = (Sb + TB * ring_nw - 1) / (TB * ring_nw);
+        const uint64_t nmap = (Sb + TB - 1) / TB;
+        const uint64_t nblk = nring > nmap ? nring : nmap;
+        const dim3 grid(unsigned(nblk < uint64_t(kRsHGrid) ? nblk : uint64_t(kRsHGrid)));
+        auto ring = [&](auto kern) {
+            hipLaunchKernelGGL(kern, grid, dim3(kRsHBS), 0, st, (uint16_t*)shards, int64_t(shard_size), data_shards,
+                               parity_shards, missing_data, parity_used, gf_exp, gf_log, nring);
+        };
+        switch (m) {
+            case 1: ring(rs16_reconstruct_ring_kernel<1, 2>); break;
+            case 2: ring(rs16_reconstruct_ring_kernel<2, 1>); break;
+            case 3: ring(rs16_reconstruct_ring_kernel<3, 2>); break;
+            default: ring(rs16_reconstruct_ring_kernel<4, 2>); break;
         }
         return check_launch("kvec_rs16_reconstruct");
     }
