@@ -157,19 +157,26 @@ def time_kernel(torch, fn, sets, steps, warmup):
 
 
 def time_us(torch, fn, n=8, pre=2):
-    """Average microseconds of `n` launches of fn(i) after `pre` untimed ones."""
+    """Microseconds per launch of fn(i): `n` launches back to back after `pre`
+    untimed ones, an event between every two, and the median of the `n`
+    intervals.  A host stall between two launches leaves the GPU idle and
+    stretches one interval only (seen once with a single pair of events
+    around all n launches: a decode averaging 806 us against 121 us in every
+    other run); the median keeps it out of the figure.  The launch count stays
+    small on purpose: VALU-heavy kernels slow down after a few milliseconds
+    of back-to-back launches."""
     stream = torch.cuda.current_stream()
     for i in range(pre):
         fn(i)
     torch.cuda.synchronize()
-    e0 = torch.cuda.Event(enable_timing=True)
-    e1 = torch.cuda.Event(enable_timing=True)
-    e0.record(stream)
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(n + 1)]
+    ev[0].record(stream)
     for i in range(n):
         fn(i)
-    e1.record(stream)
+        ev[i + 1].record(stream)
     torch.cuda.synchronize()
-    return e0.elapsed_time(e1) * 1e3 / n
+    per = sorted(ev[i].elapsed_time(ev[i + 1]) * 1e3 for i in range(n))
+    return (per[n // 2 - 1] + per[n // 2]) / 2 if n % 2 == 0 else per[n // 2]
 
 
 def decode_all_pairs(pkg, torch, sets, R, seed):
