@@ -202,61 +202,66 @@ struct RsDecodeIo {
     int dst_shard[kChunkMaxM];
 };
 
-// Rows pipelined as in the encode, with a ring of three rows of references
-// (a row's output references are still needed when its stores issue).
+// One row per wave, as in the encode: a block of ROWS waves owns one 1 KiB
+// column piece of a stripe and wave r decodes row r (RS mixes no rows).  Each
+// wave requests its K inputs' page-table entries, then the cells (parity
+// inputs straight from their buffers), stages the coefficient tables while they
+// load, and stores its NOUT outputs.  Lanes past a short last stripe's end
+// take the row's offset 0, compute lane 0's values and store them to lane 0's
+// addresses.  A wave walking its column's rows (two in flight, references in a
+// ring of three rows, 128-thread blocks) decoded the 16 x 2048-token fp8
+// chunk's three lost data shards in 114.5 us.
 template <int ROWS, int K, int NOUT>
-__global__ __launch_bounds__(kCBS) void chunk_rs_decode_kernel(PagedGeom g, ChunkGeom cg,
-                                                               RsDecodeIo io, Gf8Tab<K * NOUT> mix) {
+__global__ __launch_bounds__(ROWS * 64) void chunk_rs_decode_kernel(PagedGeom g, ChunkGeom cg, RsDecodeIo io,
+                                                                    Gf8Tab<K * NOUT> mix) {
     __shared__ uint32_t tab[K * NOUT][6];
-    stage_tables<K * NOUT>(tab, mix);
-    const ChunkPos cp = chunk_pos(g, cg, ROWS);
-    if (!cp.ok) return;
-    const uint32_t inner = cp.inner, lane = cp.o;
+    const int r = int(__builtin_amdgcn_readfirstlane(threadIdx.x >> 6));
+    const uint32_t lane = threadIdx.x & 63;
+    const RdpWave w = rdp_wave(cg.geo, ROWS, blockIdx.x, lane);
+    const uint32_t piece = uint32_t(__builtin_amdgcn_readfirstlane(w.within));  // lane 0: the piece's start
+    if (piece >= w.g) return;   // the whole block: its piece starts past the short stripe's end
+    const uint32_t o = w.within < w.g ? w.within : 0u;
+    const uint32_t w0 = fdiv(o, g.div_rec);
+    const uint32_t inner = o - w0 * g.rec;
+    const uint32_t rbase = uint32_t(r) * fdiv(uint32_t(w.g), g.div_rec) + fdiv(uint32_t(w.base), g.div_rec);
+    const uint32_t dmax = fdiv(piece + kRdpWaveBytes - 16, g.div_rec);
+    const uint32_t soff = cg.region + uint32_t(w.base) + uint32_t(r) * uint32_t(w.g) + o;
     const uint64_t nb = cg.nb;
-    auto rec = [&](int shard, int r) { return cell_rec(cg, cp, shard, r); };
-    auto row = [&](int r) { return cp.rowbase + uint32_t(r) * cp.g; };
-    CellRef rin[3][K], rout[3][NOUT];
-    auto refs = [&](int r) {
+    CellRef rin[K], rout[NOUT];
 #pragma unroll
-        for (int q = 0; q < K; ++q)
-            if (!io.in_buf[q]) rin[r % 3][q] = cell_ref(g, rec(io.src_shard[q], r));
+    for (int q = 0; q < K; ++q)
+        if (!io.in_buf[q]) rin[q] = cell_ref_run(g, uint32_t(io.src_shard[q]) * cg.recs_per_shard + rbase, w0, dmax);
 #pragma unroll
-        for (int i = 0; i < NOUT; ++i)
-            if (io.dst_shard[i] >= 0) rout[r % 3][i] = cell_ref(g, rec(io.dst_shard[i], r));
-    };
-    auto load_in = [&](int q, int r) {
-        return io.in_buf[q] ? ShardView<true>(io.in_buf[q], nb).load(row(r), lane)
-                            : cell_load_ref(g, rin[r % 3][q], inner);
-    };
-    u32x4 x[2][K];
-    refs(0);
-    if constexpr (ROWS > 1) refs(1);
+    for (int i = 0; i < NOUT; ++i)
+        if (io.dst_shard[i] >= 0)
+            rout[i] = cell_ref_run(g, uint32_t(io.dst_shard[i]) * cg.recs_per_shard + rbase, w0, dmax);
+    u32x4 x[K];
 #pragma unroll
-    for (int q = 0; q < K; ++q) x[0][q] = load_in(q, 0);
+    for (int q = 0; q < K; ++q)
+        x[q] = io.in_buf[q] ? ShardView<true>(io.in_buf[q], nb).load(0, soff) : cell_load_ref(g, rin[q], inner);
+    stage_tables<K * NOUT>(tab, mix);   // while the cells load
+    u32x4 acc[NOUT];
 #pragma unroll
-    for (int r = 0; r < ROWS; ++r) {
-        const int c = r & 1;
-        if (r + 1 < ROWS) {
+    for (int i = 0; i < NOUT; ++i) acc[i] = u32x4{0, 0, 0, 0};
 #pragma unroll
-            for (int q = 0; q < K; ++q) x[c ^ 1][q] = load_in(q, r + 1);
-        }
-        if (r + 2 < ROWS) refs(r + 2);
-        u32x4 acc[NOUT];
-#pragma unroll
-        for (int i = 0; i < NOUT; ++i) acc[i] = u32x4{0, 0, 0, 0};
-#pragma unroll
-        for (int q = 0; q < K; ++q) {
-            Gf8Fields f[4];
-            gf8_fields16(x[c][q], f);
-#pragma unroll
-            for (int i = 0; i < NOUT; ++i) acc[i] = gf8_fma16(acc[i], f, tab[i * K + q]);
-        }
+    for (int q = 0; q < K; ++q) {
+        Gf8Fields f[4];
+        gf8_fields16(x[q], f);
 #pragma unroll
         for (int i = 0; i < NOUT; ++i) {
-            if (io.dst_shard[i] >= 0) cell_store_ref(g, rout[r % 3][i], inner, acc[i]);
-            if (io.out_buf[i]) ShardView<true>(io.out_buf[i], nb).store(row(r), lane, acc[i]);
+            acc[i] = gf8_fma16(acc[i], f, tab[i * K + q]);
+            // the products are formed here, input by input, with each
+            // input's tables read from LDS next to their use: left free, the
+            // compiler sinks each output's products into its store branch and
+            // keeps every input's fields live (138 VGPRs for five inputs and
+            // three outputs)
+            asm volatile("" : "+v"(acc[i].x), "+v"(acc[i].y), "+v"(acc[i].z), "+v"(acc[i].w)::"memory");
         }
-        asm volatile("" ::: "memory");
+    }
+#pragma unroll
+    for (int i = 0; i < NOUT; ++i) {
+        if (io.dst_shard[i] >= 0) cell_store_ref(g, rout[i], inner, acc[i]);
+        if (io.out_buf[i]) ShardView<true>(io.out_buf[i], nb).store(0, soff, acc[i]);
     }
 }
 
@@ -403,16 +408,18 @@ static EncLauncher encode_launcher(int p, int k, int m) {
 }
 
 template <int ROWS, int K, int NOUT>
-static void launch_rs_decode(dim3 grid, hipStream_t st, const PagedGeom& g, const ChunkGeom& cg,
-                             const RsDecodeIo& io, const uint32_t (*tab)[6]) {
+static void launch_rs_decode(hipStream_t st, const PagedGeom& g, const ChunkGeom& cg, const RsDecodeIo& io,
+                             const uint32_t (*tab)[6]) {
     Gf8Tab<K * NOUT> t{};
     for (int i = 0; i < K * NOUT; ++i)
         for (int e = 0; e < 6; ++e) t.t[i][e] = tab[i][e];
-    hipLaunchKernelGGL((chunk_rs_decode_kernel<ROWS, K, NOUT>), grid, dim3(kCBS), 0, st, g, cg, io, t);
+    // one block of ROWS waves per 1 KiB column piece
+    hipLaunchKernelGGL((chunk_rs_decode_kernel<ROWS, K, NOUT>), dim3(cg.nwaves), dim3(ROWS * 64), 0, st, g, cg, io,
+                       t);
 }
 
-typedef void (*RsDecLauncher)(dim3, hipStream_t, const PagedGeom&, const ChunkGeom&,
-                              const RsDecodeIo&, const uint32_t (*)[6]);
+typedef void (*RsDecLauncher)(hipStream_t, const PagedGeom&, const ChunkGeom&, const RsDecodeIo&,
+                              const uint32_t (*)[6]);
 
 template <int ROWS, int K, int N = 1>
 RsDecLauncher pick_rs_dec_n(int n) {
@@ -640,7 +647,7 @@ extern "C" int kvec_chunk_decode_paged(const kvec_paged_kv* kv, void* pool,
         for (int i = 0; i < no * k; ++i) perm_tables(M[i], tab[i]);
         RsDecLauncher L = rs_dec_launcher(a.p, k, no);
         if (!L) return set_error(KVEC_EUNSUPPORTED, "%s: p=%d k=%d with %d outputs not built", fn, a.p, k, no);
-        L(grid, hs, a.g, a.cg, io, tab);
+        L(hs, a.g, a.cg, io, tab);
         rc = check_launch(fn);
         if (rc) return rc;
     } else if (nd > 0 && nd + int(eP) + int(eQ) <= 2) {
