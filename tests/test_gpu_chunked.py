@@ -147,6 +147,34 @@ def test_chunked_decode_restores_pool(pkg, gpu, keep_data):
             assert torch.equal(t, r), (er, j)
 
 
+@pytest.mark.parametrize("unit", [2048, 4096])
+def test_chunked_decode_short_last_stripe(pkg, gpu, unit):
+    """Rows of 4608 bytes in stripes of `unit` bytes (the encode test's shape):
+    the decode's blocks own one 1 KiB piece of a stripe, and those whose piece
+    starts past the short last stripe's end must write nothing, on the RS path
+    (one to three lost data shards) and the RDP path (data with RS parity
+    lost); the pool and every shard restored."""
+    L, B, pps, pt, H, D, k, p, m, ct = (2, 4, 8, 16, 1, 128, 5, 7, 3, 64)
+    _, _, pool_d, table_d, nc, st = setup(pkg, gpu, L, B, pps, pt, H, D, k, p, m, ct, True,
+                                          seed=11 + unit, unit_bytes=unit)
+    assert st.width == 4608 and st.width % unit != 0 and nc == 2
+    for c in range(nc):
+        st.encode(pkg.chunked.chunk_kv(pool_d, table_d, c, ct), c)
+    torch.cuda.synchronize()
+    ref_pool = pool_d.clone()
+    ref_sh = [t.clone() for t in st.shards()]
+    gen = torch.Generator().manual_seed(12)
+    for i, er in enumerate([[0], [1, 4], [0, 2, 3], [2, 7], [0, 7, 8], [1, 3, 7, 8, 9]]):
+        c = i % nc
+        kv = pkg.chunked.chunk_kv(pool_d, table_d, c, ct)
+        erase(pkg, st, kv, c, er, gen)
+        st.decode(kv, c, er)
+        torch.cuda.synchronize()
+        assert torch.equal(pool_d.view(torch.uint8), ref_pool.view(torch.uint8)), (unit, er)
+        for j, (t, r) in enumerate(zip(st.shards(), ref_sh)):
+            assert torch.equal(t, r), (unit, er, j)
+
+
 def test_chunked_decode_rejects_undecodable(pkg, gpu):
     L, B, pps, pt, H, D, k, p, m, ct = CONFIGS[0]
     _, _, pool_d, table_d, nc, st = setup(pkg, gpu, L, B, pps, pt, H, D, k, p, m, ct, False, seed=4)
