@@ -304,54 +304,133 @@ __global__ __launch_bounds__(kCBS) void chunk_rdp_decode_kernel(PagedGeom g, Chu
     }
 }
 
-// The same map solved at compile time (p = 7, k = 5, the chunked shape): every
-// needed cell is loaded once (page-table entries first), then the erased
-// cells are straight-line XORs of registers.
+// RS parities the RDP decode re-encodes in the same pass: n of them, to
+// out[0..n), with the encode's Cauchy rows of those parities as the tables.
+struct RsReenc {
+    uint8_t* out[kChunkMaxM];
+    int n;
+};
+
+// The same map solved at compile time (p = 7, k = 5, the chunked shape), one
+// row per wave: a block of p - 1 waves owns one 1 KiB column piece.  Wave r
+// loads the cells of row r that the map needs (page-table entries first; P and
+// Q from their buffers) and publishes them in LDS; after one barrier it
+// rebuilds the lost cells of row r from LDS (straight-line XORs of the map)
+// and stores them.  With RS parities lost as well, it then holds all k data
+// cells of its row (the surviving ones loaded, the rebuilt ones computed) and
+// re-encodes those parities of row r, so the data shards are read once.
+// Lanes past a short last stripe's end take offset 0 of the row, as in the
+// encode.  A wave walking its whole column (every needed cell in registers,
+// 146-178 VGPRs, 2-3 waves per SIMD) followed by a separate RS re-encode
+// took 77 + 78 us for two lost data shards and the three RS parities of the
+// 16 x 2048-token fp8 chunk.
 template <int P, int K, int E0, int E1>
-__global__ __launch_bounds__(kCBS) void chunk_rdp_decode_fixed(PagedGeom g, ChunkGeom cg,
-                                                               Ptrs<kChunkMaxK> d, uint8_t* Pp,
-                                                               uint8_t* Qp) {
+__global__ __launch_bounds__((P - 1) * 64) void chunk_rdp_decode_rows(PagedGeom g, ChunkGeom cg,
+                                                                      Ptrs<kChunkMaxK> d, uint8_t* Pp,
+                                                                      uint8_t* Qp, RsReenc rs,
+                                                                      Gf8Tab<K * kChunkMaxM> rtab) {
     constexpr int ROWS = P - 1, NC = (K + 2) * ROWS;
     constexpr RdpPlan plan = make_rdp_plan(P, K, E0, E1);
     static_assert(plan.ok, "RDP erasure pattern not decodable");
-    const ChunkPos cp = chunk_pos(g, cg, ROWS);
-    if (!cp.ok) return;
-    const uint32_t inner = cp.inner, lane = cp.o;
+    static_assert(NC <= 64, "the map's cells in one mask word");
+    constexpr uint64_t need = plan.need[0];
+    constexpr int NS = __builtin_popcountll(need);
+    __shared__ u32x4 cells[NS][64];   // the needed cells in cell order, lane-major
+    __shared__ uint32_t tab[K * kChunkMaxM][6];
+    const int r = int(__builtin_amdgcn_readfirstlane(threadIdx.x >> 6));
+    const uint32_t lane = threadIdx.x & 63;
+    const RdpWave w = rdp_wave(cg.geo, ROWS, blockIdx.x, lane);
+    const uint32_t piece = uint32_t(__builtin_amdgcn_readfirstlane(w.within));  // lane 0: the piece's start
+    if (piece >= w.g) return;   // the whole block: its piece starts past the short stripe's end
+    const uint32_t o = w.within < w.g ? w.within : 0u;
+    const uint32_t w0 = fdiv(o, g.div_rec);
+    const uint32_t inner = o - w0 * g.rec;
+    const uint32_t rbase = uint32_t(r) * fdiv(uint32_t(w.g), g.div_rec) + fdiv(uint32_t(w.base), g.div_rec);
+    const uint32_t dmax = fdiv(piece + kRdpWaveBytes - 16, g.div_rec);
+    const uint32_t soff = cg.region + uint32_t(w.base) + uint32_t(r) * uint32_t(w.g) + o;
     const uint64_t nb = cg.nb;
-    auto row = [&](int r) { return cp.rowbase + uint32_t(r) * cp.g; };
-    auto needed = [&](int c) { return (plan.need[c >> 6] >> (c & 63)) & 1; };
-    CellRef ref[NC], refo[plan.nout];   // c = shard * ROWS + row
-#pragma unroll
-    for (int c = 0; c < NC; ++c)
-        if (c < K * ROWS && needed(c)) ref[c] = cell_ref(g, cell_rec(cg, cp, c / ROWS, c % ROWS));
-#pragma unroll
-    for (int i = 0; i < plan.nout; ++i)
-        if (plan.out_cell[i] < K * ROWS)
-            refo[i] = cell_ref(g, cell_rec(cg, cp, plan.out_cell[i] / ROWS, plan.out_cell[i] % ROWS));
-    __builtin_amdgcn_sched_barrier(0);
     const ShardView<true> sp(Pp, nb), sq(Qp, nb);
-    u32x4 x[NC];
+    auto needed = [&](int c) { return ((need >> c) & 1) != 0; };
+    auto lost = [](int sh) { return sh == E0 || sh == E1; };
+    const bool reenc = rs.n > 0;
+    // this row's cells: the needed ones, and every surviving data cell when
+    // RS parities are re-encoded.  Every load is issued; one not wanted reads
+    // the zero cell (data) or nothing (P, Q through an empty resource).  Loads
+    // under per-row conditions left the compiler merging register copies of
+    // the cells at every join (400 moves, 149 VGPRs for one lost shard).
+    CellRef ref[K];
 #pragma unroll
-    for (int c = 0; c < NC; ++c) {
-        if (!needed(c)) continue;
-        const int s = c / ROWS, r = c % ROWS;
-        x[c] = s < K ? cell_load_ref(g, ref[c], inner) : (s == K ? sp : sq).load(row(r), lane);
+    for (int sh = 0; sh < K; ++sh) {
+        if (lost(sh)) continue;
+        ref[sh] = cell_ref_run(g, uint32_t(sh) * cg.recs_per_shard + rbase, w0, dmax);
+        if (!(reenc || needed(sh * ROWS + r))) ref[sh].base = kNoCell;
     }
-    __builtin_amdgcn_sched_barrier(0);
+    u32x4 x[K + 2];
+#pragma unroll
+    for (int sh = 0; sh < K; ++sh)
+        if (!lost(sh)) x[sh] = cell_load_ref(g, ref[sh], inner);
+    if (!lost(K)) x[K] = ShardView<true>(Pp, needed(K * ROWS + r) ? nb : 0).load(0, soff);
+    if (!lost(K + 1)) x[K + 1] = ShardView<true>(Qp, needed((K + 1) * ROWS + r) ? nb : 0).load(0, soff);
+    if (reenc)   // uniform; the barrier inside also orders the tables before their use
+        stage_tables<K * kChunkMaxM>(tab, rtab);
+    // publish the row's needed cells (slot = needed cells before c)
+#pragma unroll
+    for (int sh = 0; sh < K + 2; ++sh) {
+        if (lost(sh)) continue;
+        const int c = sh * ROWS + r;
+        if (needed(c)) cells[__builtin_popcountll(need & ((uint64_t(1) << c) - 1))][lane] = x[sh];
+    }
+    __syncthreads();
+    // the lost cells of row r
 #pragma unroll
     for (int i = 0; i < plan.nout; ++i) {
+        const int oc = plan.out_cell[i], osh = oc / ROWS;
+        if (oc % ROWS != r) continue;
+        // each output's LDS reads stay inside its branch: hoisted, the reads
+        // of all the map's outputs are held at once
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_sched_barrier(0);
         u32x4 acc = {0, 0, 0, 0};
+        int terms = 0;   // a compile-time count after unrolling
 #pragma unroll
-        for (int c = 0; c < NC; ++c)
-            if ((plan.mask[i][c >> 6] >> (c & 63)) & 1) acc ^= x[c];
-        const int c = plan.out_cell[i], s = c / ROWS, r = c % ROWS;
-        if (s < K) {
-            cell_store_ref(g, refo[i], inner, acc);
-            if (d.p[s]) st_stream(d.p[s] + uint64_t(row(r)), lane, acc);
+        for (int c = 0; c < NC; ++c) {
+            if (!((plan.mask[i][0] >> c) & 1)) continue;
+            acc ^= cells[__builtin_popcountll(need & ((uint64_t(1) << c) - 1))][lane];
+            // four LDS reads in flight at a time: unfenced, all of an output's
+            // reads are issued first (90 VGPRs for a pair of lost shards)
+            if (++terms % 4 == 0) asm volatile("" : "+v"(acc.x), "+v"(acc.y), "+v"(acc.z), "+v"(acc.w)::"memory");
+        }
+        if (osh < K) {
+            const CellRef oref = cell_ref_run(g, uint32_t(osh) * cg.recs_per_shard + rbase, w0, dmax);
+            cell_store_ref(g, oref, inner, acc);
+            if (d.p[osh]) st_stream(d.p[osh], soff, acc);
         } else {
-            (s == K ? sp : sq).store(row(r), lane, acc);
+            (osh == K ? sp : sq).store(0, soff, acc);
+        }
+        x[osh] = acc;
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    if (!reenc) return;
+    // the lost RS parities of row r from its k data cells
+    u32x4 racc[kChunkMaxM];
+#pragma unroll
+    for (int j = 0; j < kChunkMaxM; ++j) racc[j] = u32x4{0, 0, 0, 0};
+#pragma unroll
+    for (int sh = 0; sh < K; ++sh) {
+        Gf8Fields f[4];
+        gf8_fields16(x[sh], f);
+#pragma unroll
+        for (int j = 0; j < kChunkMaxM; ++j) {
+            if (j >= rs.n) break;
+            racc[j] = gf8_fma16(racc[j], f, tab[j * K + sh]);
+            // formed here, input by input (see chunk_rs_decode_kernel)
+            asm volatile("" : "+v"(racc[j].x), "+v"(racc[j].y), "+v"(racc[j].z), "+v"(racc[j].w)::"memory");
         }
     }
+#pragma unroll
+    for (int j = 0; j < kChunkMaxM; ++j)
+        if (j < rs.n) ShardView<true>(rs.out[j], nb).store(0, soff, racc[j]);
 }
 
 // ------------------------------------------------------------------ dispatch
@@ -451,29 +530,31 @@ static RsDecLauncher rs_dec_launcher(int p, int k, int n) {
     }
 }
 
-typedef void (*RdpFixedFn)(PagedGeom, ChunkGeom, Ptrs<kChunkMaxK>, uint8_t*, uint8_t*);
+template <int K>
+using RdpRowsFn = void (*)(PagedGeom, ChunkGeom, Ptrs<kChunkMaxK>, uint8_t*, uint8_t*, RsReenc,
+                           Gf8Tab<K * kChunkMaxM>);
 
 template <int P, int K, int E0, int E1 = E0 + 1>
-RdpFixedFn pick_rdp_fixed_pair(int e1) {
+RdpRowsFn<K> pick_rdp_rows_pair(int e1) {
     if constexpr (E1 > K + 1) {
         return nullptr;
     } else {
-        if (e1 == E1) return &chunk_rdp_decode_fixed<P, K, E0, E1>;
-        return pick_rdp_fixed_pair<P, K, E0, E1 + 1>(e1);
+        if (e1 == E1) return &chunk_rdp_decode_rows<P, K, E0, E1>;
+        return pick_rdp_rows_pair<P, K, E0, E1 + 1>(e1);
     }
 }
 
 // Patterns with at least one data shard (the only ones that reach the RDP path).
 template <int P, int K, int E0 = 0>
-RdpFixedFn pick_rdp_fixed(int e0, int e1) {
+RdpRowsFn<K> pick_rdp_rows(int e0, int e1) {
     if constexpr (E0 >= K) {
         return nullptr;
     } else {
         if (e0 == E0) {
-            if (e1 < 0) return &chunk_rdp_decode_fixed<P, K, E0, -1>;
-            return pick_rdp_fixed_pair<P, K, E0>(e1);
+            if (e1 < 0) return &chunk_rdp_decode_rows<P, K, E0, -1>;
+            return pick_rdp_rows_pair<P, K, E0>(e1);
         }
-        return pick_rdp_fixed<P, K, E0 + 1>(e0, e1);
+        return pick_rdp_rows<P, K, E0 + 1>(e0, e1);
     }
 }
 
@@ -658,17 +739,30 @@ extern "C" int kvec_chunk_decode_paged(const kvec_paged_kv* kv, void* pool,
         RdpPlan plan = make_rdp_plan(a.p, k, e[0], e[1]);
         if (!plan.ok) return set_error(KVEC_EDECODE, "%s: RDP pattern (%d, %d) not decodable", fn, e[0], e[1]);
         Ptrs<kChunkMaxK> dd = a.have_data ? a.d : Ptrs<kChunkMaxK>{};
-        RdpFixedFn fx = (a.p == 7 && k == 5) ? pick_rdp_fixed<7, 5>(e[0], e[1]) : nullptr;
-        if (fx)
-            hipLaunchKernelGGL(fx, grid, dim3(kCBS), 0, hs, a.g, a.cg, dd, a.par.p[0], a.par.p[1]);
-        else
-            hipLaunchKernelGGL(chunk_rdp_decode_kernel, grid, dim3(kCBS), 0, hs, a.g, a.cg, k, rows, dd,
-                               a.par.p[0], a.par.p[1], plan);
-        rc = check_launch(fn);
-        if (rc) return rc;
         reenc = 0;
         for (int i = 0; i < m; ++i)
             if (er[k + 2 + i]) reenc |= 1u << (kWRs + i);
+        RdpRowsFn<5> fx = (a.p == 7 && k == 5) ? pick_rdp_rows<7, 5>(e[0], e[1]) : nullptr;
+        if (fx) {
+            // the lost RS parities re-encoded in the same pass
+            RsReenc re{};
+            Gf8Tab<5 * kChunkMaxM> rt{};
+            uint8_t C[kRs8MaxM * kRs8MaxK];
+            cauchy(k, m, C);
+            for (int i = 0; i < m; ++i) {
+                if (!er[k + 2 + i]) continue;
+                for (int j = 0; j < k; ++j) perm_tables(C[i * k + j], rt.t[re.n * k + j]);
+                re.out[re.n++] = a.par.p[2 + i];
+            }
+            hipLaunchKernelGGL(fx, dim3(a.cg.nwaves), dim3((a.p - 1) * 64), 0, hs, a.g, a.cg, dd, a.par.p[0],
+                               a.par.p[1], re, rt);
+            reenc = 0;
+        } else {
+            hipLaunchKernelGGL(chunk_rdp_decode_kernel, grid, dim3(kCBS), 0, hs, a.g, a.cg, k, rows, dd,
+                               a.par.p[0], a.par.p[1], plan);
+        }
+        rc = check_launch(fn);
+        if (rc) return rc;
     } else if (nd > 0) {
         return set_error(KVEC_EDECODE, "%s: %d data erasures with %d of %d RS parities lost and P/Q "
                          "lost (%d, %d) cannot be decoded", fn, nd, nrs, m, int(eP), int(eQ));

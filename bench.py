@@ -603,10 +603,10 @@ def bench_chunked(pkg, torch, oracle, dev, seed, warmup):
         "decode_us": dec,
         # rs_3data: 2 data shards (pool) + 3 RS parities read, 3 data shards
         # into the pool; rdp_2data_rs_lost: 3 data + P + Q read, 2 data
-        # written, then the 3 RS parities re-encoded from the 5 data shards
-        "decode_alg_bytes": {"rs_3data": 8 * nr, "rdp_2data_rs_lost": 15 * nr},
+        # shards into the pool and the 3 RS parities written (one pass)
+        "decode_alg_bytes": {"rs_3data": 8 * nr, "rdp_2data_rs_lost": 10 * nr},
         "decode_frac_hbm_peak": {"rs_3data": frac(8 * nr, dec["rs_3data"]),
-                                 "rdp_2data_rs_lost": frac(15 * nr, dec["rdp_2data_rs_lost"])},
+                                 "rdp_2data_rs_lost": frac(10 * nr, dec["rdp_2data_rs_lost"])},
         "decode_byte_exact": True,
         "parity_offload": offload,
         "encode_at_4096_token_chunks": longer,

@@ -121,6 +121,8 @@ def erase(pkg, st, kv, c, erased, gen):
 PATTERNS = [
     [2], [0, 4], [1, 2, 3], [0, 5], [3, 6], [5, 6], [7], [0, 7, 8],
     [0, 1, 7, 8], [2, 5, 7, 8, 9], [4, 6, 9], [5, 6, 7, 8, 9],
+    # the RDP path with every RS parity re-encoded in the same pass
+    [1, 3, 7, 8, 9], [0, 7, 8, 9], [3, 6, 7, 8, 9], [0, 4, 7, 9],
 ]
 
 
