@@ -598,7 +598,7 @@ def bench_chunked(pkg, torch, oracle, dev, seed, warmup):
         "wall_us_per_chunk": round(wall * 1e6 / NCH, 2),
         "encode_us_per_chunk_by_pass": pass_us,
         "alg_bytes_note": "both codes over the same 5 shards (RDP p=7 shortened to k=5): P, Q and 3 RS "
-                          "parities of (p-1)*width bytes each; BASELINE's 518,975,215 B row counts RDP "
+                          "parities of (p-1)*width bytes each; the published 518,975,215 B row counts RDP "
                           "over 6 shards",
         "decode_us": dec,
         # rs_3data: 2 data shards (pool) + 3 RS parities read, 3 data shards

@@ -1,6 +1,6 @@
 /*
  * kvec_oracle.c -- CPU restatement of the GhostServe KV-cache erasure-coding
- * path.  TEST INFRASTRUCTURE ONLY (the checker, never the product): loaded by
+ * path.  TEST INFRASTRUCTURE ONLY (the reference for comparison, never the product): loaded by
  * tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg.
  *
  * Citations are to the reference repository (project-ghostserve/

@@ -1,7 +1,7 @@
 /*
  * kvec_oracle.h -- CPU restatement of the GhostServe KV-cache erasure-coding
- * path.  TEST INFRASTRUCTURE ONLY: this library is the checker that the HIP
- * kernels are compared against.  Only tests/, __graft_entry__.smoke() and the
+ * path.  TEST INFRASTRUCTURE ONLY: the HIP kernels are compared against this
+ * library.  Only tests/, __graft_entry__.smoke() and the
  * cpu_baseline leg of bench.py may load it; the product library never links it.
  *
  * Two codec families:

@@ -1,7 +1,7 @@
 """numpy front end of the CPU oracle (oracle/kvec_oracle.c).
 
-TEST INFRASTRUCTURE ONLY.  This module is the checker the HIP kernels are
-compared against; only tests/, ``__graft_entry__.smoke()`` and the
+TEST INFRASTRUCTURE ONLY.  The HIP kernels are compared against this
+module; only tests/, ``__graft_entry__.smoke()`` and the
 ``cpu_baseline`` leg of bench.py import it.  The product package never does.
 
 Every function takes and returns numpy arrays and mirrors one C entry point of
